@@ -1,0 +1,210 @@
+/*
+ * axf_hip.h — C-ABI of the MI355X (gfx950) quantized decode path.
+ *
+ * Shared library: llm_core_amd/lib/libaxf_hip.so
+ *
+ * Conventions
+ *   - Every entry point returns int: AXF_OK (0) or a negative AXF_ERR_* code;
+ *     axf_hip_last_error() returns the message of the calling thread's last
+ *     failure.  The C++ backend (llm_core_amd/csrc/host/hip_backend.cpp)
+ *     turns non-zero codes into std::runtime_error, as the reference's CUDA
+ *     backend does with check_cuda (src/backend/cuda/cuda_backend.cu:15-25).
+ *   - One axf_ctx = one device + one in-order HIP stream.  Kernel entry points
+ *     enqueue asynchronously on that stream; axf_hip_sync and the d2h copy
+ *     block.  Pointer arguments named W, x, y, xq8, ... are device pointers
+ *     owned by the caller (allocated with axf_hip_alloc or any HIP allocator).
+ *   - Weights are GGUF super-blocks in their native layout: Q4_K 144 B and
+ *     Q6_K 210 B per 256 weights (reference include/axonforge/dtype.hpp:136-155),
+ *     rows contiguous, row r at W + r*row_bytes.
+ *   - Q8_0 activations use the reference's block_q8_0: fp32 d followed by
+ *     32 int8 (36 B per 32 values; src/backend/cpu_x86/kernels/q8_block.hpp:8-15).
+ *   - y is overwritten (not accumulated) unless stated.
+ *   - Alignment: W 16-byte aligned with row_bytes % 16 == 0 for Q4_K; W 4-byte
+ *     aligned with row_bytes even for Q6_K; f32 vectors 16-byte aligned;
+ *     Q8_0 buffers 4-byte aligned.  Violations return AXF_ERR_INVALID_ARG.
+ */
+#ifndef AXF_HIP_H
+#define AXF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AXF_OK 0
+#define AXF_ERR_INVALID_ARG (-1)
+#define AXF_ERR_HIP (-2)
+#define AXF_ERR_UNSUPPORTED (-3)
+#define AXF_ERR_NO_DEVICE (-4)
+#define AXF_ERR_STATE (-5)
+
+/* GGML tensor type ids (reference dtype.hpp:107-124: 12 -> Q4_K_M, 14 -> Q6_K). */
+#define AXF_TYPE_F32 0
+#define AXF_TYPE_Q4_K 12
+#define AXF_TYPE_Q6_K 14
+
+typedef struct axf_ctx axf_ctx;
+
+/* ---- errors / version ---------------------------------------------------- */
+const char* axf_hip_last_error(void);
+int axf_hip_version(int* major, int* minor, int* patch);
+
+/* ---- lifecycle: replaces CudaBackend::initialize / finalize / device_id
+ *      (src/backend/cuda/cuda_backend.cu:137-165) ------------------------------ */
+int axf_hip_device_count(int* count);
+int axf_hip_create(int device, axf_ctx** out);
+int axf_hip_destroy(axf_ctx* ctx);
+int axf_hip_device_name(axf_ctx* ctx, char* buf, int buflen);
+
+/* ---- memory: replaces IBackend::allocate / transfer / synchronize
+ *      (include/axonforge/backend.hpp:51-60; cuda_backend.cu:166-182) ---------- */
+int axf_hip_alloc(axf_ctx* ctx, size_t bytes, void** dptr);
+int axf_hip_free(axf_ctx* ctx, void* dptr);
+int axf_hip_memcpy_h2d(axf_ctx* ctx, void* dst, const void* src, size_t bytes); /* blocking */
+int axf_hip_memcpy_d2h(axf_ctx* ctx, void* dst, const void* src, size_t bytes); /* blocking */
+int axf_hip_memcpy_d2d(axf_ctx* ctx, void* dst, const void* src, size_t bytes); /* async */
+int axf_hip_sync(axf_ctx* ctx);
+
+/* ---- quantized weight path ---------------------------------------------- */
+
+/* Q4_K rows -> fp32, bit-exact with the Q4_K branch of emb_lookup
+ * (src/models/llama_model.cpp:899-928).  y has 256*n_blocks floats. */
+int axf_hip_dequant_q4k(axf_ctx* ctx, float* y, const void* W, int64_t n_blocks);
+
+/* Q6_K rows -> fp32, bit-exact with q6k_row_to_f32 (llama_model.cpp:560-592). */
+int axf_hip_dequant_q6k(axf_ctx* ctx, float* y, const void* W, int64_t n_blocks);
+
+/* fp32 -> Q8_0, bit-exact with quantize_q8_avx2
+ * (src/backend/cpu_x86/kernels/quant_q8_avx2.cpp:33-84).  n % 32 == 0. */
+int axf_hip_quantize_q8_0(axf_ctx* ctx, void* xq8, const float* x, int n);
+
+/* Q4_K x F32 GEMV over all rows: replaces gemv_q4k_avx2_range
+ * (gemv_q4k_avx2.cpp:230-238) called over [0, rows).  cols % 256 == 0. */
+int axf_hip_gemv_q4k_f32(axf_ctx* ctx, float* y, const void* W, const float* x, int rows,
+                         int cols, size_t row_bytes);
+
+/* Q6_K x F32 GEMV: replaces gemv_q6k_avx2_range (gemv_q6k_avx2.cpp:236-244). */
+int axf_hip_gemv_q6k_f32(axf_ctx* ctx, float* y, const void* W, const float* x, int rows,
+                         int cols, size_t row_bytes);
+
+/* Q4_K x Q8_0 GEMV (the decode hot kernel): replaces gemv_q4k_r8_avxvnni_range /
+ * gemv_q4k_r8_avx2_range (gemv_q4k_r8_avxvnni.cpp:177-183, gemv_q4k_r8_avx2.cpp:248-254)
+ * and gemv_q4k_q8_{avx2,avxvnni}_range (gemv_q4k_q8_avx2.cpp:242-252), as dispatched
+ * by gemv_wt_q8 (llama_model.cpp:767-831).  Takes the native layout (no r8 repack).
+ * accumulate != 0 adds into y (fuses the residual add of llama_model.cpp:1277,1324). */
+int axf_hip_gemv_q4k_q8(axf_ctx* ctx, float* y, const void* W, const void* xq8, int rows,
+                        int cols, size_t row_bytes, int accumulate);
+
+/* Q6_K x Q8_0 GEMV: replaces gemv_q6k_q8_avx2_range (gemv_q6k_q8_avx2.cpp:195-205). */
+int axf_hip_gemv_q6k_q8(axf_ctx* ctx, float* y, const void* W, const void* xq8, int rows,
+                        int cols, size_t row_bytes, int accumulate);
+
+/* Batched Q4_K x Q8_0 (chunked prefill / multi-sequence decode):
+ * Y[t*rows + o] = W[o,:] . XQ8[t,:] for t < T, token-major like
+ * gemm_q4k_q8_avx2_range (gemv_q4k_q8_avx2.cpp:257-346); XQ8 row t starts at
+ * block t*(cols/32). */
+int axf_hip_gemm_q4k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
+                        int T, int cols, size_t row_bytes);
+
+/* Greedy pick: *idx_dev = first index of the maximum of x[0..n), the
+ * std::max_element of sample() (llama_model.cpp:1470-1471).  idx_dev is a
+ * device int. */
+int axf_hip_argmax_f32(axf_ctx* ctx, int* idx_dev, const float* x, int n);
+
+/* ---- decode-step operations (llama_forward_token, llama_model.cpp:1207-1333) */
+
+/* y = w*(x*s), s = 1/sqrt(mean(x^2)+eps): rms_norm_out (llama_model.cpp:396-419).
+ * y and/or yq8 (Q8_0 of the result) may be NULL.  n % 32 == 0. */
+int axf_hip_rmsnorm(axf_ctx* ctx, float* y, void* yq8, const float* x, const float* w, int n,
+                    float eps);
+
+/* Host: RopeCache::build (llama_model.cpp:1031-1043), tables [max_pos][head_dim/2]. */
+int axf_rope_table(float* cos_t, float* sin_t, int head_dim, float theta, int max_pos);
+
+/* Rotate-half RoPE with a device cos/sin table: apply_rope / rope_and_store_k
+ * (llama_model.cpp:1046-1080).  dst may equal src. */
+int axf_hip_rope(axf_ctx* ctx, float* dst, const float* src, int pos, int n_heads,
+                 int head_dim, const float* cos_t, const float* sin_t);
+
+/* Single-token GQA attention over an fp32 KV cache whose rows are
+ * n_kv_heads*head_dim floats (llama_model.cpp:1255-1272); seq = positions
+ * 0..seq-1 used.  outq8 (Q8_0 of out) may be NULL.  head_dim in {64,128,256}. */
+int axf_hip_attn_decode(axf_ctx* ctx, float* out, void* outq8, const float* q,
+                        const float* kcache, const float* vcache, int seq, int n_heads,
+                        int n_kv_heads, int head_dim);
+
+/* out = silu(gate)*up as swiglu_avx2 (llama_model.cpp:348-368); out may equal
+ * gate; outq8 may be NULL.  n % 32 == 0. */
+int axf_hip_swiglu(axf_ctx* ctx, float* out, void* outq8, const float* gate, const float* up,
+                   int n);
+
+/* y = a + b (residual add, llama_model.cpp:1277). */
+int axf_hip_add(axf_ctx* ctx, float* y, const float* a, const float* b, int n);
+
+/* out = dequantised row `token` (0 <= token < rows) of a Q4_K/Q6_K matrix
+ * (emb_lookup, llama_model.cpp:882-934). */
+int axf_hip_embed(axf_ctx* ctx, float* out, int qtype, const void* W, int token, int rows,
+                  int cols);
+
+/* ---- timing (stream-ordered HIP events on the context stream) ----------- */
+int axf_hip_timer_start(axf_ctx* ctx);
+int axf_hip_timer_stop(axf_ctx* ctx, float* ms); /* waits for the stop event */
+
+/* ---- synthetic GGUF weights (host code, deterministic) ------------------ */
+/* dst[i] ~ N(mean, std) from a counter-based generator (splitmix64 + Box-Muller);
+ * element i depends only on (seed, i). */
+int axf_synth_normal(float* dst, int64_t n, uint64_t seed, float mean, float stddev);
+/* fp32 -> GGUF blocks (qtype AXF_TYPE_Q4_K or AXF_TYPE_Q6_K), n % 256 == 0. */
+int axf_synth_quantize(int qtype, uint8_t* dst, const float* src, int64_t n);
+/* rows x cols matrix drawn N(0, std) and quantized, written row-major in GGUF
+ * layout; multi-threaded, result independent of the thread count. */
+int axf_synth_weight(int qtype, uint8_t* dst, int64_t rows, int64_t cols, uint64_t seed,
+                     float stddev);
+size_t axf_row_bytes(int qtype, int64_t cols);
+
+/* ---- LLaMA-family decoder on the device (llama_generate's `-b hip` hook,
+ *      the model-level branch of llama_model.cpp:1633-1642) ----------------- */
+typedef struct axf_llama axf_llama;
+
+typedef struct {
+    int n_layer, n_embd, n_heads, n_kv_heads, ffn_dim, n_vocab, n_ctx;
+    float rms_eps, rope_theta;
+} axf_llama_hparams;
+
+int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out);
+int axf_llama_destroy(axf_llama* m);
+/* Register a host tensor by its GGUF name (token_embd.weight, output_norm.weight,
+ * output.weight, blk.N.{attn_norm,ffn_norm,attn_q,attn_k,attn_v,attn_output,
+ * ffn_gate,ffn_up,ffn_down}.weight, optional blk.N.attn_{q,k,v}.bias).  The host
+ * buffer must stay valid until axf_llama_load returns. */
+int axf_llama_set_tensor(axf_llama* m, const char* name, int qtype, const void* host,
+                         size_t bytes);
+/* Upload all registered tensors once and allocate the KV cache and buffers. */
+int axf_llama_load(axf_llama* m);
+size_t axf_llama_device_bytes(axf_llama* m);
+/* Residual stream / KV access (host buffers). */
+int axf_llama_set_x(axf_llama* m, const float* x);
+int axf_llama_get_x(axf_llama* m, float* x);
+int axf_llama_set_kv(axf_llama* m, int layer, const float* k, const float* v, int n_pos);
+int axf_llama_fill_kv_random(axf_llama* m, int n_pos, uint64_t seed);
+int axf_llama_get_logits(axf_llama* m, float* logits);
+/* One decoder layer at `pos` on the residual stream (eager). */
+int axf_llama_forward_layer(axf_llama* m, int layer, int pos);
+/* Full single-token forward (embedding .. logits), eager. */
+int axf_llama_forward_token(axf_llama* m, int token, int pos);
+/* Greedy generation: token-by-token prefill of the prompt, then n_gen tokens
+ * (greedy loop of llama_generate_cpu_impl, llama_model.cpp:1595-1624, without
+ * EOS).  use_graph != 0 replays one captured HIP graph per step. */
+int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_gen,
+                       int32_t* out_tokens, int use_graph);
+/* Time `steps` graph-replayed decode steps starting at position start_pos
+ * (KV positions below start_pos must already be filled) after `warmup`
+ * untimed steps; *ms = elapsed milliseconds of the timed steps. */
+int axf_llama_bench_decode(axf_llama* m, int start_pos, int warmup, int steps, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,140 @@
+"""ctypes binding of include/axf_hip.h (libaxf_hip.so).
+
+The library is loaded from llm_core_amd/lib/.  There is no fallback: if the
+shared object is missing or a symbol is absent, import fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libaxf_hip.so"
+
+AXF_OK = 0
+AXF_ERR_INVALID_ARG = -1
+AXF_ERR_HIP = -2
+AXF_ERR_UNSUPPORTED = -3
+AXF_ERR_NO_DEVICE = -4
+AXF_ERR_STATE = -5
+
+AXF_TYPE_F32 = 0
+AXF_TYPE_Q4_K = 12
+AXF_TYPE_Q6_K = 14
+
+
+class AxfError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class LlamaHparams(C.Structure):
+    _fields_ = [
+        ("n_layer", C.c_int),
+        ("n_embd", C.c_int),
+        ("n_heads", C.c_int),
+        ("n_kv_heads", C.c_int),
+        ("ffn_dim", C.c_int),
+        ("n_vocab", C.c_int),
+        ("n_ctx", C.c_int),
+        ("rms_eps", C.c_float),
+        ("rope_theta", C.c_float),
+    ]
+
+
+vp = C.c_void_p
+i32 = C.c_int
+i64 = C.c_int64
+u64 = C.c_uint64
+f32 = C.c_float
+sz = C.c_size_t
+fp = C.POINTER(C.c_float)
+
+# name -> argtypes (all return int unless listed in _RESTYPES)
+SIGNATURES: dict[str, list] = {
+    "axf_hip_last_error": [],
+    "axf_hip_version": [C.POINTER(i32), C.POINTER(i32), C.POINTER(i32)],
+    "axf_hip_device_count": [C.POINTER(i32)],
+    "axf_hip_create": [i32, C.POINTER(vp)],
+    "axf_hip_destroy": [vp],
+    "axf_hip_device_name": [vp, C.c_char_p, i32],
+    "axf_hip_alloc": [vp, sz, C.POINTER(vp)],
+    "axf_hip_free": [vp, vp],
+    "axf_hip_memcpy_h2d": [vp, vp, vp, sz],
+    "axf_hip_memcpy_d2h": [vp, vp, vp, sz],
+    "axf_hip_memcpy_d2d": [vp, vp, vp, sz],
+    "axf_hip_sync": [vp],
+    "axf_hip_dequant_q4k": [vp, vp, vp, i64],
+    "axf_hip_dequant_q6k": [vp, vp, vp, i64],
+    "axf_hip_quantize_q8_0": [vp, vp, vp, i32],
+    "axf_hip_gemv_q4k_f32": [vp, vp, vp, vp, i32, i32, sz],
+    "axf_hip_gemv_q6k_f32": [vp, vp, vp, vp, i32, i32, sz],
+    "axf_hip_gemv_q4k_q8": [vp, vp, vp, vp, i32, i32, sz, i32],
+    "axf_hip_gemv_q6k_q8": [vp, vp, vp, vp, i32, i32, sz, i32],
+    "axf_hip_gemm_q4k_q8": [vp, vp, vp, vp, i32, i32, i32, sz],
+    "axf_hip_argmax_f32": [vp, vp, vp, i32],
+    "axf_hip_rmsnorm": [vp, vp, vp, vp, vp, i32, f32],
+    "axf_rope_table": [vp, vp, i32, f32, i32],
+    "axf_hip_rope": [vp, vp, vp, i32, i32, i32, vp, vp],
+    "axf_hip_attn_decode": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32],
+    "axf_hip_swiglu": [vp, vp, vp, vp, vp, i32],
+    "axf_hip_add": [vp, vp, vp, vp, i32],
+    "axf_hip_embed": [vp, vp, i32, vp, i32, i32, i32],
+    "axf_hip_timer_start": [vp],
+    "axf_hip_timer_stop": [vp, C.POINTER(f32)],
+    "axf_synth_normal": [vp, i64, u64, f32, f32],
+    "axf_synth_quantize": [i32, vp, vp, i64],
+    "axf_synth_weight": [i32, vp, i64, i64, u64, f32],
+    "axf_row_bytes": [i32, i64],
+    "axf_llama_create": [vp, C.POINTER(LlamaHparams), C.POINTER(vp)],
+    "axf_llama_destroy": [vp],
+    "axf_llama_set_tensor": [vp, C.c_char_p, i32, vp, sz],
+    "axf_llama_load": [vp],
+    "axf_llama_device_bytes": [vp],
+    "axf_llama_set_x": [vp, vp],
+    "axf_llama_get_x": [vp, vp],
+    "axf_llama_set_kv": [vp, i32, vp, vp, i32],
+    "axf_llama_fill_kv_random": [vp, i32, u64],
+    "axf_llama_get_logits": [vp, vp],
+    "axf_llama_forward_layer": [vp, i32, i32],
+    "axf_llama_forward_token": [vp, i32, i32],
+    "axf_llama_generate": [vp, vp, i32, i32, vp, i32],
+    "axf_llama_bench_decode": [vp, i32, i32, i32, C.POINTER(f32)],
+}
+
+_RESTYPES = {
+    "axf_hip_last_error": C.c_char_p,
+    "axf_row_bytes": sz,
+    "axf_llama_device_bytes": sz,
+}
+
+
+def _load() -> C.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m llm_core_amd.build` "
+            "(there is no CPU fallback for the HIP path)"
+        )
+    lib = C.CDLL(str(LIB_PATH))
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError if the symbol is missing
+        fn.argtypes = args
+        fn.restype = _RESTYPES.get(name, C.c_int)
+    return lib
+
+
+lib = _load()
+
+
+def last_error() -> str:
+    msg = lib.axf_hip_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int) -> None:
+    if rc != AXF_OK:
+        raise AxfError(rc, last_error())
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib, name)(*args))

@@ -1,0 +1,396 @@
+// capi.cpp — C-ABI entry points of libaxf_hip.so (declared in include/axf_hip.h).
+#include "capi_internal.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+namespace axf {
+
+static thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+    return fail(AXF_ERR_HIP, std::string(where) + ": " + hipGetErrorString(e));
+}
+
+int ctx_scratch(axf_ctx* ctx, size_t bytes, void** p) {
+    if (ctx->scratch_bytes < bytes) {
+        if (ctx->scratch) (void)hipFree(ctx->scratch);
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+        size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
+        hipError_t e = hipMalloc(&ctx->scratch, sz);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(scratch)");
+        ctx->scratch_bytes = sz;
+    }
+    *p = ctx->scratch;
+    return AXF_OK;
+}
+
+}  // namespace axf
+
+using namespace axf;
+
+#define AXF_CHECK_CTX(ctx) \
+    if (!(ctx)) return fail(AXF_ERR_INVALID_ARG, std::string(__func__) + ": null context")
+#define AXF_REQUIRE(cond, msg) \
+    if (!(cond)) return fail(AXF_ERR_INVALID_ARG, std::string(__func__) + ": " + (msg))
+#define AXF_HIP(call)                                          \
+    do {                                                       \
+        hipError_t e_ = (call);                                \
+        if (e_ != hipSuccess) return hip_fail(e_, __func__);   \
+    } while (0)
+
+static inline bool aligned(const void* p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+extern "C" {
+
+const char* axf_hip_last_error(void) { return g_last_error.c_str(); }
+
+int axf_hip_version(int* major, int* minor, int* patch) {
+    if (major) *major = 0;
+    if (minor) *minor = 1;
+    if (patch) *patch = 0;
+    return AXF_OK;
+}
+
+int axf_hip_device_count(int* count) {
+    AXF_REQUIRE(count, "null count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;
+    *count = n;
+    return AXF_OK;
+}
+
+int axf_hip_create(int device, axf_ctx** out) {
+    AXF_REQUIRE(out, "null out");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return fail(AXF_ERR_NO_DEVICE, "axf_hip_create: no HIP device");
+    AXF_REQUIRE(device >= 0 && device < n, "device index out of range");
+    AXF_HIP(hipSetDevice(device));
+    auto* ctx = new axf_ctx();
+    ctx->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->ev0);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->ev1);
+    if (e != hipSuccess) {
+        delete ctx;
+        return hip_fail(e, "axf_hip_create");
+    }
+    *out = ctx;
+    return AXF_OK;
+}
+
+int axf_hip_destroy(axf_ctx* ctx) {
+    if (!ctx) return AXF_OK;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    (void)hipEventDestroy(ctx->ev0);
+    (void)hipEventDestroy(ctx->ev1);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return AXF_OK;
+}
+
+int axf_hip_device_name(axf_ctx* ctx, char* buf, int buflen) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(buf && buflen > 0, "null buffer");
+    hipDeviceProp_t prop;
+    AXF_HIP(hipGetDeviceProperties(&prop, ctx->device));
+    std::snprintf(buf, (size_t)buflen, "%s (%s, %d CUs)", prop.name, prop.gcnArchName,
+                  prop.multiProcessorCount);
+    return AXF_OK;
+}
+
+int axf_hip_alloc(axf_ctx* ctx, size_t bytes, void** dptr) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(dptr, "null out pointer");
+    *dptr = nullptr;
+    if (bytes == 0) return AXF_OK;
+    AXF_HIP(hipMalloc(dptr, bytes));
+    return AXF_OK;
+}
+
+int axf_hip_free(axf_ctx* ctx, void* dptr) {
+    AXF_CHECK_CTX(ctx);
+    if (dptr) AXF_HIP(hipFree(dptr));
+    return AXF_OK;
+}
+
+int axf_hip_memcpy_h2d(axf_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    AXF_CHECK_CTX(ctx);
+    if (!bytes) return AXF_OK;
+    AXF_REQUIRE(dst && src, "null pointer");
+    AXF_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    AXF_HIP(hipStreamSynchronize(ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_memcpy_d2h(axf_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    AXF_CHECK_CTX(ctx);
+    if (!bytes) return AXF_OK;
+    AXF_REQUIRE(dst && src, "null pointer");
+    AXF_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    AXF_HIP(hipStreamSynchronize(ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_memcpy_d2d(axf_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    AXF_CHECK_CTX(ctx);
+    if (!bytes) return AXF_OK;
+    AXF_REQUIRE(dst && src, "null pointer");
+    AXF_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_sync(axf_ctx* ctx) {
+    AXF_CHECK_CTX(ctx);
+    AXF_HIP(hipStreamSynchronize(ctx->stream));
+    return AXF_OK;
+}
+
+// ---------------------------------------------------------------------------
+
+int axf_hip_dequant_q4k(axf_ctx* ctx, float* y, const void* W, int64_t n_blocks) {
+    AXF_CHECK_CTX(ctx);
+    if (n_blocks == 0) return AXF_OK;
+    AXF_REQUIRE(n_blocks > 0 && y && W, "bad arguments");
+    AXF_REQUIRE(aligned(W, 16) && aligned(y, 16), "W and y must be 16-byte aligned");
+    AXF_HIP(launch_dequant_q4k(y, W, (long)n_blocks, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_dequant_q6k(axf_ctx* ctx, float* y, const void* W, int64_t n_blocks) {
+    AXF_CHECK_CTX(ctx);
+    if (n_blocks == 0) return AXF_OK;
+    AXF_REQUIRE(n_blocks > 0 && y && W, "bad arguments");
+    AXF_REQUIRE(aligned(W, 2) && aligned(y, 4), "W must be 2-byte and y 4-byte aligned");
+    AXF_HIP(launch_dequant_q6k(y, W, (long)n_blocks, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_quantize_q8_0(axf_ctx* ctx, void* xq8, const float* x, int n) {
+    AXF_CHECK_CTX(ctx);
+    if (n == 0) return AXF_OK;
+    AXF_REQUIRE(n > 0 && n % 32 == 0, "n must be a positive multiple of 32");
+    AXF_REQUIRE(xq8 && x && aligned(x, 16) && aligned(xq8, 4), "bad pointers/alignment");
+    AXF_HIP(launch_quantize_q8_0(xq8, x, n, ctx->stream));
+    return AXF_OK;
+}
+
+static int check_gemv(const char* fn, int qtype, const void* W, const void* x, const float* y,
+                      int rows, int cols, size_t row_bytes, bool f32x) {
+    if (rows < 0 || cols < 0) return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": negative size");
+    if (cols % QK_K != 0)
+        return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": cols must be a multiple of 256");
+    const int nb = cols / QK_K;
+    if (nb > kMaxBlocksPerRow)
+        return fail(AXF_ERR_UNSUPPORTED, std::string(fn) + ": cols > 32768 not supported");
+    const size_t min_rb = (size_t)nb * (qtype == AXF_TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES);
+    if (row_bytes < min_rb)
+        return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": row_bytes smaller than one row");
+    if (!W || !x || !y) return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": null pointer");
+    if (qtype == AXF_TYPE_Q4_K) {
+        if (!aligned(W, 16) || row_bytes % 16)
+            return fail(AXF_ERR_INVALID_ARG,
+                        std::string(fn) + ": Q4_K needs 16-byte aligned W and row_bytes");
+    } else {
+        if (!aligned(W, 4) || row_bytes % 2)
+            return fail(AXF_ERR_INVALID_ARG,
+                        std::string(fn) + ": Q6_K needs 4-byte aligned W and even row_bytes");
+    }
+    if (!aligned(y, 4)) return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": y misaligned");
+    if (f32x) {
+        if (!aligned(x, 16)) return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": x misaligned");
+        const size_t lds = (size_t)cols * 4 * (qtype == AXF_TYPE_Q4_K ? 17 : 18) / 16;
+        if (lds > 65536)
+            return fail(AXF_ERR_UNSUPPORTED, std::string(fn) + ": cols too large for F32 path");
+    } else if (!aligned(x, 4)) {
+        return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": xq8 misaligned");
+    }
+    return AXF_OK;
+}
+
+static int do_gemv(axf_ctx* ctx, const char* fn, GemvKind kind, int qtype, float* y,
+                   const void* W, const void* x, int rows, int cols, size_t row_bytes,
+                   int accumulate) {
+    if (!ctx) return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": null context");
+    const bool f32x = (kind == GemvKind::Q4K_F32 || kind == GemvKind::Q6K_F32);
+    int rc = check_gemv(fn, qtype, W, x, y, rows, cols, row_bytes, f32x);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0) return AXF_OK;
+    hipError_t e = launch_gemv(kind, y, W, x, rows, cols / QK_K, (long)row_bytes,
+                               accumulate ? 1 : 0, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, fn);
+    return AXF_OK;
+}
+
+int axf_hip_gemv_q4k_f32(axf_ctx* ctx, float* y, const void* W, const float* x, int rows,
+                         int cols, size_t row_bytes) {
+    return do_gemv(ctx, __func__, GemvKind::Q4K_F32, AXF_TYPE_Q4_K, y, W, x, rows, cols,
+                   row_bytes, 0);
+}
+int axf_hip_gemv_q6k_f32(axf_ctx* ctx, float* y, const void* W, const float* x, int rows,
+                         int cols, size_t row_bytes) {
+    return do_gemv(ctx, __func__, GemvKind::Q6K_F32, AXF_TYPE_Q6_K, y, W, x, rows, cols,
+                   row_bytes, 0);
+}
+int axf_hip_gemv_q4k_q8(axf_ctx* ctx, float* y, const void* W, const void* xq8, int rows,
+                        int cols, size_t row_bytes, int accumulate) {
+    return do_gemv(ctx, __func__, GemvKind::Q4K_Q8, AXF_TYPE_Q4_K, y, W, xq8, rows, cols,
+                   row_bytes, accumulate);
+}
+int axf_hip_gemv_q6k_q8(axf_ctx* ctx, float* y, const void* W, const void* xq8, int rows,
+                        int cols, size_t row_bytes, int accumulate) {
+    return do_gemv(ctx, __func__, GemvKind::Q6K_Q8, AXF_TYPE_Q6_K, y, W, xq8, rows, cols,
+                   row_bytes, accumulate);
+}
+
+int axf_hip_gemm_q4k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows, int T,
+                        int cols, size_t row_bytes) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(T >= 0, "negative T");
+    int rc = check_gemv(__func__, AXF_TYPE_Q4_K, W, XQ8, Y, rows, cols, row_bytes, false);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0 || T == 0) return AXF_OK;
+    AXF_HIP(launch_gemm_q4k_q8(Y, W, XQ8, rows, T, cols / QK_K, (long)row_bytes, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_argmax_f32(axf_ctx* ctx, int* idx_dev, const float* x, int n) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(idx_dev && x && n > 0, "bad arguments");
+    void* scratch = nullptr;
+    const int parts = argmax_parts();
+    int rc = ctx_scratch(ctx, (size_t)parts * 8, &scratch);
+    if (rc) return rc;
+    float* pv = static_cast<float*>(scratch);
+    int* pi = reinterpret_cast<int*>(pv + parts);
+    AXF_HIP(launch_argmax(idx_dev, pv, pi, x, n, nullptr, nullptr, nullptr, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_rmsnorm(axf_ctx* ctx, float* y, void* yq8, const float* x, const float* w, int n,
+                    float eps) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(n > 0 && n % 32 == 0, "n must be a positive multiple of 32");
+    AXF_REQUIRE(x && w && (y || yq8), "bad pointers");
+    AXF_REQUIRE(aligned(x, 16) && aligned(w, 16) && (!y || aligned(y, 16)) &&
+                    (!yq8 || aligned(yq8, 4)),
+                "misaligned pointer");
+    AXF_HIP(launch_rmsnorm(y, yq8, x, w, n, eps, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_rope(axf_ctx* ctx, float* dst, const float* src, int pos, int n_heads, int head_dim,
+                 const float* cos_t, const float* sin_t) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(dst && src && cos_t && sin_t, "null pointer");
+    AXF_REQUIRE(pos >= 0 && n_heads > 0 && head_dim > 0 && head_dim % 2 == 0, "bad shape");
+    AXF_HIP(launch_rope(dst, src, nullptr, pos, n_heads, head_dim, cos_t, sin_t, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_attn_decode(axf_ctx* ctx, float* out, void* outq8, const float* q,
+                        const float* kcache, const float* vcache, int seq, int n_heads,
+                        int n_kv_heads, int head_dim) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(out && q && kcache && vcache, "null pointer");
+    AXF_REQUIRE(seq > 0 && n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                "bad shape");
+    AXF_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
+                "head_dim must be 64, 128 or 256");
+    AXF_REQUIRE(aligned(q, 16) && aligned(kcache, 16) && aligned(vcache, 16) && aligned(out, 4),
+                "misaligned pointer");
+    const int nsplit = attn_nsplit(seq);
+    void* scratch = nullptr;
+    int rc = ctx_scratch(ctx, (size_t)n_heads * nsplit * (head_dim + 2) * 4, &scratch);
+    if (rc) return rc;
+    AXF_HIP(launch_attention(out, outq8, static_cast<float*>(scratch), q, kcache, vcache,
+                             nullptr, seq, nsplit, n_heads, n_kv_heads, head_dim, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_swiglu(axf_ctx* ctx, float* out, void* outq8, const float* gate, const float* up,
+                   int n) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(n > 0 && n % 32 == 0, "n must be a positive multiple of 32");
+    AXF_REQUIRE(gate && up && (out || outq8), "null pointer");
+    AXF_REQUIRE(aligned(gate, 16) && aligned(up, 16) && (!out || aligned(out, 16)),
+                "misaligned pointer");
+    AXF_HIP(launch_swiglu(out, outq8, gate, up, n, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_add(axf_ctx* ctx, float* y, const float* a, const float* b, int n) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(y && a && b && n >= 0, "bad arguments");
+    if (n == 0) return AXF_OK;
+    AXF_HIP(launch_add(y, a, b, n, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_embed(axf_ctx* ctx, float* out, int qtype, const void* W, int token, int rows,
+                  int cols) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(out && W && cols > 0 && cols % QK_K == 0, "bad arguments");
+    AXF_REQUIRE(token >= 0 && token < rows, "token out of range");
+    AXF_REQUIRE(qtype == AXF_TYPE_Q4_K || qtype == AXF_TYPE_Q6_K, "qtype must be Q4_K or Q6_K");
+    AXF_REQUIRE(qtype == AXF_TYPE_Q6_K ? aligned(W, 2) : aligned(W, 16), "W misaligned");
+    const int nb = cols / QK_K;
+    AXF_HIP(launch_embed(qtype, out, W, nullptr, token, nb,
+                         (long)axf_row_bytes(qtype, cols), ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_timer_start(axf_ctx* ctx) {
+    AXF_CHECK_CTX(ctx);
+    AXF_HIP(hipEventRecord(ctx->ev0, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_timer_stop(axf_ctx* ctx, float* ms) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(ms, "null out");
+    AXF_HIP(hipEventRecord(ctx->ev1, ctx->stream));
+    AXF_HIP(hipEventSynchronize(ctx->ev1));
+    AXF_HIP(hipEventElapsedTime(ms, ctx->ev0, ctx->ev1));
+    return AXF_OK;
+}
+
+size_t axf_row_bytes(int qtype, int64_t cols) {
+    const int64_t nb = cols / QK_K;
+    if (qtype == AXF_TYPE_Q4_K) return (size_t)nb * Q4K_BYTES;
+    if (qtype == AXF_TYPE_Q6_K) return (size_t)nb * Q6K_BYTES;
+    if (qtype == AXF_TYPE_F32) return (size_t)cols * 4;
+    return 0;
+}
+
+int axf_rope_table(float* cos_t, float* sin_t, int hd, float theta, int max_pos) {
+    AXF_REQUIRE(cos_t && sin_t && hd > 0 && hd % 2 == 0 && max_pos > 0, "bad arguments");
+    // RopeCache::build (llama_model.cpp:1031-1043): float pow/cos/sin from libm.
+    const int half = hd / 2;
+    for (int p = 0; p < max_pos; p++) {
+        for (int i = 0; i < half; i++) {
+            const float freq = 1.f / std::pow(theta, (float)(2 * i) / (float)hd);
+            const float angle = (float)p * freq;
+            cos_t[(size_t)p * half + i] = std::cos(angle);
+            sin_t[(size_t)p * half + i] = std::sin(angle);
+        }
+    }
+    return AXF_OK;
+}
+
+}  // extern "C"

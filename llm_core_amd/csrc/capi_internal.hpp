@@ -1,0 +1,66 @@
+// capi_internal.hpp — shared between the C-ABI, the decoder and the kernels' launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/axf_hip.h"
+
+struct axf_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void* scratch = nullptr;  // grown on demand by eager entry points (never during capture)
+    size_t scratch_bytes = 0;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+namespace axf {
+
+constexpr int QK_K = 256;
+constexpr int Q4K_BYTES = 144;
+constexpr int Q6K_BYTES = 210;
+constexpr int Q8_0_BYTES = 36;
+constexpr int kMaxBlocksPerRow = 128;
+
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* where);
+int ctx_scratch(axf_ctx* ctx, size_t bytes, void** p);
+
+enum class GemvKind { Q4K_Q8, Q4K_F32, Q6K_Q8, Q6K_F32 };
+
+hipError_t launch_gemv(GemvKind kind, float* y, const void* W, const void* x, int rows, int nb,
+                       long row_bytes, int accumulate, hipStream_t st);
+hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
+                              long row_bytes, hipStream_t st);
+hipError_t launch_dequant_q4k(float* y, const void* W, long nblocks, hipStream_t st);
+hipError_t launch_dequant_q6k(float* y, const void* W, long nblocks, hipStream_t st);
+hipError_t launch_quantize_q8_0(void* y, const float* x, int n, hipStream_t st);
+hipError_t launch_rmsnorm(float* y, void* yq8, const float* x, const float* w, int n, float eps,
+                          hipStream_t st);
+hipError_t launch_rope(float* dst, const float* src, const int* pos_dev, int pos, int n_heads,
+                       int hd, const float* cos_t, const float* sin_t, hipStream_t st);
+hipError_t launch_rope_qkv(float* q, const float* k, const float* v, float* kcache,
+                           float* vcache, const int* pos_dev, int pos, int n_heads,
+                           int n_kv_heads, int hd, const float* cos_t, const float* sin_t,
+                           hipStream_t st);
+int attn_nsplit(int max_seq);
+hipError_t launch_attention(float* out, void* outq8, float* part, const float* q,
+                            const float* kcache, const float* vcache, const int* pos_dev,
+                            int seq, int nsplit, int n_heads, int n_kv_heads, int hd,
+                            hipStream_t st);
+hipError_t launch_swiglu(float* out, void* outq8, const float* gate, const float* up, int n,
+                         hipStream_t st);
+hipError_t launch_embed(int qtype, float* out, const void* W, const int* tok_dev, int tok,
+                        int nb, long row_bytes, hipStream_t st);
+int argmax_parts();
+hipError_t launch_argmax(int* out, float* pv, int* pi, const float* x, int n, int* tokens,
+                         int* step, int* pos, hipStream_t st);
+hipError_t launch_add(float* y, const float* a, const float* b, int n, hipStream_t st);
+hipError_t launch_silu(float* y, const float* x, int n, hipStream_t st);
+hipError_t launch_mul(float* y, const float* a, const float* b, int n, hipStream_t st);
+hipError_t launch_set_int(int* p, int v, hipStream_t st);
+hipError_t launch_push_token(int* tokens, int* step, const int* tok, hipStream_t st);
+
+}  // namespace axf

@@ -1,0 +1,527 @@
+// llama_hip.cpp — LLaMA-family decoder on one MI355X (the model-level `-b hip`
+// hook, mirroring what llama_generate's backend branch selects at
+// src/models/llama_model.cpp:1633-1642 and the per-token body of
+// llama_forward_token, :1207-1333).
+//
+// Device layout (allocated once by axf_llama_load):
+//   * weights in native GGUF blocks; attn_q|attn_k and ffn_gate|ffn_up are
+//     placed back to back when both are Q4_K, so each pair is one GEMV launch
+//     whose output is q|k (resp. gate|up) contiguous;
+//   * KV cache fp32 [layer][n_ctx][n_kv_heads*head_dim], K stored after RoPE
+//     (LlamaState, :1102-1106);
+//   * RoPE cos/sin table [n_ctx][head_dim/2] built on the host (:1031-1043);
+//   * token id, position and step counters in device memory, so one captured
+//     HIP graph replays every decode step: the argmax at the end of a step
+//     writes the next token and advances the position.
+//
+// Step (per layer): rmsnorm->q8 | gemv q|k | gemv v | rope q,k + store k,v |
+// attention split + combine->q8 | gemv o (+= x) | rmsnorm->q8 | gemv gate|up |
+// swiglu->q8 | gemv down (+= x); then rmsnorm->q8 | gemv head | argmax.
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../capi_internal.hpp"
+
+using namespace axf;
+
+namespace {
+
+struct HostTensor {
+    int qtype = -1;
+    const void* host = nullptr;
+    size_t bytes = 0;
+};
+
+struct DevW {
+    int qtype = -1;
+    uint8_t* d = nullptr;
+    size_t row_bytes = 0;
+};
+
+struct Layer {
+    float* attn_norm = nullptr;
+    float* ffn_norm = nullptr;
+    DevW wq, wk, wv, wo, wgate, wup, wdown;
+    bool qk_fused = false, gateup_fused = false;
+    float *bq = nullptr, *bk = nullptr, *bv = nullptr;
+};
+
+}  // namespace
+
+struct axf_llama {
+    axf_ctx* ctx = nullptr;
+    axf_llama_hparams hp{};
+    int hd = 0, kv_embd = 0;
+    std::map<std::string, HostTensor> pending;
+    bool loaded = false;
+
+    std::vector<void*> allocs;
+    size_t dev_bytes = 0;
+
+    DevW tok_embd, output;
+    float* output_norm = nullptr;
+    std::vector<Layer> layers;
+
+    float *kv_k = nullptr, *kv_v = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
+    float *x = nullptr, *qkv = nullptr, *attn_out = nullptr, *gateup = nullptr, *logits = nullptr;
+    uint8_t* xq8 = nullptr;
+    float* attn_part = nullptr;
+    int nsplit = 0;
+    float* arg_v = nullptr;
+    int* arg_i = nullptr;
+    int *d_token = nullptr, *d_pos = nullptr, *d_step = nullptr, *d_tokens = nullptr;
+    int max_tokens = 0;
+
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+int dalloc(axf_llama* m, size_t bytes, void** p) {
+    *p = nullptr;
+    if (!bytes) return AXF_OK;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) return hip_fail(e, "axf_llama: hipMalloc");
+    m->allocs.push_back(*p);
+    m->dev_bytes += bytes;
+    return AXF_OK;
+}
+
+#define LL_TRY(expr)              \
+    do {                          \
+        int rc_ = (expr);         \
+        if (rc_) return rc_;      \
+    } while (0)
+#define LL_HIP(call)                                             \
+    do {                                                         \
+        hipError_t e_ = (call);                                  \
+        if (e_ != hipSuccess) return hip_fail(e_, __func__);     \
+    } while (0)
+
+const HostTensor* find(axf_llama* m, const std::string& name) {
+    auto it = m->pending.find(name);
+    return it == m->pending.end() ? nullptr : &it->second;
+}
+
+int need(axf_llama* m, const std::string& name, const HostTensor** t) {
+    *t = find(m, name);
+    if (!*t) return fail(AXF_ERR_STATE, "axf_llama_load: missing tensor " + name);
+    return AXF_OK;
+}
+
+int upload(axf_llama* m, void* dst, const void* src, size_t bytes) {
+    LL_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, m->ctx->stream));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    return AXF_OK;
+}
+
+int upload_f32(axf_llama* m, const std::string& name, int n, float** out, bool required) {
+    const HostTensor* t = find(m, name);
+    if (!t) {
+        *out = nullptr;
+        return required ? fail(AXF_ERR_STATE, "axf_llama_load: missing tensor " + name) : AXF_OK;
+    }
+    if (t->qtype != AXF_TYPE_F32 || t->bytes != (size_t)n * 4)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_load: " + name + " must be F32 of " +
+                                             std::to_string(n) + " floats");
+    void* p;
+    LL_TRY(dalloc(m, t->bytes, &p));
+    LL_TRY(upload(m, p, t->host, t->bytes));
+    *out = static_cast<float*>(p);
+    return AXF_OK;
+}
+
+int check_q(const std::string& name, const HostTensor* t, int rows, int cols) {
+    if (t->qtype != AXF_TYPE_Q4_K && t->qtype != AXF_TYPE_Q6_K)
+        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_load: " + name + " must be Q4_K or Q6_K");
+    if (t->bytes != (size_t)rows * axf_row_bytes(t->qtype, cols))
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_load: " + name + " has wrong byte size");
+    return AXF_OK;
+}
+
+// Upload one or two quantized matrices; two matrices of the same qtype are
+// placed back to back (so they can run as one GEMV).
+int upload_pair(axf_llama* m, const std::string& n1, int rows1, const std::string& n2, int rows2,
+                int cols, DevW* w1, DevW* w2, bool* fused) {
+    const HostTensor *t1, *t2;
+    LL_TRY(need(m, n1, &t1));
+    LL_TRY(check_q(n1, t1, rows1, cols));
+    if (w2) {
+        LL_TRY(need(m, n2, &t2));
+        LL_TRY(check_q(n2, t2, rows2, cols));
+    }
+    const bool pair = w2 && t2->qtype == t1->qtype && t1->qtype == AXF_TYPE_Q4_K;
+    if (fused) *fused = pair;
+    void* p;
+    LL_TRY(dalloc(m, t1->bytes + (pair ? t2->bytes : 0), &p));
+    LL_TRY(upload(m, p, t1->host, t1->bytes));
+    *w1 = DevW{t1->qtype, static_cast<uint8_t*>(p), axf_row_bytes(t1->qtype, cols)};
+    if (w2) {
+        void* p2;
+        if (pair) {
+            p2 = static_cast<uint8_t*>(p) + t1->bytes;
+        } else {
+            LL_TRY(dalloc(m, t2->bytes, &p2));
+        }
+        LL_TRY(upload(m, p2, t2->host, t2->bytes));
+        *w2 = DevW{t2->qtype, static_cast<uint8_t*>(p2), axf_row_bytes(t2->qtype, cols)};
+    }
+    return AXF_OK;
+}
+
+hipError_t gemv(const DevW& w, float* y, const void* xq8, int rows, int cols, bool acc,
+                hipStream_t st) {
+    return launch_gemv(w.qtype == AXF_TYPE_Q4_K ? GemvKind::Q4K_Q8 : GemvKind::Q6K_Q8, y, w.d,
+                       xq8, rows, cols / QK_K, (long)w.row_bytes, acc ? 1 : 0, st);
+}
+
+// Enqueue one decoder layer; pos from device memory when pos_dev != nullptr.
+hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
+    const auto& hp = m->hp;
+    const int E = hp.n_embd, H = hp.n_heads, KVH = hp.n_kv_heads, HD = m->hd, FD = hp.ffn_dim;
+    const int qo = H * HD, kvo = KVH * HD;
+    hipStream_t st = m->ctx->stream;
+    const Layer& L = m->layers[l];
+    float* q = m->qkv;
+    float* k = m->qkv + qo;
+    float* v = m->qkv + qo + kvo;
+    const size_t loff = (size_t)l * hp.n_ctx * m->kv_embd;
+    hipError_t e;
+#define ST(call)               \
+    if ((e = (call)) != hipSuccess) return e;
+    ST(launch_rmsnorm(nullptr, m->xq8, m->x, L.attn_norm, E, hp.rms_eps, st));
+    if (L.qk_fused) {
+        ST(gemv(L.wq, q, m->xq8, qo + kvo, E, false, st));
+    } else {
+        ST(gemv(L.wq, q, m->xq8, qo, E, false, st));
+        ST(gemv(L.wk, k, m->xq8, kvo, E, false, st));
+    }
+    ST(gemv(L.wv, v, m->xq8, kvo, E, false, st));
+    if (L.bq) ST(launch_add(q, q, L.bq, qo, st));
+    if (L.bk) ST(launch_add(k, k, L.bk, kvo, st));
+    if (L.bv) ST(launch_add(v, v, L.bv, kvo, st));
+    ST(launch_rope_qkv(q, k, v, m->kv_k + loff, m->kv_v + loff, pos_dev, pos, H, KVH, HD,
+                       m->rope_cos, m->rope_sin, st));
+    ST(launch_attention(m->attn_out, m->xq8, m->attn_part, q, m->kv_k + loff, m->kv_v + loff,
+                        pos_dev, pos + 1, m->nsplit, H, KVH, HD, st));
+    ST(gemv(L.wo, m->x, m->xq8, E, E, true, st));
+    ST(launch_rmsnorm(nullptr, m->xq8, m->x, L.ffn_norm, E, hp.rms_eps, st));
+    if (L.gateup_fused) {
+        ST(gemv(L.wgate, m->gateup, m->xq8, 2 * FD, E, false, st));
+    } else {
+        ST(gemv(L.wgate, m->gateup, m->xq8, FD, E, false, st));
+        ST(gemv(L.wup, m->gateup + FD, m->xq8, FD, E, false, st));
+    }
+    ST(launch_swiglu(nullptr, m->xq8, m->gateup, m->gateup + FD, FD, st));
+    ST(gemv(L.wdown, m->x, m->xq8, E, FD, true, st));
+#undef ST
+    return hipSuccess;
+}
+
+// Whole step: embedding of *d_token (or `token`), layers, final norm, head,
+// argmax into d_token (+ tokens[step++], pos++ when record != 0).
+hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, bool record) {
+    const auto& hp = m->hp;
+    hipStream_t st = m->ctx->stream;
+    const int* pd = device_state ? m->d_pos : nullptr;
+    const int* td = device_state ? m->d_token : nullptr;
+    hipError_t e = launch_embed(m->tok_embd.qtype, m->x, m->tok_embd.d, td, token,
+                                hp.n_embd / QK_K, (long)m->tok_embd.row_bytes, st);
+    if (e != hipSuccess) return e;
+    for (int l = 0; l < hp.n_layer; l++)
+        if ((e = enqueue_layer(m, l, pd, pos)) != hipSuccess) return e;
+    if ((e = launch_rmsnorm(nullptr, m->xq8, m->x, m->output_norm, hp.n_embd, hp.rms_eps, st)) !=
+        hipSuccess)
+        return e;
+    if ((e = gemv(m->output, m->logits, m->xq8, hp.n_vocab, hp.n_embd, false, st)) != hipSuccess)
+        return e;
+    return launch_argmax(m->d_token, m->arg_v, m->arg_i, m->logits, hp.n_vocab,
+                         record ? m->d_tokens : nullptr, record ? m->d_step : nullptr,
+                         device_state ? m->d_pos : nullptr, st);
+}
+
+int ensure_graph(axf_llama* m) {
+    if (m->exec) return AXF_OK;
+    hipStream_t st = m->ctx->stream;
+    LL_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    hipError_t e = enqueue_step(m, true, 0, 0, true);
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(st, &g);
+    if (e != hipSuccess) return hip_fail(e, "axf_llama: capture");
+    if (e2 != hipSuccess) return hip_fail(e2, "axf_llama: hipStreamEndCapture");
+    m->graph = g;
+    LL_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    return AXF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out) {
+    if (!ctx || !hp || !out) return fail(AXF_ERR_INVALID_ARG, "axf_llama_create: null argument");
+    *out = nullptr;
+    const auto& h = *hp;
+    if (h.n_layer <= 0 || h.n_embd <= 0 || h.n_heads <= 0 || h.n_kv_heads <= 0 ||
+        h.ffn_dim <= 0 || h.n_vocab <= 0 || h.n_ctx <= 0)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_create: non-positive hyperparameter");
+    if (h.n_embd % h.n_heads || h.n_heads % h.n_kv_heads)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_create: heads do not divide");
+    const int hd = h.n_embd / h.n_heads;
+    if (hd != 64 && hd != 128 && hd != 256)
+        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: head_dim must be 64, 128 or 256");
+    if (h.n_embd % QK_K || h.ffn_dim % QK_K)
+        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: n_embd and ffn_dim must be multiples of 256");
+    if (h.n_embd / QK_K > kMaxBlocksPerRow || h.ffn_dim / QK_K > kMaxBlocksPerRow)
+        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: dimension above 32768");
+    auto* m = new axf_llama();
+    m->ctx = ctx;
+    m->hp = h;
+    m->hd = hd;
+    m->kv_embd = h.n_kv_heads * hd;
+    *out = m;
+    return AXF_OK;
+}
+
+int axf_llama_destroy(axf_llama* m) {
+    if (!m) return AXF_OK;
+    (void)hipStreamSynchronize(m->ctx->stream);
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (void* p : m->allocs) (void)hipFree(p);
+    delete m;
+    return AXF_OK;
+}
+
+int axf_llama_set_tensor(axf_llama* m, const char* name, int qtype, const void* host,
+                         size_t bytes) {
+    if (!m || !name || !host) return fail(AXF_ERR_INVALID_ARG, "axf_llama_set_tensor: null argument");
+    if (m->loaded) return fail(AXF_ERR_STATE, "axf_llama_set_tensor: model already loaded");
+    m->pending[name] = HostTensor{qtype, host, bytes};
+    return AXF_OK;
+}
+
+int axf_llama_load(axf_llama* m) {
+    if (!m) return fail(AXF_ERR_INVALID_ARG, "axf_llama_load: null model");
+    if (m->loaded) return AXF_OK;
+    LL_HIP(hipSetDevice(m->ctx->device));
+    const auto& hp = m->hp;
+    const int E = hp.n_embd, FD = hp.ffn_dim, qo = hp.n_heads * m->hd, kvo = m->kv_embd;
+    char nm[128];
+    {
+        const HostTensor* t;
+        LL_TRY(need(m, "token_embd.weight", &t));
+        LL_TRY(check_q("token_embd.weight", t, hp.n_vocab, E));
+        LL_TRY(upload_pair(m, "token_embd.weight", hp.n_vocab, "", 0, E, &m->tok_embd, nullptr,
+                           nullptr));
+        // output.weight falls back to token_embd (make_wt_opt, llama_model.cpp:660-667)
+        if (find(m, "output.weight"))
+            LL_TRY(upload_pair(m, "output.weight", hp.n_vocab, "", 0, E, &m->output, nullptr,
+                               nullptr));
+        else
+            m->output = m->tok_embd;
+        LL_TRY(upload_f32(m, "output_norm.weight", E, &m->output_norm, true));
+    }
+    m->layers.resize(hp.n_layer);
+    for (int l = 0; l < hp.n_layer; l++) {
+        Layer& L = m->layers[l];
+        auto n = [&](const char* s) {
+            std::snprintf(nm, sizeof(nm), "blk.%d.%s", l, s);
+            return std::string(nm);
+        };
+        LL_TRY(upload_f32(m, n("attn_norm.weight"), E, &L.attn_norm, true));
+        LL_TRY(upload_f32(m, n("ffn_norm.weight"), E, &L.ffn_norm, true));
+        LL_TRY(upload_pair(m, n("attn_q.weight"), qo, n("attn_k.weight"), kvo, E, &L.wq, &L.wk,
+                           &L.qk_fused));
+        LL_TRY(upload_pair(m, n("attn_v.weight"), kvo, "", 0, E, &L.wv, nullptr, nullptr));
+        LL_TRY(upload_pair(m, n("attn_output.weight"), E, "", 0, qo, &L.wo, nullptr, nullptr));
+        LL_TRY(upload_pair(m, n("ffn_gate.weight"), FD, n("ffn_up.weight"), FD, E, &L.wgate,
+                           &L.wup, &L.gateup_fused));
+        LL_TRY(upload_pair(m, n("ffn_down.weight"), E, "", 0, FD, &L.wdown, nullptr, nullptr));
+        LL_TRY(upload_f32(m, n("attn_q.bias"), qo, &L.bq, false));
+        LL_TRY(upload_f32(m, n("attn_k.bias"), kvo, &L.bk, false));
+        LL_TRY(upload_f32(m, n("attn_v.bias"), kvo, &L.bv, false));
+    }
+    // KV cache and buffers
+    const size_t kv_floats = (size_t)hp.n_layer * hp.n_ctx * m->kv_embd;
+    void* p;
+    LL_TRY(dalloc(m, kv_floats * 4, &p));
+    m->kv_k = static_cast<float*>(p);
+    LL_TRY(dalloc(m, kv_floats * 4, &p));
+    m->kv_v = static_cast<float*>(p);
+    LL_HIP(hipMemsetAsync(m->kv_k, 0, kv_floats * 4, m->ctx->stream));
+    LL_HIP(hipMemsetAsync(m->kv_v, 0, kv_floats * 4, m->ctx->stream));
+    {
+        std::vector<float> c((size_t)hp.n_ctx * m->hd / 2), s(c.size());
+        axf_rope_table(c.data(), s.data(), m->hd, hp.rope_theta, hp.n_ctx);
+        LL_TRY(dalloc(m, c.size() * 4, &p));
+        m->rope_cos = static_cast<float*>(p);
+        LL_TRY(upload(m, p, c.data(), c.size() * 4));
+        LL_TRY(dalloc(m, s.size() * 4, &p));
+        m->rope_sin = static_cast<float*>(p);
+        LL_TRY(upload(m, p, s.data(), s.size() * 4));
+    }
+    LL_TRY(dalloc(m, (size_t)E * 4, &p));
+    m->x = static_cast<float*>(p);
+    LL_TRY(dalloc(m, (size_t)(qo + 2 * kvo) * 4, &p));
+    m->qkv = static_cast<float*>(p);
+    LL_TRY(dalloc(m, (size_t)qo * 4, &p));
+    m->attn_out = static_cast<float*>(p);
+    LL_TRY(dalloc(m, (size_t)2 * FD * 4, &p));
+    m->gateup = static_cast<float*>(p);
+    LL_TRY(dalloc(m, (size_t)hp.n_vocab * 4, &p));
+    m->logits = static_cast<float*>(p);
+    LL_TRY(dalloc(m, (size_t)((E > FD ? E : FD) / 32) * Q8_0_BYTES, &p));
+    m->xq8 = static_cast<uint8_t*>(p);
+    m->nsplit = attn_nsplit(hp.n_ctx);
+    LL_TRY(dalloc(m, (size_t)hp.n_heads * m->nsplit * (m->hd + 2) * 4, &p));
+    m->attn_part = static_cast<float*>(p);
+    LL_TRY(dalloc(m, (size_t)argmax_parts() * 8, &p));
+    m->arg_v = static_cast<float*>(p);
+    m->arg_i = reinterpret_cast<int*>(m->arg_v + argmax_parts());
+    m->max_tokens = hp.n_ctx + 1;
+    LL_TRY(dalloc(m, (size_t)(3 + m->max_tokens) * 4, &p));
+    m->d_token = static_cast<int*>(p);
+    m->d_pos = m->d_token + 1;
+    m->d_step = m->d_token + 2;
+    m->d_tokens = m->d_token + 3;
+    LL_HIP(hipMemsetAsync(m->d_token, 0, (size_t)(3 + m->max_tokens) * 4, m->ctx->stream));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    m->pending.clear();
+    m->loaded = true;
+    return AXF_OK;
+}
+
+size_t axf_llama_device_bytes(axf_llama* m) { return m ? m->dev_bytes : 0; }
+
+#define LL_LOADED(m)                                                                       \
+    if (!(m)) return fail(AXF_ERR_INVALID_ARG, std::string(__func__) + ": null model");     \
+    if (!(m)->loaded) return fail(AXF_ERR_STATE, std::string(__func__) + ": model not loaded")
+
+int axf_llama_set_x(axf_llama* m, const float* x) {
+    LL_LOADED(m);
+    return upload(m, m->x, x, (size_t)m->hp.n_embd * 4);
+}
+
+int axf_llama_get_x(axf_llama* m, float* x) {
+    LL_LOADED(m);
+    LL_HIP(hipMemcpyAsync(x, m->x, (size_t)m->hp.n_embd * 4, hipMemcpyDeviceToHost,
+                          m->ctx->stream));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    return AXF_OK;
+}
+
+int axf_llama_set_kv(axf_llama* m, int layer, const float* k, const float* v, int n_pos) {
+    LL_LOADED(m);
+    if (layer < 0 || layer >= m->hp.n_layer || n_pos < 0 || n_pos > m->hp.n_ctx || !k || !v)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_set_kv: bad arguments");
+    const size_t off = (size_t)layer * m->hp.n_ctx * m->kv_embd;
+    const size_t bytes = (size_t)n_pos * m->kv_embd * 4;
+    LL_TRY(upload(m, m->kv_k + off, k, bytes));
+    LL_TRY(upload(m, m->kv_v + off, v, bytes));
+    return AXF_OK;
+}
+
+int axf_llama_fill_kv_random(axf_llama* m, int n_pos, uint64_t seed) {
+    LL_LOADED(m);
+    if (n_pos < 0 || n_pos > m->hp.n_ctx)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_fill_kv_random: bad n_pos");
+    std::vector<float> buf((size_t)n_pos * m->kv_embd);
+    for (int l = 0; l < m->hp.n_layer; l++) {
+        const size_t off = (size_t)l * m->hp.n_ctx * m->kv_embd;
+        LL_TRY(axf_synth_normal(buf.data(), (int64_t)buf.size(), seed + 2 * l, 0.f, 1.f));
+        LL_TRY(upload(m, m->kv_k + off, buf.data(), buf.size() * 4));
+        LL_TRY(axf_synth_normal(buf.data(), (int64_t)buf.size(), seed + 2 * l + 1, 0.f, 1.f));
+        LL_TRY(upload(m, m->kv_v + off, buf.data(), buf.size() * 4));
+    }
+    return AXF_OK;
+}
+
+int axf_llama_get_logits(axf_llama* m, float* logits) {
+    LL_LOADED(m);
+    LL_HIP(hipMemcpyAsync(logits, m->logits, (size_t)m->hp.n_vocab * 4, hipMemcpyDeviceToHost,
+                          m->ctx->stream));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    return AXF_OK;
+}
+
+int axf_llama_forward_layer(axf_llama* m, int layer, int pos) {
+    LL_LOADED(m);
+    if (layer < 0 || layer >= m->hp.n_layer || pos < 0 || pos >= m->hp.n_ctx)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_forward_layer: bad layer/pos");
+    LL_HIP(enqueue_layer(m, layer, nullptr, pos));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    return AXF_OK;
+}
+
+int axf_llama_forward_token(axf_llama* m, int token, int pos) {
+    LL_LOADED(m);
+    if (token < 0 || token >= m->hp.n_vocab || pos < 0 || pos >= m->hp.n_ctx)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_forward_token: bad token/pos");
+    LL_HIP(enqueue_step(m, false, token, pos, false));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    return AXF_OK;
+}
+
+int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_gen,
+                       int32_t* out_tokens, int use_graph) {
+    LL_LOADED(m);
+    if (!prompt || n_prompt <= 0 || n_gen < 0 || (n_gen && !out_tokens))
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_generate: bad arguments");
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= m->hp.n_vocab)
+            return fail(AXF_ERR_INVALID_ARG, "axf_llama_generate: prompt token out of range");
+    // the last generated token is produced at position n_prompt + n_gen - 2
+    if (n_prompt + (n_gen > 0 ? n_gen - 1 : 0) > m->hp.n_ctx)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_generate: context too long");
+    hipStream_t st = m->ctx->stream;
+    LL_HIP(launch_set_int(m->d_step, 0, st));
+    LL_HIP(launch_set_int(m->d_pos, 0, st));
+    if (use_graph) LL_TRY(ensure_graph(m));
+    // prefill token by token; the argmax of the last prompt step is token 0
+    for (int t = 0; t < n_prompt; t++) {
+        LL_HIP(launch_set_int(m->d_token, prompt[t], st));
+        if (use_graph)
+            LL_HIP(hipGraphLaunch(m->exec, st));
+        else
+            LL_HIP(enqueue_step(m, true, 0, 0, true));
+    }
+    LL_HIP(launch_set_int(m->d_step, 0, st));
+    if (n_gen > 0) LL_HIP(launch_push_token(m->d_tokens, m->d_step, m->d_token, st));
+    for (int i = 1; i < n_gen; i++) {
+        if (use_graph)
+            LL_HIP(hipGraphLaunch(m->exec, st));
+        else
+            LL_HIP(enqueue_step(m, true, 0, 0, true));
+    }
+    if (n_gen > 0)
+        LL_HIP(hipMemcpyAsync(out_tokens, m->d_tokens, (size_t)n_gen * 4, hipMemcpyDeviceToHost,
+                              st));
+    LL_HIP(hipStreamSynchronize(st));
+    return AXF_OK;
+}
+
+int axf_llama_bench_decode(axf_llama* m, int start_pos, int warmup, int steps, float* ms) {
+    LL_LOADED(m);
+    if (!ms || start_pos < 0 || warmup < 0 || steps <= 0 ||
+        start_pos + warmup + steps > m->hp.n_ctx || warmup + steps > m->max_tokens)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_bench_decode: bad arguments");
+    hipStream_t st = m->ctx->stream;
+    LL_TRY(ensure_graph(m));
+    LL_HIP(launch_set_int(m->d_step, 0, st));
+    LL_HIP(launch_set_int(m->d_pos, start_pos, st));
+    LL_HIP(launch_set_int(m->d_token, 1, st));
+    for (int i = 0; i < warmup; i++) LL_HIP(hipGraphLaunch(m->exec, st));
+    LL_HIP(hipEventRecord(m->ctx->ev0, st));
+    for (int i = 0; i < steps; i++) LL_HIP(hipGraphLaunch(m->exec, st));
+    LL_HIP(hipEventRecord(m->ctx->ev1, st));
+    LL_HIP(hipEventSynchronize(m->ctx->ev1));
+    LL_HIP(hipEventElapsedTime(ms, m->ctx->ev0, m->ctx->ev1));
+    return AXF_OK;
+}
+
+}  // extern "C"

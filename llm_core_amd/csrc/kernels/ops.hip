@@ -1,0 +1,697 @@
+// ops.hip — dequantisation, Q8_0 quantisation and the decode-step operations
+// around the GEMVs (RMSNorm, RoPE + KV store, single-token attention, SwiGLU,
+// embedding row, argmax) for gfx950.
+//
+// Device-side position: kernels that run inside a captured decode graph read
+// the position from device memory (pos_dev != nullptr) so one graph serves
+// every step; otherwise the immediate `pos` is used.
+#include "common.hpp"
+
+namespace axf {
+
+__device__ __forceinline__ int read_pos(const int* pos_dev, int pos) {
+    return pos_dev ? *pos_dev : pos;
+}
+
+// ---------------------------------------------------------------------------
+// Dequantisation (bit-exact with the reference's scalar dequant)
+// ---------------------------------------------------------------------------
+
+// Q4_K: out = fma(d*sc, q, -(dmin*m)); one thread per 4 qs bytes (8 outputs).
+__global__ void k_dequant_q4k(float* __restrict__ out, const uint8_t* __restrict__ W,
+                              long nblocks) {
+    const long n = nblocks * 32;
+    for (long t = (long)blockIdx.x * blockDim.x + threadIdx.x; t < n;
+         t += (long)gridDim.x * blockDim.x) {
+        const long b = t >> 5;
+        const int k = (int)(t & 31), c = k >> 3, l0 = (k & 7) * 4;
+        const uint8_t* blk = W + b * Q4K_BYTES;
+        const uint4 h = ld16(blk);
+        const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(h.y, h.z, h.w, c, sc0, m0, sc1, m1);
+        const float d1 = d * (float)sc0, mf1 = dmin * (float)m0;
+        const float d2 = d * (float)sc1, mf2 = dmin * (float)m1;
+        const uint32_t q = ld4(blk + 16 + 32 * c + l0);
+        float* o = out + b * QK_K + 64 * c + l0;
+        float4 lo, hi;
+        lo.x = fmaf(d1, (float)(q & 0xfu), -mf1);
+        lo.y = fmaf(d1, (float)((q >> 8) & 0xfu), -mf1);
+        lo.z = fmaf(d1, (float)((q >> 16) & 0xfu), -mf1);
+        lo.w = fmaf(d1, (float)((q >> 24) & 0xfu), -mf1);
+        hi.x = fmaf(d2, (float)((q >> 4) & 0xfu), -mf2);
+        hi.y = fmaf(d2, (float)((q >> 12) & 0xfu), -mf2);
+        hi.z = fmaf(d2, (float)((q >> 20) & 0xfu), -mf2);
+        hi.w = fmaf(d2, (float)((q >> 28) & 0xfu), -mf2);
+        *reinterpret_cast<float4*>(o) = lo;
+        *reinterpret_cast<float4*>(o + 32) = hi;
+    }
+}
+
+// Q6_K: out = (d*sc)*(q-32); one thread per (block, half, 4 consecutive l).
+__global__ void k_dequant_q6k(float* __restrict__ out, const uint8_t* __restrict__ W,
+                              long nblocks) {
+    const long n = nblocks * 16;
+    for (long t = (long)blockIdx.x * blockDim.x + threadIdx.x; t < n;
+         t += (long)gridDim.x * blockDim.x) {
+        const long b = t >> 4;
+        const int k = (int)(t & 15), half = k >> 3, l0 = (k & 7) * 4;
+        const uint8_t* blk = W + b * Q6K_BYTES;
+        const float d = h2f(ld2(blk + 208));
+        const uint8_t* ql = blk + 64 * half;
+        const uint8_t* qh = blk + 128 + 32 * half;
+        const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192 + 8 * half);
+        float* y = out + b * QK_K + 128 * half;
+        const int is = l0 / 16;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int l = l0 + j;
+            const int q1 = ((ql[l] & 0x0f) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            const int q2 = ((ql[l + 32] & 0x0f) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            y[l + 0] = (d * (float)sc[is + 0]) * (float)q1;
+            y[l + 32] = (d * (float)sc[is + 2]) * (float)q2;
+            y[l + 64] = (d * (float)sc[is + 4]) * (float)q3;
+            y[l + 96] = (d * (float)sc[is + 6]) * (float)q4;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 quantisation: 8 lanes per 32-element block, 4 elements per lane.
+// d = amax/127, id = 127/amax (0 when amax == 0), q = rne(x*id) saturated.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void q8_block_store(uint8_t* blk, int sub, float4 v) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+    const float d = amax / 127.f;
+    const float id = amax > 0.f ? 127.f / amax : 0.f;
+    auto q = [&](float f) -> uint32_t {
+        float r = rintf(f * id);
+        r = fminf(fmaxf(r, -128.f), 127.f);
+        return (uint32_t)((int)r & 0xff);
+    };
+    const uint32_t packed = q(v.x) | (q(v.y) << 8) | (q(v.z) << 16) | (q(v.w) << 24);
+    *reinterpret_cast<uint32_t*>(blk + 4 + 4 * sub) = packed;
+    if (sub == 0) *reinterpret_cast<float*>(blk) = d;
+}
+
+__global__ void k_quantize_q8_0(uint8_t* __restrict__ y, const float* __restrict__ x, int n) {
+    const int nthreads = n / 4;  // n % 32 == 0
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < nthreads; t += gridDim.x * blockDim.x) {
+        // all 8 lanes of a block are in the same iteration: nthreads % 8 == 0 and
+        // the grid stride is a multiple of 8
+        const float4 v = reinterpret_cast<const float4*>(x)[t];
+        q8_block_store(y + (size_t)(t >> 3) * Q8_0_BYTES, t & 7, v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm (+ optional Q8_0 of the result), one workgroup of 1024 threads:
+// y = w*(x*s), s = 1/sqrt(sum(x^2)/n + eps).
+// ---------------------------------------------------------------------------
+constexpr int kNormThreads = 1024;
+
+__device__ __forceinline__ float block_sum_1024(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float s = lane < (kNormThreads / 64) ? red[lane] : 0.f;
+    s = wave_sum(s);
+    __syncthreads();
+    return s;
+}
+
+__global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ y,
+                                                          uint8_t* __restrict__ yq8,
+                                                          const float* __restrict__ x,
+                                                          const float* __restrict__ w, int n,
+                                                          float eps) {
+    __shared__ float red[16];
+    float ss = 0.f;
+    for (int i = threadIdx.x * 4; i < n; i += kNormThreads * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(x + i);
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
+    ss = block_sum_1024(ss, red);
+    const float s = 1.f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x * 4; i < n; i += kNormThreads * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(x + i);
+        const float4 g = *reinterpret_cast<const float4*>(w + i);
+        float4 o;
+        o.x = g.x * (v.x * s);
+        o.y = g.y * (v.y * s);
+        o.z = g.z * (v.z * s);
+        o.w = g.w * (v.w * s);
+        if (y) *reinterpret_cast<float4*>(y + i) = o;
+        if (yq8) q8_block_store(yq8 + (size_t)(i >> 5) * Q8_0_BYTES, (i >> 2) & 7, o);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// RoPE (rotate-half pairs (i, i+hd/2)) with the host-built cos/sin table:
+//   a = fma(x0, c, -(x1*s)),  b = fma(x0, s, x1*c)
+// k_rope: dst may alias src.  k_rope_qkv: q in place, k -> kcache row pos,
+// v copied to vcache row pos.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void rope_pair(const float* src, float* dst, int i, int half,
+                                          const float* cr, const float* sr) {
+    const float x0 = src[i], x1 = src[i + half];
+    const float c = cr[i], s = sr[i];
+    const float a = fmaf(x0, c, -(x1 * s));
+    const float b = fmaf(x0, s, x1 * c);
+    dst[i] = a;
+    dst[i + half] = b;
+}
+
+__global__ void k_rope(float* dst, const float* src, const int* pos_dev, int pos, int n_heads,
+                       int hd, const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    const int half = hd / 2;
+    const int p = read_pos(pos_dev, pos);
+    const float* cr = cos_t + (size_t)p * half;
+    const float* sr = sin_t + (size_t)p * half;
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < n_heads * half;
+         t += gridDim.x * blockDim.x) {
+        const int h = t / half, i = t % half;
+        rope_pair(src + (size_t)h * hd, dst + (size_t)h * hd, i, half, cr, sr);
+    }
+}
+
+__global__ void k_rope_qkv(float* q, const float* __restrict__ k, const float* __restrict__ v,
+                           float* __restrict__ kcache, float* __restrict__ vcache,
+                           const int* pos_dev, int pos, int n_heads, int n_kv_heads, int hd,
+                           const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    const int half = hd / 2;
+    const int p = read_pos(pos_dev, pos);
+    const size_t kv_embd = (size_t)n_kv_heads * hd;
+    const float* cr = cos_t + (size_t)p * half;
+    const float* sr = sin_t + (size_t)p * half;
+    float* krow = kcache + (size_t)p * kv_embd;
+    float* vrow = vcache + (size_t)p * kv_embd;
+    const int nq = n_heads * half, nk = n_kv_heads * half;
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < nq + nk + (int)kv_embd;
+         t += gridDim.x * blockDim.x) {
+        if (t < nq) {
+            const int h = t / half, i = t % half;
+            rope_pair(q + (size_t)h * hd, q + (size_t)h * hd, i, half, cr, sr);
+        } else if (t < nq + nk) {
+            const int u = t - nq, h = u / half, i = u % half;
+            rope_pair(k + (size_t)h * hd, krow + (size_t)h * hd, i, half, cr, sr);
+        } else {
+            const int u = t - nq - nk;
+            vrow[u] = v[u];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Single-token attention over the fp32 KV cache, split along the sequence
+// (kAttnSplit positions per workgroup) and combined per head.
+//   partial (h, j): m_j = max score, l_j = sum exp(s - m_j), o_j = sum exp(s - m_j) v
+//   out_h = sum_j o_j e^(m_j - M) / sum_j l_j e^(m_j - M),  s = dot(q_h, k_t) * (1/sqrt(hd))
+// ---------------------------------------------------------------------------
+constexpr int kAttnSplit = 64;
+constexpr int kAttnThreads = 256;
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_split(
+    float* __restrict__ part, const float* __restrict__ q, const float* __restrict__ kcache,
+    const float* __restrict__ vcache, const int* pos_dev, int seq_imm, int n_heads,
+    int n_kv_heads, int nsplit) {
+    constexpr int DPL = HD / 8;  // dims per lane in the score phase (8 lanes per position)
+    constexpr int VPL = HD / 64; // dims per lane in the value phase
+    __shared__ float sc[kAttnSplit];
+    __shared__ float red[kAttnThreads / 64];
+    __shared__ float ov[kAttnThreads / 64][HD];
+    const int j = blockIdx.x, h = blockIdx.y;
+    const int seq = pos_dev ? (*pos_dev + 1) : seq_imm;
+    const int kvh = h / (n_heads / n_kv_heads);
+    const size_t kv_embd = (size_t)n_kv_heads * HD;
+    const int t0 = j * kAttnSplit;
+    const int t1 = min(t0 + kAttnSplit, seq);
+    float* dst = part + ((size_t)h * nsplit + j) * (HD + 2);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (t0 >= t1) {  // empty split
+        for (int d = threadIdx.x; d < HD; d += kAttnThreads) dst[2 + d] = 0.f;
+        if (threadIdx.x == 0) {
+            dst[0] = -INFINITY;
+            dst[1] = 0.f;
+        }
+        return;
+    }
+    const float scale = 1.f / sqrtf((float)HD);
+    // scores: 8 lanes per position, 8 positions per wave-iteration
+    const int sub = lane & 7, pl = lane >> 3;
+    float qv[DPL];
+    const float* qh = q + (size_t)h * HD + sub * DPL;
+#pragma unroll
+    for (int e = 0; e < DPL; e += 4) {
+        const float4 v4 = *reinterpret_cast<const float4*>(qh + e);
+        qv[e] = v4.x; qv[e + 1] = v4.y; qv[e + 2] = v4.z; qv[e + 3] = v4.w;
+    }
+    for (int tb = t0 + wave * 8; tb < t1; tb += kAttnThreads / 8) {
+        const int t = tb + pl;
+        float s = 0.f;
+        if (t < t1) {
+            const float* kr = kcache + (size_t)t * kv_embd + (size_t)kvh * HD + sub * DPL;
+#pragma unroll
+            for (int e = 0; e < DPL; e += 4) {
+                const float4 k4 = *reinterpret_cast<const float4*>(kr + e);
+                s = fmaf(qv[e], k4.x, s);
+                s = fmaf(qv[e + 1], k4.y, s);
+                s = fmaf(qv[e + 2], k4.z, s);
+                s = fmaf(qv[e + 3], k4.w, s);
+            }
+        }
+        s = group_sum<8>(s);
+        if (sub == 0 && t < t1) sc[t - t0] = s * scale;
+    }
+    __syncthreads();
+    const int n = t1 - t0;
+    // local max and exp
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += kAttnThreads) m = fmaxf(m, sc[i]);
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < kAttnThreads / 64; w++) m = fmaxf(m, red[w]);
+    __syncthreads();
+    float l = 0.f;
+    for (int i = threadIdx.x; i < n; i += kAttnThreads) {
+        const float p = expf(sc[i] - m);
+        sc[i] = p;
+        l += p;
+    }
+    l = wave_sum(l);
+    if (lane == 0) red[wave] = l;
+    __syncthreads();
+    // values: each wave takes positions t0+wave, +4, ...; lane owns VPL dims
+    float o[VPL];
+#pragma unroll
+    for (int e = 0; e < VPL; e++) o[e] = 0.f;
+    for (int i = wave; i < n; i += kAttnThreads / 64) {
+        const float p = sc[i];
+        const float* vr = vcache + (size_t)(t0 + i) * kv_embd + (size_t)kvh * HD + lane * VPL;
+#pragma unroll
+        for (int e = 0; e < VPL; e++) o[e] = fmaf(p, vr[e], o[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < VPL; e++) ov[wave][lane * VPL + e] = o[e];
+    __syncthreads();
+    for (int d = threadIdx.x; d < HD; d += kAttnThreads) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAttnThreads / 64; w++) acc += ov[w][d];
+        dst[2 + d] = acc;
+    }
+    if (threadIdx.x == 0) {
+        float lt = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAttnThreads / 64; w++) lt += red[w];
+        dst[0] = m;
+        dst[1] = lt;
+    }
+}
+
+// Combine the splits of each head; optionally also write the Q8_0 of the
+// result (HD % 32 == 0, one 32-element block per 8 threads x 4 elements).
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_combine(float* __restrict__ out,
+                                                     uint8_t* __restrict__ outq8,
+                                                     const float* __restrict__ part, int nsplit) {
+    const int h = blockIdx.x;
+    const float* ph = part + (size_t)h * nsplit * (HD + 2);
+    float M = -INFINITY;
+    for (int j = 0; j < nsplit; j++) M = fmaxf(M, ph[(size_t)j * (HD + 2)]);
+    float L = 0.f, acc = 0.f;
+    const int d = threadIdx.x;
+    for (int j = 0; j < nsplit; j++) {
+        const float* pj = ph + (size_t)j * (HD + 2);
+        const float lj = pj[1];
+        if (lj > 0.f) {
+            const float wj = expf(pj[0] - M);
+            L = fmaf(lj, wj, L);
+            acc = fmaf(pj[2 + d], wj, acc);
+        }
+    }
+    const float r = acc / L;
+    out[(size_t)h * HD + d] = r;
+    if (outq8) {
+        // gather 4 consecutive elements per lane for the Q8_0 packer
+        __shared__ float buf[HD];
+        buf[d] = r;
+        __syncthreads();
+        if (d < HD / 4) {
+            const float4 v = *reinterpret_cast<const float4*>(buf + 4 * d);
+            const size_t e0 = (size_t)h * HD + 4 * d;
+            q8_block_store(outq8 + (e0 >> 5) * Q8_0_BYTES, (int)((e0 >> 2) & 7), v);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU (reference swiglu_avx2): e = exp(-|g|) by the Cephes single-precision
+// expf method (S. L. Moshier, Cephes Math Library: Cody-Waite reduction by
+// ln2 in two constants, degree-5 polynomial, 2^n scaling), sigmoid = 1/(1+e)
+// for g >= 0 and e/(1+e) for g < 0, out = (g*sigmoid)*up.  Optional Q8_0 of
+// the result.  gate/up may be separate buffers or halves of one buffer.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float exp_cephes(float x) {
+    float xx = fminf(x, 88.3762626648f);
+    xx = fmaxf(-88.3762626648f, xx);
+    const float fx = floorf(fmaf(xx, 1.44269504089f, 0.5f));
+    xx = fmaf(-fx, 0.693359375f, xx);
+    xx = fmaf(-fx, -2.12194440e-4f, xx);
+    const float z = xx * xx;
+    float p = 1.9875691500E-4f;
+    p = fmaf(p, xx, 1.3981999507E-3f);
+    p = fmaf(p, xx, 8.3334519073E-3f);
+    p = fmaf(p, xx, 4.1665795894E-2f);
+    p = fmaf(p, xx, 1.6666665459E-1f);
+    p = fmaf(p, xx, 5.0000001201E-1f);
+    p = fmaf(p, z, xx + 1.f);
+    const int n = ((int)fx + 127) << 23;
+    return p * __int_as_float(n);
+}
+
+__device__ __forceinline__ float swiglu1(float g, float u) {
+    const float e = exp_cephes(-fabsf(g));
+    const float denom = 1.f + e;
+    const float sig = g < 0.f ? e / denom : 1.f / denom;
+    return (g * sig) * u;
+}
+
+__global__ void k_swiglu(float* __restrict__ out, uint8_t* __restrict__ outq8,
+                         const float* __restrict__ gate, const float* __restrict__ up, int n) {
+    const int nthreads = n / 4;
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < nthreads; t += gridDim.x * blockDim.x) {
+        const float4 g = reinterpret_cast<const float4*>(gate)[t];
+        const float4 u = reinterpret_cast<const float4*>(up)[t];
+        float4 o;
+        o.x = swiglu1(g.x, u.x);
+        o.y = swiglu1(g.y, u.y);
+        o.z = swiglu1(g.z, u.z);
+        o.w = swiglu1(g.w, u.w);
+        if (out) reinterpret_cast<float4*>(out)[t] = o;
+        if (outq8) q8_block_store(outq8 + (size_t)(t >> 3) * Q8_0_BYTES, t & 7, o);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Embedding row (token id from device memory or immediate): dequantise row
+// `tok` of a Q4_K / Q6_K matrix with `nb` blocks per row.
+// ---------------------------------------------------------------------------
+__global__ void k_embed_q4k(float* __restrict__ out, const uint8_t* __restrict__ W,
+                            const int* tok_dev, int tok, int nb, long row_bytes) {
+    const int id = tok_dev ? *tok_dev : tok;
+    const uint8_t* row = W + (long)id * row_bytes;
+    for (int t = threadIdx.x; t < nb * 32; t += blockDim.x) {
+        const int b = t >> 5, k = t & 31, c = k >> 3, l0 = (k & 7) * 4;
+        const uint8_t* blk = row + (long)b * Q4K_BYTES;
+        const uint4 h = ld16(blk);
+        const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(h.y, h.z, h.w, c, sc0, m0, sc1, m1);
+        const float d1 = d * (float)sc0, mf1 = dmin * (float)m0;
+        const float d2 = d * (float)sc1, mf2 = dmin * (float)m1;
+        const uint32_t q = ld4(blk + 16 + 32 * c + l0);
+        float* o = out + b * QK_K + 64 * c + l0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            o[e] = fmaf(d1, (float)((q >> (8 * e)) & 0xfu), -mf1);
+            o[32 + e] = fmaf(d2, (float)((q >> (8 * e + 4)) & 0xfu), -mf2);
+        }
+    }
+}
+
+__global__ void k_embed_q6k(float* __restrict__ out, const uint8_t* __restrict__ W,
+                            const int* tok_dev, int tok, int nb, long row_bytes) {
+    const int id = tok_dev ? *tok_dev : tok;
+    const uint8_t* row = W + (long)id * row_bytes;
+    for (int t = threadIdx.x; t < nb * 128; t += blockDim.x) {
+        const int b = t >> 7, k = t & 127, half = k >> 6, l = k & 31, s = (k >> 5) & 1;
+        const uint8_t* blk = row + (long)b * Q6K_BYTES;
+        const float d = h2f(ld2(blk + 208));
+        const uint8_t* ql = blk + 64 * half;
+        const uint8_t* qh = blk + 128 + 32 * half;
+        const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192 + 8 * half);
+        const int is = l / 16;
+        float* y = out + b * QK_K + 128 * half;
+        if (s == 0) {
+            const int q1 = ((ql[l] & 0x0f) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            y[l] = (d * (float)sc[is]) * (float)q1;
+            y[l + 64] = (d * (float)sc[is + 4]) * (float)q3;
+        } else {
+            const int q2 = ((ql[l + 32] & 0x0f) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            y[l + 32] = (d * (float)sc[is + 2]) * (float)q2;
+            y[l + 96] = (d * (float)sc[is + 6]) * (float)q4;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// argmax (first index of the maximum, std::max_element semantics), two stages.
+// ---------------------------------------------------------------------------
+constexpr int kArgThreads = 256;
+
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__device__ __forceinline__ void block_argmax(float& v, int& i) {
+    __shared__ float sv[kArgThreads / 64];
+    __shared__ int si[kArgThreads / 64];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float v2 = __shfl_xor(v, off, 64);
+        const int i2 = __shfl_xor(i, off, 64);
+        argmax_merge(v, i, v2, i2);
+    }
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) {
+        sv[w] = v;
+        si[w] = i;
+    }
+    __syncthreads();
+    v = sv[0];
+    i = si[0];
+#pragma unroll
+    for (int k = 1; k < kArgThreads / 64; k++) argmax_merge(v, i, sv[k], si[k]);
+}
+
+__global__ __launch_bounds__(kArgThreads) void k_argmax_partial(float* __restrict__ pv,
+                                                                int* __restrict__ pi,
+                                                                const float* __restrict__ x,
+                                                                int n) {
+    float v = -INFINITY;
+    int i = 0x7fffffff;
+    for (int t = blockIdx.x * kArgThreads + threadIdx.x; t < n; t += gridDim.x * kArgThreads)
+        argmax_merge(v, i, x[t], t);
+    block_argmax(v, i);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = v;
+        pi[blockIdx.x] = i;
+    }
+}
+
+// Final stage; also appends the token to `tokens[*step]` and advances the
+// device-side position/step counters when they are given (decode graph).
+__global__ __launch_bounds__(kArgThreads) void k_argmax_final(int* __restrict__ out,
+                                                              const float* __restrict__ pv,
+                                                              const int* __restrict__ pi,
+                                                              int nparts, int* tokens,
+                                                              int* step, int* pos) {
+    float v = -INFINITY;
+    int i = 0x7fffffff;
+    for (int t = threadIdx.x; t < nparts; t += kArgThreads) argmax_merge(v, i, pv[t], pi[t]);
+    block_argmax(v, i);
+    if (threadIdx.x == 0) {
+        if (i == 0x7fffffff) i = 0;  // all NaN: std::max_element returns the first
+        *out = i;
+        if (tokens && step) {
+            tokens[*step] = i;
+            *step += 1;
+        }
+        if (pos) *pos += 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise
+// ---------------------------------------------------------------------------
+__global__ void k_add(float* __restrict__ y, const float* __restrict__ a,
+                      const float* __restrict__ b, int n) {
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < n; t += gridDim.x * blockDim.x)
+        y[t] = a[t] + b[t];
+}
+
+// silu(x) = x/(1+exp(-x)) (llama_model.cpp:313-315) and elementwise product.
+__global__ void k_silu(float* __restrict__ y, const float* __restrict__ x, int n) {
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < n; t += gridDim.x * blockDim.x)
+        y[t] = x[t] / (1.f + expf(-x[t]));
+}
+
+__global__ void k_mul(float* __restrict__ y, const float* __restrict__ a,
+                      const float* __restrict__ b, int n) {
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < n; t += gridDim.x * blockDim.x)
+        y[t] = a[t] * b[t];
+}
+
+__global__ void k_set_int(int* p, int v) { *p = v; }
+
+// tokens[*step] = *tok; ++*step  (records the token chosen from the prefill logits)
+__global__ void k_push_token(int* tokens, int* step, const int* tok) {
+    tokens[*step] = *tok;
+    *step += 1;
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+static inline unsigned grid_for(long work, int threads, long cap = 65536) {
+    long g = (work + threads - 1) / threads;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (unsigned)g;
+}
+
+hipError_t launch_dequant_q4k(float* y, const void* W, long nblocks, hipStream_t st) {
+    hipLaunchKernelGGL(k_dequant_q4k, dim3(grid_for(nblocks * 32, 256)), dim3(256), 0, st, y,
+                       static_cast<const uint8_t*>(W), nblocks);
+    return hipGetLastError();
+}
+hipError_t launch_dequant_q6k(float* y, const void* W, long nblocks, hipStream_t st) {
+    hipLaunchKernelGGL(k_dequant_q6k, dim3(grid_for(nblocks * 16, 256)), dim3(256), 0, st, y,
+                       static_cast<const uint8_t*>(W), nblocks);
+    return hipGetLastError();
+}
+hipError_t launch_quantize_q8_0(void* y, const float* x, int n, hipStream_t st) {
+    hipLaunchKernelGGL(k_quantize_q8_0, dim3(grid_for(n / 4, 256)), dim3(256), 0, st,
+                       static_cast<uint8_t*>(y), x, n);
+    return hipGetLastError();
+}
+hipError_t launch_rmsnorm(float* y, void* yq8, const float* x, const float* w, int n, float eps,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kNormThreads), 0, st, y,
+                       static_cast<uint8_t*>(yq8), x, w, n, eps);
+    return hipGetLastError();
+}
+hipError_t launch_rope(float* dst, const float* src, const int* pos_dev, int pos, int n_heads,
+                       int hd, const float* cos_t, const float* sin_t, hipStream_t st) {
+    hipLaunchKernelGGL(k_rope, dim3(grid_for((long)n_heads * hd / 2, 256, 1024)), dim3(256), 0,
+                       st, dst, src, pos_dev, pos, n_heads, hd, cos_t, sin_t);
+    return hipGetLastError();
+}
+hipError_t launch_rope_qkv(float* q, const float* k, const float* v, float* kcache,
+                           float* vcache, const int* pos_dev, int pos, int n_heads,
+                           int n_kv_heads, int hd, const float* cos_t, const float* sin_t,
+                           hipStream_t st) {
+    const long work = (long)(n_heads + n_kv_heads) * hd / 2 + (long)n_kv_heads * hd;
+    hipLaunchKernelGGL(k_rope_qkv, dim3(grid_for(work, 256, 1024)), dim3(256), 0, st, q, k, v,
+                       kcache, vcache, pos_dev, pos, n_heads, n_kv_heads, hd, cos_t, sin_t);
+    return hipGetLastError();
+}
+
+int attn_nsplit(int max_seq) { return (max_seq + kAttnSplit - 1) / kAttnSplit; }
+
+hipError_t launch_attention(float* out, void* outq8, float* part, const float* q,
+                            const float* kcache, const float* vcache, const int* pos_dev,
+                            int seq, int nsplit, int n_heads, int n_kv_heads, int hd,
+                            hipStream_t st) {
+    const dim3 g1((unsigned)nsplit, (unsigned)n_heads);
+    auto* oq = static_cast<uint8_t*>(outq8);
+    switch (hd) {
+        case 64:
+            hipLaunchKernelGGL(k_attn_split<64>, g1, dim3(kAttnThreads), 0, st, part, q, kcache,
+                               vcache, pos_dev, seq, n_heads, n_kv_heads, nsplit);
+            hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_heads), dim3(64), 0, st, out, oq, part,
+                               nsplit);
+            break;
+        case 128:
+            hipLaunchKernelGGL(k_attn_split<128>, g1, dim3(kAttnThreads), 0, st, part, q, kcache,
+                               vcache, pos_dev, seq, n_heads, n_kv_heads, nsplit);
+            hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_heads), dim3(128), 0, st, out, oq,
+                               part, nsplit);
+            break;
+        case 256:
+            hipLaunchKernelGGL(k_attn_split<256>, g1, dim3(kAttnThreads), 0, st, part, q, kcache,
+                               vcache, pos_dev, seq, n_heads, n_kv_heads, nsplit);
+            hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_heads), dim3(256), 0, st, out, oq,
+                               part, nsplit);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(float* out, void* outq8, const float* gate, const float* up, int n,
+                         hipStream_t st) {
+    hipLaunchKernelGGL(k_swiglu, dim3(grid_for(n / 4, 256)), dim3(256), 0, st, out,
+                       static_cast<uint8_t*>(outq8), gate, up, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(int qtype, float* out, const void* W, const int* tok_dev, int tok,
+                        int nb, long row_bytes, hipStream_t st) {
+    if (qtype == 12)
+        hipLaunchKernelGGL(k_embed_q4k, dim3(1), dim3(1024), 0, st, out,
+                           static_cast<const uint8_t*>(W), tok_dev, tok, nb, row_bytes);
+    else
+        hipLaunchKernelGGL(k_embed_q6k, dim3(1), dim3(1024), 0, st, out,
+                           static_cast<const uint8_t*>(W), tok_dev, tok, nb, row_bytes);
+    return hipGetLastError();
+}
+
+constexpr int kArgParts = 256;
+int argmax_parts() { return kArgParts; }
+
+hipError_t launch_argmax(int* out, float* pv, int* pi, const float* x, int n, int* tokens,
+                         int* step, int* pos, hipStream_t st) {
+    const int parts = (int)grid_for(n, kArgThreads, kArgParts);
+    hipLaunchKernelGGL(k_argmax_partial, dim3(parts), dim3(kArgThreads), 0, st, pv, pi, x, n);
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(kArgThreads), 0, st, out, pv, pi, parts,
+                       tokens, step, pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(float* y, const float* a, const float* b, int n, hipStream_t st) {
+    hipLaunchKernelGGL(k_add, dim3(grid_for(n, 256)), dim3(256), 0, st, y, a, b, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu(float* y, const float* x, int n, hipStream_t st) {
+    hipLaunchKernelGGL(k_silu, dim3(grid_for(n, 256)), dim3(256), 0, st, y, x, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_mul(float* y, const float* a, const float* b, int n, hipStream_t st) {
+    hipLaunchKernelGGL(k_mul, dim3(grid_for(n, 256)), dim3(256), 0, st, y, a, b, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_set_int(int* p, int v, hipStream_t st) {
+    hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, st, p, v);
+    return hipGetLastError();
+}
+
+hipError_t launch_push_token(int* tokens, int* step, const int* tok, hipStream_t st) {
+    hipLaunchKernelGGL(k_push_token, dim3(1), dim3(1), 0, st, tokens, step, tok);
+    return hipGetLastError();
+}
+
+}  // namespace axf

@@ -1,0 +1,181 @@
+"""Synthetic LLaMA-family models and the device decoder handle.
+
+SynthLlama draws every weight N(0, std) from a seed and quantizes it with the
+Q4_K_M mix of the reference's benchmarks (Q4_K: token_embd, attn_q, attn_k,
+attn_output, ffn_gate, ffn_up; Q6_K: attn_v, ffn_down, output); norm weights
+are 1.0 unless norm_std > 0.  LlamaHip uploads such a model once and drives the
+decode step on the GPU through the C-ABI.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import hip
+from ._ffi import AXF_TYPE_F32, AXF_TYPE_Q4_K, AXF_TYPE_Q6_K, LlamaHparams, call, lib
+
+
+@dataclass
+class Hparams:
+    n_layer: int
+    n_embd: int
+    n_heads: int
+    n_kv_heads: int
+    ffn_dim: int
+    n_vocab: int
+    n_ctx: int
+    rms_eps: float = 1e-5
+    rope_theta: float = 10000.0
+
+    @property
+    def head_dim(self) -> int:
+        return self.n_embd // self.n_heads
+
+    def to_c(self) -> LlamaHparams:
+        return LlamaHparams(self.n_layer, self.n_embd, self.n_heads, self.n_kv_heads,
+                            self.ffn_dim, self.n_vocab, self.n_ctx, self.rms_eps, self.rope_theta)
+
+
+# LLaMA-2-7B architecture and the Qwen2.5-3B-like layer (config 3)
+LLAMA2_7B = dict(n_layer=32, n_embd=4096, n_heads=32, n_kv_heads=32, ffn_dim=11008,
+                 n_vocab=32000, rms_eps=1e-5, rope_theta=10000.0)
+QWEN25_3B_LAYER = dict(n_layer=1, n_embd=2048, n_heads=16, n_kv_heads=2, ffn_dim=11008,
+                       n_vocab=151936, rms_eps=1e-6, rope_theta=1e6)
+
+Q4K_M_TYPES = {
+    "attn_q": AXF_TYPE_Q4_K,
+    "attn_k": AXF_TYPE_Q4_K,
+    "attn_v": AXF_TYPE_Q6_K,
+    "attn_output": AXF_TYPE_Q4_K,
+    "ffn_gate": AXF_TYPE_Q4_K,
+    "ffn_up": AXF_TYPE_Q4_K,
+    "ffn_down": AXF_TYPE_Q6_K,
+}
+
+
+@dataclass
+class SynthLlama:
+    hp: Hparams
+    seed: int = 5
+    std: float = 0.02
+    norm_std: float = 0.0
+    with_bias: bool = False
+    tensors: dict = field(default_factory=dict)  # name -> (qtype, ndarray)
+
+    def __post_init__(self) -> None:
+        hp = self.hp
+        E, FD, hd = hp.n_embd, hp.ffn_dim, hp.head_dim
+        qo, kvo = hp.n_heads * hd, hp.n_kv_heads * hd
+        k = 0
+
+        def seed() -> int:
+            nonlocal k
+            k += 1
+            return self.seed * 1000003 + k
+
+        def qw(name: str, qtype: int, rows: int, cols: int) -> None:
+            self.tensors[name] = (qtype, hip.synth_weight(qtype, rows, cols, seed(), self.std))
+
+        def norm(name: str, n: int) -> None:
+            if self.norm_std > 0:
+                v = hip.synth_normal(n, seed(), 1.0, self.norm_std)
+            else:
+                v = np.ones(n, np.float32)
+            self.tensors[name] = (AXF_TYPE_F32, v)
+
+        qw("token_embd.weight", AXF_TYPE_Q4_K, hp.n_vocab, E)
+        qw("output.weight", AXF_TYPE_Q6_K, hp.n_vocab, E)
+        norm("output_norm.weight", E)
+        shapes = {"attn_q": (qo, E), "attn_k": (kvo, E), "attn_v": (kvo, E),
+                  "attn_output": (E, qo), "ffn_gate": (FD, E), "ffn_up": (FD, E),
+                  "ffn_down": (E, FD)}
+        for layer in range(hp.n_layer):
+            norm(f"blk.{layer}.attn_norm.weight", E)
+            norm(f"blk.{layer}.ffn_norm.weight", E)
+            for base, (rows, cols) in shapes.items():
+                qw(f"blk.{layer}.{base}.weight", Q4K_M_TYPES[base], rows, cols)
+            if self.with_bias:
+                for base, n in (("attn_q", qo), ("attn_k", kvo), ("attn_v", kvo)):
+                    self.tensors[f"blk.{layer}.{base}.bias"] = (
+                        AXF_TYPE_F32, hip.synth_normal(n, seed(), 0.0, 0.02))
+
+    def weight_bytes_per_token(self) -> int:
+        """Bytes of quantized and norm weights one decode step reads (one embedding row)."""
+        total = 0
+        for name, (qt, arr) in self.tensors.items():
+            if name == "token_embd.weight":
+                total += hip.row_bytes(qt, self.hp.n_embd)
+            else:
+                total += arr.nbytes
+        return total
+
+
+class LlamaHip:
+    """Device-resident decoder (axf_llama_* in include/axf_hip.h)."""
+
+    def __init__(self, ctx: hip.Context, model: SynthLlama):
+        self.ctx = ctx
+        self.hp = model.hp
+        h = C.c_void_p()
+        hpc = model.hp.to_c()
+        call("axf_llama_create", ctx.handle, C.byref(hpc), C.byref(h))
+        self.handle = h
+        keep = []
+        for name, (qt, arr) in model.tensors.items():
+            a = np.ascontiguousarray(arr)
+            keep.append(a)
+            call("axf_llama_set_tensor", self.handle, name.encode(), qt,
+                 a.ctypes.data_as(C.c_void_p), C.c_size_t(a.nbytes))
+        call("axf_llama_load", self.handle)
+        del keep
+
+    def close(self) -> None:
+        if self.handle:
+            call("axf_llama_destroy", self.handle)
+            self.handle = None
+
+    def device_bytes(self) -> int:
+        return int(lib.axf_llama_device_bytes(self.handle))
+
+    def set_x(self, x: np.ndarray) -> None:
+        a = np.ascontiguousarray(x, np.float32)
+        call("axf_llama_set_x", self.handle, a.ctypes.data_as(C.c_void_p))
+
+    def get_x(self) -> np.ndarray:
+        out = np.empty(self.hp.n_embd, np.float32)
+        call("axf_llama_get_x", self.handle, out.ctypes.data_as(C.c_void_p))
+        return out
+
+    def set_kv(self, layer: int, k: np.ndarray, v: np.ndarray, n_pos: int) -> None:
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        call("axf_llama_set_kv", self.handle, layer, k.ctypes.data_as(C.c_void_p),
+             v.ctypes.data_as(C.c_void_p), n_pos)
+
+    def fill_kv_random(self, n_pos: int, seed: int) -> None:
+        call("axf_llama_fill_kv_random", self.handle, n_pos, C.c_uint64(seed))
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.hp.n_vocab, np.float32)
+        call("axf_llama_get_logits", self.handle, out.ctypes.data_as(C.c_void_p))
+        return out
+
+    def forward_layer(self, layer: int, pos: int) -> None:
+        call("axf_llama_forward_layer", self.handle, layer, pos)
+
+    def forward_token(self, token: int, pos: int) -> None:
+        call("axf_llama_forward_token", self.handle, token, pos)
+
+    def generate(self, prompt, n_gen: int, use_graph: bool = True) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(n_gen, 1), np.int32)
+        call("axf_llama_generate", self.handle, p.ctypes.data_as(C.c_void_p), int(p.size), n_gen,
+             out.ctypes.data_as(C.c_void_p), 1 if use_graph else 0)
+        return out[:n_gen]
+
+    def bench_decode(self, start_pos: int, warmup: int, steps: int) -> float:
+        ms = C.c_float(0)
+        call("axf_llama_bench_decode", self.handle, start_pos, warmup, steps, C.byref(ms))
+        return ms.value

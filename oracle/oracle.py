@@ -1,0 +1,303 @@
+"""ctypes wrapper of the CPU parity oracle — TEST INFRASTRUCTURE ONLY.
+
+Used by tests/, __graft_entry__.smoke() (as the checker) and bench.py's
+cpu_baseline leg.  Never used by llm_core_amd.
+
+  orc : liboracle.so, the plain-C restatement (oracle/axf_oracle.c)
+  ref : oracle/_ref/libaxf_ref.so, the reference's own x86 kernels compiled
+        from their sources (None when it was not built)
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORC_PATH = HERE / "liboracle.so"
+REF_PATH = HERE / "_ref" / "libaxf_ref.so"
+
+Q4K, Q6K, F32 = 12, 14, 0
+BLOCK_BYTES = {Q4K: 144, Q6K: 210}
+Q8_0_BYTES = 36
+
+vp, i32, i64, sz, f32 = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _load_orc() -> C.CDLL:
+    if not ORC_PATH.exists():
+        raise ImportError(f"{ORC_PATH} missing: run `make -C oracle`")
+    lib = C.CDLL(str(ORC_PATH))
+    sig = {
+        "orc_fp16_to_fp32": ([C.c_uint16], f32),
+        "orc_dequant_q4k": ([vp, vp, i64], None),
+        "orc_dequant_q6k": ([vp, vp, i64], None),
+        "orc_gemv_q4k_f32": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "orc_gemv_q6k_f32": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "orc_quantize_q8_0": ([vp, vp, i32], None),
+        "orc_gemv_q4k_q8": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "orc_gemv_q6k_q8": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "orc_repack_q4k_r8": ([vp, vp, i32, i32], None),
+        "orc_gemm_q4k_q8": ([vp, vp, vp, i32, i32, i32, sz, i32, i32], None),
+        "orc_rmsnorm": ([vp, vp, vp, i32, f32], None),
+        "orc_rope_table": ([vp, vp, i32, f32, i32], None),
+        "orc_rope": ([vp, vp, i32, i32, i32, vp, vp], None),
+        "orc_dot_f32": ([vp, vp, i32], f32),
+        "orc_softmax": ([vp, i32], None),
+        "orc_attention": ([vp, vp, vp, vp, i32, i32, i32, i32, vp], None),
+        "orc_exp_cephes": ([f32], f32),
+        "orc_swiglu": ([vp, vp, i32], None),
+        "orc_argmax": ([vp, i32], i32),
+        "orc_top2_margin": ([vp, i32], f32),
+        "orc_state_new": ([vp], vp),
+        "orc_state_free": ([vp], None),
+        "orc_state_logits": ([vp], C.POINTER(C.c_float)),
+        "orc_state_x": ([vp], C.POINTER(C.c_float)),
+        "orc_state_kv_k": ([vp], C.POINTER(C.c_float)),
+        "orc_state_kv_v": ([vp], C.POINTER(C.c_float)),
+        "orc_forward_token": ([vp, vp, i32, i32], None),
+        "orc_forward_layer": ([vp, vp, i32, i32], None),
+        "orc_forward_batch": ([vp, vp, vp, i32, i32], None),
+        "orc_generate_greedy": ([vp, vp, i32, i32, i32, vp, vp], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    return lib
+
+
+def _load_ref() -> C.CDLL | None:
+    if not REF_PATH.exists():
+        return None
+    lib = C.CDLL(str(REF_PATH))
+    sig = {
+        "ref_has_avxvnni": ([], i32),
+        "ref_has_avx2": ([], i32),
+        "ref_gemv_q4k_f32": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "ref_gemv_q6k_f32": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "ref_quantize_q8_0": ([vp, vp, i32], None),
+        "ref_gemv_q4k_q8": ([vp, vp, vp, i32, i32, i32, sz, i32], None),
+        "ref_repack_q4k_r8": ([vp, vp, i32, i32], None),
+        "ref_gemv_q4k_r8": ([vp, vp, vp, i32, i32, i32, i32], None),
+        "ref_gemv_q6k_q8": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "ref_gemm_q4k_q8": ([vp, vp, vp, i32, i32, i32, sz, i32, i32, i32], None),
+        "ref_time_decode_gemv": ([i32, C.POINTER(vp), i32, i32, i32, vp, vp, i32, i32,
+                                  C.POINTER(i32)], C.c_double),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    return lib
+
+
+orc = _load_orc()
+ref = _load_ref()
+
+
+def row_bytes(qtype: int, cols: int) -> int:
+    return (cols // 256) * BLOCK_BYTES[qtype]
+
+
+# ---- oracle (restatement) -------------------------------------------------
+
+def dequant(qtype: int, blocks: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    nb = blocks.size // BLOCK_BYTES[qtype]
+    out = np.empty(nb * 256, np.float32)
+    fn = orc.orc_dequant_q4k if qtype == Q4K else orc.orc_dequant_q6k
+    fn(_ptr(out), _ptr(blocks), nb)
+    return out
+
+
+def gemv_f32(qtype: int, W: np.ndarray, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    fn = orc.orc_gemv_q4k_f32 if qtype == Q4K else orc.orc_gemv_q6k_f32
+    fn(_ptr(y), _ptr(W), _ptr(x), 0, rows, cols, row_bytes(qtype, cols))
+    return y
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.size // 32 * Q8_0_BYTES, np.uint8)
+    orc.orc_quantize_q8_0(_ptr(out), _ptr(x), x.size)
+    return out
+
+
+def gemv_q8(qtype: int, W: np.ndarray, xq8: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    y = np.empty(rows, np.float32)
+    fn = orc.orc_gemv_q4k_q8 if qtype == Q4K else orc.orc_gemv_q6k_q8
+    fn(_ptr(y), _ptr(W), _ptr(xq8), 0, rows, cols, row_bytes(qtype, cols))
+    return y
+
+
+def gemm_q4k_q8(W: np.ndarray, XQ8: np.ndarray, rows: int, T: int, cols: int) -> np.ndarray:
+    Y = np.empty(T * rows, np.float32)
+    orc.orc_gemm_q4k_q8(_ptr(Y), _ptr(W), _ptr(XQ8), rows, T, cols, row_bytes(Q4K, cols), 0, rows)
+    return Y.reshape(T, rows)
+
+
+def repack_r8(W: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    out = np.empty(W.size, np.uint8)
+    orc.orc_repack_q4k_r8(_ptr(out), _ptr(W), rows, cols)
+    return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    orc.orc_rmsnorm(_ptr(y), _ptr(x), _ptr(w), x.size, eps)
+    return y
+
+
+def rope_table(hd: int, theta: float, max_pos: int) -> tuple[np.ndarray, np.ndarray]:
+    c = np.empty(max_pos * (hd // 2), np.float32)
+    s = np.empty_like(c)
+    orc.orc_rope_table(_ptr(c), _ptr(s), hd, theta, max_pos)
+    return c, s
+
+
+def rope(x: np.ndarray, pos: int, n_heads: int, hd: int, cos_t: np.ndarray,
+         sin_t: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    orc.orc_rope(_ptr(y), _ptr(x), pos, n_heads, hd, _ptr(cos_t), _ptr(sin_t))
+    return y
+
+
+def attention(q, kc, vc, seq, n_heads, n_kv_heads, hd) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.float32)
+    kc = np.ascontiguousarray(kc, np.float32)
+    vc = np.ascontiguousarray(vc, np.float32)
+    out = np.empty(n_heads * hd, np.float32)
+    scores = np.empty(max(seq, 1), np.float32)
+    orc.orc_attention(_ptr(out), _ptr(q), _ptr(kc), _ptr(vc), seq, n_heads, n_kv_heads, hd,
+                      _ptr(scores))
+    return out
+
+
+def swiglu(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    g = np.array(g, np.float32, copy=True)
+    u = np.ascontiguousarray(u, np.float32)
+    orc.orc_swiglu(_ptr(g), _ptr(u), g.size)
+    return g
+
+
+def argmax(x: np.ndarray) -> int:
+    x = np.ascontiguousarray(x, np.float32)
+    return int(orc.orc_argmax(_ptr(x), x.size))
+
+
+def top2_margin(x: np.ndarray) -> float:
+    x = np.ascontiguousarray(x, np.float32)
+    return float(orc.orc_top2_margin(_ptr(x), x.size))
+
+
+# ---- oracle decoder ---------------------------------------------------------
+
+class OrcWt(C.Structure):
+    _fields_ = [("type", C.c_int), ("data", C.c_void_p)]
+
+
+class OrcLayer(C.Structure):
+    _fields_ = [("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p)] + [
+        (n, OrcWt) for n in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
+    ] + [("bq", C.c_void_p), ("bk", C.c_void_p), ("bv", C.c_void_p)]
+
+
+class OrcModel(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layer", "n_embd", "n_heads", "n_kv_heads", "ffn_dim",
+                                        "n_vocab", "n_ctx")] + [
+        ("rms_eps", C.c_float), ("rope_theta", C.c_float), ("tok_embd", OrcWt),
+        ("output_norm", C.c_void_p), ("output", OrcWt), ("layers", C.POINTER(OrcLayer))]
+
+
+class OracleModel:
+    """The oracle's decoder over the same host tensors a SynthLlama holds."""
+
+    def __init__(self, hp, tensors: dict):
+        self.hp = hp
+        self._keep = []
+
+        def arr(name):
+            qt, a = tensors[name]
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            return qt, a.ctypes.data
+
+        def wt(name):
+            qt, p = arr(name)
+            return OrcWt(qt, p)
+
+        def opt(name):
+            return arr(name)[1] if name in tensors else None
+
+        layers = (OrcLayer * hp.n_layer)()
+        for i in range(hp.n_layer):
+            b = f"blk.{i}."
+            L = layers[i]
+            L.attn_norm = arr(b + "attn_norm.weight")[1]
+            L.ffn_norm = arr(b + "ffn_norm.weight")[1]
+            for field_name, t in (("wq", "attn_q"), ("wk", "attn_k"), ("wv", "attn_v"),
+                                  ("wo", "attn_output"), ("wgate", "ffn_gate"),
+                                  ("wup", "ffn_up"), ("wdown", "ffn_down")):
+                setattr(L, field_name, wt(b + t + ".weight"))
+            L.bq = opt(b + "attn_q.bias")
+            L.bk = opt(b + "attn_k.bias")
+            L.bv = opt(b + "attn_v.bias")
+        self._layers = layers
+        out_name = "output.weight" if "output.weight" in tensors else "token_embd.weight"
+        self.m = OrcModel(hp.n_layer, hp.n_embd, hp.n_heads, hp.n_kv_heads, hp.ffn_dim,
+                          hp.n_vocab, hp.n_ctx, hp.rms_eps, hp.rope_theta,
+                          wt("token_embd.weight"), arr("output_norm.weight")[1], wt(out_name),
+                          layers)
+        self.state = orc.orc_state_new(C.byref(self.m))
+
+    def close(self):
+        if self.state:
+            orc.orc_state_free(self.state)
+            self.state = None
+
+    def reset(self):
+        self.close()
+        self.state = orc.orc_state_new(C.byref(self.m))
+
+    def kv_view(self):
+        hp = self.hp
+        n = hp.n_layer * hp.n_ctx * hp.n_kv_heads * hp.head_dim
+        shape = (hp.n_layer, hp.n_ctx, hp.n_kv_heads * hp.head_dim)
+        k = np.ctypeslib.as_array(orc.orc_state_kv_k(self.state), (n,)).reshape(shape)
+        v = np.ctypeslib.as_array(orc.orc_state_kv_v(self.state), (n,)).reshape(shape)
+        return k, v
+
+    def x_view(self):
+        return np.ctypeslib.as_array(orc.orc_state_x(self.state), (self.hp.n_embd,))
+
+    def logits(self):
+        return np.ctypeslib.as_array(orc.orc_state_logits(self.state), (self.hp.n_vocab,)).copy()
+
+    def forward_layer(self, layer, pos):
+        orc.orc_forward_layer(C.byref(self.m), self.state, layer, pos)
+
+    def forward_token(self, token, pos):
+        orc.orc_forward_token(C.byref(self.m), self.state, token, pos)
+
+    def forward_batch(self, tokens, pos_start=0):
+        t = np.ascontiguousarray(tokens, np.int32)
+        orc.orc_forward_batch(C.byref(self.m), self.state, _ptr(t), t.size, pos_start)
+
+    def generate(self, prompt, n_gen, batched_prefill=True):
+        p = np.ascontiguousarray(prompt, np.int32)
+        toks = np.zeros(max(n_gen, 1), np.int32)
+        margins = np.zeros(max(n_gen, 1), np.float32)
+        n = orc.orc_generate_greedy(C.byref(self.m), _ptr(p), p.size, n_gen,
+                                    1 if batched_prefill else 0, _ptr(toks), _ptr(margins))
+        return toks[:n], margins[:n]

@@ -1,0 +1,312 @@
+"""GPU parity of every kernel of the path against the CPU oracle (which is
+itself bit-exact against the reference's compiled x86 kernels, see
+test_oracle_ref.py).  Integer/byte work and dequantisation are compared bit
+for bit; fp32 reductions within |gpu - ref| <= 1e-4 + 1e-3*|ref| (the
+north-star GEMV tolerance) unless a tighter bound is stated."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+Q4K, Q6K = 12, 14
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def close(gpu, ref, rtol=RTOL, atol=ATOL):
+    gpu = np.asarray(gpu, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(gpu - ref) - (atol + rtol * np.abs(ref))
+    return bool(np.all(err <= 0)), float(np.max(np.abs(gpu - ref)) if gpu.size else 0.0)
+
+
+def weights(qtype, rows, cols, seed):
+    from llm_core_amd import hip
+    return hip.synth_weight(qtype, rows, cols, seed)
+
+
+def finite_random_blocks(qtype, nblocks, seed):
+    """Random bytes with finite fp16 scales (zero, subnormal and normal)."""
+    rng = np.random.default_rng(seed)
+    bb = O.BLOCK_BYTES[qtype]
+    blk = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    h = rng.integers(0, 0x7c00, size=(nblocks, 2), dtype=np.uint16)  # exponent < 31
+    h |= (rng.integers(0, 2, size=(nblocks, 2), dtype=np.uint16) << 15)
+    h[0] = 0
+    hb = h.view(np.uint8).reshape(nblocks, 4)
+    if qtype == Q4K:
+        blk[:, 0:4] = hb
+    else:
+        blk[:, 208:210] = hb[:, 0:2]
+    return blk.reshape(-1)
+
+
+# ---------------------------------------------------------------------------
+# dequantisation / quantisation (bit-exact)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("qtype", [Q4K, Q6K])
+@pytest.mark.parametrize("kind", ["synthetic", "random_bytes"])
+def test_dequant_bitexact(ctx, qtype, kind):
+    nb = 1031
+    blk = weights(qtype, nb, 256, 3) if kind == "synthetic" else finite_random_blocks(qtype, nb, 4)
+    W = ctx.upload(blk)
+    y = ctx.alloc(nb * 256 * 4)
+    ctx.dequant(qtype, y, W, nb)
+    got = ctx.download(y, np.float32, nb * 256)
+    want = O.dequant(qtype, blk)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_quantize_q8_0_bitexact(ctx):
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(4096) * rng.choice([1e-30, 1e-3, 1.0, 1e3], 4096)).astype(np.float32)
+    # edge blocks: all zero; exact .5 ties (amax 127 -> id == 1); one large outlier
+    x[:32] = 0
+    x[32:64] = np.arange(-15.5, 16.5, 1.0, dtype=np.float32)
+    x[63] = 127.0
+    x[64:96] = 1e-3
+    x[64] = 1e6
+    xd = ctx.upload(x)
+    q = ctx.alloc(4096 // 32 * 36)
+    ctx.quantize_q8_0(q, xd, 4096)
+    got = ctx.download(q, np.uint8, 4096 // 32 * 36)
+    assert np.array_equal(got, O.quantize_q8_0(x))
+
+
+def test_q8_0_zero_length_and_bad_n(ctx):
+    from llm_core_amd._ffi import AxfError
+    xd = ctx.alloc(256)
+    ctx.quantize_q8_0(xd, xd, 0)  # no-op
+    with pytest.raises(AxfError):
+        ctx.quantize_q8_0(xd, xd, 33)
+
+
+# ---------------------------------------------------------------------------
+# GEMV
+# ---------------------------------------------------------------------------
+
+GEMV_SHAPES = [
+    (Q4K, 4096, 4096),   # config 1
+    (Q4K, 1, 256),
+    (Q4K, 37, 512),
+    (Q4K, 100, 2048),
+    (Q4K, 75, 11008),    # 43 blocks per row
+    (Q4K, 33, 16384),
+    (Q6K, 1, 256),
+    (Q6K, 37, 2048),
+    (Q6K, 64, 4096),
+    (Q6K, 101, 11008),   # 9030-byte rows: odd rows start 2 bytes past a dword
+    (Q6K, 17, 14336),
+]
+
+
+@pytest.mark.parametrize("qtype,rows,cols", GEMV_SHAPES)
+def test_gemv_q8(ctx, qtype, rows, cols):
+    W = weights(qtype, rows, cols, rows + cols)
+    x = (np.random.default_rng(rows).standard_normal(cols)).astype(np.float32)
+    xq = O.quantize_q8_0(x)
+    want = O.gemv_q8(qtype, W, xq, rows, cols)
+    dW, dx, dy = ctx.upload(W), ctx.upload(xq), ctx.alloc(rows * 4)
+    ctx.gemv_q8(qtype, dy, dW, dx, rows, cols, O.row_bytes(qtype, cols))
+    ok, err = close(ctx.download(dy, np.float32, rows), want)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("qtype,rows,cols", [s for s in GEMV_SHAPES if s[2] <= 11008])
+def test_gemv_f32(ctx, qtype, rows, cols):
+    W = weights(qtype, rows, cols, 3 * rows + cols)
+    x = (np.random.default_rng(cols).standard_normal(cols)).astype(np.float32)
+    want = O.gemv_f32(qtype, W, x, rows, cols)
+    dW, dx, dy = ctx.upload(W), ctx.upload(x), ctx.alloc(rows * 4)
+    ctx.gemv_f32(qtype, dy, dW, dx, rows, cols, O.row_bytes(qtype, cols))
+    got = ctx.download(dy, np.float32, rows)
+    ok, err = close(got, want)
+    assert ok, f"max abs err {err}"
+    # and against a float64 product of the bit-exact dequantised weights
+    d = O.dequant(qtype, W).reshape(rows, cols).astype(np.float64)
+    ok, err = close(got, d @ x.astype(np.float64))
+    assert ok, f"vs float64: {err}"
+
+
+@pytest.mark.parametrize("qtype", [Q4K, Q6K])
+def test_gemv_accumulate(ctx, qtype):
+    rows, cols = 300, 2048
+    W = weights(qtype, rows, cols, 9)
+    x = np.random.default_rng(1).standard_normal(cols).astype(np.float32)
+    y0 = np.random.default_rng(2).standard_normal(rows).astype(np.float32)
+    xq = O.quantize_q8_0(x)
+    dW, dx, dy = ctx.upload(W), ctx.upload(xq), ctx.upload(y0)
+    ctx.gemv_q8(qtype, dy, dW, dx, rows, cols, O.row_bytes(qtype, cols), accumulate=True)
+    want = y0 + O.gemv_q8(qtype, W, xq, rows, cols)
+    ok, err = close(ctx.download(dy, np.float32, rows), want)
+    assert ok, err
+
+
+def test_gemv_rejects_bad_arguments(ctx):
+    from llm_core_amd._ffi import AXF_ERR_INVALID_ARG, AXF_ERR_UNSUPPORTED, AxfError
+    W = ctx.alloc(1 << 20)
+    x = ctx.alloc(1 << 16)
+    y = ctx.alloc(1 << 16)
+    with pytest.raises(AxfError) as e:  # cols not a multiple of 256
+        ctx.gemv_q8(Q4K, y, W, x, 4, 300, 144)
+    assert e.value.code == AXF_ERR_INVALID_ARG
+    with pytest.raises(AxfError) as e:  # Q4_K weights must be 16-byte aligned
+        ctx.gemv_q8(Q4K, y, W.at(8), x, 4, 256, 144)
+    assert e.value.code == AXF_ERR_INVALID_ARG
+    with pytest.raises(AxfError) as e:  # row_bytes below one row
+        ctx.gemv_q8(Q6K, y, W, x, 4, 512, 210)
+    assert e.value.code == AXF_ERR_INVALID_ARG
+    with pytest.raises(AxfError) as e:  # above the largest supported K
+        ctx.gemv_q8(Q4K, y, W, x, 1, 33024, 129 * 144)
+    assert e.value.code == AXF_ERR_UNSUPPORTED
+    with pytest.raises(AxfError) as e:  # F32 activation too large for LDS staging
+        ctx.gemv_f32(Q6K, y, W, x, 1, 16384, 64 * 210)
+    assert e.value.code == AXF_ERR_UNSUPPORTED
+    ctx.gemv_q8(Q4K, y, W, x, 0, 256, 144)  # empty: no-op
+
+
+# ---------------------------------------------------------------------------
+# batched Q4_K x Q8_0
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,cols,T", [(11008, 4096, 1), (11008, 4096, 4), (1024, 4096, 16),
+                                         (512, 4096, 64), (75, 11008, 5), (33, 256, 9)])
+def test_gemm_q4k_q8(ctx, rows, cols, T):
+    W = weights(Q4K, rows, cols, 4)
+    X = np.random.default_rng(T).standard_normal(T * cols).astype(np.float32)
+    XQ = O.quantize_q8_0(X)
+    want = O.gemm_q4k_q8(W, XQ, rows, T, cols)
+    dW, dX, dY = ctx.upload(W), ctx.upload(XQ), ctx.alloc(T * rows * 4)
+    ctx.gemm_q4k_q8(dY, dW, dX, rows, T, cols, O.row_bytes(Q4K, cols))
+    got = ctx.download(dY, np.float32, T * rows).reshape(T, rows)
+    ok, err = close(got, want)
+    assert ok, err
+    # row t of the batched product equals the GEMV of token t
+    t = T // 2
+    dy = ctx.alloc(rows * 4)
+    ctx.gemv_q8(Q4K, dy, dW, dX.at(t * cols // 32 * 36), rows, cols, O.row_bytes(Q4K, cols))
+    ok, err = close(got[t], ctx.download(dy, np.float32, rows), rtol=1e-5, atol=1e-6)
+    assert ok, err
+
+
+# ---------------------------------------------------------------------------
+# decode-step operations
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 2, 255, 256, 257, 32000, 151936])
+def test_argmax_first_index(ctx, n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32)
+    if n > 10:
+        x[n // 3] = x[n - 2] = x.max() + 1.0  # tie: the first index wins
+    dx, di = ctx.upload(x), ctx.alloc(4)
+    ctx.argmax(di, dx, n)
+    assert int(ctx.download(di, np.int32, 1)[0]) == O.argmax(x) == int(np.argmax(x))
+
+
+def test_argmax_all_equal_and_neg_inf(ctx):
+    x = np.full(5000, -np.inf, np.float32)
+    x[4000:] = -1.0
+    dx, di = ctx.upload(x), ctx.alloc(4)
+    ctx.argmax(di, dx, x.size)
+    assert int(ctx.download(di, np.int32, 1)[0]) == 4000
+
+
+@pytest.mark.parametrize("n", [32, 2048, 4096, 11008])
+def test_rmsnorm(ctx, n):
+    x = np.random.default_rng(n).standard_normal(n).astype(np.float32) * 3
+    w = (1 + 0.1 * np.random.default_rng(n + 1).standard_normal(n)).astype(np.float32)
+    dx, dw, dy, dq = ctx.upload(x), ctx.upload(w), ctx.alloc(n * 4), ctx.alloc(n // 32 * 36)
+    ctx.rmsnorm(dy, dq, dx, dw, n, 1e-6)
+    got = ctx.download(dy, np.float32, n)
+    ok, err = close(got, O.rmsnorm(x, w, 1e-6), rtol=2e-6, atol=1e-7)
+    assert ok, err
+    # the fused Q8_0 output is the Q8_0 of the fused f32 output
+    assert np.array_equal(ctx.download(dq, np.uint8, n // 32 * 36), O.quantize_q8_0(got))
+
+
+def test_rmsnorm_closed_form(ctx):
+    # reference tests/test_backend_x86.cpp:84-116: x = 1..8 (tiled), w = 1
+    x = np.tile(np.arange(1, 9, dtype=np.float32), 4)
+    w = np.ones(32, np.float32)
+    dx, dw, dy = ctx.upload(x), ctx.upload(w), ctx.alloc(128)
+    ctx.rmsnorm(dy, None, dx, dw, 32, 1e-5)
+    want = x / np.sqrt(np.float32(204.0 / 8.0 + 1e-5))
+    assert np.allclose(ctx.download(dy, np.float32, 32), want, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("hd,n_heads", [(128, 16), (64, 4), (128, 2)])
+def test_rope_bitexact(ctx, hd, n_heads):
+    from llm_core_amd import hip
+    max_pos = 300
+    c, s = hip.rope_table(hd, 1e6, max_pos)
+    oc, os_ = O.rope_table(hd, 1e6, max_pos)
+    assert np.array_equal(c, oc) and np.array_equal(s, os_)
+    dc, ds = ctx.upload(c), ctx.upload(s)
+    x = np.random.default_rng(hd).standard_normal(n_heads * hd).astype(np.float32)
+    dx, dy = ctx.upload(x), ctx.alloc(x.nbytes)
+    for pos in (0, 1, 17, max_pos - 1):
+        ctx.rope(dy, dx, pos, n_heads, hd, dc, ds)
+        got = ctx.download(dy, np.float32, x.size)
+        assert np.array_equal(got, O.rope(x, pos, n_heads, hd, oc, os_))
+    ctx.rope(dx, dx, 5, n_heads, hd, dc, ds)  # in place
+    assert np.array_equal(ctx.download(dx, np.float32, x.size), O.rope(x, 5, n_heads, hd, oc, os_))
+
+
+@pytest.mark.parametrize("seq,H,KVH,hd", [(1, 16, 2, 128), (5, 16, 2, 128), (64, 4, 4, 64),
+                                          (65, 8, 2, 128), (1024, 16, 2, 128), (2048, 32, 32, 128),
+                                          (300, 4, 1, 256)])
+def test_attention(ctx, seq, H, KVH, hd):
+    rng = np.random.default_rng(seq + H)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kc = rng.standard_normal(seq * KVH * hd).astype(np.float32)
+    vc = rng.standard_normal(seq * KVH * hd).astype(np.float32)
+    dq, dk, dv = ctx.upload(q), ctx.upload(kc), ctx.upload(vc)
+    do, dq8 = ctx.alloc(H * hd * 4), ctx.alloc(H * hd // 32 * 36)
+    ctx.attn_decode(do, dq8, dq, dk, dv, seq, H, KVH, hd)
+    got = ctx.download(do, np.float32, H * hd)
+    want = O.attention(q, kc, vc, seq, H, KVH, hd)
+    ok, err = close(got, want, rtol=1e-5, atol=1e-6)
+    assert ok, err
+    if seq == 1:  # a single position returns V of its kv head exactly
+        assert np.array_equal(got.reshape(H, hd), np.repeat(vc.reshape(KVH, hd), H // KVH, 0))
+    assert np.array_equal(ctx.download(dq8, np.uint8, H * hd // 32 * 36), O.quantize_q8_0(got))
+
+
+@pytest.mark.parametrize("n", [32, 11008])
+def test_swiglu_bitexact(ctx, n):
+    rng = np.random.default_rng(n)
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    g[:4] = [0.0, -0.0, 100.0, -100.0]
+    u = rng.standard_normal(n).astype(np.float32)
+    dg, du, do, dq = ctx.upload(g), ctx.upload(u), ctx.alloc(n * 4), ctx.alloc(n // 32 * 36)
+    ctx.swiglu(do, dq, dg, du, n)
+    got = ctx.download(do, np.float32, n)
+    assert np.array_equal(got, O.swiglu(g, u))
+    assert np.array_equal(ctx.download(dq, np.uint8, n // 32 * 36), O.quantize_q8_0(got))
+
+
+@pytest.mark.parametrize("qtype", [Q4K, Q6K])
+def test_embed_row_bitexact(ctx, qtype):
+    rows, cols = 50, 2048
+    W = weights(qtype, rows, cols, 12)
+    dW, do = ctx.upload(W), ctx.alloc(cols * 4)
+    for tok in (0, 7, rows - 1):
+        ctx.embed(do, qtype, dW, tok, rows, cols)
+        want = O.dequant(qtype, W).reshape(rows, cols)[tok]
+        assert np.array_equal(ctx.download(do, np.float32, cols), want)
+    from llm_core_amd._ffi import AxfError
+    with pytest.raises(AxfError):
+        ctx.embed(do, qtype, dW, rows, rows, cols)
+
+
+def test_add(ctx):
+    a = np.arange(1000, dtype=np.float32)
+    b = np.ones(1000, np.float32) * 0.5
+    da, db, dy = ctx.upload(a), ctx.upload(b), ctx.alloc(4000)
+    ctx.add(dy, da, db, 1000)
+    assert np.array_equal(ctx.download(dy, np.float32, 1000), a + b)
