@@ -152,6 +152,14 @@ int axf_hip_embed(axf_ctx* ctx, float* out, int qtype, const void* W, int token,
 int axf_hip_timer_start(axf_ctx* ctx);
 int axf_hip_timer_stop(axf_ctx* ctx, float* ms); /* waits for the stop event */
 
+/* Benchmark helper (no reference counterpart): captures one HIP graph of n_w
+ * GEMV launches, launch i reading weight copy W_list[i] (so consecutive
+ * launches stream different memory), replays it once untimed and then `reps`
+ * times between two events; *ms = elapsed milliseconds for reps*n_w launches.
+ * kind: 0 Q4_K x Q8_0, 1 Q6_K x Q8_0, 2 Q4_K x F32, 3 Q6_K x F32. */
+int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_list, int n_w,
+                       const void* x, int rows, int cols, size_t row_bytes, int reps, float* ms);
+
 /* ---- synthetic GGUF weights (host code, deterministic) ------------------ */
 /* dst[i] ~ N(mean, std) from a counter-based generator (splitmix64 + Box-Muller);
  * element i depends only on (seed, i). */
@@ -199,10 +207,12 @@ int axf_llama_forward_token(axf_llama* m, int token, int pos);
  * EOS).  use_graph != 0 replays one captured HIP graph per step. */
 int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_gen,
                        int32_t* out_tokens, int use_graph);
-/* Time `steps` graph-replayed decode steps starting at position start_pos
- * (KV positions below start_pos must already be filled) after `warmup`
- * untimed steps; *ms = elapsed milliseconds of the timed steps. */
-int axf_llama_bench_decode(axf_llama* m, int start_pos, int warmup, int steps, float* ms);
+/* Time `steps` graph-replayed decode steps, each at position `pos` (the
+ * attention reads KV rows 0..pos; rows below pos must already be filled, row
+ * pos is rewritten by every step), after `warmup` untimed steps; each step
+ * feeds the previous step's argmax.  *ms = elapsed milliseconds of the timed
+ * steps (HIP events on the context stream). */
+int axf_llama_bench_decode(axf_llama* m, int pos, int warmup, int steps, float* ms);
 
 #ifdef __cplusplus
 }

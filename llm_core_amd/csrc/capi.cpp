@@ -370,6 +370,40 @@ int axf_hip_timer_stop(axf_ctx* ctx, float* ms) {
     return AXF_OK;
 }
 
+int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_list, int n_w,
+                       const void* x, int rows, int cols, size_t row_bytes, int reps, float* ms) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(kind >= 0 && kind <= 3 && W_list && n_w > 0 && reps > 0 && ms, "bad arguments");
+    static const GemvKind kinds[4] = {GemvKind::Q4K_Q8, GemvKind::Q6K_Q8, GemvKind::Q4K_F32,
+                                      GemvKind::Q6K_F32};
+    const int qtype = (kind == 0 || kind == 2) ? AXF_TYPE_Q4_K : AXF_TYPE_Q6_K;
+    for (int i = 0; i < n_w; i++) {
+        int rc = check_gemv(__func__, qtype, W_list[i], x, y, rows, cols, row_bytes, kind >= 2);
+        if (rc) return rc;
+    }
+    hipStream_t st = ctx->stream;
+    AXF_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < n_w && e == hipSuccess; i++)
+        e = launch_gemv(kinds[kind], y, W_list[i], x, rows, cols / QK_K, (long)row_bytes, 0, st);
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(st, &g);
+    if (e != hipSuccess) return hip_fail(e, "axf_hip_bench_gemv: capture");
+    if (e2 != hipSuccess) return hip_fail(e2, "axf_hip_bench_gemv: end capture");
+    hipGraphExec_t ex = nullptr;
+    e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e == hipSuccess) e = hipGraphLaunch(ex, st);
+    if (e == hipSuccess) e = hipEventRecord(ctx->ev0, st);
+    for (int r = 0; r < reps && e == hipSuccess; r++) e = hipGraphLaunch(ex, st);
+    if (e == hipSuccess) e = hipEventRecord(ctx->ev1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(ctx->ev1);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, ctx->ev0, ctx->ev1);
+    if (ex) (void)hipGraphExecDestroy(ex);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "axf_hip_bench_gemv");
+    return AXF_OK;
+}
+
 size_t axf_row_bytes(int qtype, int64_t cols) {
     const int64_t nb = cols / QK_K;
     if (qtype == AXF_TYPE_Q4_K) return (size_t)nb * Q4K_BYTES;

@@ -75,8 +75,10 @@ struct axf_llama {
     int *d_token = nullptr, *d_pos = nullptr, *d_step = nullptr, *d_tokens = nullptr;
     int max_tokens = 0;
 
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // graph[0]: generation step (records the token, advances the position);
+    // graph[1]: fixed-position step used to time decode at a given context
+    hipGraph_t graph[2] = {nullptr, nullptr};
+    hipGraphExec_t exec[2] = {nullptr, nullptr};
 };
 
 namespace {
@@ -223,7 +225,7 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
 }
 
 // Whole step: embedding of *d_token (or `token`), layers, final norm, head,
-// argmax into d_token (+ tokens[step++], pos++ when record != 0).
+// argmax into d_token (+ tokens[step++] and pos++ when record != 0).
 hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, bool record) {
     const auto& hp = m->hp;
     hipStream_t st = m->ctx->stream;
@@ -241,20 +243,21 @@ hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, boo
         return e;
     return launch_argmax(m->d_token, m->arg_v, m->arg_i, m->logits, hp.n_vocab,
                          record ? m->d_tokens : nullptr, record ? m->d_step : nullptr,
-                         device_state ? m->d_pos : nullptr, st);
+                         (device_state && record) ? m->d_pos : nullptr, st);
 }
 
-int ensure_graph(axf_llama* m) {
-    if (m->exec) return AXF_OK;
+// kind 0: generation step; kind 1: fixed-position step (no token record, no pos advance)
+int ensure_graph(axf_llama* m, int kind) {
+    if (m->exec[kind]) return AXF_OK;
     hipStream_t st = m->ctx->stream;
     LL_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    hipError_t e = enqueue_step(m, true, 0, 0, true);
+    hipError_t e = enqueue_step(m, true, 0, 0, kind == 0);
     hipGraph_t g = nullptr;
     hipError_t e2 = hipStreamEndCapture(st, &g);
     if (e != hipSuccess) return hip_fail(e, "axf_llama: capture");
     if (e2 != hipSuccess) return hip_fail(e2, "axf_llama: hipStreamEndCapture");
-    m->graph = g;
-    LL_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    m->graph[kind] = g;
+    LL_HIP(hipGraphInstantiate(&m->exec[kind], g, nullptr, nullptr, 0));
     return AXF_OK;
 }
 
@@ -290,8 +293,10 @@ int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out)
 int axf_llama_destroy(axf_llama* m) {
     if (!m) return AXF_OK;
     (void)hipStreamSynchronize(m->ctx->stream);
-    if (m->exec) (void)hipGraphExecDestroy(m->exec);
-    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (int k = 0; k < 2; k++) {
+        if (m->exec[k]) (void)hipGraphExecDestroy(m->exec[k]);
+        if (m->graph[k]) (void)hipGraphDestroy(m->graph[k]);
+    }
     for (void* p : m->allocs) (void)hipFree(p);
     delete m;
     return AXF_OK;
@@ -481,12 +486,12 @@ int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_
     hipStream_t st = m->ctx->stream;
     LL_HIP(launch_set_int(m->d_step, 0, st));
     LL_HIP(launch_set_int(m->d_pos, 0, st));
-    if (use_graph) LL_TRY(ensure_graph(m));
+    if (use_graph) LL_TRY(ensure_graph(m, 0));
     // prefill token by token; the argmax of the last prompt step is token 0
     for (int t = 0; t < n_prompt; t++) {
         LL_HIP(launch_set_int(m->d_token, prompt[t], st));
         if (use_graph)
-            LL_HIP(hipGraphLaunch(m->exec, st));
+            LL_HIP(hipGraphLaunch(m->exec[0], st));
         else
             LL_HIP(enqueue_step(m, true, 0, 0, true));
     }
@@ -494,7 +499,7 @@ int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_
     if (n_gen > 0) LL_HIP(launch_push_token(m->d_tokens, m->d_step, m->d_token, st));
     for (int i = 1; i < n_gen; i++) {
         if (use_graph)
-            LL_HIP(hipGraphLaunch(m->exec, st));
+            LL_HIP(hipGraphLaunch(m->exec[0], st));
         else
             LL_HIP(enqueue_step(m, true, 0, 0, true));
     }
@@ -505,19 +510,17 @@ int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_
     return AXF_OK;
 }
 
-int axf_llama_bench_decode(axf_llama* m, int start_pos, int warmup, int steps, float* ms) {
+int axf_llama_bench_decode(axf_llama* m, int pos, int warmup, int steps, float* ms) {
     LL_LOADED(m);
-    if (!ms || start_pos < 0 || warmup < 0 || steps <= 0 ||
-        start_pos + warmup + steps > m->hp.n_ctx || warmup + steps > m->max_tokens)
+    if (!ms || pos < 0 || pos >= m->hp.n_ctx || warmup < 0 || steps <= 0)
         return fail(AXF_ERR_INVALID_ARG, "axf_llama_bench_decode: bad arguments");
     hipStream_t st = m->ctx->stream;
-    LL_TRY(ensure_graph(m));
-    LL_HIP(launch_set_int(m->d_step, 0, st));
-    LL_HIP(launch_set_int(m->d_pos, start_pos, st));
+    LL_TRY(ensure_graph(m, 1));
+    LL_HIP(launch_set_int(m->d_pos, pos, st));
     LL_HIP(launch_set_int(m->d_token, 1, st));
-    for (int i = 0; i < warmup; i++) LL_HIP(hipGraphLaunch(m->exec, st));
+    for (int i = 0; i < warmup; i++) LL_HIP(hipGraphLaunch(m->exec[1], st));
     LL_HIP(hipEventRecord(m->ctx->ev0, st));
-    for (int i = 0; i < steps; i++) LL_HIP(hipGraphLaunch(m->exec, st));
+    for (int i = 0; i < steps; i++) LL_HIP(hipGraphLaunch(m->exec[1], st));
     LL_HIP(hipEventRecord(m->ctx->ev1, st));
     LL_HIP(hipEventSynchronize(m->ctx->ev1));
     LL_HIP(hipEventElapsedTime(ms, m->ctx->ev0, m->ctx->ev1));

@@ -162,6 +162,16 @@ class Context:
         call("axf_hip_timer_stop", self.handle, C.byref(ms))
         return ms.value
 
+    def bench_gemv(self, kind: int, y: int, W_list, x: int, rows: int, cols: int, rb: int,
+                   reps: int) -> float:
+        """Milliseconds for reps*len(W_list) graph-replayed GEMV launches
+        (kind 0 Q4_K x Q8_0, 1 Q6_K x Q8_0, 2 Q4_K x F32, 3 Q6_K x F32)."""
+        arr = (C.c_void_p * len(W_list))(*[int(w) for w in W_list])
+        ms = C.c_float(0)
+        call("axf_hip_bench_gemv", self.handle, kind, C.c_void_p(int(y)), arr, len(W_list),
+             C.c_void_p(int(x)), rows, cols, C.c_size_t(rb), reps, C.byref(ms))
+        return ms.value
+
 
 def rope_table(head_dim: int, theta: float, max_pos: int) -> tuple[np.ndarray, np.ndarray]:
     c = np.empty(max_pos * (head_dim // 2), np.float32)

@@ -175,7 +175,8 @@ class LlamaHip:
              out.ctypes.data_as(C.c_void_p), 1 if use_graph else 0)
         return out[:n_gen]
 
-    def bench_decode(self, start_pos: int, warmup: int, steps: int) -> float:
+    def bench_decode(self, pos: int, warmup: int, steps: int) -> float:
+        """Milliseconds for `steps` graph-replayed decode steps at position `pos`."""
         ms = C.c_float(0)
-        call("axf_llama_bench_decode", self.handle, start_pos, warmup, steps, C.byref(ms))
+        call("axf_llama_bench_decode", self.handle, pos, warmup, steps, C.byref(ms))
         return ms.value

@@ -89,6 +89,8 @@ def _load_ref() -> C.CDLL | None:
         "ref_gemm_q4k_q8": ([vp, vp, vp, i32, i32, i32, sz, i32, i32, i32], None),
         "ref_time_decode_gemv": ([i32, C.POINTER(vp), i32, i32, i32, vp, vp, i32, i32,
                                   C.POINTER(i32)], C.c_double),
+        "ref_time_decode_step": ([vp, vp, vp, i32, i32, i32, i32, C.POINTER(i32),
+                                  C.POINTER(i32)], C.c_double),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -194,6 +196,33 @@ def swiglu(g: np.ndarray, u: np.ndarray) -> np.ndarray:
 def argmax(x: np.ndarray) -> int:
     x = np.ascontiguousarray(x, np.float32)
     return int(orc.orc_argmax(_ptr(x), x.size))
+
+
+def ref_time_decode_gemv(qtype: int, W: np.ndarray, rows: int, cols: int, x: np.ndarray,
+                         n_copies: int, iters: int, n_threads: int = 0):
+    """Median seconds per reference decode GEMV (quantize + r8/4-row kernel on the
+    reference ThreadPool), weights rotated over n_copies host buffers."""
+    assert ref is not None, "oracle/_ref not built"
+    if qtype == Q4K:
+        W = repack_r8(W, rows, cols)  # the reference repacks at load (llama_model.cpp:963-971)
+    copies = [W] + [W.copy() for _ in range(n_copies - 1)]
+    arr = (C.c_void_p * n_copies)(*[c.ctypes.data for c in copies])
+    y = np.empty(rows, np.float32)
+    used = C.c_int(0)
+    x = np.ascontiguousarray(x, np.float32)
+    t = ref.ref_time_decode_gemv(qtype, arr, n_copies, rows, cols, _ptr(x), _ptr(y), iters,
+                                 n_threads, C.byref(used))
+    return t, used.value
+
+
+def ref_time_decode_step(model: "OracleModel", kv_k: np.ndarray, kv_v: np.ndarray, pos: int,
+                         warmup: int, steps: int, n_threads: int = 0):
+    """Median seconds per reference decode step (see ref_shim.cpp)."""
+    assert ref is not None, "oracle/_ref not built"
+    used, last = C.c_int(0), C.c_int(0)
+    t = ref.ref_time_decode_step(C.byref(model.m), _ptr(kv_k), _ptr(kv_v), pos, warmup, steps,
+                                 n_threads, C.byref(used), C.byref(last))
+    return t, used.value, last.value
 
 
 def top2_margin(x: np.ndarray) -> float:

@@ -159,4 +159,169 @@ double ref_time_decode_gemv(int qtype, const uint8_t* const* W_copies, int n_cop
     return t[iters / 2];
 }
 
+// ---------------------------------------------------------------------------
+// CPU baseline for the whole decode step: llama_forward_token
+// (llama_model.cpp:1207-1333) with the reference's dispatch — Q8_0 quantize,
+// r8 Q4_K GEMV (VNNI or AVX2 by CPUID) over 8-row groups, Q6_K 4-row GEMV,
+// gate+up+SwiGLU fused in one parallel_for (Fusion C, :1284-1314) — on the
+// reference ThreadPool.  The ops that live as static functions in
+// llama_model.cpp (RMSNorm, RoPE, attention, SwiGLU, embedding dequant) come
+// from the oracle's restatement of them (axf_oracle.c), single-threaded as in
+// the reference.  Every timed step runs at position `pos` (rows below pos of
+// the caller's KV cache must be filled; row pos is rewritten).  Returns the
+// median seconds per step.
+// ---------------------------------------------------------------------------
 }  // extern "C"
+
+#include "axf_oracle.h"
+
+namespace {
+
+struct WtR {
+    const orc_wt* w;
+    std::vector<uint8_t> r8;  // repacked copy when Q4_K with rows % 8 == 0
+};
+
+WtR make_wt(const orc_wt* w, int rows, int cols) {
+    WtR r{w, {}};
+    if (w->type == ORC_TYPE_Q4_K && rows % 8 == 0) {
+        r.r8.resize((size_t)(rows / 8) * (cols / 256) * 1152);
+        cx::repack_q4k_8rows(r.r8.data(), w->data, rows, cols);
+    }
+    return r;
+}
+
+// gemv_wt_q8 (llama_model.cpp:767-831)
+void gemv_wt_q8(float* y, const WtR& W, const block_q8_0* xq8, int out, int in,
+                axonforge::ThreadPool* pool, bool vnni) {
+    if (W.w->type == ORC_TYPE_Q4_K && !W.r8.empty()) {
+        const uint8_t* R8 = W.r8.data();
+        const int n8 = out / 8;
+        auto fn = [&](int gs, int ge) {
+            if (vnni)
+                cx::gemv_q4k_r8_avxvnni_range(y, R8, xq8, gs * 8, ge * 8, in);
+            else
+                cx::gemv_q4k_r8_avx2_range(y, R8, xq8, gs * 8, ge * 8, in);
+        };
+        if (pool && n8 >= 2) pool->parallel_for(n8, fn); else fn(0, n8);
+        return;
+    }
+    const size_t rb = (size_t)(in / 256) * (W.w->type == ORC_TYPE_Q6_K ? 210 : 144);
+    auto fn = [&](int s, int e) {
+        if (W.w->type == ORC_TYPE_Q6_K)
+            cx::gemv_q6k_q8_avx2_range(y, W.w->data, xq8, s, e, in, rb);
+        else if (vnni)
+            cx::gemv_q4k_q8_avxvnni_range(y, W.w->data, xq8, s, e, in, rb);
+        else
+            cx::gemv_q4k_q8_avx2_range(y, W.w->data, xq8, s, e, in, rb);
+    };
+    if (pool && out >= 32) pool->parallel_for(out, fn); else fn(0, out);
+}
+
+}  // namespace
+
+extern "C" double ref_time_decode_step(const orc_model* m, float* kv_k, float* kv_v, int pos,
+                                       int warmup, int steps, int n_threads, int* threads_used,
+                                       int* last_token) {
+    if (n_threads <= 0) n_threads = std::min(16, (int)std::thread::hardware_concurrency());
+    if (threads_used) *threads_used = n_threads;
+    const int E = m->n_embd, H = m->n_heads, KVH = m->n_kv_heads, HD = E / H, FD = m->ffn_dim;
+    const int kve = KVH * HD, L = m->n_layer, NC = m->n_ctx;
+    const bool vnni = cx::cpu_features().avxvnni;
+
+    // build_weights + repack_q4k_if_avx2 (llama_model.cpp:963-1019), untimed
+    std::vector<WtR> wq, wk, wv, wo, wg, wu, wd;
+    for (int l = 0; l < L; l++) {
+        const orc_layer& lw = m->layers[l];
+        wq.push_back(make_wt(&lw.wq, H * HD, E));
+        wk.push_back(make_wt(&lw.wk, kve, E));
+        wv.push_back(make_wt(&lw.wv, kve, E));
+        wo.push_back(make_wt(&lw.wo, E, H * HD));
+        wg.push_back(make_wt(&lw.wgate, FD, E));
+        wu.push_back(make_wt(&lw.wup, FD, E));
+        wd.push_back(make_wt(&lw.wdown, E, FD));
+    }
+    WtR head = make_wt(&m->output, m->n_vocab, E);
+
+    cpu_set_t orig_aff;
+    sched_getaffinity(0, sizeof(orig_aff), &orig_aff);
+    const int nw = n_threads - 1;
+    std::unique_ptr<axonforge::ThreadPool> pool;
+    if (nw > 0) {
+        pool = std::make_unique<axonforge::ThreadPool>(nw);
+        axonforge::ThreadPool::pin_caller(nw);
+    }
+    std::vector<float> x(E), xb(E), q(H * HD), k(kve), v(kve), attn(NC), ao(E), gate(FD), up(FD),
+        ffn(E), logits(m->n_vocab), rc((size_t)NC * HD / 2), rs((size_t)NC * HD / 2);
+    std::vector<block_q8_0> xq8((size_t)std::max(E, FD) / 32);
+    orc_rope_table(rc.data(), rs.data(), HD, m->rope_theta, NC);
+    int token = 1;
+
+    auto step = [&]() {
+        const size_t rbe = (size_t)(E / 256) * (m->tok_embd.type == ORC_TYPE_Q6_K ? 210 : 144);
+        if (m->tok_embd.type == ORC_TYPE_Q6_K)
+            orc_dequant_q6k(x.data(), m->tok_embd.data + (size_t)token * rbe, E / 256);
+        else
+            orc_dequant_q4k(x.data(), m->tok_embd.data + (size_t)token * rbe, E / 256);
+        block_q8_0* xq = xq8.data();
+        for (int l = 0; l < L; l++) {
+            const orc_layer& lw = m->layers[l];
+            float* kc = kv_k + (size_t)l * NC * kve;
+            float* vc = kv_v + (size_t)l * NC * kve;
+            orc_rmsnorm(xb.data(), x.data(), lw.attn_norm, E, m->rms_eps);
+            cx::quantize_q8_avx2(xq, xb.data(), E);
+            gemv_wt_q8(q.data(), wq[l], xq, H * HD, E, pool.get(), vnni);
+            gemv_wt_q8(k.data(), wk[l], xq, kve, E, pool.get(), vnni);
+            gemv_wt_q8(v.data(), wv[l], xq, kve, E, pool.get(), vnni);
+            orc_rope(q.data(), q.data(), pos, H, HD, rc.data(), rs.data());
+            orc_rope(kc + (size_t)pos * kve, k.data(), pos, KVH, HD, rc.data(), rs.data());
+            std::memcpy(vc + (size_t)pos * kve, v.data(), sizeof(float) * kve);
+            orc_attention(ao.data(), q.data(), kc, vc, pos + 1, H, KVH, HD, attn.data());
+            cx::quantize_q8_avx2(xq, ao.data(), E);
+            gemv_wt_q8(xb.data(), wo[l], xq, E, E, pool.get(), vnni);
+            for (int i = 0; i < E; i++) x[i] += xb[i];
+            orc_rmsnorm(xb.data(), x.data(), lw.ffn_norm, E, m->rms_eps);
+            cx::quantize_q8_avx2(xq, xb.data(), E);
+            if (!wg[l].r8.empty() && !wu[l].r8.empty() && pool) {
+                const uint8_t* R8g = wg[l].r8.data();
+                const uint8_t* R8u = wu[l].r8.data();
+                pool->parallel_for(FD / 8, [&](int gs, int ge) {
+                    const int s0 = gs * 8, e0 = ge * 8;
+                    if (vnni) {
+                        cx::gemv_q4k_r8_avxvnni_range(gate.data(), R8g, xq, s0, e0, E);
+                        cx::gemv_q4k_r8_avxvnni_range(up.data(), R8u, xq, s0, e0, E);
+                    } else {
+                        cx::gemv_q4k_r8_avx2_range(gate.data(), R8g, xq, s0, e0, E);
+                        cx::gemv_q4k_r8_avx2_range(up.data(), R8u, xq, s0, e0, E);
+                    }
+                    orc_swiglu(gate.data() + s0, up.data() + s0, e0 - s0);
+                });
+            } else {
+                gemv_wt_q8(gate.data(), wg[l], xq, FD, E, pool.get(), vnni);
+                gemv_wt_q8(up.data(), wu[l], xq, FD, E, pool.get(), vnni);
+                orc_swiglu(gate.data(), up.data(), FD);
+            }
+            cx::quantize_q8_avx2(xq, gate.data(), FD);
+            gemv_wt_q8(ffn.data(), wd[l], xq, E, FD, pool.get(), vnni);
+            for (int i = 0; i < E; i++) x[i] += ffn[i];
+        }
+        orc_rmsnorm(x.data(), x.data(), m->output_norm, E, m->rms_eps);
+        cx::quantize_q8_avx2(xq, x.data(), E);
+        gemv_wt_q8(logits.data(), head, xq, m->n_vocab, E, pool.get(), vnni);
+        token = orc_argmax(logits.data(), m->n_vocab);
+    };
+
+    for (int i = 0; i < warmup; i++) step();
+    std::vector<double> t((size_t)std::max(steps, 1));
+    for (int i = 0; i < steps; i++) {
+        auto t0 = std::chrono::steady_clock::now();
+        step();
+        auto t1 = std::chrono::steady_clock::now();
+        t[i] = std::chrono::duration<double>(t1 - t0).count();
+    }
+    pool.reset();
+    sched_setaffinity(0, sizeof(orig_aff), &orig_aff);
+    if (last_token) *last_token = token;
+    std::sort(t.begin(), t.begin() + steps);
+    return steps > 0 ? t[steps / 2] : 0.0;
+}
