@@ -32,6 +32,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = [
     "kernels/gemv.hip",
     "kernels/ops.hip",
+    "kernels/attention.hip",
     "capi.cpp",
     "host/synth.cpp",
     "host/llama_hip.cpp",

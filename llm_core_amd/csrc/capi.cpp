@@ -312,14 +312,28 @@ int axf_hip_attn_decode(axf_ctx* ctx, float* out, void* outq8, const float* q,
                 "bad shape");
     AXF_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
                 "head_dim must be 64, 128 or 256");
-    AXF_REQUIRE(aligned(q, 16) && aligned(kcache, 16) && aligned(vcache, 16) && aligned(out, 4),
+    AXF_REQUIRE(aligned(q, 4) && aligned(kcache, 16) && aligned(vcache, 16) && aligned(out, 4) &&
+                    aligned(outq8, 4),
                 "misaligned pointer");
+    AXF_REQUIRE(n_heads / n_kv_heads <= 8, "more than 8 query heads per kv head");
     const int nsplit = attn_nsplit(seq);
+    AXF_REQUIRE(nsplit <= 512, "seq above 32768");
     void* scratch = nullptr;
     int rc = ctx_scratch(ctx, (size_t)n_heads * nsplit * (head_dim + 2) * 4, &scratch);
     if (rc) return rc;
-    AXF_HIP(launch_attention(out, outq8, static_cast<float*>(scratch), q, kcache, vcache,
-                             nullptr, seq, nsplit, n_heads, n_kv_heads, head_dim, ctx->stream));
+    AttnArgs a{};
+    a.q = q;
+    a.kcache = const_cast<float*>(kcache);
+    a.vcache = const_cast<float*>(vcache);
+    a.pos = seq - 1;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.nsplit = nsplit;
+    a.store_kv = 0;
+    a.part = static_cast<float*>(scratch);
+    a.out = out;
+    a.outq8 = static_cast<uint8_t*>(outq8);
+    AXF_HIP(launch_attention_fused(a, head_dim, ctx->stream));
     return AXF_OK;
 }
 

@@ -45,11 +45,28 @@ hipError_t launch_rope_qkv(float* q, const float* k, const float* v, float* kcac
                            float* vcache, const int* pos_dev, int pos, int n_heads,
                            int n_kv_heads, int hd, const float* cos_t, const float* sin_t,
                            hipStream_t st);
+// Single-token attention with RoPE and KV store fused (kernels/attention.hip).
+struct AttnArgs {
+    const float* q;      // [H*HD] query (raw projection; RoPE applied when cos_t != nullptr)
+    const float* k;      // [KVH*HD] new key before bias and RoPE (used when store_kv)
+    const float* v;      // [KVH*HD] new value before bias (used when store_kv)
+    const float* bq;     // optional biases
+    const float* bk;
+    const float* bv;
+    const float* cos_t;  // [n_ctx][HD/2] or nullptr (query already rotated)
+    const float* sin_t;
+    float* kcache;       // this layer, rows of KVH*HD floats
+    float* vcache;
+    const int* pos_dev;  // device position (graph replay) or nullptr
+    int pos;             // current position: attention over rows 0..pos
+    int n_heads, n_kv_heads, nsplit;
+    int store_kv;        // write RoPE(k+bk) and v+bv to cache row pos
+    float* part;         // [H][nsplit][HD + 2]
+    float* out;          // [H*HD]
+    uint8_t* outq8;      // Q8_0 blocks of out, or nullptr
+};
 int attn_nsplit(int max_seq);
-hipError_t launch_attention(float* out, void* outq8, float* part, const float* q,
-                            const float* kcache, const float* vcache, const int* pos_dev,
-                            int seq, int nsplit, int n_heads, int n_kv_heads, int hd,
-                            hipStream_t st);
+hipError_t launch_attention_fused(const AttnArgs& a, int head_dim, hipStream_t st);
 hipError_t launch_swiglu(float* out, void* outq8, const float* gate, const float* up, int n,
                          hipStream_t st);
 hipError_t launch_embed(int qtype, float* out, const void* W, const int* tok_dev, int tok,

@@ -203,13 +203,29 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
         ST(gemv(L.wk, k, m->xq8, kvo, E, false, st));
     }
     ST(gemv(L.wv, v, m->xq8, kvo, E, false, st));
-    if (L.bq) ST(launch_add(q, q, L.bq, qo, st));
-    if (L.bk) ST(launch_add(k, k, L.bk, kvo, st));
-    if (L.bv) ST(launch_add(v, v, L.bv, kvo, st));
-    ST(launch_rope_qkv(q, k, v, m->kv_k + loff, m->kv_v + loff, pos_dev, pos, H, KVH, HD,
-                       m->rope_cos, m->rope_sin, st));
-    ST(launch_attention(m->attn_out, m->xq8, m->attn_part, q, m->kv_k + loff, m->kv_v + loff,
-                        pos_dev, pos + 1, m->nsplit, H, KVH, HD, st));
+    {
+        AttnArgs a{};
+        a.q = q;
+        a.k = k;
+        a.v = v;
+        a.bq = L.bq;
+        a.bk = L.bk;
+        a.bv = L.bv;
+        a.cos_t = m->rope_cos;
+        a.sin_t = m->rope_sin;
+        a.kcache = m->kv_k + loff;
+        a.vcache = m->kv_v + loff;
+        a.pos_dev = pos_dev;
+        a.pos = pos;
+        a.n_heads = H;
+        a.n_kv_heads = KVH;
+        a.nsplit = m->nsplit;
+        a.store_kv = 1;
+        a.part = m->attn_part;
+        a.out = m->attn_out;
+        a.outq8 = m->xq8;
+        ST(launch_attention_fused(a, HD, st));
+    }
     ST(gemv(L.wo, m->x, m->xq8, E, E, true, st));
     ST(launch_rmsnorm(nullptr, m->xq8, m->x, L.ffn_norm, E, hp.rms_eps, st));
     if (L.gateup_fused) {
@@ -275,6 +291,10 @@ int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out)
     if (h.n_embd % h.n_heads || h.n_heads % h.n_kv_heads)
         return fail(AXF_ERR_INVALID_ARG, "axf_llama_create: heads do not divide");
     const int hd = h.n_embd / h.n_heads;
+    if (h.n_heads / h.n_kv_heads > 8)
+        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: more than 8 query heads per kv head");
+    if (h.n_ctx > 32768)
+        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: n_ctx above 32768");
     if (hd != 64 && hd != 128 && hd != 256)
         return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: head_dim must be 64, 128 or 256");
     if (h.n_embd % QK_K || h.ffn_dim % QK_K)

@@ -212,153 +212,6 @@ __global__ void k_rope_qkv(float* q, const float* __restrict__ k, const float* _
 }
 
 // ---------------------------------------------------------------------------
-// Single-token attention over the fp32 KV cache, split along the sequence
-// (kAttnSplit positions per workgroup) and combined per head.
-//   partial (h, j): m_j = max score, l_j = sum exp(s - m_j), o_j = sum exp(s - m_j) v
-//   out_h = sum_j o_j e^(m_j - M) / sum_j l_j e^(m_j - M),  s = dot(q_h, k_t) * (1/sqrt(hd))
-// ---------------------------------------------------------------------------
-constexpr int kAttnSplit = 64;
-constexpr int kAttnThreads = 256;
-
-template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_split(
-    float* __restrict__ part, const float* __restrict__ q, const float* __restrict__ kcache,
-    const float* __restrict__ vcache, const int* pos_dev, int seq_imm, int n_heads,
-    int n_kv_heads, int nsplit) {
-    constexpr int DPL = HD / 8;  // dims per lane in the score phase (8 lanes per position)
-    constexpr int VPL = HD / 64; // dims per lane in the value phase
-    __shared__ float sc[kAttnSplit];
-    __shared__ float red[kAttnThreads / 64];
-    __shared__ float ov[kAttnThreads / 64][HD];
-    const int j = blockIdx.x, h = blockIdx.y;
-    const int seq = pos_dev ? (*pos_dev + 1) : seq_imm;
-    const int kvh = h / (n_heads / n_kv_heads);
-    const size_t kv_embd = (size_t)n_kv_heads * HD;
-    const int t0 = j * kAttnSplit;
-    const int t1 = min(t0 + kAttnSplit, seq);
-    float* dst = part + ((size_t)h * nsplit + j) * (HD + 2);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (t0 >= t1) {  // empty split
-        for (int d = threadIdx.x; d < HD; d += kAttnThreads) dst[2 + d] = 0.f;
-        if (threadIdx.x == 0) {
-            dst[0] = -INFINITY;
-            dst[1] = 0.f;
-        }
-        return;
-    }
-    const float scale = 1.f / sqrtf((float)HD);
-    // scores: 8 lanes per position, 8 positions per wave-iteration
-    const int sub = lane & 7, pl = lane >> 3;
-    float qv[DPL];
-    const float* qh = q + (size_t)h * HD + sub * DPL;
-#pragma unroll
-    for (int e = 0; e < DPL; e += 4) {
-        const float4 v4 = *reinterpret_cast<const float4*>(qh + e);
-        qv[e] = v4.x; qv[e + 1] = v4.y; qv[e + 2] = v4.z; qv[e + 3] = v4.w;
-    }
-    for (int tb = t0 + wave * 8; tb < t1; tb += kAttnThreads / 8) {
-        const int t = tb + pl;
-        float s = 0.f;
-        if (t < t1) {
-            const float* kr = kcache + (size_t)t * kv_embd + (size_t)kvh * HD + sub * DPL;
-#pragma unroll
-            for (int e = 0; e < DPL; e += 4) {
-                const float4 k4 = *reinterpret_cast<const float4*>(kr + e);
-                s = fmaf(qv[e], k4.x, s);
-                s = fmaf(qv[e + 1], k4.y, s);
-                s = fmaf(qv[e + 2], k4.z, s);
-                s = fmaf(qv[e + 3], k4.w, s);
-            }
-        }
-        s = group_sum<8>(s);
-        if (sub == 0 && t < t1) sc[t - t0] = s * scale;
-    }
-    __syncthreads();
-    const int n = t1 - t0;
-    // local max and exp
-    float m = -INFINITY;
-    for (int i = threadIdx.x; i < n; i += kAttnThreads) m = fmaxf(m, sc[i]);
-    m = wave_max(m);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    m = red[0];
-#pragma unroll
-    for (int w = 1; w < kAttnThreads / 64; w++) m = fmaxf(m, red[w]);
-    __syncthreads();
-    float l = 0.f;
-    for (int i = threadIdx.x; i < n; i += kAttnThreads) {
-        const float p = expf(sc[i] - m);
-        sc[i] = p;
-        l += p;
-    }
-    l = wave_sum(l);
-    if (lane == 0) red[wave] = l;
-    __syncthreads();
-    // values: each wave takes positions t0+wave, +4, ...; lane owns VPL dims
-    float o[VPL];
-#pragma unroll
-    for (int e = 0; e < VPL; e++) o[e] = 0.f;
-    for (int i = wave; i < n; i += kAttnThreads / 64) {
-        const float p = sc[i];
-        const float* vr = vcache + (size_t)(t0 + i) * kv_embd + (size_t)kvh * HD + lane * VPL;
-#pragma unroll
-        for (int e = 0; e < VPL; e++) o[e] = fmaf(p, vr[e], o[e]);
-    }
-#pragma unroll
-    for (int e = 0; e < VPL; e++) ov[wave][lane * VPL + e] = o[e];
-    __syncthreads();
-    for (int d = threadIdx.x; d < HD; d += kAttnThreads) {
-        float acc = 0.f;
-#pragma unroll
-        for (int w = 0; w < kAttnThreads / 64; w++) acc += ov[w][d];
-        dst[2 + d] = acc;
-    }
-    if (threadIdx.x == 0) {
-        float lt = 0.f;
-#pragma unroll
-        for (int w = 0; w < kAttnThreads / 64; w++) lt += red[w];
-        dst[0] = m;
-        dst[1] = lt;
-    }
-}
-
-// Combine the splits of each head; optionally also write the Q8_0 of the
-// result (HD % 32 == 0, one 32-element block per 8 threads x 4 elements).
-template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_combine(float* __restrict__ out,
-                                                     uint8_t* __restrict__ outq8,
-                                                     const float* __restrict__ part, int nsplit) {
-    const int h = blockIdx.x;
-    const float* ph = part + (size_t)h * nsplit * (HD + 2);
-    float M = -INFINITY;
-    for (int j = 0; j < nsplit; j++) M = fmaxf(M, ph[(size_t)j * (HD + 2)]);
-    float L = 0.f, acc = 0.f;
-    const int d = threadIdx.x;
-    for (int j = 0; j < nsplit; j++) {
-        const float* pj = ph + (size_t)j * (HD + 2);
-        const float lj = pj[1];
-        if (lj > 0.f) {
-            const float wj = expf(pj[0] - M);
-            L = fmaf(lj, wj, L);
-            acc = fmaf(pj[2 + d], wj, acc);
-        }
-    }
-    const float r = acc / L;
-    out[(size_t)h * HD + d] = r;
-    if (outq8) {
-        // gather 4 consecutive elements per lane for the Q8_0 packer
-        __shared__ float buf[HD];
-        buf[d] = r;
-        __syncthreads();
-        if (d < HD / 4) {
-            const float4 v = *reinterpret_cast<const float4*>(buf + 4 * d);
-            const size_t e0 = (size_t)h * HD + 4 * d;
-            q8_block_store(outq8 + (e0 >> 5) * Q8_0_BYTES, (int)((e0 >> 2) & 7), v);
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // SwiGLU (reference swiglu_avx2): e = exp(-|g|) by the Cephes single-precision
 // expf method (S. L. Moshier, Cephes Math Library: Cody-Waite reduction by
 // ln2 in two constants, degree-5 polynomial, 2^n scaling), sigmoid = 1/(1+e)
@@ -603,39 +456,6 @@ hipError_t launch_rope_qkv(float* q, const float* k, const float* v, float* kcac
     const long work = (long)(n_heads + n_kv_heads) * hd / 2 + (long)n_kv_heads * hd;
     hipLaunchKernelGGL(k_rope_qkv, dim3(grid_for(work, 256, 1024)), dim3(256), 0, st, q, k, v,
                        kcache, vcache, pos_dev, pos, n_heads, n_kv_heads, hd, cos_t, sin_t);
-    return hipGetLastError();
-}
-
-int attn_nsplit(int max_seq) { return (max_seq + kAttnSplit - 1) / kAttnSplit; }
-
-hipError_t launch_attention(float* out, void* outq8, float* part, const float* q,
-                            const float* kcache, const float* vcache, const int* pos_dev,
-                            int seq, int nsplit, int n_heads, int n_kv_heads, int hd,
-                            hipStream_t st) {
-    const dim3 g1((unsigned)nsplit, (unsigned)n_heads);
-    auto* oq = static_cast<uint8_t*>(outq8);
-    switch (hd) {
-        case 64:
-            hipLaunchKernelGGL(k_attn_split<64>, g1, dim3(kAttnThreads), 0, st, part, q, kcache,
-                               vcache, pos_dev, seq, n_heads, n_kv_heads, nsplit);
-            hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_heads), dim3(64), 0, st, out, oq, part,
-                               nsplit);
-            break;
-        case 128:
-            hipLaunchKernelGGL(k_attn_split<128>, g1, dim3(kAttnThreads), 0, st, part, q, kcache,
-                               vcache, pos_dev, seq, n_heads, n_kv_heads, nsplit);
-            hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_heads), dim3(128), 0, st, out, oq,
-                               part, nsplit);
-            break;
-        case 256:
-            hipLaunchKernelGGL(k_attn_split<256>, g1, dim3(kAttnThreads), 0, st, part, q, kcache,
-                               vcache, pos_dev, seq, n_heads, n_kv_heads, nsplit);
-            hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_heads), dim3(256), 0, st, out, oq,
-                               part, nsplit);
-            break;
-        default:
-            return hipErrorInvalidValue;
-    }
     return hipGetLastError();
 }
 
