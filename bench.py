@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-Workload (BASELINE config 5, one GPU): one greedy decode step of a
+Workload (one GPU): one greedy decode step of a
 LLaMA-2-7B-architecture model (32 layers, hidden 4096, 32x128 heads, FFN 11008
 SwiGLU, vocab 32000, RoPE theta 1e4) with random N(0, 0.02) weights quantized
 Q4_K_M (Q6_K for attn_v, ffn_down and output), at context 2048 (KV rows
@@ -12,7 +12,7 @@ K timed steps are replayed from one captured HIP graph between HIP events.
 
 Also measured in the same run:
   roofline      the dominant kernel, the Q4_K x Q8_0 GEMV at 11008 x 4096,
-                M = 1 (the shape of the BASELINE 70%-of-HBM target), over 24
+                M = 1 (the shape of the 70%-of-HBM north-star target), over 24
                 rotating weight copies (610 MB > 2 x the 256 MB MALL)
   cpu_baseline  the reference's decode step on this host's cores: the
                 reference x86 kernels compiled from source (oracle/_ref) on
@@ -89,7 +89,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
-              "(the decode path shards by tensor parallelism, see DESIGN.md)", file=sys.stderr)
+              "(one GPU per run; the decode path would shard by tensor parallelism)", file=sys.stderr)
         return 2
 
     from llm_core_amd import hip
@@ -207,7 +207,7 @@ def main() -> int:
             "dtype": "q4_k/q6_k x q8_0 int8 dot, fp32 accumulate",
             "data": "synthetic (random N(0,0.02) weights quantized Q4_K_M; KV N(0,1))",
             "config": {
-                "workload": "LLaMA-2-7B-architecture Q4_K_M greedy decode step at context 2048 (BASELINE config 5)",
+                "workload": "LLaMA-2-7B-architecture Q4_K_M greedy decode step at context 2048",
                 "context": args.ctx,
                 "n_layer": 32, "hidden": 4096, "heads": 32, "kv_heads": 32, "ffn": 11008,
                 "vocab": 32000,

@@ -38,7 +38,8 @@ class Hparams:
                             self.ffn_dim, self.n_vocab, self.n_ctx, self.rms_eps, self.rope_theta)
 
 
-# LLaMA-2-7B architecture and the Qwen2.5-3B-like layer (config 3)
+# LLaMA-2-7B architecture (the decode benchmark) and a Qwen2.5-3B-like layer
+# (hidden 2048, 16/2 heads, FFN 11008: tests/test_gguf_reader.cpp:429-444 of the reference)
 LLAMA2_7B = dict(n_layer=32, n_embd=4096, n_heads=32, n_kv_heads=32, ffn_dim=11008,
                  n_vocab=32000, rms_eps=1e-5, rope_theta=10000.0)
 QWEN25_3B_LAYER = dict(n_layer=1, n_embd=2048, n_heads=16, n_kv_heads=2, ffn_dim=11008,
@@ -135,6 +136,12 @@ class LlamaHip:
         if self.handle:
             call("axf_llama_destroy", self.handle)
             self.handle = None
+
+    def __enter__(self) -> "LlamaHip":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
 
     def device_bytes(self) -> int:
         return int(lib.axf_llama_device_bytes(self.handle))

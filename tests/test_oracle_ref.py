@@ -1,0 +1,121 @@
+"""The CPU oracle against the reference's x86 kernels compiled from their
+sources (oracle/_ref/libaxf_ref.so, built by oracle/Makefile where the
+reference tree exists), on larger and ragged shapes than the committed goldens,
+bit for bit.  Skipped where oracle/_ref was not built."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.skipif(O.ref is None, reason="oracle/_ref not built (no reference tree)")
+R = O.ref
+
+
+def p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def blocks(qt, n, seed):
+    rng = np.random.default_rng(seed)
+    bb = O.BLOCK_BYTES[qt]
+    blk = rng.integers(0, 256, size=(n, bb), dtype=np.uint8)
+    h = rng.uniform(1e-4, 1e-2, size=(n, 2)).astype(np.float16).view(np.uint16)
+    hb = np.ascontiguousarray(h).view(np.uint8).reshape(n, 4)
+    if qt == O.Q4K:
+        blk[:, 0:4] = hb
+    else:
+        blk[:, 208:210] = hb[:, :2]
+    return blk.reshape(-1)
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+SHAPES = [(8, 256), (13, 4096), (64, 11008), (40, 2048)]
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+@pytest.mark.parametrize("qt", [O.Q4K, O.Q6K])
+def test_gemv_f32(qt, rows, cols):
+    W = blocks(qt, rows * cols // 256, rows + cols)
+    x = np.random.default_rng(cols).standard_normal(cols).astype(np.float32)
+    y = np.empty(rows, np.float32)
+    fn = R.ref_gemv_q4k_f32 if qt == O.Q4K else R.ref_gemv_q6k_f32
+    fn(p(y), p(W), p(x), 0, rows, cols, O.row_bytes(qt, cols))
+    assert np.array_equal(bits(O.gemv_f32(qt, W, x, rows, cols)), bits(y))
+
+
+@pytest.mark.parametrize("n", [32, 4096, 11008 * 3])
+def test_quantize_q8_0(n):
+    x = np.random.default_rng(n).standard_normal(n).astype(np.float32) * 7
+    want = np.empty(n // 32 * 36, np.uint8)
+    R.ref_quantize_q8_0(p(want), p(x), n)
+    assert np.array_equal(O.quantize_q8_0(x), want)
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_gemv_q4k_q8_all_reference_variants(rows, cols):
+    W = blocks(O.Q4K, rows * cols // 256, 3 * rows + cols)
+    x = np.random.default_rng(rows).standard_normal(cols).astype(np.float32)
+    xq = O.quantize_q8_0(x)
+    got = bits(O.gemv_q8(O.Q4K, W, xq, rows, cols))
+    rb = O.row_bytes(O.Q4K, cols)
+    y = np.empty(rows, np.float32)
+    variants = [0, 1] if R.ref_has_avxvnni() else [0]
+    for vnni in variants:
+        R.ref_gemv_q4k_q8(p(y), p(W), p(xq), 0, rows, cols, rb, vnni)
+        assert np.array_equal(got, bits(y)), f"4-row kernel vnni={vnni}"
+        if rows % 8 == 0:
+            r8 = O.repack_r8(W, rows, cols)
+            R.ref_gemv_q4k_r8(p(y), p(r8), p(xq), 0, rows, cols, vnni)
+            assert np.array_equal(got, bits(y)), f"r8 kernel vnni={vnni}"
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_gemv_q6k_q8(rows, cols):
+    W = blocks(O.Q6K, rows * cols // 256, 5 * rows + cols)
+    x = np.random.default_rng(cols + 1).standard_normal(cols).astype(np.float32)
+    xq = O.quantize_q8_0(x)
+    y = np.empty(rows, np.float32)
+    R.ref_gemv_q6k_q8(p(y), p(W), p(xq), 0, rows, cols, O.row_bytes(O.Q6K, cols))
+    assert np.array_equal(bits(O.gemv_q8(O.Q6K, W, xq, rows, cols)), bits(y))
+
+
+@pytest.mark.parametrize("rows,cols", [(16, 256), (64, 4096)])
+def test_repack_r8(rows, cols):
+    W = blocks(O.Q4K, rows * cols // 256, 11)
+    want = np.empty_like(W)
+    R.ref_repack_q4k_r8(p(want), p(W), rows, cols)
+    assert np.array_equal(O.repack_r8(W, rows, cols), want)
+
+
+@pytest.mark.parametrize("rows,cols,T", [(12, 512, 1), (40, 4096, 4), (16, 2048, 16), (8, 1024, 19)])
+def test_gemm_q4k_q8(rows, cols, T):
+    W = blocks(O.Q4K, rows * cols // 256, rows * T)
+    X = np.random.default_rng(T).standard_normal(T * cols).astype(np.float32)
+    XQ = O.quantize_q8_0(X)
+    got = bits(O.gemm_q4k_q8(W, XQ, rows, T, cols))
+    Y = np.empty(T * rows, np.float32)
+    for vnni in ([0, 1] if R.ref_has_avxvnni() else [0]):
+        R.ref_gemm_q4k_q8(p(Y), p(W), p(XQ), rows, T, cols, O.row_bytes(O.Q4K, cols), 0, rows, vnni)
+        assert np.array_equal(got.reshape(-1), bits(Y)), f"vnni={vnni}"
+
+
+def test_dequant_via_onehot_reference_gemv():
+    """The reference GEMV with x = e_j returns column j of the dequantised
+    matrix exactly; compare with the oracle's dequantisation."""
+    rows, cols = 8, 256
+    for qt in (O.Q4K, O.Q6K):
+        W = blocks(qt, rows * cols // 256, 17 + qt)
+        D = O.dequant(qt, W).reshape(rows, cols)
+        fn = R.ref_gemv_q4k_f32 if qt == O.Q4K else R.ref_gemv_q6k_f32
+        e = np.zeros(cols, np.float32)
+        y = np.empty(rows, np.float32)
+        for j in range(cols):
+            e[:] = 0
+            e[j] = 1
+            fn(p(y), p(W), p(e), 0, rows, cols, O.row_bytes(qt, cols))
+            assert np.array_equal(y, D[:, j])
