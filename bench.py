@@ -74,6 +74,102 @@ def gemv_case(ctx, kind, qtype, rows, cols, reps, seed, min_bytes=2 * MALL_BYTES
     return res, W, x
 
 
+def copy_probe(ctx, nbytes=256 << 20, reps=10):
+    """Plain device-to-device copy of nbytes (the runtime's copy kernel): the
+    calibration kernel for the HBM traffic counters and a practical
+    read+write bandwidth reference."""
+    src, dst = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    ctx.copy(dst, src, nbytes)
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(reps):
+        ctx.copy(dst, src, nbytes)
+    ms = ctx.timer_stop()
+    src.free()
+    dst.free()
+    us = ms * 1000.0 / reps
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": round(us, 2),
+            "GBs_read_plus_write": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}
+
+
+ROOF_KERNEL = "k_gemv_q4k_q8<64, 1, 4>"
+ROOF_GRID = 176128  # threads of one 11008-row launch (688 workgroups x 256)
+COPY_GRID = 131072  # threads of the runtime's 256 MiB copy kernel
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "gemv_q4k_q8_11008x4096_traffic.txt")
+
+
+def _csv(d: str, suffix: str):
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True))
+    return [r for f in files for r in csv.DictReader(open(f))]
+
+
+def summarize_stats(d: str) -> str:
+    """Per-kernel table from a rocprofv3 --kernel-trace --stats -f csv directory,
+    plus per-(kernel, grid) mean/median duration from the kernel trace."""
+    import statistics
+    lines = ["kernel stats (rocprofv3 --stats): calls, avg us, min us, max us, % of GPU time"]
+    for r in _csv(d, "_kernel_stats.csv"):
+        lines.append(f"  {int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.3f} "
+                     f"{float(r['MinNs']) / 1e3:9.3f} {float(r['MaxNs']) / 1e3:9.3f} "
+                     f"{float(r['Percentage']):6.2f}%  {r['Name'][:110]}")
+    groups: dict = {}
+    for r in _csv(d, "_kernel_trace.csv"):
+        k = (r["Kernel_Name"][:90], int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
+        groups.setdefault(k, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines.append("kernel trace by (kernel, grid threads): calls, mean us, median us")
+    for (name, grid), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"  {len(v):7d} {statistics.mean(v):9.3f} {statistics.median(v):9.3f}  "
+                     f"grid {grid:8d}  {name}")
+    return "\n".join(lines)
+
+
+def summarize_traffic(fetch_dir: str, write_dir: str) -> tuple[str, float | None]:
+    """HBM bytes per launch of the roofline kernel from a FETCH_SIZE pass and a
+    WRITE_SIZE pass (rocprofv3 --pmc ... -f csv), each scaled by what the same
+    counter reads for the runtime's 256 MiB device-to-device copy."""
+    import statistics
+    med = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        vals: dict = {}
+        for r in _csv(d, "_counter_collection.csv"):
+            if r["Counter_Name"] != counter:
+                continue
+            grid = int(r["Grid_Size"])
+            if ROOF_KERNEL in r["Kernel_Name"] and grid == ROOF_GRID:
+                vals.setdefault("kernel", []).append(float(r["Counter_Value"]))
+            elif "copyBuffer" in r["Kernel_Name"] and grid == COPY_GRID:
+                vals.setdefault("copy", []).append(float(r["Counter_Value"]))
+        if "kernel" not in vals or "copy" not in vals:
+            return f"{counter}: roofline kernel or calibration copy missing in {d}", None
+        med[counter] = (statistics.median(vals["kernel"]), len(vals["kernel"]),
+                        statistics.median(vals["copy"]), len(vals["copy"]))
+    copy_kib = 256 * 1024
+    lines = ["counter      kernel KiB/dispatch (n)   copy KiB/dispatch (n)   scale   scaled bytes"]
+    total = 0.0
+    for counter, (k, nk, c, nc) in med.items():
+        scale = copy_kib / c
+        b = k * 1024 * scale
+        total += b
+        lines.append(f"{counter:11s} {k:12.1f} ({nk:4d})     {c:12.1f} ({nc:3d})      {scale:6.4f}  {b:12.0f}")
+    lines.append(f"traffic_bytes_per_launch: {total:.0f}")
+    return "\n".join(lines), total
+
+
+def committed_traffic() -> float | None:
+    """traffic_bytes_per_launch from the committed rocprofv3 --pmc summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    return float(ln.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -85,7 +181,22 @@ def main() -> int:
                     help="approximate CPU seconds spent on the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--only", choices=["all", "gemv", "decode"], default="all")
+    ap.add_argument("--mall-warm", action="store_true",
+                    help="also time the roofline GEMV on one weight copy (Infinity-Cache warm)")
+    ap.add_argument("--summarize", nargs="+", metavar="DIR",
+                    help="print a summary of rocprofv3 csv output directories and exit")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="HBM traffic of the roofline kernel from two rocprofv3 --pmc csv "
+                         "directories (FETCH_SIZE, WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.summarize or args.traffic:
+        for d in args.summarize or []:
+            print(f"== {d}")
+            print(summarize_stats(d))
+        if args.traffic:
+            text, _ = summarize_traffic(*args.traffic)
+            print(text)
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
@@ -104,9 +215,13 @@ def main() -> int:
     if args.only in ("all", "gemv"):
         g, W_up, x_up = gemv_case(ctx, 0, hip.AXF_TYPE_Q4_K, 11008, 4096, args.gemv_reps, 4)
         log(f"gemv q4k 11008x4096: {g['us_per_launch']:.2f} us/launch, {g['gbs']:.0f} GB/s")
-        warm, _, _ = gemv_case(ctx, 0, hip.AXF_TYPE_Q4_K, 11008, 4096, args.gemv_reps, 4,
-                               warm=True)
-        log(f"gemv q4k 11008x4096 (one copy, MALL-warm): {warm['us_per_launch']:.2f} us")
+        warm = None
+        if args.mall_warm:
+            warm, _, _ = gemv_case(ctx, 0, hip.AXF_TYPE_Q4_K, 11008, 4096, args.gemv_reps, 4,
+                                   warm=True)
+            log(f"gemv q4k 11008x4096 (one copy, MALL-warm): {warm['us_per_launch']:.2f} us")
+        cp = copy_probe(ctx)
+        log(f"d2d copy 256 MiB: {cp['us']:.1f} us, {cp['GBs_read_plus_write']:.0f} GB/s read+write")
         c1, _, _ = gemv_case(ctx, 2, hip.AXF_TYPE_Q4_K, 4096, 4096, args.gemv_reps, 1)
         log(f"gemv q4k x f32 4096x4096 (config 1): {c1['us_per_launch']:.2f} us, {c1['gbs']:.0f} GB/s")
         c2, _, _ = gemv_case(ctx, 1, hip.AXF_TYPE_Q6_K, 151936, 2048, max(4, args.gemv_reps // 4), 2)
@@ -118,13 +233,16 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": committed_traffic(),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes, copy-kernel "
+                              "scaled: profiles/gemv_q4k_q8_11008x4096_traffic.txt",
             "us_per_launch": round(g["us_per_launch"], 3),
             "algorithmic_bytes_per_launch": g["algorithmic_bytes"],
             "weight_copies": g["n_copies"],
-            "mall_warm_us_per_launch": round(warm["us_per_launch"], 3),
+            "mall_warm_us_per_launch": round(warm["us_per_launch"], 3) if warm else None,
         }
         out["kernels"] = {
+            "copy_256MiB_d2d": cp,
             "c1_q4k_f32_4096x4096": {"us": round(c1["us_per_launch"], 3), "GBs": round(c1["gbs"], 1)},
             "c2_q6k_q8_151936x2048": {"us": round(c2["us_per_launch"], 3), "GBs": round(c2["gbs"], 1)},
         }
@@ -202,9 +320,13 @@ def main() -> int:
             "ms_per_step": round(result["ms_step"], 4),
             "higher_is_better": True,
             "scaling": "weak",
-            "vs_baseline": round(result["tok_s"] / PUBLISHED_TOK_S, 2),
-            "vs_baseline_ref": "11.5 tok/s LLaMA-2-7B Q4_K_M decode, i9-12900K 16 threads, short context (reference README.md:324)",
-            "dtype": "q4_k/q6_k x q8_0 int8 dot, fp32 accumulate",
+            "vs_baseline": None,
+            "published_reference": {
+                "value": PUBLISHED_TOK_S, "unit": "tokens/s",
+                "what": "LLaMA-2-7B Q4_K_M decode, i9-12900K DDR4-3200, 16 threads, short "
+                        "context (reference README.md:324); other hardware and context, so "
+                        "not used as vs_baseline"},
+            "dtype": "i8 (Q4_K/Q6_K x Q8_0 int8 dot products, fp32 scales, norms and attention)",
             "data": "synthetic (random N(0,0.02) weights quantized Q4_K_M; KV N(0,1))",
             "config": {
                 "workload": "LLaMA-2-7B-architecture Q4_K_M greedy decode step at context 2048",

@@ -92,6 +92,11 @@ class Context:
         call("axf_hip_memcpy_h2d", self.handle, C.c_void_p(int(dst)), a.ctypes.data_as(C.c_void_p),
              C.c_size_t(a.nbytes))
 
+    def copy(self, dst: int, src: int, nbytes: int) -> None:
+        """Device-to-device copy, asynchronous on the context stream."""
+        call("axf_hip_memcpy_d2d", self.handle, C.c_void_p(int(dst)), C.c_void_p(int(src)),
+             C.c_size_t(int(nbytes)))
+
     def download(self, src: int, dtype, count: int) -> np.ndarray:
         out = np.empty(int(count), dtype=dtype)
         call("axf_hip_memcpy_d2h", self.handle, out.ctypes.data_as(C.c_void_p), C.c_void_p(int(src)),
