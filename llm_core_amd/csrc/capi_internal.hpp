@@ -32,6 +32,35 @@ enum class GemvKind { Q4K_Q8, Q4K_F32, Q6K_Q8, Q6K_F32 };
 
 hipError_t launch_gemv(GemvKind kind, float* y, const void* W, const void* x, int rows, int nb,
                        long row_bytes, int accumulate, hipStream_t st);
+// Q8_0-activation GEMV family with fused activation producers / consumers
+// (kernels/gemv.hip, k_qgemv / k_qgemv2).
+struct QGemvArgs {
+    const uint8_t* W0;  // segment 0 weights, rows0 rows of rb0 bytes, output y0
+    long rb0;
+    int rows0;
+    float* y0;
+    const uint8_t* W1;  // segment 1 (two-type launch only)
+    long rb1;
+    int rows1;
+    float* y1;
+    int nwg0;           // workgroups of segment 0 (two-type launch; set by the launcher)
+    int nb;             // 256-weight super-blocks per row (K / 256)
+    int accumulate;     // y += v instead of y = v
+    const uint8_t* xq8; // activation as Q8_0 blocks (QAct::Q8)
+    const float* x;     // activation fp32 (QAct::Norm, QAct::F32)
+    const float* nw;    // RMSNorm weight (QAct::Norm)
+    float eps;
+};
+enum class QAct { Q8, Norm, F32 };
+// One weight type (qtype 12 or 14).  swiglu: rows are blocks of R/2 gate rows
+// then R/2 up rows (R = qgemv_rows_per_wg(nb, threads)); y0[i] = swiglu(gate_i, up_i).
+hipError_t launch_qgemv(int qtype, QAct act, bool swiglu, QGemvArgs a, int threads,
+                        hipStream_t st);
+// Q4_K segment (W0) and Q6_K segment (W1) over the same activation, one launch.
+hipError_t launch_qgemv2(QAct act, QGemvArgs a, int threads, hipStream_t st);
+int qgemv_threads(QAct act, int nb);  // default workgroup size for launch_qgemv
+bool qgemv_threads_ok(QAct act, int nb, int threads);
+int qgemv_rows_per_wg(int nb, int threads);
 hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
                               long row_bytes, hipStream_t st);
 hipError_t launch_dequant_q4k(float* y, const void* W, long nblocks, hipStream_t st);

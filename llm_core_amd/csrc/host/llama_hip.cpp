@@ -4,9 +4,11 @@
 // llama_forward_token, :1207-1333).
 //
 // Device layout (allocated once by axf_llama_load):
-//   * weights in native GGUF blocks; attn_q|attn_k and ffn_gate|ffn_up are
-//     placed back to back when both are Q4_K, so each pair is one GEMV launch
-//     whose output is q|k (resp. gate|up) contiguous;
+//   * weights in native GGUF blocks; attn_q|attn_k are placed back to back
+//     when both are Q4_K (one GEMV whose output is q|k contiguous); ffn_gate
+//     and ffn_up of one type are interleaved by row blocks (B gate rows, then
+//     the same B up rows, B = half the rows of one GEMV workgroup), so one
+//     GEMV workgroup holds both halves of its SwiGLU pairs;
 //   * KV cache fp32 [layer][n_ctx][n_kv_heads*head_dim], K stored after RoPE
 //     (LlamaState, :1102-1106);
 //   * RoPE cos/sin table [n_ctx][head_dim/2] built on the host (:1031-1043);
@@ -14,9 +16,15 @@
 //     HIP graph replays every decode step: the argmax at the end of a step
 //     writes the next token and advances the position.
 //
-// Step (per layer): rmsnorm->q8 | gemv q|k | gemv v | rope q,k + store k,v |
-// attention split + combine->q8 | gemv o (+= x) | rmsnorm->q8 | gemv gate|up |
-// swiglu->q8 | gemv down (+= x); then rmsnorm->q8 | gemv head | argmax.
+// Step, per layer (six kernels):
+//   1. q|k (Q4_K) and v (Q6_K) GEMVs in one launch, each workgroup computing
+//      RMSNorm(x)*attn_norm -> Q8_0 in its prologue;
+//   2./3. attention split (RoPE of q and k, store of k and v) and combine -> Q8_0;
+//   4. o GEMV, x += o;
+//   5. gate|up GEMV with RMSNorm(x)*ffn_norm -> Q8_0 prologue and SwiGLU
+//      epilogue -> h (fp32);
+//   6. down GEMV quantising h to Q8_0 in its prologue, x += down.
+// Then the head GEMV with the final RMSNorm in its prologue, and argmax.
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -45,7 +53,8 @@ struct Layer {
     float* attn_norm = nullptr;
     float* ffn_norm = nullptr;
     DevW wq, wk, wv, wo, wgate, wup, wdown;
-    bool qk_fused = false, gateup_fused = false;
+    bool qk_fused = false;
+    bool gu_interleaved = false;  // wgate holds gate and up rows interleaved by row blocks
     float *bq = nullptr, *bk = nullptr, *bv = nullptr;
 };
 
@@ -67,6 +76,7 @@ struct axf_llama {
 
     float *kv_k = nullptr, *kv_v = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
     float *x = nullptr, *qkv = nullptr, *attn_out = nullptr, *gateup = nullptr, *logits = nullptr;
+    float* h = nullptr;  // SwiGLU output, FD floats
     uint8_t* xq8 = nullptr;
     float* attn_part = nullptr;
     int nsplit = 0;
@@ -175,10 +185,74 @@ int upload_pair(axf_llama* m, const std::string& n1, int rows1, const std::strin
     return AXF_OK;
 }
 
-hipError_t gemv(const DevW& w, float* y, const void* xq8, int rows, int cols, bool acc,
-                hipStream_t st) {
-    return launch_gemv(w.qtype == AXF_TYPE_Q4_K ? GemvKind::Q4K_Q8 : GemvKind::Q6K_Q8, y, w.d,
-                       xq8, rows, cols / QK_K, (long)w.row_bytes, acc ? 1 : 0, st);
+// workgroup size of the gate|up GEMV with the SwiGLU epilogue
+int gateup_threads(int E) { return qgemv_threads_ok(QAct::Norm, E / QK_K, 1024) ? 1024 : 512; }
+
+// ffn_gate and ffn_up: of one qtype and with FD a multiple of the block B,
+// uploaded as one matrix of row blocks [gate B rows][up B rows] ...; else
+// separately.
+int upload_gate_up(axf_llama* m, int l, Layer& L) {
+    const auto& hp = m->hp;
+    const int E = hp.n_embd, FD = hp.ffn_dim;
+    const std::string b = "blk." + std::to_string(l) + ".";
+    const HostTensor *tg, *tu;
+    LL_TRY(need(m, b + "ffn_gate.weight", &tg));
+    LL_TRY(check_q(b + "ffn_gate.weight", tg, FD, E));
+    LL_TRY(need(m, b + "ffn_up.weight", &tu));
+    LL_TRY(check_q(b + "ffn_up.weight", tu, FD, E));
+    const int B = qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2;
+    L.gu_interleaved = tg->qtype == tu->qtype && FD % B == 0;
+    if (!L.gu_interleaved) {
+        LL_TRY(upload_pair(m, b + "ffn_gate.weight", FD, "", 0, E, &L.wgate, nullptr, nullptr));
+        LL_TRY(upload_pair(m, b + "ffn_up.weight", FD, "", 0, E, &L.wup, nullptr, nullptr));
+        return AXF_OK;
+    }
+    const size_t rb = axf_row_bytes(tg->qtype, E);
+    std::vector<uint8_t> host(2 * (size_t)FD * rb);
+    const auto* g = static_cast<const uint8_t*>(tg->host);
+    const auto* u = static_cast<const uint8_t*>(tu->host);
+    for (int j = 0; j < FD / B; j++) {
+        std::memcpy(host.data() + (size_t)(2 * j) * B * rb, g + (size_t)j * B * rb, (size_t)B * rb);
+        std::memcpy(host.data() + (size_t)(2 * j + 1) * B * rb, u + (size_t)j * B * rb,
+                    (size_t)B * rb);
+    }
+    void* p;
+    LL_TRY(dalloc(m, host.size(), &p));
+    LL_TRY(upload(m, p, host.data(), host.size()));
+    L.wgate = DevW{tg->qtype, static_cast<uint8_t*>(p), rb};
+    L.wup = DevW{};
+    return AXF_OK;
+}
+
+QGemvArgs weights(const DevW& w, int rows, float* y, int cols) {
+    QGemvArgs a{};
+    a.W0 = w.d;
+    a.rb0 = (long)w.row_bytes;
+    a.rows0 = rows;
+    a.y0 = y;
+    a.nb = cols / QK_K;
+    return a;
+}
+
+// y (+)= W * Q8_0(x) with x already Q8_0
+hipError_t gemv_q8(const DevW& w, float* y, const void* xq8, int rows, int cols, bool acc,
+                   hipStream_t st) {
+    QGemvArgs a = weights(w, rows, y, cols);
+    a.xq8 = static_cast<const uint8_t*>(xq8);
+    a.accumulate = acc ? 1 : 0;
+    return launch_qgemv(w.qtype, QAct::Q8, false, a, qgemv_threads(QAct::Q8, a.nb), st);
+}
+
+// y = W * Q8_0(RMSNorm(x) * nw), the normalisation in the GEMV prologue;
+// the SwiGLU variant (gate|up interleaved) runs 1024-thread workgroups
+hipError_t gemv_norm(const DevW& w, float* y, const float* x, const float* nw, float eps,
+                     int rows, int cols, bool swiglu, hipStream_t st) {
+    QGemvArgs a = weights(w, rows, y, cols);
+    a.x = x;
+    a.nw = nw;
+    a.eps = eps;
+    const int threads = swiglu ? gateup_threads(cols) : qgemv_threads(QAct::Norm, a.nb);
+    return launch_qgemv(w.qtype, QAct::Norm, swiglu, a, threads, st);
 }
 
 // Enqueue one decoder layer; pos from device memory when pos_dev != nullptr.
@@ -195,14 +269,27 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
     hipError_t e;
 #define ST(call)               \
     if ((e = (call)) != hipSuccess) return e;
-    ST(launch_rmsnorm(nullptr, m->xq8, m->x, L.attn_norm, E, hp.rms_eps, st));
-    if (L.qk_fused) {
-        ST(gemv(L.wq, q, m->xq8, qo + kvo, E, false, st));
+    // 1. q|k and v from RMSNorm(x) * attn_norm
+    if (L.qk_fused && L.wv.qtype == AXF_TYPE_Q6_K) {
+        QGemvArgs a = weights(L.wq, qo + kvo, q, E);
+        a.W1 = L.wv.d;
+        a.rb1 = (long)L.wv.row_bytes;
+        a.rows1 = kvo;
+        a.y1 = v;
+        a.x = m->x;
+        a.nw = L.attn_norm;
+        a.eps = hp.rms_eps;
+        ST(launch_qgemv2(QAct::Norm, a, qgemv_threads(QAct::Norm, a.nb), st));
     } else {
-        ST(gemv(L.wq, q, m->xq8, qo, E, false, st));
-        ST(gemv(L.wk, k, m->xq8, kvo, E, false, st));
+        if (L.qk_fused) {
+            ST(gemv_norm(L.wq, q, m->x, L.attn_norm, hp.rms_eps, qo + kvo, E, false, st));
+        } else {
+            ST(gemv_norm(L.wq, q, m->x, L.attn_norm, hp.rms_eps, qo, E, false, st));
+            ST(gemv_norm(L.wk, k, m->x, L.attn_norm, hp.rms_eps, kvo, E, false, st));
+        }
+        ST(gemv_norm(L.wv, v, m->x, L.attn_norm, hp.rms_eps, kvo, E, false, st));
     }
-    ST(gemv(L.wv, v, m->xq8, kvo, E, false, st));
+    // 2./3. attention -> Q8_0 of its output
     {
         AttnArgs a{};
         a.q = q;
@@ -226,16 +313,23 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
         a.outq8 = m->xq8;
         ST(launch_attention_fused(a, HD, st));
     }
-    ST(gemv(L.wo, m->x, m->xq8, E, E, true, st));
-    ST(launch_rmsnorm(nullptr, m->xq8, m->x, L.ffn_norm, E, hp.rms_eps, st));
-    if (L.gateup_fused) {
-        ST(gemv(L.wgate, m->gateup, m->xq8, 2 * FD, E, false, st));
+    // 4. x += o
+    ST(gemv_q8(L.wo, m->x, m->xq8, E, qo, true, st));
+    // 5. h = SwiGLU(gate, up) from RMSNorm(x) * ffn_norm
+    if (L.gu_interleaved) {
+        ST(gemv_norm(L.wgate, m->h, m->x, L.ffn_norm, hp.rms_eps, 2 * FD, E, true, st));
     } else {
-        ST(gemv(L.wgate, m->gateup, m->xq8, FD, E, false, st));
-        ST(gemv(L.wup, m->gateup + FD, m->xq8, FD, E, false, st));
+        ST(gemv_norm(L.wgate, m->gateup, m->x, L.ffn_norm, hp.rms_eps, FD, E, false, st));
+        ST(gemv_norm(L.wup, m->gateup + FD, m->x, L.ffn_norm, hp.rms_eps, FD, E, false, st));
+        ST(launch_swiglu(m->h, nullptr, m->gateup, m->gateup + FD, FD, st));
     }
-    ST(launch_swiglu(nullptr, m->xq8, m->gateup, m->gateup + FD, FD, st));
-    ST(gemv(L.wdown, m->x, m->xq8, E, FD, true, st));
+    // 6. x += down(Q8_0(h))
+    {
+        QGemvArgs a = weights(L.wdown, E, m->x, FD);
+        a.x = m->h;
+        a.accumulate = 1;
+        ST(launch_qgemv(L.wdown.qtype, QAct::F32, false, a, qgemv_threads(QAct::F32, a.nb), st));
+    }
 #undef ST
     return hipSuccess;
 }
@@ -252,10 +346,8 @@ hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, boo
     if (e != hipSuccess) return e;
     for (int l = 0; l < hp.n_layer; l++)
         if ((e = enqueue_layer(m, l, pd, pos)) != hipSuccess) return e;
-    if ((e = launch_rmsnorm(nullptr, m->xq8, m->x, m->output_norm, hp.n_embd, hp.rms_eps, st)) !=
-        hipSuccess)
-        return e;
-    if ((e = gemv(m->output, m->logits, m->xq8, hp.n_vocab, hp.n_embd, false, st)) != hipSuccess)
+    if ((e = gemv_norm(m->output, m->logits, m->x, m->output_norm, hp.rms_eps, hp.n_vocab,
+                       hp.n_embd, false, st)) != hipSuccess)
         return e;
     return launch_argmax(m->d_token, m->arg_v, m->arg_i, m->logits, hp.n_vocab,
                          record ? m->d_tokens : nullptr, record ? m->d_step : nullptr,
@@ -301,6 +393,8 @@ int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out)
         return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: n_embd and ffn_dim must be multiples of 256");
     if (h.n_embd / QK_K > kMaxBlocksPerRow || h.ffn_dim / QK_K > kMaxBlocksPerRow)
         return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: dimension above 32768");
+    if (h.n_embd > 8192)  // the GEMVs that fuse RMSNorm take K <= 8192
+        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: n_embd above 8192");
     auto* m = new axf_llama();
     m->ctx = ctx;
     m->hp = h;
@@ -364,8 +458,7 @@ int axf_llama_load(axf_llama* m) {
                            &L.qk_fused));
         LL_TRY(upload_pair(m, n("attn_v.weight"), kvo, "", 0, E, &L.wv, nullptr, nullptr));
         LL_TRY(upload_pair(m, n("attn_output.weight"), E, "", 0, qo, &L.wo, nullptr, nullptr));
-        LL_TRY(upload_pair(m, n("ffn_gate.weight"), FD, n("ffn_up.weight"), FD, E, &L.wgate,
-                           &L.wup, &L.gateup_fused));
+        LL_TRY(upload_gate_up(m, l, L));
         LL_TRY(upload_pair(m, n("ffn_down.weight"), E, "", 0, FD, &L.wdown, nullptr, nullptr));
         LL_TRY(upload_f32(m, n("attn_q.bias"), qo, &L.bq, false));
         LL_TRY(upload_f32(m, n("attn_k.bias"), kvo, &L.bk, false));
@@ -398,6 +491,8 @@ int axf_llama_load(axf_llama* m) {
     m->attn_out = static_cast<float*>(p);
     LL_TRY(dalloc(m, (size_t)2 * FD * 4, &p));
     m->gateup = static_cast<float*>(p);
+    LL_TRY(dalloc(m, (size_t)FD * 4, &p));
+    m->h = static_cast<float*>(p);
     LL_TRY(dalloc(m, (size_t)hp.n_vocab * 4, &p));
     m->logits = static_cast<float*>(p);
     LL_TRY(dalloc(m, (size_t)((E > FD ? E : FD) / 32) * Q8_0_BYTES, &p));

@@ -3,12 +3,13 @@
 // (llama_forward_token, llama_model.cpp:1241-1272).
 //
 // Two kernels:
-//   k_attn_split   grid (nsplit, n_kv_heads).  Workgroup (j, kvh) serves the
+//   k_attn_split   grid (n_kv_heads, nsplit).  Workgroup (kvh, j) serves the
 //                  G = n_heads / n_kv_heads query heads of kv head kvh over
 //                  positions [j*S, min(j*S+S, seq)), S = kAttnSplit, so every
 //                  K/V row is read once per group.  All K and V loads of the
-//                  tile are issued before any arithmetic (the tile lives in
-//                  registers), so a workgroup pays one HBM round trip.  It
+//                  tile are issued right after the small operands (query,
+//                  new K/V row, RoPE row) and before any arithmetic (the tile
+//                  lives in registers), so a workgroup pays one HBM round trip.  It
 //                  writes, per head, the split's max score m_j, the sum
 //                  l_j = sum exp(s - m_j) and o_j = sum exp(s - m_j) v.
 //                  Splits past the current position exit at once, so the grid
@@ -32,6 +33,8 @@ constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kMaxSplit = 512;  // contexts up to 32768 positions
 
+// rotate-half RoPE of n_vec head vectors held in LDS; cr/sr: this position's
+// table row (LDS)
 template <int HD>
 __device__ __forceinline__ void rope_in_lds(float* v, int n_vec, const float* cr, const float* sr) {
     constexpr int half = HD / 2;
@@ -85,13 +88,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     constexpr int RPW = kAttnSplit / kAttnWaves;
     constexpr int NI = RPW / RPI;
     static_assert(RPW % RPI == 0, "tile shape");
+    constexpr int QPT = (GM * HD + kAttnThreads - 1) / kAttnThreads;
+    static_assert(HD <= kAttnThreads, "one new K/V element per thread");
     __shared__ float qs[GM * HD];
     __shared__ float knew[HD], vnew[HD];
+    __shared__ float crs[HD / 2], srs[HD / 2];
     __shared__ float sc[GM][kAttnSplit];
     __shared__ float ov[kAttnWaves][GM * HD];
     __shared__ float stat[GM][2];
 
-    const int j = blockIdx.x, kvh = blockIdx.y;
+    // kv head fastest: workgroups dispatched together read adjacent bytes of each KV row
+    const int kvh = blockIdx.x, j = blockIdx.y;
     const int G = a.n_heads / a.n_kv_heads;
     const int p = a.pos_dev ? *a.pos_dev : a.pos;
     const int t0 = j * kAttnSplit;
@@ -101,50 +108,67 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = (lane % LPR) * 4, rsub = lane / LPR;
     const bool owns_new = a.store_kv && p - t0 < kAttnSplit;
+    const int tid = threadIdx.x;
 
-    // 1. the whole K/V tile into registers (rows past n and the new row read as 0)
+    // 1. small operands first, so their latency hides under the tile loads:
+    //    query (and bias) elements, the new key/value row, this position's RoPE
+    //    row.  Every load below is unconditional (clamped, in-bounds addresses;
+    //    unused values are discarded by selects), so the compiler can wait for
+    //    exactly the loads each use needs instead of draining the tile.
+    float qraw[QPT], qb[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const int t = min(tid + k * kAttnThreads, G * HD - 1);
+        const size_t e = ((size_t)kvh * G + t / HD) * HD + t % HD;
+        qraw[k] = a.q[e];
+        qb[k] = (a.bq ? a.bq : a.q)[e];
+    }
+    const int d1 = min(tid, HD - 1);
+    const size_t e1 = (size_t)kvh * HD + d1;  // < n_kv_heads * HD <= n_heads * HD
+    const float kk = (a.store_kv ? a.k : a.q)[e1];
+    const float vv = (a.store_kv ? a.v : a.q)[e1];
+    const float kb = (a.bk ? a.bk : a.q)[e1];
+    const float vb = (a.bv ? a.bv : a.q)[e1];
+    const int d2 = min(tid, HD / 2 - 1);
+    const float cv = a.cos_t ? a.cos_t[(size_t)p * (HD / 2) + d2] : 0.f;
+    const float sv = a.cos_t ? a.sin_t[(size_t)p * (HD / 2) + d2] : 0.f;
+
+    // 2. the whole K/V tile into registers.  Rows past n re-read row t0 (a
+    //    written, finite row); their score is -inf and their weight 0 below.
+    //    The new row p (still stale in the cache) is replaced after the RoPE.
     float4 kr[NI], vr[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         const int r = wave * RPW + i * RPI + rsub;
-        const int t = t0 + r;
-        kr[i] = vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (r < n && !(owns_new && t == p)) {
-            const size_t off = (size_t)t * kve + (size_t)kvh * HD + col;
-            kr[i] = *reinterpret_cast<const float4*>(a.kcache + off);
-            vr[i] = *reinterpret_cast<const float4*>(a.vcache + off);
-        }
+        const size_t off = (size_t)(r < n ? t0 + r : t0) * kve + (size_t)kvh * HD + col;
+        kr[i] = *reinterpret_cast<const float4*>(a.kcache + off);
+        vr[i] = *reinterpret_cast<const float4*>(a.vcache + off);
     }
 
-    // 2. query heads of this group (+ bias), new key/value (+ bias), RoPE
-    for (int t = threadIdx.x; t < G * HD; t += kAttnThreads) {
-        const size_t h = (size_t)kvh * G + t / HD;
-        const int d = t % HD;
-        float v = a.q[h * HD + d];
-        if (a.bq) v += a.bq[h * HD + d];
-        qs[t] = v;
+    // 3. bias and RoPE in LDS, store the new K/V row
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const int t = tid + k * kAttnThreads;
+        if (t < G * HD) qs[t] = a.bq ? qraw[k] + qb[k] : qraw[k];
     }
-    if (owns_new) {
-        for (int d = threadIdx.x; d < HD; d += kAttnThreads) {
-            float kk = a.k[(size_t)kvh * HD + d], vv = a.v[(size_t)kvh * HD + d];
-            if (a.bk) kk += a.bk[(size_t)kvh * HD + d];
-            if (a.bv) vv += a.bv[(size_t)kvh * HD + d];
-            knew[d] = kk;
-            vnew[d] = vv;
-        }
+    if (owns_new && tid < HD) {
+        knew[tid] = a.bk ? kk + kb : kk;
+        vnew[tid] = a.bv ? vv + vb : vv;
+    }
+    if (a.cos_t && tid < HD / 2) {
+        crs[tid] = cv;
+        srs[tid] = sv;
     }
     __syncthreads();
     if (a.cos_t) {
-        const float* cr = a.cos_t + (size_t)p * (HD / 2);
-        const float* sr = a.sin_t + (size_t)p * (HD / 2);
-        rope_in_lds<HD>(qs, G, cr, sr);
-        if (owns_new) rope_in_lds<HD>(knew, 1, cr, sr);
+        rope_in_lds<HD>(qs, G, crs, srs);
+        if (owns_new) rope_in_lds<HD>(knew, 1, crs, srs);
     }
     __syncthreads();
     if (owns_new) {
-        for (int d = threadIdx.x; d < HD; d += kAttnThreads) {
-            a.kcache[(size_t)p * kve + (size_t)kvh * HD + d] = knew[d];
-            a.vcache[(size_t)p * kve + (size_t)kvh * HD + d] = vnew[d];
+        if (tid < HD) {
+            a.kcache[(size_t)p * kve + (size_t)kvh * HD + tid] = knew[tid];
+            a.vcache[(size_t)p * kve + (size_t)kvh * HD + tid] = vnew[tid];
         }
 #pragma unroll
         for (int i = 0; i < NI; i++) {
@@ -155,7 +179,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
         }
     }
 
-    // 3. scores
+    // 4. scores
     const float scale = 1.f / sqrtf((float)HD);
     float4 qv[GM];
 #pragma unroll
@@ -175,7 +199,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     }
     __syncthreads();
 
-    // 4. per-head max, exp, sum: wave w takes heads w, w+4, ...; lane = row
+    // 5. per-head max, exp, sum: wave w takes heads w, w+4, ...; lane = row
     for (int g = wave; g < G; g += kAttnWaves) {
         const float s = sc[g][lane];
         const float m = wave_max(s);
@@ -189,7 +213,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     }
     __syncthreads();
 
-    // 5. values: lane-local rows, then across the RPI rows of an instruction, then waves
+    // 6. values: lane-local rows, then across the RPI rows of an instruction, then waves
     float4 o[GM];
 #pragma unroll
     for (int g = 0; g < GM; g++) o[g] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -228,76 +252,89 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     }
 }
 
-// One workgroup per query head.  Thread t accumulates float4 column t % (HD/4)
-// over the splits js, js + NJS, ... (js = t / (HD/4)); the NJS partial sums are
-// added in LDS.
+// One workgroup per query head.  Thread t owns float4 column c = t % (HD/4)
+// and the splits js, js + NJS, ... (js = t / (HD/4)); it loads m, l and o of
+// those splits in one pass and merges them online (running max, rescaled sums).
+// The NJS partial states of a column are then merged in LDS:
+//   out = sum_j o_j e^(m_j - M) / sum_j l_j e^(m_j - M),  M = max_j m_j.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(AttnArgs a) {
     constexpr int C4 = HD / 4;
     constexpr int NJS = kAttnThreads / C4;
-    __shared__ float wsplit[kMaxSplit];
-    __shared__ float red[kAttnWaves];
-    __shared__ float4 acc4[NJS][C4];
-    __shared__ float outv[HD];
+    constexpr int U = 4;  // splits loaded per step
+    __shared__ float4 accs[NJS][C4];
+    __shared__ float ms[NJS], ls[NJS];
 
     const int h = blockIdx.x;
     const int p = a.pos_dev ? *a.pos_dev : a.pos;
     const int ns = p / kAttnSplit + 1;  // non-empty splits
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float* ph = a.part + (size_t)h * a.nsplit * (HD + 2);
-
-    float mx = -INFINITY;
-    for (int jj = threadIdx.x; jj < ns; jj += kAttnThreads) mx = fmaxf(mx, ph[(size_t)jj * (HD + 2)]);
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    float M = red[0];
-#pragma unroll
-    for (int w = 1; w < kAttnWaves; w++) M = fmaxf(M, red[w]);
-    __syncthreads();
-    float lsum = 0.f;
-    for (int jj = threadIdx.x; jj < ns; jj += kAttnThreads) {
-        const float w = expf(ph[(size_t)jj * (HD + 2)] - M);
-        wsplit[jj] = w;
-        lsum = fmaf(ph[(size_t)jj * (HD + 2) + 1], w, lsum);
-    }
-    lsum = wave_sum(lsum);
-    if (lane == 0) red[wave] = lsum;
-    __syncthreads();
-    float L = red[0];
-#pragma unroll
-    for (int w = 1; w < kAttnWaves; w++) L += red[w];
-
     const int c = threadIdx.x % C4, js = threadIdx.x / C4;
+
+    float m = -INFINITY, l = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    int jj = js;
-    for (; jj + 3 * NJS < ns; jj += 4 * NJS) {
-        float4 v[4];
+    for (int j0 = js; j0 < ns; j0 += U * NJS) {
+        float mj[U], lj[U];
+        float4 oj[U];
 #pragma unroll
-        for (int u = 0; u < 4; u++)
-            v[u] = *reinterpret_cast<const float4*>(ph + (size_t)(jj + u * NJS) * (HD + 2) + 2 + 4 * c);
+        for (int u = 0; u < U; u++) {
+            const int jj = j0 + u * NJS;
+            mj[u] = -INFINITY;
+            lj[u] = 0.f;
+            oj[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (jj < ns) {
+                const float* pj = ph + (size_t)jj * (HD + 2);
+                mj[u] = pj[0];
+                lj[u] = pj[1];
+                oj[u] = make_float4(pj[2 + 4 * c], pj[3 + 4 * c], pj[4 + 4 * c], pj[5 + 4 * c]);
+            }
+        }
 #pragma unroll
-        for (int u = 0; u < 4; u++) acc = fma4(wsplit[jj + u * NJS], v[u], acc);
+        for (int u = 0; u < U; u++) {
+            if (j0 + u * NJS < ns) {
+                const float mn = fmaxf(m, mj[u]);
+                const float so = expf(m - mn);  // 0 while m is -inf
+                const float sj = expf(mj[u] - mn);
+                l = fmaf(l, so, lj[u] * sj);
+                acc = make_float4(fmaf(acc.x, so, oj[u].x * sj), fmaf(acc.y, so, oj[u].y * sj),
+                                  fmaf(acc.z, so, oj[u].z * sj), fmaf(acc.w, so, oj[u].w * sj));
+                m = mn;
+            }
+        }
     }
-    for (; jj < ns; jj += NJS)
-        acc = fma4(wsplit[jj], *reinterpret_cast<const float4*>(ph + (size_t)jj * (HD + 2) + 2 + 4 * c), acc);
-    acc4[js][c] = acc;
+    accs[js][c] = acc;
+    if (c == 0) {
+        ms[js] = m;
+        ls[js] = l;
+    }
     __syncthreads();
-    const float invL = 1.f / L;
-    for (int d = threadIdx.x; d < HD; d += kAttnThreads) {
-        float s = 0.f;
+    if (threadIdx.x < C4) {
+        float M = -INFINITY;
 #pragma unroll
-        for (int q = 0; q < NJS; q++) s += reinterpret_cast<const float*>(&acc4[q][0])[d];
-        const float r = s * invL;
-        a.out[(size_t)h * HD + d] = r;
-        outv[d] = r;
-    }
-    if (a.outq8) {
-        __syncthreads();
-        if (threadIdx.x < C4) {
-            const float4 v = *reinterpret_cast<const float4*>(outv + 4 * threadIdx.x);
-            const size_t e0 = (size_t)h * HD + 4 * threadIdx.x;
-            q8_store4(a.outq8 + (e0 >> 5) * Q8_0_BYTES, threadIdx.x & 7, v);
+        for (int q = 0; q < NJS; q++) M = fmaxf(M, ms[q]);
+        float L = 0.f;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int q = 0; q < NJS; q++) {
+            if (ls[q] > 0.f) {
+                const float w = expf(ms[q] - M);
+                L = fmaf(ls[q], w, L);
+                const float4 aq = accs[q][c];
+                o = make_float4(fmaf(aq.x, w, o.x), fmaf(aq.y, w, o.y), fmaf(aq.z, w, o.z),
+                                fmaf(aq.w, w, o.w));
+            }
+        }
+        const float inv = 1.f / L;
+        o = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        float* dst = a.out + (size_t)h * HD + 4 * c;
+        dst[0] = o.x;
+        dst[1] = o.y;
+        dst[2] = o.z;
+        dst[3] = o.w;
+        if (a.outq8) {
+            // lanes 0..C4-1 of wave 0: 8 consecutive lanes hold one 32-value block
+            const size_t e0 = (size_t)h * HD + 4 * c;
+            q8_store4(a.outq8 + (e0 >> 5) * Q8_0_BYTES, c & 7, o);
         }
     }
 }
@@ -306,7 +343,7 @@ int attn_nsplit(int max_seq) { return (max_seq + kAttnSplit - 1) / kAttnSplit; }
 
 template <int HD>
 static hipError_t launch_attn_hd(const AttnArgs& a, int G, hipStream_t st) {
-    const dim3 grid((unsigned)a.nsplit, (unsigned)a.n_kv_heads);
+    const dim3 grid((unsigned)a.n_kv_heads, (unsigned)a.nsplit);
     if (G == 1)
         hipLaunchKernelGGL((k_attn_split<HD, 1>), grid, dim3(kAttnThreads), 0, st, a);
     else if (G == 2)

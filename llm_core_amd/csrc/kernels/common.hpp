@@ -52,6 +52,110 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// SwiGLU of the reference (swiglu_avx2, llama_model.cpp:319-368): e = exp(-|g|)
+// by the Cephes single-precision expf method (S. L. Moshier, Cephes Math
+// Library: Cody-Waite reduction by ln2 in two constants, degree-5 polynomial,
+// 2^n scaling), sigmoid = 1/(1+e) for g >= 0 and e/(1+e) for g < 0,
+// out = (g*sigmoid)*up.
+__device__ __forceinline__ float exp_cephes(float x) {
+    float xx = fminf(x, 88.3762626648f);
+    xx = fmaxf(-88.3762626648f, xx);
+    const float fx = floorf(fmaf(xx, 1.44269504089f, 0.5f));
+    xx = fmaf(-fx, 0.693359375f, xx);
+    xx = fmaf(-fx, -2.12194440e-4f, xx);
+    const float z = xx * xx;
+    float p = 1.9875691500E-4f;
+    p = fmaf(p, xx, 1.3981999507E-3f);
+    p = fmaf(p, xx, 8.3334519073E-3f);
+    p = fmaf(p, xx, 4.1665795894E-2f);
+    p = fmaf(p, xx, 1.6666665459E-1f);
+    p = fmaf(p, xx, 5.0000001201E-1f);
+    p = fmaf(p, z, xx + 1.f);
+    const int n = ((int)fx + 127) << 23;
+    return p * __int_as_float(n);
+}
+
+__device__ __forceinline__ float swiglu1(float g, float u) {
+    const float e = exp_cephes(-fabsf(g));
+    const float denom = 1.f + e;
+    const float sig = g < 0.f ? e / denom : 1.f / denom;
+    return (g * sig) * u;
+}
+
+// Q8_0 of 32 values held by one thread (quantize_q8_avx2, quant_q8_avx2.cpp:33-84):
+// d = amax/127, q = rint(v * 127/amax) saturated to int8, packed 4 per dword.
+__device__ __forceinline__ void q8_quant32(const float (&v)[32], uint32_t (&q)[8], float& d) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    d = amax / 127.f;
+    const float id = amax > 0.f ? 127.f / amax : 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float r = rintf(v[4 * k + j] * id);
+            r = fminf(fmaxf(r, -128.f), 127.f);
+            w |= ((uint32_t)((int)r & 0xff)) << (8 * j);
+        }
+        q[k] = w;
+    }
+}
+
+// RMS normalisation scale 1/sqrt(mean(x^2) + eps) over n floats (n % 4 == 0)
+// with one fixed summation order, so every kernel that normalises the same x
+// gets the same bits whatever its workgroup size: 1024 slots, slot s
+// accumulating the squares of float4 s, s+1024, ... in ascending order (fmaf
+// chain x, y, z, w); slots 64w..64w+63 reduced by the xor tree into partial
+// w; the 16 partials added in order.  Called by all NT threads of a workgroup
+// (NT = 256, 512 or 1024) with the thread's float4s of x: xv[k] = float4
+// t + NT*k, zero past the end (thread t holds slots t + NT*j, j < 1024/NT).
+// red: 16 floats of LDS.  Ends with a barrier.
+template <int NT, int KPT>
+__device__ __forceinline__ float rms_scale(const float4 (&xv)[KPT], int n, float eps, float* red) {
+    constexpr int NS = 1024 / NT;
+    static_assert(NS * NT == 1024, "workgroup of 256, 512 or 1024 threads");
+    float s[NS];
+#pragma unroll
+    for (int j = 0; j < NS; j++) s[j] = 0.f;
+#pragma unroll
+    for (int k = 0; k < KPT; k++) {
+        float& a = s[k % NS];
+        a = fmaf(xv[k].x, xv[k].x, a);
+        a = fmaf(xv[k].y, xv[k].y, a);
+        a = fmaf(xv[k].z, xv[k].z, a);
+        a = fmaf(xv[k].w, xv[k].w, a);
+    }
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+        const float v = wave_sum(s[j]);
+        if ((threadIdx.x & 63) == 0) red[(threadIdx.x >> 6) + (NT / 64) * j] = v;
+    }
+    __syncthreads();
+    float ss = red[0];
+#pragma unroll
+    for (int w = 1; w < 16; w++) ss += red[w];
+    return 1.f / sqrtf(ss / (float)n + eps);
+}
+
+// Q8_0 of one 32-value block held as float4 by 8 consecutive lanes
+// (sub = lane & 7): returns this lane's 4 packed int8 and, in d, the block scale.
+__device__ __forceinline__ uint32_t q8_quant4(float4 v, float& d) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+    d = amax / 127.f;
+    const float id = amax > 0.f ? 127.f / amax : 0.f;
+    auto q = [&](float f) -> uint32_t {
+        float r = rintf(f * id);
+        r = fminf(fmaxf(r, -128.f), 127.f);
+        return (uint32_t)((int)r & 0xff);
+    };
+    return q(v.x) | (q(v.y) << 8) | (q(v.z) << 16) | (q(v.w) << 24);
+}
+
 // Q4_K scale/min pair for sub-blocks j0 = 2*part and j1 = 2*part + 1 from the
 // 12 packed scale bytes s[0..11] held in three dwords (get_scale_min_k4 logic:
 // j<4: sc=s[j]&63, m=s[j+4]&63;  j>=4: sc=(s[j+4]&15)|((s[j-4]>>6)<<4),

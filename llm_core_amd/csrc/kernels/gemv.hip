@@ -30,13 +30,34 @@ struct KernCfg {
     int lpr, cpl, nr;
 };
 
+// LPR lanes per row (rows of <= 16 / 32 chunks share a wave), CPL chunks per
+// lane, NR rows per lane.  Every (LPR, CPL, NR) it returns is in AXF_GEMV_CFGS.
 static inline KernCfg pick_cfg(int nchunks) {
     KernCfg k;
     k.lpr = nchunks <= 16 ? 16 : (nchunks <= 32 ? 32 : 64);
     k.cpl = (nchunks + k.lpr - 1) / k.lpr;
-    k.nr = k.cpl >= 4 ? 1 : (k.cpl == 3 ? 1 : 4 / k.cpl);
+    k.nr = k.cpl == 1 ? 2 : 1;
     return k;
 }
+#define AXF_GEMV_CFGS(X) \
+    X(16, 1, 2) X(32, 1, 2) X(64, 1, 2) X(64, 2, 1) X(64, 3, 1) X(64, 4, 1) X(64, 5, 1) X(64, 6, 1) \
+    X(64, 7, 1) X(64, 8, 1)
+// fp32 activations above 4 chunks per lane (256 threads)
+#define AXF_GEMV_CFGS_GT4(X) X(64, 5, 1) X(64, 6, 1) X(64, 7, 1) X(64, 8, 1)
+
+// Register-prologue workgroups: 512 threads use pick_cfg; 1024 threads one
+// row per lane beyond 64-lane rows of one chunk (about 32 rows per workgroup).
+static inline KernCfg pick_cfg_nt(int nchunks, int nt) {
+    KernCfg k = pick_cfg(nchunks);
+    if (nt == 1024) k.nr = (k.lpr == 64 && k.cpl == 1) ? 2 : 1;
+    return k;
+}
+// K <= 8192 (fused normalisation); fp32 activations up to K = 16384 at 512
+// threads and K = 12288 at 1024 (the 128-VGPR budget holds 3 Q6_K chunks per lane)
+#define AXF_GEMV_CFGS_512_NORM(X) X(16, 1, 2) X(32, 1, 2) X(64, 1, 2) X(64, 2, 1)
+#define AXF_GEMV_CFGS_512(X) AXF_GEMV_CFGS_512_NORM(X) X(64, 3, 1) X(64, 4, 1)
+#define AXF_GEMV_CFGS_1024_NORM(X) X(16, 1, 1) X(32, 1, 1) X(64, 1, 2) X(64, 2, 1)
+#define AXF_GEMV_CFGS_1024(X) AXF_GEMV_CFGS_1024_NORM(X) X(64, 3, 1)
 
 // ---------------------------------------------------------------------------
 // Activation staging
@@ -58,21 +79,6 @@ __device__ __forceinline__ void stage_q8_q4k(uint32_t* rec, const uint8_t* xq8, 
             }
             r[16 + j] = ld4(b);
             r[18 + j] = (uint32_t)s;
-        }
-    }
-}
-
-// Q6_K chunk record c: Q8_0 blocks P1 = 2c-(c&1) and P1+2 -> {qs1[8 dw], qs2[8 dw], d1, d2, pad}.
-__device__ __forceinline__ void stage_q8_q6k(uint32_t* rec, const uint8_t* xq8, int nchunks) {
-    for (int c = threadIdx.x; c < nchunks; c += kThreads) {
-        uint32_t* r = rec + 20 * c;
-        const int p1 = 2 * c - (c & 1);
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint8_t* b = xq8 + (size_t)(p1 + 2 * j) * Q8_0_BYTES;
-#pragma unroll
-            for (int k = 0; k < 8; k++) r[8 * j + k] = ld4(b + 4 + 4 * k);
-            r[16 + j] = ld4(b);
         }
     }
 }
@@ -123,94 +129,6 @@ __device__ __forceinline__ void load_q6_tail(const uint8_t* blk, uint32_t (&sc)[
     }
 #pragma unroll
     for (int k = 0; k < 4; k++) sc[k] = alignbyte(w[k + 1], w[k], sh);
-}
-
-// ---------------------------------------------------------------------------
-// Q4_K x Q8_0
-// ---------------------------------------------------------------------------
-template <int LPR, int CPL, int NR>
-__global__ __launch_bounds__(kThreads) void k_gemv_q4k_q8(float* __restrict__ y,
-                                                          const uint8_t* __restrict__ W,
-                                                          const uint8_t* __restrict__ xq8,
-                                                          int rows, int nb, long row_bytes,
-                                                          int accumulate) {
-    extern __shared__ uint4 smem[];
-    uint32_t* rec = reinterpret_cast<uint32_t*>(smem);
-    constexpr int RPP = 64 / LPR;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rl = lane % LPR, rg = lane / LPR;
-    const int nchunks = 4 * nb;
-    const long row0 = ((long)blockIdx.x * kWaves + wave) * (RPP * NR) + rg;
-
-    uint4 hdr[NR][CPL], qa[NR][CPL], qb[NR][CPL];
-#pragma unroll
-    for (int n = 0; n < NR; n++) {
-        const long row = row0 + (long)n * RPP;
-#pragma unroll
-        for (int i = 0; i < CPL; i++) {
-            const int c = rl + i * LPR;
-            if (row < rows && c < nchunks) {
-                const uint8_t* blk = W + row * row_bytes + (long)(c >> 2) * Q4K_BYTES;
-                const int part = c & 3;
-                hdr[n][i] = ld16(blk);
-                qa[n][i] = ld16(blk + 16 + 32 * part);
-                qb[n][i] = ld16(blk + 32 + 32 * part);
-            } else {
-                hdr[n][i] = make_uint4(0, 0, 0, 0);
-                qa[n][i] = qb[n][i] = make_uint4(0, 0, 0, 0);
-            }
-        }
-    }
-
-    stage_q8_q4k(rec, xq8, nchunks);
-    __syncthreads();
-
-    float acc[NR];
-#pragma unroll
-    for (int n = 0; n < NR; n++) acc[n] = 0.f;
-
-#pragma unroll
-    for (int i = 0; i < CPL; i++) {
-        const int c = rl + i * LPR;
-        if (c < nchunks) {
-            const uint4* r4 = reinterpret_cast<const uint4*>(rec + 20 * c);
-            const uint4 xa0 = r4[0], xa1 = r4[1], xb0 = r4[2], xb1 = r4[3], meta = r4[4];
-            const float dx0 = __uint_as_float(meta.x), dx1 = __uint_as_float(meta.y);
-            const float sx0 = (float)(int)meta.z, sx1 = (float)(int)meta.w;
-            const uint32_t xa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
-            const uint32_t xb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
-            const int part = c & 3;
-#pragma unroll
-            for (int n = 0; n < NR; n++) {
-                const uint4 h = hdr[n][i];
-                const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
-                uint32_t sc0, m0, sc1, m1;
-                q4k_scales(h.y, h.z, h.w, part, sc0, m0, sc1, m1);
-                const uint32_t q[8] = {qa[n][i].x, qa[n][i].y, qa[n][i].z, qa[n][i].w,
-                                       qb[n][i].x, qb[n][i].y, qb[n][i].z, qb[n][i].w};
-                int dlo = 0, dhi = 0;
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    dlo = dot4((int)(q[k] & 0x0f0f0f0fu), (int)xa[k], dlo);
-                    dhi = dot4((int)((q[k] >> 4) & 0x0f0f0f0fu), (int)xb[k], dhi);
-                }
-                const float s0 = ((float)sc0 * d) * dx0, mm0 = ((float)m0 * dmin) * dx0;
-                const float s1 = ((float)sc1 * d) * dx1, mm1 = ((float)m1 * dmin) * dx1;
-                float a = acc[n];
-                a = fmaf(s0, (float)dlo, a);
-                a = fmaf(-mm0, sx0, a);
-                a = fmaf(s1, (float)dhi, a);
-                a = fmaf(-mm1, sx1, a);
-                acc[n] = a;
-            }
-        }
-    }
-#pragma unroll
-    for (int n = 0; n < NR; n++) {
-        const float v = group_sum<LPR>(acc[n]);
-        const long row = row0 + (long)n * RPP;
-        if (rl == 0 && row < rows) y[row] = accumulate ? y[row] + v : v;
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -305,7 +223,8 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_f32(float* __restrict__ y
 }
 
 // ---------------------------------------------------------------------------
-// Q6_K x Q8_0
+// Q6_K chunk loads: ql bytes of the chunk's two streams, the qh bytes of its
+// half, the 16 scales and d, all from 2-byte-aligned block addresses.
 // ---------------------------------------------------------------------------
 struct Q6Chunk {
     uint32_t ql[8], qh[8], sc[4], dbits;
@@ -318,99 +237,321 @@ __device__ __forceinline__ void load_q6_chunk(const uint8_t* blk, int c, Q6Chunk
     load_q6_tail(blk, k.sc, k.dbits);
 }
 
-template <int LPR, int CPL, int NR>
-__global__ __launch_bounds__(kThreads) void k_gemv_q6k_q8(float* __restrict__ y,
-                                                          const uint8_t* __restrict__ W,
-                                                          const uint8_t* __restrict__ xq8,
-                                                          int rows, int nb, long row_bytes,
-                                                          int accumulate) {
-    extern __shared__ uint4 smem[];
-    uint32_t* rec = reinterpret_cast<uint32_t*>(smem);
-    constexpr int RPP = 64 / LPR;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rl = lane % LPR, rg = lane / LPR;
-    const int nchunks = 4 * nb;
-    const long row0 = ((long)blockIdx.x * kWaves + wave) * (RPP * NR) + rg;
+// ---------------------------------------------------------------------------
+// Q8_0-activation GEMV family: Q4_K or Q6_K weights, the activation staged in
+// LDS as per-chunk records, with optional fused producer / consumer work:
+//   QAct::Q8    activation given as Q8_0 blocks (256-thread workgroups)
+//   QAct::Norm  activation = Q8_0(w * (x * rms_scale(x))) computed by every
+//               workgroup (rms_scale + q8_quant4: the same bits as
+//               k_rmsnorm followed by Q8_0), so no normalisation kernel runs
+//   QAct::F32   activation = Q8_0(x)
+//   EPI_Y       y[row] = v, or y[row] += v (accumulate: residual adds)
+//   EPI_SWIGLU  the rows of a workgroup are R/2 gate rows then R/2 up rows;
+//               y[i] = swiglu(gate_i, up_i) (no SwiGLU kernel runs)
+// Norm and F32 (K <= 16384) run 512- or 1024-thread workgroups whose threads load
+// their float4s of x (and w) before issuing the weight loads, and build the
+// records from registers while the weights stream in.
+// Activation record of chunk c (20 dwords): int8 values of Q8_0 blocks A and
+// B (8 dwords each), scales d_A and d_B, and integer sums of A and B: for
+// Q4_K the sum of the 32 values (the dmin*m term), for Q6_K the sums of
+// values 0-15 and 16-31 as two int16 (the -32 offset of the 6-bit weights
+// under one scale per 16 weights).  Q4_K chunk c: A = 2c, B = 2c+1; Q6_K
+// chunk c: A = 2c-(c&1), B = A+2.
+// Weight loads use clamped (in-range) addresses; rows and chunks past the end
+// are computed on those bytes and never stored.
+// ---------------------------------------------------------------------------
+enum { EPI_Y = 0, EPI_SWIGLU = 1 };
+constexpr int kQ4K = AXF_TYPE_Q4_K, kQ6K = AXF_TYPE_Q6_K;
+constexpr int kWide = 512, kWider = 1024;  // workgroups of the register prologue
 
-    Q6Chunk wk[NR][CPL];
+template <int QT>
+__device__ __forceinline__ uint32_t* rec_of_block(uint32_t* rec, int b, int& slot) {
+    slot = QT == kQ4K ? (b & 1) : ((b >> 1) & 1);
+    return rec + 20 * (QT == kQ4K ? (b >> 1) : 2 * (b >> 2) + (b & 1));
+}
+
+template <int QT>
+__device__ __forceinline__ void rec_put(uint32_t* rec, int b, const uint32_t (&q)[8], float d) {
+    int slot;
+    uint32_t* r = rec_of_block<QT>(rec, b, slot);
+    uint4* r4 = reinterpret_cast<uint4*>(r + 8 * slot);
+    r4[0] = make_uint4(q[0], q[1], q[2], q[3]);
+    r4[1] = make_uint4(q[4], q[5], q[6], q[7]);
+    r[16 + slot] = __float_as_uint(d);
+    int lo = 0, hi = 0;
 #pragma unroll
-    for (int n = 0; n < NR; n++) {
-        const long row = row0 + (long)n * RPP;
+    for (int k = 0; k < 4; k++) lo = dot4((int)q[k], 0x01010101, lo);
 #pragma unroll
-        for (int i = 0; i < CPL; i++) {
-            const int c = rl + i * LPR;
-            if (row < rows && c < nchunks) {
-                load_q6_chunk(W + row * row_bytes + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
-            } else {
+    for (int k = 4; k < 8; k++) hi = dot4((int)q[k], 0x01010101, hi);
+    r[18 + slot] = QT == kQ4K ? (uint32_t)(lo + hi) : (((uint32_t)lo & 0xffffu) | ((uint32_t)hi << 16));
+}
+
+// 256-thread staging: one Q8_0 block per thread and step (after the weight loads)
+template <int QT, int NT, int ACT>
+__device__ __forceinline__ void stage_act(uint32_t* rec, const QGemvArgs& a) {
+    const int nblk = a.nb * QK_K / 32;
+    for (int b = threadIdx.x; b < nblk; b += NT) {
+        uint32_t q[8];
+        float d;
+        if (ACT == (int)QAct::Q8) {
+            const uint8_t* p = a.xq8 + (size_t)b * Q8_0_BYTES;
 #pragma unroll
-                for (int k = 0; k < 8; k++) wk[n][i].ql[k] = wk[n][i].qh[k] = 0;
+            for (int k = 0; k < 8; k++) q[k] = ld4(p + 4 + 4 * k);
+            d = __uint_as_float(ld4(p));
+        } else {
+            const float4* xp = reinterpret_cast<const float4*>(a.x + 32 * (size_t)b);
+            float v[32];
 #pragma unroll
-                for (int k = 0; k < 4; k++) wk[n][i].sc[k] = 0;
-                wk[n][i].dbits = 0;
+            for (int k = 0; k < 8; k++) {
+                const float4 t = xp[k];
+                v[4 * k] = t.x;
+                v[4 * k + 1] = t.y;
+                v[4 * k + 2] = t.z;
+                v[4 * k + 3] = t.w;
+            }
+            q8_quant32(v, q, d);
+        }
+        rec_put<QT>(rec, b, q, d);
+    }
+}
+
+// Staging from registers: thread t holds float4 t + NT*k of x (and w); 8
+// consecutive threads hold one Q8_0 block.
+template <int QT, int NT, int KPT, int ACT>
+__device__ __forceinline__ void stage_regs(uint32_t* rec, float4 (&xv)[KPT],
+                                           const float4 (&wv)[KPT], int n4, float eps,
+                                           float* red) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < KPT; k++)
+        if (tid + NT * k >= n4) xv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    float rs = 1.f;
+    if (ACT == (int)QAct::Norm) rs = rms_scale<NT, KPT>(xv, 4 * n4, eps, red);
+#pragma unroll
+    for (int k = 0; k < KPT; k++) {
+        const int i4 = tid + NT * k;
+        float4 v = xv[k];
+        if (ACT == (int)QAct::Norm) {
+            const float4 g = wv[k];
+            v = make_float4(g.x * (v.x * rs), g.y * (v.y * rs), g.z * (v.z * rs), g.w * (v.w * rs));
+        }
+        float d;
+        const uint32_t q = q8_quant4(v, d);
+        // integer sums over the block (Q4_K) or its two halves (Q6_K)
+        int s = dot4((int)q, 0x01010101, 0);
+        s += __shfl_xor(s, 1, 8);
+        s += __shfl_xor(s, 2, 8);
+        const int s_hi = __shfl_xor(s, 4, 8);  // lane sub 0 receives the sum of lanes 4-7
+        const int sub = i4 & 7;
+        if (i4 < n4) {
+            int slot;
+            uint32_t* r = rec_of_block<QT>(rec, i4 >> 3, slot);
+            r[8 * slot + sub] = q;
+            if (sub == 0) {
+                r[16 + slot] = __float_as_uint(d);
+                r[18 + slot] = QT == kQ4K ? (uint32_t)(s + s_hi)
+                                          : (((uint32_t)s & 0xffffu) | ((uint32_t)s_hi << 16));
             }
         }
     }
+}
 
-    stage_q8_q6k(rec, xq8, nchunks);
-    __syncthreads();
-
+template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI>
+__device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __restrict__ W,
+                                           long rb, int rows, float* __restrict__ y, int wg,
+                                           uint32_t* rec, float* red) {
+    constexpr int RPP = 64 / LPR;
+    constexpr int RW = (NT / 64) * RPP * NR;  // rows per workgroup
+    constexpr bool REG = NT >= kWide;          // activation built from registers
+    // float4s of x per thread: K / 4 <= 16 * LPR * CPL
+    constexpr int KPT = (16 * LPR * CPL + NT - 1) / NT;
+    static_assert(REG ? ACT != (int)QAct::Q8 : ACT != (int)QAct::Norm, "prologue / workgroup");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rl = lane % LPR, rg = lane / LPR;
+    const int nchunks = 4 * a.nb;
+    const int rloc0 = wave * (RPP * NR) + rg;
+    const long row0 = (long)wg * RW + rloc0;
     float acc[NR];
 #pragma unroll
     for (int n = 0; n < NR; n++) acc[n] = 0.f;
 
+    float4 xv[KPT], wv[KPT];
+    const int n4 = a.nb * (QK_K / 4);
+    if constexpr (REG) {
 #pragma unroll
-    for (int i = 0; i < CPL; i++) {
-        const int c = rl + i * LPR;
-        if (c < nchunks) {
-            const uint4* r4 = reinterpret_cast<const uint4*>(rec + 20 * c);
-            const uint4 xa0 = r4[0], xa1 = r4[1], xb0 = r4[2], xb1 = r4[3], meta = r4[4];
-            const float dxa = __uint_as_float(meta.x), dxb = __uint_as_float(meta.y);
-            const uint32_t xa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
-            const uint32_t xb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
-            const int h = (c >> 1) & 1, t = c & 1;
+        for (int k = 0; k < KPT; k++) {
+            const int i4 = min((int)threadIdx.x + NT * k, n4 - 1);
+            xv[k] = reinterpret_cast<const float4*>(a.x)[i4];
+            wv[k] = ACT == (int)QAct::Norm ? reinterpret_cast<const float4*>(a.nw)[i4]
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    if constexpr (QT == kQ4K) {
+        uint4 hdr[NR][CPL], qa[NR][CPL], qb[NR][CPL];
 #pragma unroll
-            for (int n = 0; n < NR; n++) {
-                const Q6Chunk& k6 = wk[n][i];
-                const float d = h2f(k6.dbits);
-                const uint32_t sa = h ? k6.sc[2] : k6.sc[0], sb = h ? k6.sc[3] : k6.sc[1];
-                const int sA0 = (int8_t)(sa >> (16 * t)), sA1 = (int8_t)(sa >> (16 * t + 8));
-                const int sB0 = (int8_t)(sb >> (16 * t)), sB1 = (int8_t)(sb >> (16 * t + 8));
-                int iA0 = 0, iA1 = 0, iB0 = 0, iB1 = 0;
+        for (int n = 0; n < NR; n++) {
+            const long row = min(row0 + (long)n * RPP, (long)rows - 1);
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const uint32_t l = k6.ql[k], hb = k6.qh[k];
-                    const uint32_t qA = (l & 0x0f0f0f0fu) | (((hb >> (2 * t)) & 0x03030303u) << 4);
-                    const uint32_t qB =
-                        ((l >> 4) & 0x0f0f0f0fu) | (((hb >> (2 * t + 4)) & 0x03030303u) << 4);
-                    // sum (q - 32) * x: -32 per byte is 0xE0 as int8
-                    if (k < 4) {
-                        iA0 = dot4((int)qA, (int)xa[k], iA0);
-                        iA0 = dot4((int)0xE0E0E0E0u, (int)xa[k], iA0);
-                        iB0 = dot4((int)qB, (int)xb[k], iB0);
-                        iB0 = dot4((int)0xE0E0E0E0u, (int)xb[k], iB0);
-                    } else {
-                        iA1 = dot4((int)qA, (int)xa[k], iA1);
-                        iA1 = dot4((int)0xE0E0E0E0u, (int)xa[k], iA1);
-                        iB1 = dot4((int)qB, (int)xb[k], iB1);
-                        iB1 = dot4((int)0xE0E0E0E0u, (int)xb[k], iB1);
+            for (int i = 0; i < CPL; i++) {
+                const int c = min(rl + i * LPR, nchunks - 1);
+                const uint8_t* blk = W + row * rb + (long)(c >> 2) * Q4K_BYTES;
+                const int part = c & 3;
+                hdr[n][i] = ld16(blk);
+                qa[n][i] = ld16(blk + 16 + 32 * part);
+                qb[n][i] = ld16(blk + 32 + 32 * part);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (REG)
+            stage_regs<QT, NT, KPT, ACT>(rec, xv, wv, n4, a.eps, red);
+        else
+            stage_act<QT, NT, ACT>(rec, a);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+            const int c = rl + i * LPR;
+            if (c < nchunks) {
+                const uint4* r4 = reinterpret_cast<const uint4*>(rec + 20 * c);
+                const uint4 xa0 = r4[0], xa1 = r4[1], xb0 = r4[2], xb1 = r4[3], meta = r4[4];
+                const float dx0 = __uint_as_float(meta.x), dx1 = __uint_as_float(meta.y);
+                const float sx0 = (float)(int)meta.z, sx1 = (float)(int)meta.w;
+                const uint32_t xa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
+                const uint32_t xb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
+                const int part = c & 3;
+#pragma unroll
+                for (int n = 0; n < NR; n++) {
+                    const uint4 h = hdr[n][i];
+                    const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+                    uint32_t sc0, m0, sc1, m1;
+                    q4k_scales(h.y, h.z, h.w, part, sc0, m0, sc1, m1);
+                    const uint32_t q[8] = {qa[n][i].x, qa[n][i].y, qa[n][i].z, qa[n][i].w,
+                                           qb[n][i].x, qb[n][i].y, qb[n][i].z, qb[n][i].w};
+                    int dlo = 0, dhi = 0;
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        dlo = dot4((int)(q[k] & 0x0f0f0f0fu), (int)xa[k], dlo);
+                        dhi = dot4((int)((q[k] >> 4) & 0x0f0f0f0fu), (int)xb[k], dhi);
                     }
+                    const float s0 = ((float)sc0 * d) * dx0, mm0 = ((float)m0 * dmin) * dx0;
+                    const float s1 = ((float)sc1 * d) * dx1, mm1 = ((float)m1 * dmin) * dx1;
+                    float v = acc[n];
+                    v = fmaf(s0, (float)dlo, v);
+                    v = fmaf(-mm0, sx0, v);
+                    v = fmaf(s1, (float)dhi, v);
+                    v = fmaf(-mm1, sx1, v);
+                    acc[n] = v;
                 }
-                float a = acc[n];
-                a = fmaf((d * (float)sA0) * dxa, (float)iA0, a);
-                a = fmaf((d * (float)sA1) * dxa, (float)iA1, a);
-                a = fmaf((d * (float)sB0) * dxb, (float)iB0, a);
-                a = fmaf((d * (float)sB1) * dxb, (float)iB1, a);
-                acc[n] = a;
+            }
+        }
+    } else {
+        Q6Chunk wk[NR][CPL];
+#pragma unroll
+        for (int n = 0; n < NR; n++) {
+            const long row = min(row0 + (long)n * RPP, (long)rows - 1);
+#pragma unroll
+            for (int i = 0; i < CPL; i++) {
+                const int c = min(rl + i * LPR, nchunks - 1);
+                load_q6_chunk(W + row * rb + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (REG)
+            stage_regs<QT, NT, KPT, ACT>(rec, xv, wv, n4, a.eps, red);
+        else
+            stage_act<QT, NT, ACT>(rec, a);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+            const int c = rl + i * LPR;
+            if (c < nchunks) {
+                const uint4* r4 = reinterpret_cast<const uint4*>(rec + 20 * c);
+                const uint4 xa0 = r4[0], xa1 = r4[1], xb0 = r4[2], xb1 = r4[3], meta = r4[4];
+                const float dxa = __uint_as_float(meta.x), dxb = __uint_as_float(meta.y);
+                // -32 * (sum of the 16 activation values under each scale)
+                const int oA0 = -32 * (int)(int16_t)(meta.z & 0xffffu), oA1 = -32 * ((int)meta.z >> 16);
+                const int oB0 = -32 * (int)(int16_t)(meta.w & 0xffffu), oB1 = -32 * ((int)meta.w >> 16);
+                const uint32_t xa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
+                const uint32_t xb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
+                const int h = (c >> 1) & 1, t = c & 1;
+#pragma unroll
+                for (int n = 0; n < NR; n++) {
+                    const Q6Chunk& k6 = wk[n][i];
+                    const float d = h2f(k6.dbits);
+                    const uint32_t sa = h ? k6.sc[2] : k6.sc[0], sb = h ? k6.sc[3] : k6.sc[1];
+                    const int sA0 = (int8_t)(sa >> (16 * t)), sA1 = (int8_t)(sa >> (16 * t + 8));
+                    const int sB0 = (int8_t)(sb >> (16 * t)), sB1 = (int8_t)(sb >> (16 * t + 8));
+                    int iA0 = oA0, iA1 = oA1, iB0 = oB0, iB1 = oB1;
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        const uint32_t l = k6.ql[k], hs = k6.qh[k] >> (2 * t);
+                        // 6-bit values: low nibble from ql, bits 4-5 from qh
+                        const uint32_t qA = (l & 0x0f0f0f0fu) | ((hs << 4) & 0x30303030u);
+                        const uint32_t qB = ((l >> 4) & 0x0f0f0f0fu) | (hs & 0x30303030u);
+                        if (k < 4) {
+                            iA0 = dot4((int)qA, (int)xa[k], iA0);
+                            iB0 = dot4((int)qB, (int)xb[k], iB0);
+                        } else {
+                            iA1 = dot4((int)qA, (int)xa[k], iA1);
+                            iB1 = dot4((int)qB, (int)xb[k], iB1);
+                        }
+                    }
+                    float v = acc[n];
+                    v = fmaf((d * (float)sA0) * dxa, (float)iA0, v);
+                    v = fmaf((d * (float)sA1) * dxa, (float)iA1, v);
+                    v = fmaf((d * (float)sB0) * dxb, (float)iB0, v);
+                    v = fmaf((d * (float)sB1) * dxb, (float)iB1, v);
+                    acc[n] = v;
+                }
             }
         }
     }
+
+    if constexpr (EPI == EPI_Y) {
 #pragma unroll
-    for (int n = 0; n < NR; n++) {
-        const float v = group_sum<LPR>(acc[n]);
-        const long row = row0 + (long)n * RPP;
-        if (rl == 0 && row < rows) y[row] = accumulate ? y[row] + v : v;
+        for (int n = 0; n < NR; n++) {
+            const float v = group_sum<LPR>(acc[n]);
+            const long row = row0 + (long)n * RPP;
+            if (rl == 0 && row < rows) y[row] = a.accumulate ? y[row] + v : v;
+        }
+    } else {
+        float* hv = red + 16;  // RW row results of this workgroup
+#pragma unroll
+        for (int n = 0; n < NR; n++) {
+            const float v = group_sum<LPR>(acc[n]);
+            if (rl == 0) hv[rloc0 + n * RPP] = v;
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < RW / 2) {
+            const long i = (long)wg * (RW / 2) + threadIdx.x;
+            if (2 * i < rows) y[i] = swiglu1(hv[threadIdx.x], hv[RW / 2 + threadIdx.x]);
+        }
     }
 }
+
+template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI>
+__global__ __launch_bounds__(NT) void k_qgemv(QGemvArgs a) {
+    extern __shared__ uint4 smem[];
+    uint32_t* rec = reinterpret_cast<uint32_t*>(smem);
+    float* red = reinterpret_cast<float*>(rec + 80 * a.nb);
+    qgemv_body<QT, NT, LPR, CPL, NR, ACT, EPI>(a, a.W0, a.rb0, a.rows0, a.y0, blockIdx.x, rec, red);
+}
+
+// Workgroups [0, nwg0) run the Q4_K segment, the rest the Q6_K segment.
+template <int NT, int LPR, int CPL, int NR, int ACT>
+__global__ __launch_bounds__(NT) void k_qgemv2(QGemvArgs a) {
+    extern __shared__ uint4 smem[];
+    uint32_t* rec = reinterpret_cast<uint32_t*>(smem);
+    float* red = reinterpret_cast<float*>(rec + 80 * a.nb);
+    if ((int)blockIdx.x < a.nwg0)
+        qgemv_body<kQ4K, NT, LPR, CPL, NR, ACT, EPI_Y>(a, a.W0, a.rb0, a.rows0, a.y0, blockIdx.x,
+                                                        rec, red);
+    else
+        qgemv_body<kQ6K, NT, LPR, CPL, NR, ACT, EPI_Y>(a, a.W1, a.rb1, a.rows1, a.y1,
+                                                        blockIdx.x - a.nwg0, rec, red);
+}
+
 
 // ---------------------------------------------------------------------------
 // Q6_K x F32
@@ -611,36 +752,136 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k_q8(float* __restrict__ Y,
 // Host launchers
 // ---------------------------------------------------------------------------
 
+static inline size_t qgemv_lds(int nb) { return (size_t)320 * nb + 4 * (16 + 256); }
+
+template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI>
+static hipError_t qgemv_cfg(const QGemvArgs& a, hipStream_t st) {
+    constexpr int RW = (NT / 64) * (64 / LPR) * NR;
+    const dim3 grid((unsigned)((a.rows0 + RW - 1) / RW));
+    hipLaunchKernelGGL((k_qgemv<QT, NT, LPR, CPL, NR, ACT, EPI>), grid, dim3(NT), qgemv_lds(a.nb),
+                       st, a);
+    return hipGetLastError();
+}
+
+template <int QT, int NT, int ACT, int EPI>
+static hipError_t qgemv_pick(const QGemvArgs& a, hipStream_t st) {
+    const KernCfg k = pick_cfg_nt(4 * a.nb, NT);
+#define AXF_Q(L, C, N) \
+    if (k.lpr == L && k.cpl == C && k.nr == N) return qgemv_cfg<QT, NT, L, C, N, ACT, EPI>(a, st);
+    if constexpr (NT == kWider && ACT == (int)QAct::Norm) {
+        AXF_GEMV_CFGS_1024_NORM(AXF_Q)
+    } else if constexpr (NT == kWider) {
+        AXF_GEMV_CFGS_1024(AXF_Q)
+    } else if constexpr (NT == kWide && ACT == (int)QAct::Norm) {
+        AXF_GEMV_CFGS_512_NORM(AXF_Q)
+    } else if constexpr (NT == kWide) {
+        AXF_GEMV_CFGS_512(AXF_Q)
+    } else if constexpr (ACT == (int)QAct::F32) {
+        AXF_GEMV_CFGS_GT4(AXF_Q)
+    } else {
+        AXF_GEMV_CFGS(AXF_Q)
+    }
+#undef AXF_Q
+    return hipErrorInvalidValue;
+}
+
+bool qgemv_threads_ok(QAct act, int nb, int threads) {
+    const int cpl = pick_cfg(4 * nb).cpl;
+    switch (act) {
+        case QAct::Q8: return threads == kThreads;
+        case QAct::Norm: return nb <= 32 && (threads == kWide || threads == kWider);
+        case QAct::F32:
+            return threads == kWider ? cpl <= 3 : (threads == kWide ? cpl <= 4 : threads == kThreads && cpl > 4);
+    }
+    return false;
+}
+
+int qgemv_threads(QAct act, int nb) {
+    if (act == QAct::Q8) return kThreads;
+    if (act == QAct::Norm) return kWide;
+    const int cpl = pick_cfg(4 * nb).cpl;
+    return cpl <= 3 ? kWider : (cpl == 4 ? kWide : kThreads);
+}
+
+int qgemv_rows_per_wg(int nb, int threads) {
+    const KernCfg k = pick_cfg_nt(4 * nb, threads);
+    return (threads / 64) * (64 / k.lpr) * k.nr;
+}
+
+// Instantiated: Q8 activations at 256 threads (the C-ABI GEMVs, residual
+// projections); fused normalisation (K <= 8192, optionally with the SwiGLU
+// epilogue) at 512 and 1024 threads; fp32 activations at 1024 (K <= 12288),
+// 512 (K <= 16384) or 256 threads (qgemv_threads_ok).
+hipError_t launch_qgemv(int qtype, QAct act, bool swiglu, QGemvArgs a, int threads,
+                        hipStream_t st) {
+    if (a.nb <= 0 || a.nb > kMaxBlocksPerRow || a.rows0 <= 0) return hipErrorInvalidValue;
+    if (qtype != kQ4K && qtype != kQ6K) return hipErrorInvalidValue;
+    if (!qgemv_threads_ok(act, a.nb, threads)) return hipErrorInvalidValue;
+    const bool q4 = qtype == kQ4K;
+    constexpr int Q8 = (int)QAct::Q8, NORM = (int)QAct::Norm, F32 = (int)QAct::F32;
+#define AXF_QT(NT, ACT, EPI) \
+    (q4 ? qgemv_pick<kQ4K, NT, ACT, EPI>(a, st) : qgemv_pick<kQ6K, NT, ACT, EPI>(a, st))
+    if (swiglu) {
+        if (act != QAct::Norm || a.rows0 % qgemv_rows_per_wg(a.nb, threads) != 0)
+            return hipErrorInvalidValue;
+        return threads == kWider ? AXF_QT(kWider, NORM, EPI_SWIGLU) : AXF_QT(kWide, NORM, EPI_SWIGLU);
+    }
+    if (act == QAct::Q8) return AXF_QT(kThreads, Q8, EPI_Y);
+    if (act == QAct::Norm)
+        return threads == kWider ? AXF_QT(kWider, NORM, EPI_Y) : AXF_QT(kWide, NORM, EPI_Y);
+    if (threads == kWider) return AXF_QT(kWider, F32, EPI_Y);
+    if (threads == kWide) return AXF_QT(kWide, F32, EPI_Y);
+    return AXF_QT(kThreads, F32, EPI_Y);
+#undef AXF_QT
+}
+
+hipError_t launch_qgemv2(QAct act, QGemvArgs a, int threads, hipStream_t st) {
+    if (act != QAct::Norm || threads != kWide || a.nb <= 0 || a.nb > 32 || a.rows0 <= 0 ||
+        a.rows1 <= 0)
+        return hipErrorInvalidValue;
+    const KernCfg k = pick_cfg_nt(4 * a.nb, threads);
+    const int rw = qgemv_rows_per_wg(a.nb, threads);
+    a.nwg0 = (a.rows0 + rw - 1) / rw;
+    const dim3 grid((unsigned)(a.nwg0 + (a.rows1 + rw - 1) / rw));
+#define AXF_Q2(L, C, N)                                                                      \
+    if (k.lpr == L && k.cpl == C && k.nr == N) {                                             \
+        hipLaunchKernelGGL((k_qgemv2<kWide, L, C, N, (int)QAct::Norm>), grid, dim3(kWide),   \
+                           qgemv_lds(a.nb), st, a);                                         \
+        return hipGetLastError();                                                            \
+    }
+    AXF_GEMV_CFGS_512_NORM(AXF_Q2)
+#undef AXF_Q2
+    return hipErrorInvalidValue;
+}
+
 template <int LPR, int CPL, int NR>
 static hipError_t launch_cfg(GemvKind kind, float* y, const void* W, const void* x, int rows,
                              int nb, long row_bytes, int accumulate, hipStream_t st) {
     constexpr int rows_per_wg = kWaves * (64 / LPR) * NR;
     const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg));
     const dim3 block(kThreads);
-    const int nchunks = 4 * nb;
     const auto* Wb = static_cast<const uint8_t*>(W);
-    switch (kind) {
-        case GemvKind::Q4K_Q8:
-            hipLaunchKernelGGL((k_gemv_q4k_q8<LPR, CPL, NR>), grid, block, (size_t)nchunks * 80, st,
-                               y, Wb, static_cast<const uint8_t*>(x), rows, nb, row_bytes,
-                               accumulate);
-            break;
-        case GemvKind::Q6K_Q8:
-            hipLaunchKernelGGL((k_gemv_q6k_q8<LPR, CPL, NR>), grid, block, (size_t)nchunks * 80, st,
-                               y, Wb, static_cast<const uint8_t*>(x), rows, nb, row_bytes,
-                               accumulate);
-            break;
-        case GemvKind::Q4K_F32:
-            hipLaunchKernelGGL((k_gemv_q4k_f32<LPR, CPL, NR>), grid, block,
-                               (size_t)nb * QK_K * 4 * 17 / 16, st, y, Wb,
-                               static_cast<const float*>(x), rows, nb, row_bytes, accumulate);
-            break;
-        case GemvKind::Q6K_F32:
-            hipLaunchKernelGGL((k_gemv_q6k_f32<LPR, CPL, NR>), grid, block,
-                               (size_t)nb * QK_K * 4 * 9 / 8, st, y, Wb,
-                               static_cast<const float*>(x), rows, nb, row_bytes, accumulate);
-            break;
+    if (kind == GemvKind::Q4K_Q8 || kind == GemvKind::Q6K_Q8) {
+        QGemvArgs a{};
+        a.W0 = Wb;
+        a.rb0 = row_bytes;
+        a.rows0 = rows;
+        a.y0 = y;
+        a.nb = nb;
+        a.accumulate = accumulate;
+        a.xq8 = static_cast<const uint8_t*>(x);
+        return kind == GemvKind::Q4K_Q8
+                   ? qgemv_cfg<kQ4K, kThreads, LPR, CPL, NR, (int)QAct::Q8, EPI_Y>(a, st)
+                   : qgemv_cfg<kQ6K, kThreads, LPR, CPL, NR, (int)QAct::Q8, EPI_Y>(a, st);
     }
+    if (kind == GemvKind::Q4K_F32)
+        hipLaunchKernelGGL((k_gemv_q4k_f32<LPR, CPL, NR>), grid, block,
+                           (size_t)nb * QK_K * 4 * 17 / 16, st, y, Wb,
+                           static_cast<const float*>(x), rows, nb, row_bytes, accumulate);
+    else
+        hipLaunchKernelGGL((k_gemv_q6k_f32<LPR, CPL, NR>), grid, block,
+                           (size_t)nb * QK_K * 4 * 9 / 8, st, y, Wb,
+                           static_cast<const float*>(x), rows, nb, row_bytes, accumulate);
     return hipGetLastError();
 }
 
@@ -648,19 +889,10 @@ static hipError_t launch_cfg(GemvKind kind, float* y, const void* W, const void*
 hipError_t launch_gemv(GemvKind kind, float* y, const void* W, const void* x, int rows, int nb,
                        long row_bytes, int accumulate, hipStream_t st) {
     const KernCfg k = pick_cfg(4 * nb);
-#define AXF_GEMV_CASE(L, C, N)                                                                \
+#define AXF_GEMV_CASE(L, C, N) \
     if (k.lpr == L && k.cpl == C && k.nr == N)                                                \
         return launch_cfg<L, C, N>(kind, y, W, x, rows, nb, row_bytes, accumulate, st);
-    AXF_GEMV_CASE(16, 1, 4)
-    AXF_GEMV_CASE(32, 1, 4)
-    AXF_GEMV_CASE(64, 1, 4)
-    AXF_GEMV_CASE(64, 2, 2)
-    AXF_GEMV_CASE(64, 3, 1)
-    AXF_GEMV_CASE(64, 4, 1)
-    AXF_GEMV_CASE(64, 5, 1)
-    AXF_GEMV_CASE(64, 6, 1)
-    AXF_GEMV_CASE(64, 7, 1)
-    AXF_GEMV_CASE(64, 8, 1)
+    AXF_GEMV_CFGS(AXF_GEMV_CASE)
 #undef AXF_GEMV_CASE
     return hipErrorInvalidValue;
 }
@@ -691,16 +923,7 @@ static hipError_t launch_gemm_tt(float* Y, const void* W, const void* XQ8, int r
 #define AXF_GEMM_CASE(L, C, N)                                                             \
     if (k.lpr == L && k.cpl == C && k.nr == N)                                             \
         return launch_gemm_cfg<L, C, N, TT>(Y, W, XQ8, rows, T, nb, row_bytes, st);
-    AXF_GEMM_CASE(16, 1, 4)
-    AXF_GEMM_CASE(32, 1, 4)
-    AXF_GEMM_CASE(64, 1, 4)
-    AXF_GEMM_CASE(64, 2, 2)
-    AXF_GEMM_CASE(64, 3, 1)
-    AXF_GEMM_CASE(64, 4, 1)
-    AXF_GEMM_CASE(64, 5, 1)
-    AXF_GEMM_CASE(64, 6, 1)
-    AXF_GEMM_CASE(64, 7, 1)
-    AXF_GEMM_CASE(64, 8, 1)
+    AXF_GEMV_CFGS(AXF_GEMM_CASE)
 #undef AXF_GEMM_CASE
     return hipErrorInvalidValue;
 }

@@ -111,20 +111,12 @@ __global__ void k_quantize_q8_0(uint8_t* __restrict__ y, const float* __restrict
 
 // ---------------------------------------------------------------------------
 // RMSNorm (+ optional Q8_0 of the result), one workgroup of 1024 threads:
-// y = w*(x*s), s = 1/sqrt(sum(x^2)/n + eps).
+// y = w*(x*s), s = 1/sqrt(sum(x^2)/n + eps) (rms_norm_out, llama_model.cpp:396-419).
+// The scale is rms_scale's, the same bits the GEMV prologues that fuse
+// this norm compute (the extra zero float4s of n <= 8192 add exact zeros).
+// n <= 32768.
 // ---------------------------------------------------------------------------
 constexpr int kNormThreads = 1024;
-
-__device__ __forceinline__ float block_sum_1024(float v, float* red) {
-    v = wave_sum(v);
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (lane == 0) red[w] = v;
-    __syncthreads();
-    float s = lane < (kNormThreads / 64) ? red[lane] : 0.f;
-    s = wave_sum(s);
-    __syncthreads();
-    return s;
-}
 
 __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ y,
                                                           uint8_t* __restrict__ yq8,
@@ -132,26 +124,28 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ y,
                                                           const float* __restrict__ w, int n,
                                                           float eps) {
     __shared__ float red[16];
-    float ss = 0.f;
-    for (int i = threadIdx.x * 4; i < n; i += kNormThreads * 4) {
-        const float4 v = *reinterpret_cast<const float4*>(x + i);
-        ss = fmaf(v.x, v.x, ss);
-        ss = fmaf(v.y, v.y, ss);
-        ss = fmaf(v.z, v.z, ss);
-        ss = fmaf(v.w, v.w, ss);
+    const int n4 = n / 4;
+    float4 xv[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i4 = threadIdx.x + kNormThreads * k;
+        xv[k] = i4 < n4 ? reinterpret_cast<const float4*>(x)[i4] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    ss = block_sum_1024(ss, red);
-    const float s = 1.f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x * 4; i < n; i += kNormThreads * 4) {
-        const float4 v = *reinterpret_cast<const float4*>(x + i);
-        const float4 g = *reinterpret_cast<const float4*>(w + i);
-        float4 o;
-        o.x = g.x * (v.x * s);
-        o.y = g.y * (v.y * s);
-        o.z = g.z * (v.z * s);
-        o.w = g.w * (v.w * s);
-        if (y) *reinterpret_cast<float4*>(y + i) = o;
-        if (yq8) q8_block_store(yq8 + (size_t)(i >> 5) * Q8_0_BYTES, (i >> 2) & 7, o);
+    const float s = rms_scale<kNormThreads, 8>(xv, n, eps, red);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i4 = threadIdx.x + kNormThreads * k;
+        if (i4 < n4) {
+            const float4 v = xv[k];
+            const float4 g = reinterpret_cast<const float4*>(w)[i4];
+            float4 o;
+            o.x = g.x * (v.x * s);
+            o.y = g.y * (v.y * s);
+            o.z = g.z * (v.z * s);
+            o.w = g.w * (v.w * s);
+            if (y) reinterpret_cast<float4*>(y)[i4] = o;
+            if (yq8) q8_block_store(yq8 + (size_t)(i4 >> 3) * Q8_0_BYTES, i4 & 7, o);
+        }
     }
 }
 
@@ -212,37 +206,9 @@ __global__ void k_rope_qkv(float* q, const float* __restrict__ k, const float* _
 }
 
 // ---------------------------------------------------------------------------
-// SwiGLU (reference swiglu_avx2): e = exp(-|g|) by the Cephes single-precision
-// expf method (S. L. Moshier, Cephes Math Library: Cody-Waite reduction by
-// ln2 in two constants, degree-5 polynomial, 2^n scaling), sigmoid = 1/(1+e)
-// for g >= 0 and e/(1+e) for g < 0, out = (g*sigmoid)*up.  Optional Q8_0 of
-// the result.  gate/up may be separate buffers or halves of one buffer.
+// SwiGLU (swiglu1 in common.hpp).  Optional Q8_0 of the result.  gate/up may
+// be separate buffers or halves of one buffer.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float exp_cephes(float x) {
-    float xx = fminf(x, 88.3762626648f);
-    xx = fmaxf(-88.3762626648f, xx);
-    const float fx = floorf(fmaf(xx, 1.44269504089f, 0.5f));
-    xx = fmaf(-fx, 0.693359375f, xx);
-    xx = fmaf(-fx, -2.12194440e-4f, xx);
-    const float z = xx * xx;
-    float p = 1.9875691500E-4f;
-    p = fmaf(p, xx, 1.3981999507E-3f);
-    p = fmaf(p, xx, 8.3334519073E-3f);
-    p = fmaf(p, xx, 4.1665795894E-2f);
-    p = fmaf(p, xx, 1.6666665459E-1f);
-    p = fmaf(p, xx, 5.0000001201E-1f);
-    p = fmaf(p, z, xx + 1.f);
-    const int n = ((int)fx + 127) << 23;
-    return p * __int_as_float(n);
-}
-
-__device__ __forceinline__ float swiglu1(float g, float u) {
-    const float e = exp_cephes(-fabsf(g));
-    const float denom = 1.f + e;
-    const float sig = g < 0.f ? e / denom : 1.f / denom;
-    return (g * sig) * u;
-}
-
 __global__ void k_swiglu(float* __restrict__ out, uint8_t* __restrict__ outq8,
                          const float* __restrict__ gate, const float* __restrict__ up, int n) {
     const int nthreads = n / 4;
