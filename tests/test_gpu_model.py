@@ -24,16 +24,16 @@ def within(gpu, ref, rtol=1e-3, atol=1e-4):
     return (not bad.any()), float(np.max(np.abs(gpu - ref)))
 
 
-def test_layer_parity_qwen25_3b(ctx):
+def _layer_parity(ctx, cfg, prior, with_bias, seed):
     from llm_core_amd import hip
-    from llm_core_amd.model import QWEN25_3B_LAYER, Hparams, LlamaHip, SynthLlama
+    from llm_core_amd.model import Hparams, LlamaHip, SynthLlama
 
-    cfg = dict(QWEN25_3B_LAYER)
+    cfg = dict(cfg)
     cfg["n_vocab"] = 256  # the head is not exercised by a single layer
-    hp = Hparams(n_ctx=1025, **cfg)
-    m = SynthLlama(hp, seed=3, norm_std=0.1, with_bias=True)
+    cfg["n_layer"] = 1
+    hp = Hparams(n_ctx=prior + 1, **cfg)
+    m = SynthLlama(hp, seed=seed, norm_std=0.1, with_bias=with_bias)
     kve = hp.n_kv_heads * hp.head_dim
-    prior = 1024
     kv_k = hip.synth_normal(prior * kve, 31).reshape(prior, kve)
     kv_v = hip.synth_normal(prior * kve, 32).reshape(prior, kve)
     x0 = hip.synth_normal(hp.n_embd, 33)
@@ -66,6 +66,21 @@ def test_layer_parity_qwen25_3b(ctx):
     # the layer added a non-trivial update to the residual
     assert np.max(np.abs(want_x - x0)) > 1e-2
     del want_k, want_v
+
+
+def test_layer_parity_qwen25_3b(ctx):
+    """Config 3: hidden 2048 (32-lane rows), GQA 16/2, FFN 11008, KV 1024, biases."""
+    from llm_core_amd.model import QWEN25_3B_LAYER
+
+    _layer_parity(ctx, QWEN25_3B_LAYER, 1024, True, 3)
+
+
+def test_layer_parity_llama7b_shape(ctx):
+    """One LLaMA-2-7B-shaped layer (hidden 4096: 64-lane rows, 32/32 heads,
+    FFN 11008) at context 2048: the shapes of the decode benchmark."""
+    from llm_core_amd.model import LLAMA2_7B
+
+    _layer_parity(ctx, LLAMA2_7B, 2047, False, 4)
 
 
 def test_layer_stepwise_qwen25_3b(ctx):
