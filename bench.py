@@ -92,8 +92,8 @@ def copy_probe(ctx, nbytes=256 << 20, reps=10):
             "GBs_read_plus_write": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}
 
 
-ROOF_KERNEL = "k_qgemv<12, 256, 64, 1, 2, 0, 0>"  # Q4_K, Q8_0 activations, 8 rows per workgroup
-ROOF_GRID = 352256  # threads of one 11008-row launch (1376 workgroups x 256)
+ROOF_KERNEL = "k_qgemv<12, 256, 64, 1, 1, 0, 0>"  # Q4_K, Q8_0 activations, 4 rows per workgroup
+ROOF_GRID = 704512  # threads of one 11008-row launch (2752 workgroups x 256)
 COPY_GRID = 131072  # threads of the runtime's 256 MiB copy kernel
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "gemv_q4k_q8_11008x4096_traffic.txt")
@@ -228,7 +228,7 @@ def main() -> int:
         log(f"gemv q6k 151936x2048 (config 2 head): {c2['us_per_launch']:.2f} us, {c2['gbs']:.0f} GB/s")
         roof = {
             "bound": "hbm",
-            "kernel": "axf::k_qgemv<12,256,64,1,2,0,0> (Q4_K x Q8_0 GEMV, 11008x4096, M=1)",
+            "kernel": "axf::k_qgemv<12,256,64,1,1,0,0> (Q4_K x Q8_0 GEMV, 11008x4096, M=1)",
             "achieved": round(g["gbs"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

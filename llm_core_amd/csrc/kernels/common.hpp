@@ -46,6 +46,22 @@ __device__ __forceinline__ float group_sum(float v) {
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
+// Sum over groups of `width` consecutive lanes (16, 32 or 64) with DPP row
+// operations (no LDS round trips); the sum is valid in the LAST lane of each
+// group.  quad_perm swaps, row_half_mirror and row_mirror reduce each 16-lane
+// row; row_bcast:15 / row_bcast:31 carry row sums into rows 1, 3 and 2, 3.
+template <int width>
+__device__ __forceinline__ float group_sum_last(float v) {
+    static_assert(width == 16 || width == 32 || width == 64, "DPP group width");
+    v += __builtin_amdgcn_update_dpp(0.f, v, 0xb1, 0xf, 0xf, false);   // quad_perm 1,0,3,2
+    v += __builtin_amdgcn_update_dpp(0.f, v, 0x4e, 0xf, 0xf, false);   // quad_perm 2,3,0,1
+    v += __builtin_amdgcn_update_dpp(0.f, v, 0x141, 0xf, 0xf, false);  // row_half_mirror
+    v += __builtin_amdgcn_update_dpp(0.f, v, 0x140, 0xf, 0xf, false);  // row_mirror
+    if (width >= 32) v += __builtin_amdgcn_update_dpp(0.f, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    if (width >= 64) v += __builtin_amdgcn_update_dpp(0.f, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

@@ -18,7 +18,7 @@
 //     lanes hit 64 distinct banks), for the F32 kernels as padded float rows.
 //   * the integer dot of a 32-weight Q8_0 block is exact (v_dot4_i32_i8);
 //     fp32 scale products follow the reference kernels: (d*sc)*dx, (dmin*m)*dx.
-//   * partial sums are reduced over the LPR lanes with cross-lane shuffles.
+//   * partial sums are reduced over the LPR lanes with DPP row operations.
 #include "common.hpp"
 
 namespace axf {
@@ -36,19 +36,21 @@ static inline KernCfg pick_cfg(int nchunks) {
     KernCfg k;
     k.lpr = nchunks <= 16 ? 16 : (nchunks <= 32 ? 32 : 64);
     k.cpl = (nchunks + k.lpr - 1) / k.lpr;
-    k.nr = k.cpl == 1 ? 2 : 1;
+    k.nr = (k.cpl == 1 && k.lpr < 64) ? 2 : 1;
     return k;
 }
 #define AXF_GEMV_CFGS(X) \
-    X(16, 1, 2) X(32, 1, 2) X(64, 1, 2) X(64, 2, 1) X(64, 3, 1) X(64, 4, 1) X(64, 5, 1) X(64, 6, 1) \
+    X(16, 1, 2) X(32, 1, 2) X(64, 1, 1) X(64, 2, 1) X(64, 3, 1) X(64, 4, 1) X(64, 5, 1) X(64, 6, 1) \
     X(64, 7, 1) X(64, 8, 1)
 // fp32 activations above 4 chunks per lane (256 threads)
 #define AXF_GEMV_CFGS_GT4(X) X(64, 5, 1) X(64, 6, 1) X(64, 7, 1) X(64, 8, 1)
 
-// Register-prologue workgroups: 512 threads use pick_cfg; 1024 threads one
-// row per lane beyond 64-lane rows of one chunk (about 32 rows per workgroup).
+// Register-prologue workgroups: two rows per lane at one chunk per lane (512
+// threads), one row per lane beyond 64-lane rows of one chunk (1024 threads;
+// about 32 rows per workgroup).
 static inline KernCfg pick_cfg_nt(int nchunks, int nt) {
     KernCfg k = pick_cfg(nchunks);
+    if (nt == 512) k.nr = k.cpl == 1 ? 2 : 1;
     if (nt == 1024) k.nr = (k.lpr == 64 && k.cpl == 1) ? 2 : 1;
     return k;
 }
@@ -216,9 +218,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_f32(float* __restrict__ y
     }
 #pragma unroll
     for (int n = 0; n < NR; n++) {
-        const float v = group_sum<LPR>(acc[n]);
+        const float v = group_sum_last<LPR>(acc[n]);
         const long row = row0 + (long)n * RPP;
-        if (rl == 0 && row < rows) y[row] = accumulate ? y[row] + v : v;
+        if (rl == LPR - 1 && row < rows) y[row] = accumulate ? y[row] + v : v;
     }
 }
 
@@ -356,6 +358,29 @@ __device__ __forceinline__ void stage_regs(uint32_t* rec, float4 (&xv)[KPT],
     }
 }
 
+// Integer sums of a directly loaded record (dx[0..1] block A, dx[2..3] block
+// B) into dx[4].z / .w, encoded as in rec_put.
+template <int QT>
+__device__ __forceinline__ void direct_sums(uint4 (&dx)[5]) {
+    const uint32_t a[8] = {dx[0].x, dx[0].y, dx[0].z, dx[0].w, dx[1].x, dx[1].y, dx[1].z, dx[1].w};
+    const uint32_t b[8] = {dx[2].x, dx[2].y, dx[2].z, dx[2].w, dx[3].x, dx[3].y, dx[3].z, dx[3].w};
+    int alo = 0, ahi = 0, blo = 0, bhi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        alo = dot4((int)a[k], 0x01010101, alo);
+        ahi = dot4((int)a[k + 4], 0x01010101, ahi);
+        blo = dot4((int)b[k], 0x01010101, blo);
+        bhi = dot4((int)b[k + 4], 0x01010101, bhi);
+    }
+    if (QT == kQ4K) {
+        dx[4].z = (uint32_t)(alo + ahi);
+        dx[4].w = (uint32_t)(blo + bhi);
+    } else {
+        dx[4].z = ((uint32_t)alo & 0xffffu) | ((uint32_t)ahi << 16);
+        dx[4].w = ((uint32_t)blo & 0xffffu) | ((uint32_t)bhi << 16);
+    }
+}
+
 template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI>
 __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __restrict__ W,
                                            long rb, int rows, float* __restrict__ y, int wg,
@@ -374,6 +399,24 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
     float acc[NR];
 #pragma unroll
     for (int n = 0; n < NR; n++) acc[n] = 0.f;
+
+    // One chunk per lane with Q8_0 input: each lane reads its chunk's two Q8_0
+    // blocks itself (L2-resident), before its weight loads; no LDS staging.
+    constexpr bool DIRECT = ACT == (int)QAct::Q8 && CPL == 1 && NT == kThreads;
+    uint4 dx[5];  // the chunk's activation record (DIRECT)
+    if constexpr (DIRECT) {
+        const int c = min(rl, nchunks - 1);
+        const int A = QT == kQ4K ? 2 * c : 2 * c - (c & 1);
+        const int B = QT == kQ4K ? A + 1 : A + 2;
+        const uint8_t* pa = a.xq8 + (size_t)A * Q8_0_BYTES;
+        const uint8_t* pb = a.xq8 + (size_t)B * Q8_0_BYTES;
+        dx[0] = make_uint4(ld4(pa + 4), ld4(pa + 8), ld4(pa + 12), ld4(pa + 16));
+        dx[1] = make_uint4(ld4(pa + 20), ld4(pa + 24), ld4(pa + 28), ld4(pa + 32));
+        dx[2] = make_uint4(ld4(pb + 4), ld4(pb + 8), ld4(pb + 12), ld4(pb + 16));
+        dx[3] = make_uint4(ld4(pb + 20), ld4(pb + 24), ld4(pb + 28), ld4(pb + 32));
+        dx[4] = make_uint4(ld4(pa), ld4(pb), 0u, 0u);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     float4 xv[KPT], wv[KPT];
     const int n4 = a.nb * (QK_K / 4);
@@ -404,17 +447,24 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (REG)
+        if constexpr (DIRECT)
+            direct_sums<QT>(dx);
+        else if constexpr (REG)
             stage_regs<QT, NT, KPT, ACT>(rec, xv, wv, n4, a.eps, red);
         else
             stage_act<QT, NT, ACT>(rec, a);
-        __syncthreads();
+        if constexpr (!DIRECT) __syncthreads();
+        // every chunk is computed on clamped (valid) data and its contribution
+        // selected, so no load is sunk into a branch
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
-            const int c = rl + i * LPR;
-            if (c < nchunks) {
+            const bool live = rl + i * LPR < nchunks;
+            const int c = min(rl + i * LPR, nchunks - 1);
+            {
                 const uint4* r4 = reinterpret_cast<const uint4*>(rec + 20 * c);
-                const uint4 xa0 = r4[0], xa1 = r4[1], xb0 = r4[2], xb1 = r4[3], meta = r4[4];
+                const uint4 xa0 = DIRECT ? dx[0] : r4[0], xa1 = DIRECT ? dx[1] : r4[1];
+                const uint4 xb0 = DIRECT ? dx[2] : r4[2], xb1 = DIRECT ? dx[3] : r4[3];
+                const uint4 meta = DIRECT ? dx[4] : r4[4];
                 const float dx0 = __uint_as_float(meta.x), dx1 = __uint_as_float(meta.y);
                 const float sx0 = (float)(int)meta.z, sx1 = (float)(int)meta.w;
                 const uint32_t xa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
@@ -441,7 +491,7 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
                     v = fmaf(-mm0, sx0, v);
                     v = fmaf(s1, (float)dhi, v);
                     v = fmaf(-mm1, sx1, v);
-                    acc[n] = v;
+                    acc[n] = live ? v : acc[n];
                 }
             }
         }
@@ -457,17 +507,22 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (REG)
+        if constexpr (DIRECT)
+            direct_sums<QT>(dx);
+        else if constexpr (REG)
             stage_regs<QT, NT, KPT, ACT>(rec, xv, wv, n4, a.eps, red);
         else
             stage_act<QT, NT, ACT>(rec, a);
-        __syncthreads();
+        if constexpr (!DIRECT) __syncthreads();
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
-            const int c = rl + i * LPR;
-            if (c < nchunks) {
+            const bool live = rl + i * LPR < nchunks;
+            const int c = min(rl + i * LPR, nchunks - 1);
+            {
                 const uint4* r4 = reinterpret_cast<const uint4*>(rec + 20 * c);
-                const uint4 xa0 = r4[0], xa1 = r4[1], xb0 = r4[2], xb1 = r4[3], meta = r4[4];
+                const uint4 xa0 = DIRECT ? dx[0] : r4[0], xa1 = DIRECT ? dx[1] : r4[1];
+                const uint4 xb0 = DIRECT ? dx[2] : r4[2], xb1 = DIRECT ? dx[3] : r4[3];
+                const uint4 meta = DIRECT ? dx[4] : r4[4];
                 const float dxa = __uint_as_float(meta.x), dxb = __uint_as_float(meta.y);
                 // -32 * (sum of the 16 activation values under each scale)
                 const int oA0 = -32 * (int)(int16_t)(meta.z & 0xffffu), oA1 = -32 * ((int)meta.z >> 16);
@@ -502,7 +557,7 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
                     v = fmaf((d * (float)sA1) * dxa, (float)iA1, v);
                     v = fmaf((d * (float)sB0) * dxb, (float)iB0, v);
                     v = fmaf((d * (float)sB1) * dxb, (float)iB1, v);
-                    acc[n] = v;
+                    acc[n] = live ? v : acc[n];
                 }
             }
         }
@@ -511,16 +566,16 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
     if constexpr (EPI == EPI_Y) {
 #pragma unroll
         for (int n = 0; n < NR; n++) {
-            const float v = group_sum<LPR>(acc[n]);
+            const float v = group_sum_last<LPR>(acc[n]);
             const long row = row0 + (long)n * RPP;
-            if (rl == 0 && row < rows) y[row] = a.accumulate ? y[row] + v : v;
+            if (rl == LPR - 1 && row < rows) y[row] = a.accumulate ? y[row] + v : v;
         }
     } else {
         float* hv = red + 16;  // RW row results of this workgroup
 #pragma unroll
         for (int n = 0; n < NR; n++) {
-            const float v = group_sum<LPR>(acc[n]);
-            if (rl == 0) hv[rloc0 + n * RPP] = v;
+            const float v = group_sum_last<LPR>(acc[n]);
+            if (rl == LPR - 1) hv[rloc0 + n * RPP] = v;
         }
         __syncthreads();
         if ((int)threadIdx.x < RW / 2) {
@@ -636,9 +691,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q6k_f32(float* __restrict__ y
     }
 #pragma unroll
     for (int n = 0; n < NR; n++) {
-        const float v = group_sum<LPR>(acc[n]);
+        const float v = group_sum_last<LPR>(acc[n]);
         const long row = row0 + (long)n * RPP;
-        if (rl == 0 && row < rows) y[row] = accumulate ? y[row] + v : v;
+        if (rl == LPR - 1 && row < rows) y[row] = accumulate ? y[row] + v : v;
     }
 }
 
@@ -742,8 +797,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k_q8(float* __restrict__ Y,
         const long row = row0 + (long)n * RPP;
 #pragma unroll
         for (int t = 0; t < TT; t++) {
-            const float v = group_sum<LPR>(acc[n][t]);
-            if (rl == 0 && row < rows && t < nt) Y[(size_t)(t0 + t) * rows + row] = v;
+            const float v = group_sum_last<LPR>(acc[n][t]);
+            if (rl == LPR - 1 && row < rows && t < nt) Y[(size_t)(t0 + t) * rows + row] = v;
         }
     }
 }
