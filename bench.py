@@ -74,6 +74,30 @@ def gemv_case(ctx, kind, qtype, rows, cols, reps, seed, min_bytes=2 * MALL_BYTES
     return res, W, x
 
 
+def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL_BYTES + (96 << 20)):
+    """The T-token Q4_K x Q8_0 GEMM (config 4: 11008x4096, M tokens), weights
+    rotated like gemv_case; X = M x cols fp32 N(0,1) quantized to Q8_0 on the GPU."""
+    from llm_core_amd import hip
+
+    W = hip.synth_weight(hip.AXF_TYPE_Q4_K, rows, cols, seed)
+    rb = hip.row_bytes(hip.AXF_TYPE_Q4_K, cols)
+    n_copies = max(1, math.ceil(min_bytes / W.nbytes))
+    bufs = [ctx.upload(W) for _ in range(n_copies)]
+    X = hip.synth_normal(M * cols, seed + 7)
+    dX = ctx.upload(X)
+    xq = ctx.alloc(M * cols // 32 * 36)
+    ctx.quantize_q8_0(xq, dX, M * cols)
+    dY = ctx.alloc(M * rows * 4)
+    ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2)
+    ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps)
+    us = ms * 1000.0 / (reps * n_copies)
+    alg = W.nbytes + M * (cols // 32 * 36) + 4 * M * rows
+    for b in bufs:
+        b.free()
+    return {"M": M, "us": round(us, 3), "GBs": round(alg / (us * 1e-6) / 1e9, 1),
+            "TOPs": round(2.0 * M * rows * cols / (us * 1e-6) / 1e12, 2)}
+
+
 def copy_probe(ctx, nbytes=256 << 20, reps=10):
     """Plain device-to-device copy of nbytes (the runtime's copy kernel): the
     calibration kernel for the HBM traffic counters and a practical
@@ -241,8 +265,13 @@ def main() -> int:
             "weight_copies": g["n_copies"],
             "mall_warm_us_per_launch": round(warm["us_per_launch"], 3) if warm else None,
         }
+        c4 = [gemm_case(ctx, M) for M in (1, 4, 16, 64)]
+        for g4 in c4:
+            log(f"gemm q4k 11008x4096 M={g4['M']} (config 4): {g4['us']:.2f} us, {g4['GBs']:.0f} GB/s, "
+                f"{g4['TOPs']:.2f} TOP/s")
         out["kernels"] = {
             "copy_256MiB_d2d": cp,
+            "c4_q4k_q8_gemm_11008x4096": c4,
             "c1_q4k_f32_4096x4096": {"us": round(c1["us_per_launch"], 3), "GBs": round(c1["gbs"], 1)},
             "c2_q6k_q8_151936x2048": {"us": round(c2["us_per_launch"], 3), "GBs": round(c2["gbs"], 1)},
         }

@@ -160,6 +160,12 @@ int axf_hip_timer_stop(axf_ctx* ctx, float* ms); /* waits for the stop event */
 int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_list, int n_w,
                        const void* x, int rows, int cols, size_t row_bytes, int reps, float* ms);
 
+/* Benchmark helper (no reference counterpart): as axf_hip_bench_gemv for the
+ * T-token GEMM of axf_hip_gemm_q4k_q8 (Q4_K weights, Q8_0 activations). */
+int axf_hip_bench_gemm(axf_ctx* ctx, float* Y, const void* const* W_list, int n_w,
+                       const void* XQ8, int rows, int T, int cols, size_t row_bytes, int reps,
+                       float* ms);
+
 /* ---- synthetic GGUF weights (host code, deterministic) ------------------ */
 /* dst[i] ~ N(mean, std) from a counter-based generator (splitmix64 + Box-Muller);
  * element i depends only on (seed, i). */

@@ -384,6 +384,39 @@ int axf_hip_timer_stop(axf_ctx* ctx, float* ms) {
     return AXF_OK;
 }
 
+}  // extern "C"
+
+// Capture n launches (launch(i, stream)) into one graph, replay it once
+// untimed, then `reps` times between the context's two events.
+template <class F>
+static int bench_graph(axf_ctx* ctx, const char* fn, int n, int reps, float* ms, F launch) {
+    hipStream_t st = ctx->stream;
+    AXF_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < n && e == hipSuccess; i++) e = launch(i, st);
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(st, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return hip_fail(e, fn);
+    }
+    if (e2 != hipSuccess) return hip_fail(e2, fn);
+    hipGraphExec_t ex = nullptr;
+    e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e == hipSuccess) e = hipGraphLaunch(ex, st);
+    if (e == hipSuccess) e = hipEventRecord(ctx->ev0, st);
+    for (int r = 0; r < reps && e == hipSuccess; r++) e = hipGraphLaunch(ex, st);
+    if (e == hipSuccess) e = hipEventRecord(ctx->ev1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(ctx->ev1);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, ctx->ev0, ctx->ev1);
+    if (ex) (void)hipGraphExecDestroy(ex);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, fn);
+    return AXF_OK;
+}
+
+extern "C" {
+
 int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_list, int n_w,
                        const void* x, int rows, int cols, size_t row_bytes, int reps, float* ms) {
     AXF_CHECK_CTX(ctx);
@@ -395,27 +428,24 @@ int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_li
         int rc = check_gemv(__func__, qtype, W_list[i], x, y, rows, cols, row_bytes, kind >= 2);
         if (rc) return rc;
     }
-    hipStream_t st = ctx->stream;
-    AXF_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    hipError_t e = hipSuccess;
-    for (int i = 0; i < n_w && e == hipSuccess; i++)
-        e = launch_gemv(kinds[kind], y, W_list[i], x, rows, cols / QK_K, (long)row_bytes, 0, st);
-    hipGraph_t g = nullptr;
-    hipError_t e2 = hipStreamEndCapture(st, &g);
-    if (e != hipSuccess) return hip_fail(e, "axf_hip_bench_gemv: capture");
-    if (e2 != hipSuccess) return hip_fail(e2, "axf_hip_bench_gemv: end capture");
-    hipGraphExec_t ex = nullptr;
-    e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-    if (e == hipSuccess) e = hipGraphLaunch(ex, st);
-    if (e == hipSuccess) e = hipEventRecord(ctx->ev0, st);
-    for (int r = 0; r < reps && e == hipSuccess; r++) e = hipGraphLaunch(ex, st);
-    if (e == hipSuccess) e = hipEventRecord(ctx->ev1, st);
-    if (e == hipSuccess) e = hipEventSynchronize(ctx->ev1);
-    if (e == hipSuccess) e = hipEventElapsedTime(ms, ctx->ev0, ctx->ev1);
-    if (ex) (void)hipGraphExecDestroy(ex);
-    (void)hipGraphDestroy(g);
-    if (e != hipSuccess) return hip_fail(e, "axf_hip_bench_gemv");
-    return AXF_OK;
+    return bench_graph(ctx, __func__, n_w, reps, ms, [&](int i, hipStream_t st) {
+        return launch_gemv(kinds[kind], y, W_list[i], x, rows, cols / QK_K, (long)row_bytes, 0, st);
+    });
+}
+
+int axf_hip_bench_gemm(axf_ctx* ctx, float* Y, const void* const* W_list, int n_w,
+                       const void* XQ8, int rows, int T, int cols, size_t row_bytes, int reps,
+                       float* ms) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(W_list && n_w > 0 && reps > 0 && ms && T > 0 && rows > 0 && cols > 0,
+                "bad arguments");
+    for (int i = 0; i < n_w; i++) {
+        int rc = check_gemv(__func__, AXF_TYPE_Q4_K, W_list[i], XQ8, Y, rows, cols, row_bytes, false);
+        if (rc) return rc;
+    }
+    return bench_graph(ctx, __func__, n_w, reps, ms, [&](int i, hipStream_t st) {
+        return launch_gemm_q4k_q8(Y, W_list[i], XQ8, rows, T, cols / QK_K, (long)row_bytes, st);
+    });
 }
 
 size_t axf_row_bytes(int qtype, int64_t cols) {

@@ -177,6 +177,16 @@ class Context:
              C.c_void_p(int(x)), rows, cols, C.c_size_t(rb), reps, C.byref(ms))
         return ms.value
 
+    def bench_gemm(self, Y: int, W_list, XQ8: int, rows: int, T: int, cols: int, rb: int,
+                   reps: int) -> float:
+        """Milliseconds for reps*len(W_list) graph-replayed Q4_K x Q8_0 GEMM
+        launches of T tokens."""
+        arr = (C.c_void_p * len(W_list))(*[int(w) for w in W_list])
+        ms = C.c_float(0)
+        call("axf_hip_bench_gemm", self.handle, C.c_void_p(int(Y)), arr, len(W_list),
+             C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb), reps, C.byref(ms))
+        return ms.value
+
 
 def rope_table(head_dim: int, theta: float, max_pos: int) -> tuple[np.ndarray, np.ndarray]:
     c = np.empty(max_pos * (head_dim // 2), np.float32)
