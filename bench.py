@@ -74,6 +74,15 @@ def gemv_case(ctx, kind, qtype, rows, cols, reps, seed, min_bytes=2 * MALL_BYTES
     return res, W, x
 
 
+def c4_sweep(ctx, Ms=(1, 2, 4, 8, 16, 32, 64)):
+    res = [gemm_case(ctx, M) for M in Ms]
+    for g4 in res:
+        log(f"gemm q4k 11008x4096 M={g4['M']} (config 4): dot4 {g4['dot4_us']:.2f} us, "
+            f"mfma {g4['mfma_us']:.2f} us, auto {g4['auto_us']:.2f} us = {g4['GBs']:.0f} GB/s, "
+            f"{g4['TOPs']:.2f} TOP/s")
+    return res
+
+
 def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL_BYTES + (96 << 20)):
     """The T-token Q4_K x Q8_0 GEMM (config 4: 11008x4096, M tokens), weights
     rotated like gemv_case; X = M x cols fp32 N(0,1) quantized to Q8_0 on the GPU."""
@@ -88,14 +97,18 @@ def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL
     xq = ctx.alloc(M * cols // 32 * 36)
     ctx.quantize_q8_0(xq, dX, M * cols)
     dY = ctx.alloc(M * rows * 4)
-    ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2)
-    ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps)
-    us = ms * 1000.0 / (reps * n_copies)
     alg = W.nbytes + M * (cols // 32 * 36) + 4 * M * rows
+    res = {"M": M}
+    for name, path in (("dot4", 1), ("mfma", 2), ("auto", 0)):
+        ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2, path)
+        ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps, path)
+        res[f"{name}_us"] = round(ms * 1000.0 / (reps * n_copies), 3)
+    us = res["auto_us"]
     for b in bufs:
         b.free()
-    return {"M": M, "us": round(us, 3), "GBs": round(alg / (us * 1e-6) / 1e9, 1),
-            "TOPs": round(2.0 * M * rows * cols / (us * 1e-6) / 1e12, 2)}
+    res.update({"GBs": round(alg / (us * 1e-6) / 1e9, 1),
+                "TOPs": round(2.0 * M * rows * cols / (us * 1e-6) / 1e12, 2)})
+    return res
 
 
 def copy_probe(ctx, nbytes=256 << 20, reps=10):
@@ -204,7 +217,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="approximate CPU seconds spent on the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["all", "gemv", "decode"], default="all")
+    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm"], default="all")
     ap.add_argument("--mall-warm", action="store_true",
                     help="also time the roofline GEMV on one weight copy (Infinity-Cache warm)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
@@ -233,6 +246,10 @@ def main() -> int:
     ctx = hip.Context(0)
     log(f"device: {ctx.device_name()}")
     out: dict = {}
+
+    if args.only == "gemm":  # config 4 sweep alone (not a bench line)
+        print(json.dumps({"c4_q4k_q8_gemm_11008x4096": c4_sweep(ctx)}))
+        return 0
 
     # ---- dominant kernel: Q4_K x Q8_0 GEMV, 11008 x 4096, M = 1 ----------------
     roof = None
@@ -265,10 +282,7 @@ def main() -> int:
             "weight_copies": g["n_copies"],
             "mall_warm_us_per_launch": round(warm["us_per_launch"], 3) if warm else None,
         }
-        c4 = [gemm_case(ctx, M) for M in (1, 4, 16, 64)]
-        for g4 in c4:
-            log(f"gemm q4k 11008x4096 M={g4['M']} (config 4): {g4['us']:.2f} us, {g4['GBs']:.0f} GB/s, "
-                f"{g4['TOPs']:.2f} TOP/s")
+        c4 = c4_sweep(ctx)
         out["kernels"] = {
             "copy_256MiB_d2d": cp,
             "c4_q4k_q8_gemm_11008x4096": c4,

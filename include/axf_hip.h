@@ -107,6 +107,12 @@ int axf_hip_gemv_q6k_q8(axf_ctx* ctx, float* y, const void* W, const void* xq8, 
  * block t*(cols/32). */
 int axf_hip_gemm_q4k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
                         int T, int cols, size_t row_bytes);
+/* The same GEMM with the kernel chosen explicitly (no reference counterpart;
+ * for tests and measurement): path 0 automatic (matrix cores from 8 tokens up),
+ * 1 the dot4 kernel, 2 the matrix-core (int8 MFMA) kernel.  Results of the two
+ * kernels differ only in float summation order. */
+int axf_hip_gemm_q4k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
+                             int T, int cols, size_t row_bytes, int path);
 
 /* Greedy pick: *idx_dev = first index of the maximum of x[0..n), the
  * std::max_element of sample() (llama_model.cpp:1470-1471).  idx_dev is a
@@ -161,10 +167,11 @@ int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_li
                        const void* x, int rows, int cols, size_t row_bytes, int reps, float* ms);
 
 /* Benchmark helper (no reference counterpart): as axf_hip_bench_gemv for the
- * T-token GEMM of axf_hip_gemm_q4k_q8 (Q4_K weights, Q8_0 activations). */
+ * T-token GEMM of axf_hip_gemm_q4k_q8 (Q4_K weights, Q8_0 activations); path as for
+ * axf_hip_gemm_q4k_q8_path. */
 int axf_hip_bench_gemm(axf_ctx* ctx, float* Y, const void* const* W_list, int n_w,
-                       const void* XQ8, int rows, int T, int cols, size_t row_bytes, int reps,
-                       float* ms);
+                       const void* XQ8, int rows, int T, int cols, size_t row_bytes, int path,
+                       int reps, float* ms);
 
 /* ---- synthetic GGUF weights (host code, deterministic) ------------------ */
 /* dst[i] ~ N(mean, std) from a counter-based generator (splitmix64 + Box-Muller);

@@ -31,6 +31,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = [
     "kernels/gemv.hip",
+    "kernels/gemm_mfma.hip",
     "kernels/ops.hip",
     "kernels/attention.hip",
     "capi.cpp",
@@ -62,9 +63,17 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
         print(out, file=sys.stderr)
 
 
+# per-source additions: the matrix-core GEMM keeps MFMA results in VGPRs
+# (the default heuristic places them in AGPRs and copies every result out)
+EXTRA_FLAGS = {
+    "kernels/gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> Path:
     obj = BUILD / (src.replace("/", "_") + ".o")
-    _run([HIPCC, "-x", "hip", *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    _run([HIPCC, "-x", "hip", *COMMON_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src),
+          "-o", str(obj)])
     return obj
 
 

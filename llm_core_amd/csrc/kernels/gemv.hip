@@ -983,8 +983,8 @@ static hipError_t launch_gemm_tt(float* Y, const void* W, const void* XQ8, int r
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
-                              long row_bytes, hipStream_t st) {
+static hipError_t launch_gemm_dot4(float* Y, const void* W, const void* XQ8, int rows, int T,
+                                   int nb, long row_bytes, hipStream_t st) {
     // token tile: as many tokens as fit 64 KiB of LDS records (80 B per chunk)
     const size_t per_tok = (size_t)4 * nb * 80;
     int tt = (int)(65536 / per_tok);
@@ -992,6 +992,22 @@ hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows
     if (T >= 4 && tt >= 4) return launch_gemm_tt<4>(Y, W, XQ8, rows, T, nb, row_bytes, st);
     if (T >= 2 && tt >= 2) return launch_gemm_tt<2>(Y, W, XQ8, rows, T, nb, row_bytes, st);
     return launch_gemm_tt<1>(Y, W, XQ8, rows, T, nb, row_bytes, st);
+}
+
+GemmPath gemm_resolve(GemmPath path, int T) {
+    if (path != GemmPath::Auto) return path;
+    return T >= kGemmMfmaMinT ? GemmPath::Mfma : GemmPath::Dot4;
+}
+
+size_t gemm_scratch_bytes(GemmPath path, int T, int nb) {
+    return gemm_resolve(path, T) == GemmPath::Mfma ? gemm_mfma_scratch_bytes(T, nb) : 0;
+}
+
+hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
+                              long row_bytes, GemmPath path, void* scratch, hipStream_t st) {
+    if (gemm_resolve(path, T) == GemmPath::Mfma)
+        return launch_gemm_mfma_q4k_q8(Y, W, XQ8, rows, T, nb, row_bytes, scratch, st);
+    return launch_gemm_dot4(Y, W, XQ8, rows, T, nb, row_bytes, st);
 }
 
 }  // namespace axf

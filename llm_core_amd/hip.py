@@ -125,9 +125,15 @@ class Context:
         call(name, self.handle, C.c_void_p(int(y)), C.c_void_p(int(W)), C.c_void_p(int(xq8)),
              rows, cols, C.c_size_t(rb), 1 if accumulate else 0)
 
-    def gemm_q4k_q8(self, Y: int, W: int, XQ8: int, rows: int, T: int, cols: int, rb: int) -> None:
-        call("axf_hip_gemm_q4k_q8", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
-             C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb))
+    def gemm_q4k_q8(self, Y: int, W: int, XQ8: int, rows: int, T: int, cols: int, rb: int,
+                    path: int | None = None) -> None:
+        """Token-major Q4_K x Q8_0 GEMM; path None = automatic, 1 dot4, 2 matrix cores."""
+        if path is None:
+            call("axf_hip_gemm_q4k_q8", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
+                 C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb))
+        else:
+            call("axf_hip_gemm_q4k_q8_path", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
+                 C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb), int(path))
 
     def argmax(self, idx: int, x: int, n: int) -> None:
         call("axf_hip_argmax_f32", self.handle, C.c_void_p(int(idx)), C.c_void_p(int(x)), n)
@@ -178,13 +184,13 @@ class Context:
         return ms.value
 
     def bench_gemm(self, Y: int, W_list, XQ8: int, rows: int, T: int, cols: int, rb: int,
-                   reps: int) -> float:
+                   reps: int, path: int = 0) -> float:
         """Milliseconds for reps*len(W_list) graph-replayed Q4_K x Q8_0 GEMM
-        launches of T tokens."""
+        launches of T tokens (path 0 automatic, 1 dot4, 2 matrix cores)."""
         arr = (C.c_void_p * len(W_list))(*[int(w) for w in W_list])
         ms = C.c_float(0)
         call("axf_hip_bench_gemm", self.handle, C.c_void_p(int(Y)), arr, len(W_list),
-             C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb), reps, C.byref(ms))
+             C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb), int(path), reps, C.byref(ms))
         return ms.value
 
 
