@@ -11,23 +11,30 @@
 // 16 rows x 16 tokens.  Y is token-major like the reference's.
 //
 // A prep kernel re-lays the Q8_0 activations so that a 16-token fragment is
-// one contiguous 512-byte load and precomputes dx*bsum.  Then per (16-row,
-// 16-token, sub-block) tile one wave issues
-//   v_mfma_i32_16x16x32_i8   A = weight nibbles, B = int8 activations  -> S
+// one contiguous 512-byte block and precomputes dx*bsum.  The GEMM kernel then
+// streams the K dimension one Q4_K block (256 weights per row) at a time
+// through an S-deep ring of LDS stages, each filled by global_load_lds_dwordx4
+// copies (1 KiB per wave instruction, no VGPR staging): the workgroup's weight
+// rows, the tokens' int8 values, dx and dx*bsum.  Per (16-token, 16-row,
+// sub-block) tile one wave issues
+//   v_mfma_i32_16x16x32_i8   A = int8 activations, B = weight nibbles  -> S
 // scaled on the VALU by sc (24-bit integer multiply) and dx (fp32 FMA), and per
-// 256-element block two v_mfma_f32_16x16x4_f32 fold the min term
-// (A = dmin*m per row and sub-block, B = dx*bsum per sub-block and token).
-// The integer parts are exact; the float combination differs from the scalar
-// dot only in summation order.
+// block two v_mfma_f32_16x16x4_f32 fold the min term (A = dx*bsum per token
+// and sub-block, B = dmin*m per sub-block and weight row).  The integer parts
+// are exact; the float combination differs from the scalar dot only in
+// summation order.
 //
 // MFMA operand layout (16x16xK, wave64): A lane l holds row l%16, k-group
 // l/16; B lane l holds column l%16, k-group l/16; result lane l holds rows
 // 4*(l/16)+i (i = 0..3) of column l%16.  Within a k-group any element order
-// works as long as A and B agree; both use natural order here.
+// works as long as A and B agree; both use natural order here.  With tokens
+// as A's rows and weight rows as B's columns, every weight-side scale of a
+// result lane belongs to that lane's own weight row.
 //
-// Work split: a workgroup owns a (16*RT rows) x (16*TT tokens) tile; its waves
-// split the Q4_K blocks of the rows between them and their partial tiles are
-// summed in a fixed order in LDS (deterministic results).
+// Work split: a workgroup owns a (16*RT rows) x (16*TT tokens) tile; each wave
+// takes whole 16x16 tiles, or, when there are fewer tiles than waves, a
+// subset of the sub-blocks of one tile, whose partial tiles are then summed in
+// a fixed order in LDS (deterministic results).
 #include "common.hpp"
 
 namespace axf {
@@ -75,157 +82,279 @@ __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
     return (long)(((uint64_t)hi << 32) | lo);
 }
 
-// Workgroup = NW waves on one (16*RT rows) x (16*TT tokens) tile; wave w takes
-// the Q4_K blocks w, w+NW, ... of the rows and the partial tiles are summed in
-// a fixed order in LDS.  grid = (row tiles, token tiles); Tp % (16*TT) == 0.
-template <int NW, int RT, int TT>
+typedef __attribute__((address_space(1))) const void gmem_t;
+typedef __attribute__((address_space(3))) void lmem_t;
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] bits 3:0,
+// vmcnt[5:4] bits 15:14, expcnt and lgkmcnt at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// One K-chunk (one Q4_K block, 256 weights per row) as staged in LDS:
+//   [RW rows][144 B] weights | [8 records][TW tokens][32 B] int8 activations |
+//   [8][TW] dx | [8][TW] dx*bsum.
+// It is copied by 1 KiB pieces (64 lanes x 16 B, global_load_lds_dwordx4);
+// wave w copies pieces w, w+NW, ...
+template <int RT, int TT, int NW, int S>
+struct Stage {
+    static constexpr int RW = kTile * RT, TW = kTile * TT;
+    static constexpr int WB = RW * Q4K_BYTES;
+    static constexpr int XB = 8 * TW * 32;
+    static constexpr int DB = 8 * TW * 4;
+    static constexpr int BYTES = WB + XB + 2 * DB;
+    static constexpr int PIECES = (BYTES + 1023) / 1024;
+    static constexpr int ALLOC = PIECES * 1024;
+    static constexpr int PMAX = (PIECES + NW - 1) / NW;  // pieces of the busiest wave
+    static constexpr int PMIN = PIECES / NW;             // pieces of every wave
+    static constexpr int NTILE = RT * TT;
+    static constexpr int WT = NTILE >= NW ? NTILE / NW : 1;  // tiles per wave
+    static constexpr int KS = NTILE >= NW ? 1 : NW / NTILE;  // waves per tile (sub-block split)
+    static_assert(WB % 16 == 0 && XB % 1024 == 0 && DB % 16 == 0, "piece alignment");
+    static_assert(NTILE % NW == 0 || NW % NTILE == 0, "tile split");
+    static_assert(TT % WT == 0 && 8 % KS == 0, "tile split");
+};
+
+// The sub-blocks s = KPH, KPH+KS, ... of one staged chunk for this wave's
+// tiles.  MFMA operands: A = 16 tokens (row l%16 of A is token col), B = 16
+// weight rows (column l%16 is weight row col), so result lane l holds tokens
+// 4g+i of weight row col: every weight-side scale is lane-local.  All LDS
+// reads are issued first, then the MFMAs back to back, then the scaling
+// (integer sc via a 24-bit multiply, dx via an fp32 FMA).
+template <class G, int KPH>
+__device__ __forceinline__ void mfma_sub_blocks(const uint8_t* wl, const uint8_t* xl,
+                                                const float* dl, int g, int col, int tt0,
+                                                uint32_t sc03, uint32_t sc47,
+                                                v4f_t (&accb)[G::WT]) {
+    constexpr int TW = G::TW, NS = 8 / G::KS;
+    const v4i_t zi = {0, 0, 0, 0};
+    uint2 qv[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) qv[p] = *reinterpret_cast<const uint2*>(wl + 16 + 32 * p + 8 * g);
+    uint2 xv[G::WT][NS];
+    float4 dx[G::WT][NS];
+#pragma unroll
+    for (int w = 0; w < G::WT; w++)
+#pragma unroll
+        for (int sj = 0; sj < NS; sj++) {
+            const int s = KPH + G::KS * sj;
+            const int tok = kTile * (tt0 + w);
+            xv[w][sj] = *reinterpret_cast<const uint2*>(xl + (s * TW + tok + col) * 32 + 8 * g);
+            dx[w][sj] = *reinterpret_cast<const float4*>(dl + s * TW + tok + 4 * g);
+        }
+    v4i_t c[G::WT][NS];
+#pragma unroll
+    for (int sj = 0; sj < NS; sj++) {
+        const int s = KPH + G::KS * sj;
+        const int sh = (s & 1) * 4;
+        const long bw = pack2((qv[s >> 1].x >> sh) & 0x0f0f0f0fu, (qv[s >> 1].y >> sh) & 0x0f0f0f0fu);
+#pragma unroll
+        for (int w = 0; w < G::WT; w++)
+            c[w][sj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(pack2(xv[w][sj].x, xv[w][sj].y), bw,
+                                                             zi, 0, 0, 0);
+    }
+#pragma unroll
+    for (int sj = 0; sj < NS; sj++) {
+        const int s = KPH + G::KS * sj;
+        const int scv = (int)(((s < 4 ? sc03 : sc47) >> (8 * (s & 3))) & 0xffu);
+#pragma unroll
+        for (int w = 0; w < G::WT; w++) {
+            // |S| < 2^17 and sc < 64: the 24-bit multiply is exact
+            accb[w][0] = fmaf((float)__mul24(c[w][sj][0], scv), dx[w][sj].x, accb[w][0]);
+            accb[w][1] = fmaf((float)__mul24(c[w][sj][1], scv), dx[w][sj].y, accb[w][1]);
+            accb[w][2] = fmaf((float)__mul24(c[w][sj][2], scv), dx[w][sj].z, accb[w][2]);
+            accb[w][3] = fmaf((float)__mul24(c[w][sj][3], scv), dx[w][sj].w, accb[w][3]);
+        }
+    }
+}
+
+// One step of the K loop (inlined): copy chunk `bnext` into `nxt`, then, for
+// i >= 0, wait for chunk i and compute it from `cur`.
+template <int RT, int TT, int NW, int S>
+__device__ __forceinline__ void gemm_step(
+    const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt, bool do_copy, int bnext, int i,
+    int nb, const uint8_t* const (&src)[Stage<RT, TT, NW, S>::PMAX],
+    const uint32_t (&step)[Stage<RT, TT, NW, S>::PMAX], int wave, int lane, int col, int g,
+    int kph, int tt0, int wrow, v4f_t (&acc)[Stage<RT, TT, NW, S>::WT],
+    v4f_t (&macc)[Stage<RT, TT, NW, S>::WT]) {
+    using G = Stage<RT, TT, NW, S>;
+    constexpr int TW = G::TW;
+    if (do_copy) {
+#pragma unroll
+        for (int j = 0; j < G::PMAX; j++) {
+            if (wave + NW * j < G::PIECES)
+                __builtin_amdgcn_global_load_lds((gmem_t*)(src[j] + (size_t)bnext * step[j]),
+                                                 (lmem_t*)(nxt + (wave + NW * j) * 1024), 16, 0,
+                                                 0);
+        }
+    }
+    if (i < 0) return;
+        // own copies of chunk i done (at most min(S-1, nb-1-i) later chunks in flight)
+        const int later = min(S - 1, nb - 1 - i);
+        if constexpr (S >= 4) {
+            if (later >= 3) wait_vmcnt<3 * G::PMIN>();
+            else if (later == 2) wait_vmcnt<2 * G::PMIN>();
+            else if (later == 1) wait_vmcnt<G::PMIN>();
+            else wait_vmcnt<0>();
+        } else {
+            if (later >= 2) wait_vmcnt<2 * G::PMIN>();
+            else if (later == 1) wait_vmcnt<G::PMIN>();
+            else wait_vmcnt<0>();
+        }
+        // every wave's copies of chunk i are in LDS (a bare barrier: the
+        // fence of __syncthreads would also wait for the later chunks)
+        __builtin_amdgcn_s_barrier();
+
+        const uint8_t* stg = cur;
+        const uint8_t* wl = stg + wrow;
+        const uint8_t* xl = stg + G::WB;
+        const float* dl = reinterpret_cast<const float*>(stg + G::WB + G::XB);
+        const float* gl = dl + 8 * TW;
+
+        // this lane's weight row (col of the wave's row tile): scales and mins
+        const uint4 h = *reinterpret_cast<const uint4*>(wl);
+        const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+        const uint32_t sc03 = h.y & 0x3f3f3f3fu;
+        const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+        v4f_t accb[G::WT];
+#pragma unroll
+        for (int w = 0; w < G::WT; w++) accb[w] = v4f_t{0.f, 0.f, 0.f, 0.f};
+        // sub-blocks of this wave's phase, the phase a compile-time constant
+        if (kph == 0) mfma_sub_blocks<G, 0>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
+        if constexpr (G::KS > 1) {
+            if (kph == 1) mfma_sub_blocks<G, 1>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
+        }
+        if constexpr (G::KS > 2) {
+            if (kph == 2) mfma_sub_blocks<G, 2>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
+            if (kph == 3) mfma_sub_blocks<G, 3>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
+        }
+#pragma unroll
+        for (int w = 0; w < G::WT; w++) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) acc[w][ii] = fmaf(d, accb[w][ii], acc[w][ii]);
+        }
+        if (kph == 0) {
+            // min term: A = dq*sum (token col, sub-blocks g / 4+g), B = dmin*m
+            // (weight row col, the same sub-blocks)
+            const uint32_t m03 = h.z & 0x3f3f3f3fu;
+            const uint32_t m47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+            const float am0 = dmin * (float)((m03 >> (8 * g)) & 0xffu);
+            const float am1 = dmin * (float)((m47 >> (8 * g)) & 0xffu);
+#pragma unroll
+            for (int w = 0; w < G::WT; w++) {
+                const int tok = kTile * (tt0 + w) + col;
+                macc[w] = __builtin_amdgcn_mfma_f32_16x16x4f32(gl[g * TW + tok], am0, macc[w], 0, 0, 0);
+                macc[w] = __builtin_amdgcn_mfma_f32_16x16x4f32(gl[(4 + g) * TW + tok], am1, macc[w], 0, 0, 0);
+            }
+        }
+        // stage u is free for chunk i + S (its reads were consumed above)
+        __builtin_amdgcn_s_barrier();
+}
+
+// Workgroup = NW waves on a (16*RT rows) x (16*TT tokens) tile; the K loop
+// streams one Q4_K block per step through an S-deep ring of LDS stages.
+// grid = (row tiles, token tiles); Tp % (16*TT) == 0.
+template <int RT, int TT, int NW, int S>
 __global__ __launch_bounds__(NW * 64) void k_gemm_mfma_q4k(
     float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ xs,
     const float* __restrict__ dxs, const float* __restrict__ gxs, int rows, int nb,
     long row_bytes, int T, int Tp) {
-    __shared__ v4f_t red[NW > 1 ? NW - 1 : 1][RT * TT][64];
+    using G = Stage<RT, TT, NW, S>;
+    constexpr int RW = G::RW, TW = G::TW;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[S * G::ALLOC];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, g = lane >> 4;
-    const int row_base = blockIdx.x * (kTile * RT);
-    const int tok_base = blockIdx.y * (kTile * TT);
-    // uniform bases + 32-bit lane offsets; rows past the end are computed on
-    // clamped (valid) data and never stored, token slots past T hold zeros
-    const uint8_t* wbase = W + (long)row_base * row_bytes;
-    uint32_t wo[RT];
-#pragma unroll
-    for (int r = 0; r < RT; r++)
-        wo[r] = (uint32_t)(min(row_base + kTile * r + col, rows - 1) - row_base) *
-                (uint32_t)row_bytes;
-    const uint32_t xo = (uint32_t)(tok_base + col) * 32u + 8u * (uint32_t)g;
-    const uint32_t kb_stride = (uint32_t)Tp * 32u;
+    const int row_base = blockIdx.x * RW;
+    const int tok_base = blockIdx.y * TW;
 
-    const v4i_t zi = {0, 0, 0, 0};
-    v4f_t acc[RT][TT], macc[RT][TT];
+    // ---- copy plan: per piece this lane's source (chunk 0) and its step per chunk
+    const uint8_t* src[G::PMAX];
+    uint32_t step[G::PMAX];
 #pragma unroll
-    for (int r = 0; r < RT; r++)
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-            acc[r][t] = v4f_t{0.f, 0.f, 0.f, 0.f};
-            macc[r][t] = v4f_t{0.f, 0.f, 0.f, 0.f};
-        }
-
-    for (int b = wave; b < nb; b += NW) {
-        uint4 h[RT];
-        uint32_t q[RT][4][2];
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const uint8_t* blk = wbase + (uint32_t)b * Q4K_BYTES + wo[r];
-            h[r] = ld16(blk);
-#pragma unroll
-            for (int p = 0; p < 4; p++) {
-                q[r][p][0] = ld4(blk + 16 + 32 * p + 8 * g);
-                q[r][p][1] = ld4(blk + 20 + 32 * p + 8 * g);
-            }
-        }
-        const uint8_t* xsb = xs + (size_t)b * 8 * kb_stride;
-        const float* dxb = dxs + (size_t)b * 8 * Tp + tok_base + col;
-        const float* gxb = gxs + (size_t)b * 8 * Tp + tok_base + col;
-        uint32_t xb[TT][8][2];
-        float dx[TT][8], gx[TT][2];
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-#pragma unroll
-            for (int s = 0; s < 8; s++) {
-                const uint8_t* xp = xsb + s * kb_stride + xo + t * (kTile * 32);
-                xb[t][s][0] = ld4(xp);
-                xb[t][s][1] = ld4(xp + 4);
-                dx[t][s] = dxb[s * Tp + t * kTile];
-            }
-            gx[t][0] = gxb[g * Tp + t * kTile];
-            gx[t][1] = gxb[(4 + g) * Tp + t * kTile];
-        }
-        // all of the block's loads are in flight before the first use
-        __builtin_amdgcn_sched_barrier(0);
-
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            // this lane's weight row (col of tile r): 6-bit scales and mins
-            const float d = h2f(h[r].x & 0xffffu), dmin = h2f(h[r].x >> 16);
-            const uint32_t sc03 = h[r].y & 0x3f3f3f3fu;
-            const uint32_t sc47 = (h[r].w & 0x0f0f0f0fu) | ((h[r].y >> 2) & 0x30303030u);
-            const uint32_t m03 = h[r].z & 0x3f3f3f3fu;
-            const uint32_t m47 = ((h[r].w >> 4) & 0x0f0f0f0fu) | ((h[r].z >> 2) & 0x30303030u);
-            // min-term A operand: row col, sub-blocks g and 4+g
-            const float am0 = dmin * (float)((m03 >> (8 * g)) & 0xffu);
-            const float am1 = dmin * (float)((m47 >> (8 * g)) & 0xffu);
-            // result-side scales: rows 4g+i live in lanes 4g+i
-            uint32_t rs03[4], rs47[4];
-            float rd[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int src = 4 * g + i;
-                rs03[i] = (uint32_t)__shfl((int)sc03, src);
-                rs47[i] = (uint32_t)__shfl((int)sc47, src);
-                rd[i] = __shfl(d, src);
-            }
-#pragma unroll
-            for (int t = 0; t < TT; t++) {
-                v4f_t accb = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < 8; s++) {
-                    const uint32_t* qp = q[r][s >> 1];
-                    const int sh = (s & 1) * 4;
-                    const long a =
-                        pack2((qp[0] >> sh) & 0x0f0f0f0fu, (qp[1] >> sh) & 0x0f0f0f0fu);
-                    const long bx = pack2(xb[t][s][0], xb[t][s][1]);
-                    const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bx, zi, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        // |S| < 2^17 and sc < 64: the 24-bit multiply is exact
-                        const int scv =
-                            (int)(((s < 4 ? rs03[i] : rs47[i]) >> (8 * (s & 3))) & 0xffu);
-                        accb[i] = fmaf((float)__mul24(c[i], scv), dx[t][s], accb[i]);
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[r][t][i] = fmaf(rd[i], accb[i], acc[r][t][i]);
-                macc[r][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(am0, gx[t][0], macc[r][t], 0, 0, 0);
-                macc[r][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(am1, gx[t][1], macc[r][t], 0, 0, 0);
-            }
+    for (int j = 0; j < G::PMAX; j++) {
+        int o = (wave + NW * j) * 1024 + lane * 16;
+        if (o >= G::BYTES) o = 0;  // tail of the last piece: a harmless duplicate
+        if (o < G::WB) {
+            const int r = o / Q4K_BYTES;
+            src[j] = W + (long)min(row_base + r, rows - 1) * row_bytes + (o - r * Q4K_BYTES);
+            step[j] = Q4K_BYTES;
+        } else if (o < G::WB + G::XB) {
+            const int x = o - G::WB, k = x / (TW * 32);
+            src[j] = xs + ((size_t)k * Tp + tok_base) * 32 + (x - k * TW * 32);
+            step[j] = 8u * (uint32_t)Tp * 32u;
+        } else {
+            const int y = o - G::WB - G::XB;
+            const int which = y / G::DB, z = y - which * G::DB, k = z / (TW * 4);
+            const float* base = which == 0 ? dxs : gxs;
+            src[j] = reinterpret_cast<const uint8_t*>(base + (size_t)k * Tp + tok_base) +
+                     (z - k * TW * 4);
+            step[j] = 8u * (uint32_t)Tp * 4u;
         }
     }
+    // ---- this wave's tiles and sub-blocks
+    const int tg = wave % (NW / G::KS);     // tile group
+    const int kph = wave / (NW / G::KS);    // sub-block phase
+    const int t0 = tg * G::WT;              // first tile (tile = rt*TT + tt)
+    const int rt = t0 / TT, tt0 = t0 % TT;
+    const int wrow = (kTile * rt + col) * Q4K_BYTES;
 
+    v4f_t acc[G::WT], macc[G::WT];
 #pragma unroll
-    for (int r = 0; r < RT; r++)
+    for (int w = 0; w < G::WT; w++) {
+        acc[w] = v4f_t{0.f, 0.f, 0.f, 0.f};
+        macc[w] = v4f_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // Step i copies chunk i+S-1 and (from i = 0) computes chunk i.  Every
+    // copy is issued by the same instruction inside gemm_step, whose stage
+    // pointers are __restrict__: the copy target and the stage being read are
+    // distinct, so the compiler adds no wait for the copies in flight before
+    // the LDS reads; the explicit vmcnt wait orders chunk i itself.
+    for (int i = 1 - S; i < nb; i++) {
+        const int inext = i + S - 1;
+        gemm_step<RT, TT, NW, S>(smem + ((i + S) % S) * G::ALLOC, smem + (inext % S) * G::ALLOC,
+                                 inext < nb, inext, i, nb, src, step, wave, lane, col, g, kph,
+                                 tt0, wrow, acc, macc);
+    }
+
+    // ---- sum the KS sub-block phases of each tile (fixed order), store
+    v4f_t* red = reinterpret_cast<v4f_t*>(smem);
+    if constexpr (G::KS > 1) {
+        if (kph > 0) {
 #pragma unroll
-        for (int t = 0; t < TT; t++) {
-            acc[r][t] -= macc[r][t];
-            if (NW > 1 && wave > 0) red[wave - 1][r * TT + t][lane] = acc[r][t];
+            for (int w = 0; w < G::WT; w++)
+                red[((kph - 1) * (NW / G::KS) + tg) * G::WT * 64 + w * 64 + lane] = acc[w] - macc[w];
         }
-    if (NW > 1) __syncthreads();
-    if (wave == 0) {
+        __syncthreads();
+    }
+    if (kph == 0) {
 #pragma unroll
-        for (int r = 0; r < RT; r++)
+        for (int w = 0; w < G::WT; w++) {
+            v4f_t v = acc[w] - macc[w];
 #pragma unroll
-            for (int t = 0; t < TT; t++) {
-                v4f_t v = acc[r][t];
+            for (int k = 1; k < G::KS; k++) v += red[((k - 1) * (NW / G::KS) + tg) * G::WT * 64 + w * 64 + lane];
+            const int o = row_base + kTile * rt + col;
+            if (o < rows) {
 #pragma unroll
-                for (int w = 0; w < NW - 1; w++) v += red[w][r * TT + t][lane];
-                const int tok = tok_base + kTile * t + col;
-                if (tok < T) {
-                    float* yr = Y + (size_t)tok * rows;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int o = row_base + kTile * r + 4 * g + i;
-                        if (o < rows) yr[o] = v[i];
-                    }
+                for (int ii = 0; ii < 4; ii++) {
+                    const int tok = tok_base + kTile * (tt0 + w) + 4 * g + ii;
+                    if (tok < T) Y[(size_t)tok * rows + o] = v[ii];
                 }
             }
+        }
     }
 }
 
 struct MfmaCfg {
-    int nw, rt, tt;
+    int rt, tt;
 };
 
 MfmaCfg pick_mfma(int T, int nb) {
-    const int nw = nb >= 8 ? 8 : 4;
-    return {nw, 2, T > kTile ? 2 : 1};
+    (void)nb;
+    if (T <= 16) return {2, 1};
+    return {2, T > 32 ? 4 : 2};
 }
 
 int padded_tokens(int T, const MfmaCfg& c) {
@@ -233,14 +362,14 @@ int padded_tokens(int T, const MfmaCfg& c) {
     return (T + q - 1) / q * q;
 }
 
-template <int NW, int RT, int TT>
+template <int RT, int TT, int NW, int S>
 void launch_cfg(float* Y, const uint8_t* W, const uint8_t* xs, const float* dxs,
                 const float* gxs, int rows, int nb, long row_bytes, int T, int Tp,
                 hipStream_t st) {
     const dim3 grid((unsigned)((rows + kTile * RT - 1) / (kTile * RT)),
                     (unsigned)(Tp / (kTile * TT)));
-    hipLaunchKernelGGL((k_gemm_mfma_q4k<NW, RT, TT>), grid, dim3(NW * 64), 0, st, Y, W, xs, dxs,
-                       gxs, rows, nb, row_bytes, T, Tp);
+    hipLaunchKernelGGL((k_gemm_mfma_q4k<RT, TT, NW, S>), grid, dim3(NW * 64), 0, st, Y, W, xs,
+                       dxs, gxs, rows, nb, row_bytes, T, Tp);
 }
 
 }  // namespace
@@ -269,14 +398,13 @@ hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int
     hipLaunchKernelGGL(k_gemm_prep, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        static_cast<const uint8_t*>(XQ8), T, Tp, nkb, xs, dxs, gxs);
     const auto* w = static_cast<const uint8_t*>(W);
-#define AXF_MFMA_CASE(NW, RT, TT)                                                          \
-    if (c.nw == NW && c.rt == RT && c.tt == TT)                                            \
-        launch_cfg<NW, RT, TT>(Y, w, xs, dxs, gxs, rows, nb, row_bytes, T, Tp, st);        \
+#define AXF_MFMA_CASE(RT, TT, NW, S)                                                       \
+    if (c.rt == RT && c.tt == TT)                                                          \
+        launch_cfg<RT, TT, NW, S>(Y, w, xs, dxs, gxs, rows, nb, row_bytes, T, Tp, st);     \
     else
-    AXF_MFMA_CASE(8, 2, 2)
-    AXF_MFMA_CASE(8, 2, 1)
-    AXF_MFMA_CASE(4, 2, 2)
-    AXF_MFMA_CASE(4, 2, 1)
+    AXF_MFMA_CASE(2, 1, 4, 4)
+    AXF_MFMA_CASE(2, 2, 4, 4)
+    AXF_MFMA_CASE(2, 4, 8, 3)
     return hipErrorInvalidValue;
 #undef AXF_MFMA_CASE
     return hipGetLastError();
