@@ -107,6 +107,11 @@ int axf_hip_gemv_q6k_q8(axf_ctx* ctx, float* y, const void* W, const void* xq8, 
  * block t*(cols/32). */
 int axf_hip_gemm_q4k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
                         int T, int cols, size_t row_bytes);
+/* Batched Q6_K x Q8_0: Y[t*rows + o] = W[o,:] . XQ8[t,:], token-major; replaces
+ * the per-token gemv_q6k_q8_avx2_range loop of gemm_wt_q8 for Q6_K weights
+ * (llama_model.cpp:860-873). */
+int axf_hip_gemm_q6k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
+                        int T, int cols, size_t row_bytes);
 /* The same GEMM with the kernel chosen explicitly (no reference counterpart;
  * for tests and measurement): path 0 automatic (matrix cores from 8 tokens up),
  * 1 the dot4 kernel, 2 the matrix-core (int8 MFMA) kernel.  Results of the two
@@ -215,11 +220,27 @@ int axf_llama_get_logits(axf_llama* m, float* logits);
 int axf_llama_forward_layer(axf_llama* m, int layer, int pos);
 /* Full single-token forward (embedding .. logits), eager. */
 int axf_llama_forward_token(axf_llama* m, int token, int pos);
-/* Greedy generation: token-by-token prefill of the prompt, then n_gen tokens
- * (greedy loop of llama_generate_cpu_impl, llama_model.cpp:1595-1624, without
- * EOS).  use_graph != 0 replays one captured HIP graph per step. */
+/* Batched prefill: replaces llama_forward_batch (llama_model.cpp:1339-1462).
+ * Runs tokens[0..T) at positions pos_start..pos_start+T-1 (K/V rows written),
+ * Q4_K projections as T-token GEMMs, Q6_K ones with the multi-token kernel,
+ * causal attention per row; leaves the last row's logits (get_logits) and,
+ * as the reference leaves s.x, that row after the final RMSNorm (get_x).
+ * Long prompts run in chunks of up to 256 tokens. */
+int axf_llama_forward_batch(axf_llama* m, const int32_t* tokens, int T, int pos_start);
+/* Greedy generation (greedy loop of llama_generate_cpu_impl,
+ * llama_model.cpp:1568-1624, without EOS): the prompt is prefilled as one batch
+ * when n_prompt > 1 (as the reference does), then n_gen tokens are decoded.
+ * use_graph != 0 replays one captured HIP graph per decode step. */
 int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_gen,
                        int32_t* out_tokens, int use_graph);
+/* As axf_llama_generate; batched_prefill == 0 prefills token by token (the
+ * llama_forward_token path) instead. */
+int axf_llama_generate_ex(axf_llama* m, const int32_t* prompt, int n_prompt, int n_gen,
+                          int32_t* out_tokens, int use_graph, int batched_prefill);
+/* Benchmark helper (no reference counterpart): mean milliseconds of `reps`
+ * axf_llama_forward_batch calls on T synthetic tokens at positions 0..T-1,
+ * after one untimed call (HIP events on the context stream). */
+int axf_llama_bench_prefill(axf_llama* m, int T, int reps, float* ms);
 /* Time `steps` graph-replayed decode steps, each at position `pos` (the
  * attention reads KV rows 0..pos; rows below pos must already be filled, row
  * pos is rewritten by every step), after `warmup` untimed steps; each step

@@ -73,6 +73,7 @@ SIGNATURES: dict[str, list] = {
     "axf_hip_gemv_q6k_q8": [vp, vp, vp, vp, i32, i32, sz, i32],
     "axf_hip_gemm_q4k_q8": [vp, vp, vp, vp, i32, i32, i32, sz],
     "axf_hip_gemm_q4k_q8_path": [vp, vp, vp, vp, i32, i32, i32, sz, i32],
+    "axf_hip_gemm_q6k_q8": [vp, vp, vp, vp, i32, i32, i32, sz],
     "axf_hip_argmax_f32": [vp, vp, vp, i32],
     "axf_hip_rmsnorm": [vp, vp, vp, vp, vp, i32, f32],
     "axf_rope_table": [vp, vp, i32, f32, i32],
@@ -103,6 +104,9 @@ SIGNATURES: dict[str, list] = {
     "axf_llama_forward_layer": [vp, i32, i32],
     "axf_llama_forward_token": [vp, i32, i32],
     "axf_llama_generate": [vp, vp, i32, i32, vp, i32],
+    "axf_llama_generate_ex": [vp, vp, i32, i32, vp, i32, i32],
+    "axf_llama_forward_batch": [vp, vp, i32, i32],
+    "axf_llama_bench_prefill": [vp, i32, i32, C.POINTER(f32)],
     "axf_llama_bench_decode": [vp, i32, i32, i32, C.POINTER(f32)],
 }
 

@@ -282,6 +282,17 @@ int axf_hip_gemm_q4k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, 
     return do_gemm(ctx, __func__, Y, W, XQ8, rows, T, cols, row_bytes, 0);
 }
 
+int axf_hip_gemm_q6k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows, int T,
+                        int cols, size_t row_bytes) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(T >= 0, "negative T");
+    int rc = check_gemv(__func__, AXF_TYPE_Q6_K, W, XQ8, Y, rows, cols, row_bytes, false);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0 || T == 0) return AXF_OK;
+    AXF_HIP(launch_gemm_q6k_q8(Y, W, XQ8, rows, T, cols / QK_K, (long)row_bytes, ctx->stream));
+    return AXF_OK;
+}
+
 int axf_hip_gemm_q4k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
                              int T, int cols, size_t row_bytes, int path) {
     return do_gemm(ctx, __func__, Y, W, XQ8, rows, T, cols, row_bytes, path);

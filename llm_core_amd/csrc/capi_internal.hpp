@@ -71,6 +71,9 @@ size_t gemm_scratch_bytes(GemmPath path, int T, int nb);
 hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
                               long row_bytes, GemmPath path, void* scratch, hipStream_t st);
 size_t gemm_mfma_scratch_bytes(int T, int nb);
+// Q6_K x Q8_0 for T tokens (dot4; weights decoded once per token tile), Y token-major.
+hipError_t launch_gemm_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
+                              long row_bytes, hipStream_t st);
 hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
                                    int nb, long row_bytes, void* scratch, hipStream_t st);
 hipError_t launch_dequant_q4k(float* y, const void* W, long nblocks, hipStream_t st);
@@ -78,6 +81,16 @@ hipError_t launch_dequant_q6k(float* y, const void* W, long nblocks, hipStream_t
 hipError_t launch_quantize_q8_0(void* y, const float* x, int n, hipStream_t st);
 hipError_t launch_rmsnorm(float* y, void* yq8, const float* x, const float* w, int n, float eps,
                           hipStream_t st);
+// rows independent RMSNorms of [rows][n] (same arithmetic as launch_rmsnorm)
+hipError_t launch_rmsnorm_rows(float* y, void* yq8, const float* x, const float* w, int n,
+                               float eps, int rows, hipStream_t st);
+hipError_t launch_rope_kv_rows(const float* k, int k_ld, const float* v, int v_ld,
+                               const float* bk, const float* bv, float* kcache, float* vcache,
+                               int pos0, int T, int n_kv_heads, int hd, const float* cos_t,
+                               const float* sin_t, hipStream_t st);
+hipError_t launch_swiglu_gu(void* outq8, const float* gu, int T, int n, int B, hipStream_t st);
+hipError_t launch_embed_rows(int qtype, float* out, const void* W, const int* toks_dev, int T,
+                             int nb, long row_bytes, hipStream_t st);
 hipError_t launch_rope(float* dst, const float* src, const int* pos_dev, int pos, int n_heads,
                        int hd, const float* cos_t, const float* sin_t, hipStream_t st);
 hipError_t launch_rope_qkv(float* q, const float* k, const float* v, float* kcache,
@@ -100,9 +113,12 @@ struct AttnArgs {
     int pos;             // current position: attention over rows 0..pos
     int n_heads, n_kv_heads, nsplit;
     int store_kv;        // write RoPE(k+bk) and v+bv to cache row pos
-    float* part;         // [H][nsplit][HD + 2]
-    float* out;          // [H*HD]
+    float* part;         // [n_tok][H][nsplit][HD + 2]
+    float* out;          // [H*HD] (row t at out + t*out_ld)
     uint8_t* outq8;      // Q8_0 blocks of out, or nullptr
+    // Batched prefill: n_tok query rows (0 means 1), row t at q + t*q_ld, at
+    // position pos + t, attending to cache rows 0..pos+t (store_kv must be 0).
+    int n_tok, q_ld, out_ld;
 };
 int attn_nsplit(int max_seq);
 hipError_t launch_attention_fused(const AttnArgs& a, int head_dim, hipStream_t st);

@@ -85,6 +85,13 @@ struct axf_llama {
     int *d_token = nullptr, *d_pos = nullptr, *d_step = nullptr, *d_tokens = nullptr;
     int max_tokens = 0;
 
+    // batched prefill buffers, allocated on first use for chunks of pf_cap tokens
+    int pf_cap = 0;
+    int* pf_tok = nullptr;
+    float *pf_x = nullptr, *pf_qk = nullptr, *pf_v = nullptr, *pf_ao = nullptr, *pf_tmp = nullptr,
+          *pf_gu = nullptr, *pf_part = nullptr;
+    uint8_t *pf_q8 = nullptr, *pf_gemm = nullptr;
+
     // graph[0]: generation step (records the token, advances the position);
     // graph[1]: fixed-position step used to time decode at a given context
     hipGraph_t graph[2] = {nullptr, nullptr};
@@ -354,6 +361,168 @@ hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, boo
                          (device_state && record) ? m->d_pos : nullptr, st);
 }
 
+// ---------------------------------------------------------------------------
+// Batched prefill (llama_forward_batch, src/models/llama_model.cpp:1339-1462):
+// per layer, for a chunk of T tokens at positions pos0 .. pos0+T-1,
+//   RMSNorm rows -> Q8_0; q|k, v projections as T-token GEMMs (Q4_K on the
+//   matrix cores, Q6_K with the dot4 kernel; the reference runs Q6_K per
+//   token, gemm_wt_q8 :860-873); K (+bias, RoPE) and V (+bias) of every row
+//   into the cache; causal attention of every row (q bias and RoPE inside);
+//   o GEMM, x += o; RMSNorm rows -> Q8_0; gate|up GEMM, SwiGLU -> Q8_0;
+//   down GEMM, x += down.
+// Long prompts run as consecutive chunks; every row's arithmetic depends only
+// on its own activations and the cache rows before it, so chunking does not
+// change any result.  After the last chunk: the head of the last row.
+// ---------------------------------------------------------------------------
+int prefill_alloc(axf_llama* m) {
+    if (m->pf_cap) return AXF_OK;
+    const auto& hp = m->hp;
+    const int E = hp.n_embd, FD = hp.ffn_dim, qo = hp.n_heads * m->hd, kvo = m->kv_embd;
+    // chunk: up to 256 tokens, the attention partials within 256 MiB
+    const size_t part_per_tok = (size_t)hp.n_heads * m->nsplit * (m->hd + 2) * 4;
+    int cap = 256;
+    while (cap > 16 && (size_t)cap * part_per_tok > ((size_t)256 << 20)) cap /= 2;
+    if (cap > hp.n_ctx) cap = hp.n_ctx;
+    const size_t C = (size_t)cap;
+    const int kmax = E > FD ? E : FD;
+    void* p;
+    LL_TRY(dalloc(m, C * 4, &p));
+    m->pf_tok = static_cast<int*>(p);
+    LL_TRY(dalloc(m, C * E * 4, &p));
+    m->pf_x = static_cast<float*>(p);
+    LL_TRY(dalloc(m, C * (qo + kvo) * 4, &p));
+    m->pf_qk = static_cast<float*>(p);
+    LL_TRY(dalloc(m, C * kvo * 4, &p));
+    m->pf_v = static_cast<float*>(p);
+    LL_TRY(dalloc(m, C * qo * 4, &p));
+    m->pf_ao = static_cast<float*>(p);
+    LL_TRY(dalloc(m, C * (E > qo ? E : qo) * 4, &p));
+    m->pf_tmp = static_cast<float*>(p);
+    LL_TRY(dalloc(m, C * 2 * FD * 4, &p));
+    m->pf_gu = static_cast<float*>(p);
+    LL_TRY(dalloc(m, C * part_per_tok, &p));
+    m->pf_part = static_cast<float*>(p);
+    LL_TRY(dalloc(m, C * (kmax > qo ? kmax : qo) / 32 * Q8_0_BYTES, &p));
+    m->pf_q8 = static_cast<uint8_t*>(p);
+    const size_t gs = gemm_scratch_bytes(GemmPath::Auto, cap, kmax / QK_K);
+    LL_TRY(dalloc(m, gs > 16 ? gs : 16, &p));
+    m->pf_gemm = static_cast<uint8_t*>(p);
+    m->pf_cap = cap;
+    return AXF_OK;
+}
+
+// Y[T][rows] = W * XQ8 rows (token-major), by weight type
+hipError_t gemm_rows(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, int rows, int T,
+                     int cols, hipStream_t st) {
+    if (w.qtype == AXF_TYPE_Q4_K)
+        return launch_gemm_q4k_q8(Y, w.d, xq8, rows, T, cols / QK_K, (long)w.row_bytes,
+                                  GemmPath::Auto, m->pf_gemm, st);
+    return launch_gemm_q6k_q8(Y, w.d, xq8, rows, T, cols / QK_K, (long)w.row_bytes, st);
+}
+
+hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
+    const auto& hp = m->hp;
+    const int E = hp.n_embd, H = hp.n_heads, KVH = hp.n_kv_heads, HD = m->hd, FD = hp.ffn_dim;
+    const int qo = H * HD, kvo = KVH * HD;
+    hipStream_t st = m->ctx->stream;
+    const Layer& L = m->layers[l];
+    const size_t loff = (size_t)l * hp.n_ctx * m->kv_embd;
+    hipError_t e;
+#define ST(call)               \
+    if ((e = (call)) != hipSuccess) return e;
+    // q|k and v projections of RMSNorm(x) * attn_norm
+    ST(launch_rmsnorm_rows(nullptr, m->pf_q8, m->pf_x, L.attn_norm, E, hp.rms_eps, T, st));
+    float* q = m->pf_qk;
+    float* k;
+    int q_ld, k_ld;
+    if (L.qk_fused) {
+        ST(gemm_rows(m, L.wq, q, m->pf_q8, qo + kvo, T, E, st));
+        k = q + qo;
+        q_ld = k_ld = qo + kvo;
+    } else {
+        k = q + (size_t)T * qo;
+        q_ld = qo;
+        k_ld = kvo;
+        ST(gemm_rows(m, L.wq, q, m->pf_q8, qo, T, E, st));
+        ST(gemm_rows(m, L.wk, k, m->pf_q8, kvo, T, E, st));
+    }
+    ST(gemm_rows(m, L.wv, m->pf_v, m->pf_q8, kvo, T, E, st));
+    // K, V rows into the cache, then attention of every row -> Q8_0
+    ST(launch_rope_kv_rows(k, k_ld, m->pf_v, kvo, L.bk, L.bv, m->kv_k + loff, m->kv_v + loff,
+                           pos0, T, KVH, HD, m->rope_cos, m->rope_sin, st));
+    {
+        AttnArgs a{};
+        a.q = q;
+        a.bq = L.bq;
+        a.cos_t = m->rope_cos;
+        a.sin_t = m->rope_sin;
+        a.kcache = m->kv_k + loff;
+        a.vcache = m->kv_v + loff;
+        a.pos = pos0;
+        a.n_heads = H;
+        a.n_kv_heads = KVH;
+        a.nsplit = m->nsplit;
+        a.store_kv = 0;
+        a.part = m->pf_part;
+        a.out = m->pf_ao;
+        a.outq8 = m->pf_q8;
+        a.n_tok = T;
+        a.q_ld = q_ld;
+        a.out_ld = qo;
+        ST(launch_attention_fused(a, HD, st));
+    }
+    // x += o
+    ST(gemm_rows(m, L.wo, m->pf_tmp, m->pf_q8, E, T, qo, st));
+    ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
+    // SwiGLU(gate, up) of RMSNorm(x) * ffn_norm -> Q8_0
+    ST(launch_rmsnorm_rows(nullptr, m->pf_q8, m->pf_x, L.ffn_norm, E, hp.rms_eps, T, st));
+    if (L.gu_interleaved) {
+        ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, 2 * FD, T, E, st));
+        const int B = qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2;
+        ST(launch_swiglu_gu(m->pf_q8, m->pf_gu, T, FD, B, st));
+    } else {
+        ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, FD, T, E, st));
+        ST(gemm_rows(m, L.wup, m->pf_gu + (size_t)T * FD, m->pf_q8, FD, T, E, st));
+        ST(launch_swiglu(nullptr, m->pf_q8, m->pf_gu, m->pf_gu + (size_t)T * FD, T * FD, st));
+    }
+    // x += down
+    ST(gemm_rows(m, L.wdown, m->pf_tmp, m->pf_q8, E, T, FD, st));
+    ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
+#undef ST
+    return hipSuccess;
+}
+
+// Tokens already on the device in pf_tok; logits of the last row when `head`.
+int enqueue_prefill_chunk(axf_llama* m, int T, int pos0, bool head) {
+    const auto& hp = m->hp;
+    hipStream_t st = m->ctx->stream;
+    LL_HIP(launch_embed_rows(m->tok_embd.qtype, m->pf_x, m->tok_embd.d, m->pf_tok, T,
+                             hp.n_embd / QK_K, (long)m->tok_embd.row_bytes, st));
+    for (int l = 0; l < hp.n_layer; l++) LL_HIP(enqueue_prefill_layer(m, l, T, pos0));
+    if (head) {
+        const float* xl = m->pf_x + (size_t)(T - 1) * hp.n_embd;
+        LL_HIP(gemv_norm(m->output, m->logits, xl, m->output_norm, hp.rms_eps, hp.n_vocab,
+                         hp.n_embd, false, st));
+        // x = the last row after the final norm, as llama_forward_batch leaves s.x
+        // (its in-place rms_norm_avx2 before the copy, :1452-1461)
+        LL_HIP(launch_rmsnorm(m->x, nullptr, xl, m->output_norm, hp.n_embd, hp.rms_eps, st));
+    }
+    return AXF_OK;
+}
+
+int forward_batch(axf_llama* m, const int32_t* tokens, int T, int pos0) {
+    LL_TRY(prefill_alloc(m));
+    hipStream_t st = m->ctx->stream;
+    for (int c0 = 0; c0 < T; c0 += m->pf_cap) {
+        const int n = T - c0 < m->pf_cap ? T - c0 : m->pf_cap;
+        LL_HIP(hipMemcpyAsync(m->pf_tok, tokens + c0, (size_t)n * 4, hipMemcpyHostToDevice, st));
+        LL_TRY(enqueue_prefill_chunk(m, n, pos0 + c0, c0 + n == T));
+        // the host token buffer of the next chunk reuses pf_tok
+        LL_HIP(hipStreamSynchronize(st));
+    }
+    return AXF_OK;
+}
+
 // kind 0: generation step; kind 1: fixed-position step (no token record, no pos advance)
 int ensure_graph(axf_llama* m, int kind) {
     if (m->exec[kind]) return AXF_OK;
@@ -587,8 +756,46 @@ int axf_llama_forward_token(axf_llama* m, int token, int pos) {
     return AXF_OK;
 }
 
+int axf_llama_forward_batch(axf_llama* m, const int32_t* tokens, int T, int pos_start) {
+    LL_LOADED(m);
+    if (!tokens || T <= 0 || pos_start < 0 || pos_start + T > m->hp.n_ctx)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_forward_batch: bad tokens/positions");
+    for (int i = 0; i < T; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->hp.n_vocab)
+            return fail(AXF_ERR_INVALID_ARG, "axf_llama_forward_batch: token out of range");
+    LL_TRY(forward_batch(m, tokens, T, pos_start));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    return AXF_OK;
+}
+
+int axf_llama_bench_prefill(axf_llama* m, int T, int reps, float* ms) {
+    LL_LOADED(m);
+    if (!ms || T <= 0 || T > m->hp.n_ctx || reps <= 0)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_bench_prefill: bad arguments");
+    std::vector<int32_t> toks(T);
+    for (int i = 0; i < T; i++) toks[i] = (int32_t)((1 + 7 * (int64_t)i) % m->hp.n_vocab);
+    LL_TRY(forward_batch(m, toks.data(), T, 0));  // warm-up (allocations, code)
+    float total = 0.f;
+    for (int r = 0; r < reps; r++) {
+        LL_HIP(hipEventRecord(m->ctx->ev0, m->ctx->stream));
+        LL_TRY(forward_batch(m, toks.data(), T, 0));
+        LL_HIP(hipEventRecord(m->ctx->ev1, m->ctx->stream));
+        LL_HIP(hipEventSynchronize(m->ctx->ev1));
+        float t = 0.f;
+        LL_HIP(hipEventElapsedTime(&t, m->ctx->ev0, m->ctx->ev1));
+        total += t;
+    }
+    *ms = total / (float)reps;
+    return AXF_OK;
+}
+
 int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_gen,
                        int32_t* out_tokens, int use_graph) {
+    return axf_llama_generate_ex(m, prompt, n_prompt, n_gen, out_tokens, use_graph, 1);
+}
+
+int axf_llama_generate_ex(axf_llama* m, const int32_t* prompt, int n_prompt, int n_gen,
+                          int32_t* out_tokens, int use_graph, int batched_prefill) {
     LL_LOADED(m);
     if (!prompt || n_prompt <= 0 || n_gen < 0 || (n_gen && !out_tokens))
         return fail(AXF_ERR_INVALID_ARG, "axf_llama_generate: bad arguments");
@@ -602,13 +809,22 @@ int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_
     LL_HIP(launch_set_int(m->d_step, 0, st));
     LL_HIP(launch_set_int(m->d_pos, 0, st));
     if (use_graph) LL_TRY(ensure_graph(m, 0));
-    // prefill token by token; the argmax of the last prompt step is token 0
-    for (int t = 0; t < n_prompt; t++) {
-        LL_HIP(launch_set_int(m->d_token, prompt[t], st));
-        if (use_graph)
-            LL_HIP(hipGraphLaunch(m->exec[0], st));
-        else
-            LL_HIP(enqueue_step(m, true, 0, 0, true));
+    if (batched_prefill && n_prompt > 1) {
+        // llama_generate_cpu_impl (:1568-1576): one batch for the whole prompt;
+        // the argmax of its last row is token 0, decoding continues at n_prompt
+        LL_TRY(forward_batch(m, prompt, n_prompt, 0));
+        LL_HIP(launch_argmax(m->d_token, m->arg_v, m->arg_i, m->logits, m->hp.n_vocab, nullptr,
+                             nullptr, nullptr, st));
+        LL_HIP(launch_set_int(m->d_pos, n_prompt, st));
+    } else {
+        // prefill token by token; the argmax of the last prompt step is token 0
+        for (int t = 0; t < n_prompt; t++) {
+            LL_HIP(launch_set_int(m->d_token, prompt[t], st));
+            if (use_graph)
+                LL_HIP(hipGraphLaunch(m->exec[0], st));
+            else
+                LL_HIP(enqueue_step(m, true, 0, 0, true));
+        }
     }
     LL_HIP(launch_set_int(m->d_step, 0, st));
     if (n_gen > 0) LL_HIP(launch_push_token(m->d_tokens, m->d_step, m->d_token, st));

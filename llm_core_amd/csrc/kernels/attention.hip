@@ -98,9 +98,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     __shared__ float stat[GM][2];
 
     // kv head fastest: workgroups dispatched together read adjacent bytes of each KV row
-    const int kvh = blockIdx.x, j = blockIdx.y;
+    const int kvh = blockIdx.x, j = blockIdx.y, tok = blockIdx.z;
     const int G = a.n_heads / a.n_kv_heads;
-    const int p = a.pos_dev ? *a.pos_dev : a.pos;
+    const int p = (a.pos_dev ? *a.pos_dev : a.pos) + tok;
+    // query row tok and its partials (tok > 0 only in batched prefill)
+    const float* qp = a.q + (size_t)tok * a.q_ld;
+    float* part = a.part + (size_t)tok * a.n_heads * a.nsplit * (HD + 2);
     const int t0 = j * kAttnSplit;
     if (t0 > p) return;  // split past the current position: nothing to do
     const int n = min(kAttnSplit, p + 1 - t0);
@@ -120,15 +123,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     for (int k = 0; k < QPT; k++) {
         const int t = min(tid + k * kAttnThreads, G * HD - 1);
         const size_t e = ((size_t)kvh * G + t / HD) * HD + t % HD;
-        qraw[k] = a.q[e];
-        qb[k] = (a.bq ? a.bq : a.q)[e];
+        qraw[k] = qp[e];
+        qb[k] = (a.bq ? a.bq : qp)[e];
     }
     const int d1 = min(tid, HD - 1);
     const size_t e1 = (size_t)kvh * HD + d1;  // < n_kv_heads * HD <= n_heads * HD
-    const float kk = (a.store_kv ? a.k : a.q)[e1];
-    const float vv = (a.store_kv ? a.v : a.q)[e1];
-    const float kb = (a.bk ? a.bk : a.q)[e1];
-    const float vb = (a.bv ? a.bv : a.q)[e1];
+    const float kk = (a.store_kv ? a.k : qp)[e1];
+    const float vv = (a.store_kv ? a.v : qp)[e1];
+    const float kb = (a.bk ? a.bk : qp)[e1];
+    const float vb = (a.bv ? a.bv : qp)[e1];
     const int d2 = min(tid, HD / 2 - 1);
     const float cv = a.cos_t ? a.cos_t[(size_t)p * (HD / 2) + d2] : 0.f;
     const float sv = a.cos_t ? a.sin_t[(size_t)p * (HD / 2) + d2] : 0.f;
@@ -243,10 +246,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
         float acc = ov[0][t];
 #pragma unroll
         for (int w = 1; w < kAttnWaves; w++) acc += ov[w][t];
-        a.part[((size_t)(kvh * G + g) * a.nsplit + j) * (HD + 2) + 2 + d] = acc;
+        part[((size_t)(kvh * G + g) * a.nsplit + j) * (HD + 2) + 2 + d] = acc;
     }
     if (threadIdx.x < G) {
-        float* dst = a.part + ((size_t)(kvh * G + threadIdx.x) * a.nsplit + j) * (HD + 2);
+        float* dst = part + ((size_t)(kvh * G + threadIdx.x) * a.nsplit + j) * (HD + 2);
         dst[0] = stat[threadIdx.x][0];
         dst[1] = stat[threadIdx.x][1];
     }
@@ -265,10 +268,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(AttnArgs a) {
     __shared__ float4 accs[NJS][C4];
     __shared__ float ms[NJS], ls[NJS];
 
-    const int h = blockIdx.x;
-    const int p = a.pos_dev ? *a.pos_dev : a.pos;
+    const int h = blockIdx.x, tok = blockIdx.y;
+    const int p = (a.pos_dev ? *a.pos_dev : a.pos) + tok;
     const int ns = p / kAttnSplit + 1;  // non-empty splits
-    const float* ph = a.part + (size_t)h * a.nsplit * (HD + 2);
+    const float* ph = a.part + ((size_t)tok * a.n_heads + h) * a.nsplit * (HD + 2);
     const int c = threadIdx.x % C4, js = threadIdx.x / C4;
 
     float m = -INFINITY, l = 0.f;
@@ -326,14 +329,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(AttnArgs a) {
         }
         const float inv = 1.f / L;
         o = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
-        float* dst = a.out + (size_t)h * HD + 4 * c;
+        float* dst = a.out + (size_t)tok * a.out_ld + (size_t)h * HD + 4 * c;
         dst[0] = o.x;
         dst[1] = o.y;
         dst[2] = o.z;
         dst[3] = o.w;
         if (a.outq8) {
             // lanes 0..C4-1 of wave 0: 8 consecutive lanes hold one 32-value block
-            const size_t e0 = (size_t)h * HD + 4 * c;
+            const size_t e0 = (size_t)tok * a.out_ld + (size_t)h * HD + 4 * c;
             q8_store4(a.outq8 + (e0 >> 5) * Q8_0_BYTES, c & 7, o);
         }
     }
@@ -343,7 +346,8 @@ int attn_nsplit(int max_seq) { return (max_seq + kAttnSplit - 1) / kAttnSplit; }
 
 template <int HD>
 static hipError_t launch_attn_hd(const AttnArgs& a, int G, hipStream_t st) {
-    const dim3 grid((unsigned)a.n_kv_heads, (unsigned)a.nsplit);
+    const unsigned nt = a.n_tok > 1 ? (unsigned)a.n_tok : 1u;
+    const dim3 grid((unsigned)a.n_kv_heads, (unsigned)a.nsplit, nt);
     if (G == 1)
         hipLaunchKernelGGL((k_attn_split<HD, 1>), grid, dim3(kAttnThreads), 0, st, a);
     else if (G == 2)
@@ -356,7 +360,8 @@ static hipError_t launch_attn_hd(const AttnArgs& a, int G, hipStream_t st) {
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_attn_combine<HD>), dim3((unsigned)a.n_heads), dim3(kAttnThreads), 0, st, a);
+    hipLaunchKernelGGL((k_attn_combine<HD>), dim3((unsigned)a.n_heads, nt), dim3(kAttnThreads), 0,
+                       st, a);
     return hipGetLastError();
 }
 
@@ -364,6 +369,10 @@ hipError_t launch_attention_fused(const AttnArgs& a, int head_dim, hipStream_t s
     if (a.n_kv_heads <= 0 || a.n_heads % a.n_kv_heads) return hipErrorInvalidValue;
     const int G = a.n_heads / a.n_kv_heads;
     if (a.nsplit < 1 || a.nsplit > kMaxSplit || G > 8 || (a.store_kv && !a.cos_t))
+        return hipErrorInvalidValue;
+    // several query rows: K/V rows already stored, row t at q + t*q_ld, out + t*out_ld
+    if (a.n_tok > 1 && (a.store_kv || a.q_ld < a.n_heads * head_dim ||
+                        a.out_ld < a.n_heads * head_dim || (a.outq8 && a.out_ld % 32)))
         return hipErrorInvalidValue;
     switch (head_dim) {
         case 64: return launch_attn_hd<64>(a, G, st);

@@ -804,6 +804,113 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k_q8(float* __restrict__ Y,
 }
 
 // ---------------------------------------------------------------------------
+// Batched Q6_K x Q8_0 (small M): Y[t*rows + o] for a tile of TT tokens.  The
+// reference runs one gemv_q6k_q8_avx2_range per token for Q6_K weights
+// (gemm_wt_q8, src/models/llama_model.cpp:860-873); here each lane decodes its
+// weight chunks once and applies them to the TT tokens' records in LDS (the
+// GEMV's lane decomposition and per-chunk arithmetic).
+// ---------------------------------------------------------------------------
+template <int LPR, int CPL, int NR, int TT>
+__global__ __launch_bounds__(kThreads) void k_gemm_q6k_q8(float* __restrict__ Y,
+                                                          const uint8_t* __restrict__ W,
+                                                          const uint8_t* __restrict__ XQ8,
+                                                          int rows, int nb, long row_bytes,
+                                                          int t0, int nt) {
+    extern __shared__ uint4 smem[];
+    uint32_t* rec = reinterpret_cast<uint32_t*>(smem);
+    constexpr int RPP = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rl = lane % LPR, rg = lane / LPR;
+    const int nchunks = 4 * nb;
+    const long row0 = ((long)blockIdx.x * kWaves + wave) * (RPP * NR) + rg;
+    const size_t tok_bytes = (size_t)nb * 8 * Q8_0_BYTES;
+
+    Q6Chunk wk[NR][CPL];
+#pragma unroll
+    for (int n = 0; n < NR; n++) {
+        const long row = min(row0 + (long)n * RPP, (long)rows - 1);
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+            const int c = min(rl + i * LPR, nchunks - 1);
+            load_q6_chunk(W + row * row_bytes + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
+        }
+    }
+    // token records: the clamped token t0 + min(t, nt - 1), so every record is valid
+    for (int t = 0; t < TT; t++) {
+        const uint8_t* xq = XQ8 + (size_t)(t0 + min(t, nt - 1)) * tok_bytes;
+        uint32_t* rt = rec + (size_t)t * 20 * nchunks;
+        for (int b = threadIdx.x; b < nb * 8; b += kThreads) {
+            uint32_t q[8];
+            const uint8_t* p = xq + (size_t)b * Q8_0_BYTES;
+#pragma unroll
+            for (int k = 0; k < 8; k++) q[k] = ld4(p + 4 + 4 * k);
+            rec_put<kQ6K>(rt, b, q, __uint_as_float(ld4(p)));
+        }
+    }
+    __syncthreads();
+
+    float acc[NR][TT];
+#pragma unroll
+    for (int n = 0; n < NR; n++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) acc[n][t] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+        const bool live = rl + i * LPR < nchunks;
+        const int c = min(rl + i * LPR, nchunks - 1);
+        const int h = (c >> 1) & 1, tq = c & 1;
+#pragma unroll
+        for (int n = 0; n < NR; n++) {
+            const Q6Chunk& k6 = wk[n][i];
+            const float d = h2f(k6.dbits);
+            const uint32_t sa = h ? k6.sc[2] : k6.sc[0], sb = h ? k6.sc[3] : k6.sc[1];
+            const int sA0 = (int8_t)(sa >> (16 * tq)), sA1 = (int8_t)(sa >> (16 * tq + 8));
+            const int sB0 = (int8_t)(sb >> (16 * tq)), sB1 = (int8_t)(sb >> (16 * tq + 8));
+            uint32_t qA[8], qB[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t l = k6.ql[k], hs = k6.qh[k] >> (2 * tq);
+                qA[k] = (l & 0x0f0f0f0fu) | ((hs << 4) & 0x30303030u);
+                qB[k] = ((l >> 4) & 0x0f0f0f0fu) | (hs & 0x30303030u);
+            }
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                const uint4* r4 = reinterpret_cast<const uint4*>(rec + ((size_t)t * nchunks + c) * 20);
+                const uint4 xa0 = r4[0], xa1 = r4[1], xb0 = r4[2], xb1 = r4[3], meta = r4[4];
+                const float dxa = __uint_as_float(meta.x), dxb = __uint_as_float(meta.y);
+                const int oA0 = -32 * (int)(int16_t)(meta.z & 0xffffu), oA1 = -32 * ((int)meta.z >> 16);
+                const int oB0 = -32 * (int)(int16_t)(meta.w & 0xffffu), oB1 = -32 * ((int)meta.w >> 16);
+                const uint32_t xa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
+                const uint32_t xb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
+                int iA0 = oA0, iA1 = oA1, iB0 = oB0, iB1 = oB1;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    iA0 = dot4((int)qA[k], (int)xa[k], iA0);
+                    iB0 = dot4((int)qB[k], (int)xb[k], iB0);
+                    iA1 = dot4((int)qA[k + 4], (int)xa[k + 4], iA1);
+                    iB1 = dot4((int)qB[k + 4], (int)xb[k + 4], iB1);
+                }
+                float v = acc[n][t];
+                v = fmaf((d * (float)sA0) * dxa, (float)iA0, v);
+                v = fmaf((d * (float)sA1) * dxa, (float)iA1, v);
+                v = fmaf((d * (float)sB0) * dxb, (float)iB0, v);
+                v = fmaf((d * (float)sB1) * dxb, (float)iB1, v);
+                acc[n][t] = live ? v : acc[n][t];
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NR; n++) {
+        const long row = row0 + (long)n * RPP;
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const float v = group_sum_last<LPR>(acc[n][t]);
+            if (rl == LPR - 1 && row < rows && t < nt) Y[(size_t)(t0 + t) * rows + row] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 
@@ -992,6 +1099,48 @@ static hipError_t launch_gemm_dot4(float* Y, const void* W, const void* XQ8, int
     if (T >= 4 && tt >= 4) return launch_gemm_tt<4>(Y, W, XQ8, rows, T, nb, row_bytes, st);
     if (T >= 2 && tt >= 2) return launch_gemm_tt<2>(Y, W, XQ8, rows, T, nb, row_bytes, st);
     return launch_gemm_tt<1>(Y, W, XQ8, rows, T, nb, row_bytes, st);
+}
+
+template <int LPR, int CPL, int NR, int TT>
+static hipError_t launch_gemm6_cfg(float* Y, const void* W, const void* XQ8, int rows, int T,
+                                   int nb, long row_bytes, hipStream_t st) {
+    constexpr int rows_per_wg = kWaves * (64 / LPR) * NR;
+    const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg));
+    const size_t lds = (size_t)TT * 4 * nb * 80;
+    for (int t0 = 0; t0 < T; t0 += TT) {
+        const int nt = T - t0 < TT ? T - t0 : TT;
+        hipLaunchKernelGGL((k_gemm_q6k_q8<LPR, CPL, NR, TT>), grid, dim3(kThreads), lds, st, Y,
+                           static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(XQ8), rows,
+                           nb, row_bytes, t0, nt);
+    }
+    return hipGetLastError();
+}
+
+template <int TT>
+static hipError_t launch_gemm6_tt(float* Y, const void* W, const void* XQ8, int rows, int T,
+                                  int nb, long row_bytes, hipStream_t st) {
+    const KernCfg k = pick_cfg(4 * nb);
+#define AXF_GEMM6_CASE(L, C, N)                                                            \
+    if (k.lpr == L && k.cpl == C && k.nr == N)                                             \
+        return launch_gemm6_cfg<L, C, N, TT>(Y, W, XQ8, rows, T, nb, row_bytes, st);
+    AXF_GEMV_CFGS(AXF_GEMM6_CASE)
+#undef AXF_GEMM6_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
+                              long row_bytes, hipStream_t st) {
+    // token tile: as many tokens as fit 64 KiB of LDS records (80 B per chunk),
+    // and few enough that the decoded chunks and accumulators stay in VGPRs
+    const size_t per_tok = (size_t)4 * nb * 80;
+    int tt = (int)(65536 / per_tok);
+    const int cpl = pick_cfg(4 * nb).cpl;
+    if (cpl > 3 && tt > 4) tt = 4;
+    if (cpl > 6 && tt > 2) tt = 2;
+    if (T >= 8 && tt >= 8) return launch_gemm6_tt<8>(Y, W, XQ8, rows, T, nb, row_bytes, st);
+    if (T >= 4 && tt >= 4) return launch_gemm6_tt<4>(Y, W, XQ8, rows, T, nb, row_bytes, st);
+    if (T >= 2 && tt >= 2) return launch_gemm6_tt<2>(Y, W, XQ8, rows, T, nb, row_bytes, st);
+    return launch_gemm6_tt<1>(Y, W, XQ8, rows, T, nb, row_bytes, st);
 }
 
 GemmPath gemm_resolve(GemmPath path, int T) {

@@ -124,6 +124,10 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ y,
                                                           const float* __restrict__ w, int n,
                                                           float eps) {
     __shared__ float red[16];
+    // row blockIdx.x of a [rows][n] batch
+    x += (size_t)blockIdx.x * n;
+    if (y) y += (size_t)blockIdx.x * n;
+    if (yq8) yq8 += (size_t)blockIdx.x * (n / 32) * Q8_0_BYTES;
     const int n4 = n / 4;
     float4 xv[8];
 #pragma unroll
@@ -226,12 +230,74 @@ __global__ void k_swiglu(float* __restrict__ out, uint8_t* __restrict__ outq8,
 }
 
 // ---------------------------------------------------------------------------
+// K/V of T tokens into the cache (batched prefill): row t at position pos0+t,
+//   kcache[pos] = RoPE(k_t + bk),  vcache[pos] = v_t + bv
+// (add_bias_rows then rope_and_store_k / the V copy of llama_forward_batch,
+// src/models/llama_model.cpp:1380-1406).  k_t = k + t*k_ld, v_t = v + t*v_ld.
+// ---------------------------------------------------------------------------
+__global__ void k_rope_kv_rows(const float* __restrict__ k, int k_ld, const float* __restrict__ v,
+                               int v_ld, const float* __restrict__ bk,
+                               const float* __restrict__ bv, float* __restrict__ kcache,
+                               float* __restrict__ vcache, int pos0, int n_kv_heads, int hd,
+                               const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    const int half = hd / 2;
+    const int t = blockIdx.y, p = pos0 + t;
+    const size_t kv_embd = (size_t)n_kv_heads * hd;
+    const float* cr = cos_t + (size_t)p * half;
+    const float* sr = sin_t + (size_t)p * half;
+    const float* kr = k + (size_t)t * k_ld;
+    const float* vr = v + (size_t)t * v_ld;
+    float* krow = kcache + (size_t)p * kv_embd;
+    float* vrow = vcache + (size_t)p * kv_embd;
+    const int nk = n_kv_heads * half;
+    for (int u = blockIdx.x * blockDim.x + threadIdx.x; u < nk + (int)kv_embd;
+         u += gridDim.x * blockDim.x) {
+        if (u < nk) {
+            const int h = u / half, i = u % half;
+            const size_t e0 = (size_t)h * hd + i, e1 = e0 + half;
+            const float x0 = bk ? kr[e0] + bk[e0] : kr[e0];
+            const float x1 = bk ? kr[e1] + bk[e1] : kr[e1];
+            const float c = cr[i], s = sr[i];
+            krow[e0] = fmaf(x0, c, -(x1 * s));
+            krow[e1] = fmaf(x0, s, x1 * c);
+        } else {
+            const int e = u - nk;
+            vrow[e] = bv ? vr[e] + bv[e] : vr[e];
+        }
+    }
+}
+
+// SwiGLU of T rows whose gate and up halves are interleaved by row blocks of B
+// ([gate B][up B] ... per row of 2*n), into Q8_0 blocks of the [T][n] result.
+__global__ void k_swiglu_gu(uint8_t* __restrict__ outq8, const float* __restrict__ gu, int T,
+                            int n, int B) {
+    const int n4 = n / 4;
+    for (long q = (long)blockIdx.x * blockDim.x + threadIdx.x; q < (long)T * n4;
+         q += (long)gridDim.x * blockDim.x) {
+        const long t = q / n4;
+        const int f = (int)(q - t * n4) * 4;
+        const int j = f / B, r = f - j * B;
+        const float* row = gu + (size_t)t * 2 * n + (size_t)2 * j * B + r;
+        const float4 g = *reinterpret_cast<const float4*>(row);
+        const float4 u = *reinterpret_cast<const float4*>(row + B);
+        float4 o;
+        o.x = swiglu1(g.x, u.x);
+        o.y = swiglu1(g.y, u.y);
+        o.z = swiglu1(g.z, u.z);
+        o.w = swiglu1(g.w, u.w);
+        q8_block_store(outq8 + (size_t)(q >> 3) * Q8_0_BYTES, (int)(q & 7), o);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Embedding row (token id from device memory or immediate): dequantise row
 // `tok` of a Q4_K / Q6_K matrix with `nb` blocks per row.
 // ---------------------------------------------------------------------------
 __global__ void k_embed_q4k(float* __restrict__ out, const uint8_t* __restrict__ W,
                             const int* tok_dev, int tok, int nb, long row_bytes) {
-    const int id = tok_dev ? *tok_dev : tok;
+    // row blockIdx.x: token tok_dev[blockIdx.x] (or tok) into out + blockIdx.x * nb * 256
+    const int id = tok_dev ? tok_dev[blockIdx.x] : tok;
+    out += (size_t)blockIdx.x * nb * QK_K;
     const uint8_t* row = W + (long)id * row_bytes;
     for (int t = threadIdx.x; t < nb * 32; t += blockDim.x) {
         const int b = t >> 5, k = t & 31, c = k >> 3, l0 = (k & 7) * 4;
@@ -254,7 +320,9 @@ __global__ void k_embed_q4k(float* __restrict__ out, const uint8_t* __restrict__
 
 __global__ void k_embed_q6k(float* __restrict__ out, const uint8_t* __restrict__ W,
                             const int* tok_dev, int tok, int nb, long row_bytes) {
-    const int id = tok_dev ? *tok_dev : tok;
+    // row blockIdx.x: token tok_dev[blockIdx.x] (or tok) into out + blockIdx.x * nb * 256
+    const int id = tok_dev ? tok_dev[blockIdx.x] : tok;
+    out += (size_t)blockIdx.x * nb * QK_K;
     const uint8_t* row = W + (long)id * row_bytes;
     for (int t = threadIdx.x; t < nb * 128; t += blockDim.x) {
         const int b = t >> 7, k = t & 127, half = k >> 6, l = k & 31, s = (k >> 5) & 1;
@@ -407,6 +475,38 @@ hipError_t launch_rmsnorm(float* y, void* yq8, const float* x, const float* w, i
                           hipStream_t st) {
     hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kNormThreads), 0, st, y,
                        static_cast<uint8_t*>(yq8), x, w, n, eps);
+    return hipGetLastError();
+}
+hipError_t launch_rmsnorm_rows(float* y, void* yq8, const float* x, const float* w, int n,
+                               float eps, int rows, hipStream_t st) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(kNormThreads), 0, st, y,
+                       static_cast<uint8_t*>(yq8), x, w, n, eps);
+    return hipGetLastError();
+}
+hipError_t launch_rope_kv_rows(const float* k, int k_ld, const float* v, int v_ld,
+                               const float* bk, const float* bv, float* kcache, float* vcache,
+                               int pos0, int T, int n_kv_heads, int hd, const float* cos_t,
+                               const float* sin_t, hipStream_t st) {
+    const long work = (long)n_kv_heads * hd / 2 + (long)n_kv_heads * hd;
+    hipLaunchKernelGGL(k_rope_kv_rows, dim3(grid_for(work, 256, 64), (unsigned)T), dim3(256), 0,
+                       st, k, k_ld, v, v_ld, bk, bv, kcache, vcache, pos0, n_kv_heads, hd, cos_t,
+                       sin_t);
+    return hipGetLastError();
+}
+hipError_t launch_swiglu_gu(void* outq8, const float* gu, int T, int n, int B, hipStream_t st) {
+    if (n % 32 || B % 4 || n % B) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_swiglu_gu, dim3(grid_for((long)T * n / 4, 256)), dim3(256), 0, st,
+                       static_cast<uint8_t*>(outq8), gu, T, n, B);
+    return hipGetLastError();
+}
+hipError_t launch_embed_rows(int qtype, float* out, const void* W, const int* toks_dev, int T,
+                             int nb, long row_bytes, hipStream_t st) {
+    if (qtype == 12)
+        hipLaunchKernelGGL(k_embed_q4k, dim3((unsigned)T), dim3(1024), 0, st, out,
+                           static_cast<const uint8_t*>(W), toks_dev, 0, nb, row_bytes);
+    else
+        hipLaunchKernelGGL(k_embed_q6k, dim3((unsigned)T), dim3(1024), 0, st, out,
+                           static_cast<const uint8_t*>(W), toks_dev, 0, nb, row_bytes);
     return hipGetLastError();
 }
 hipError_t launch_rope(float* dst, const float* src, const int* pos_dev, int pos, int n_heads,

@@ -135,6 +135,10 @@ class Context:
             call("axf_hip_gemm_q4k_q8_path", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
                  C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb), int(path))
 
+    def gemm_q6k_q8(self, Y: int, W: int, XQ8: int, rows: int, T: int, cols: int, rb: int) -> None:
+        call("axf_hip_gemm_q6k_q8", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
+             C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb))
+
     def argmax(self, idx: int, x: int, n: int) -> None:
         call("axf_hip_argmax_f32", self.handle, C.c_void_p(int(idx)), C.c_void_p(int(x)), n)
 

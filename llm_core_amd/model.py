@@ -175,12 +175,26 @@ class LlamaHip:
     def forward_token(self, token: int, pos: int) -> None:
         call("axf_llama_forward_token", self.handle, token, pos)
 
-    def generate(self, prompt, n_gen: int, use_graph: bool = True) -> np.ndarray:
+    def forward_batch(self, tokens, pos_start: int = 0) -> None:
+        """Batched prefill of `tokens` at positions pos_start.. (llama_forward_batch)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        call("axf_llama_forward_batch", self.handle, t.ctypes.data_as(C.c_void_p), int(t.size),
+             pos_start)
+
+    def generate(self, prompt, n_gen: int, use_graph: bool = True,
+                 batched_prefill: bool = True) -> np.ndarray:
         p = np.ascontiguousarray(prompt, np.int32)
         out = np.zeros(max(n_gen, 1), np.int32)
-        call("axf_llama_generate", self.handle, p.ctypes.data_as(C.c_void_p), int(p.size), n_gen,
-             out.ctypes.data_as(C.c_void_p), 1 if use_graph else 0)
+        call("axf_llama_generate_ex", self.handle, p.ctypes.data_as(C.c_void_p), int(p.size),
+             n_gen, out.ctypes.data_as(C.c_void_p), 1 if use_graph else 0,
+             1 if batched_prefill else 0)
         return out[:n_gen]
+
+    def bench_prefill(self, n_tokens: int, reps: int = 3) -> float:
+        """Mean milliseconds of a batched prefill of n_tokens synthetic tokens."""
+        ms = C.c_float(0)
+        call("axf_llama_bench_prefill", self.handle, n_tokens, reps, C.byref(ms))
+        return ms.value
 
     def bench_decode(self, pos: int, warmup: int, steps: int) -> float:
         """Milliseconds for `steps` graph-replayed decode steps at position `pos`."""

@@ -201,6 +201,24 @@ def test_gemm_q4k_q8(ctx, rows, cols, T, path):
     assert ok, err
 
 
+@pytest.mark.parametrize("rows,cols,T", [(4096, 4096, 1), (4096, 11008, 4), (512, 11008, 9),
+                                         (2048, 2048, 17), (40, 512, 8), (300, 1024, 33)])
+def test_gemm_q6k_q8(ctx, rows, cols, T):
+    """Batched Q6_K: row t equals the oracle's per-token GEMV of token t (the
+    reference's gemm_wt_q8 runs gemv_q6k_q8 per token for Q6_K weights)."""
+    W = weights(Q6K, rows, cols, 6)
+    X = np.random.default_rng(T + 1).standard_normal(T * cols).astype(np.float32)
+    XQ = O.quantize_q8_0(X)
+    bpt = cols // 32 * 36
+    want = np.stack([O.gemv_q8(Q6K, W, XQ[t * bpt:(t + 1) * bpt], rows, cols) for t in range(T)])
+    dW, dX, dY = ctx.upload(W), ctx.upload(XQ), ctx.alloc(T * rows * 4)
+    ctx.write(dY, np.full(T * rows, np.nan, np.float32))  # every output must be written
+    ctx.gemm_q6k_q8(dY, dW, dX, rows, T, cols, O.row_bytes(Q6K, cols))
+    got = ctx.download(dY, np.float32, T * rows).reshape(T, rows)
+    ok, err = close(got, want)
+    assert ok, err
+
+
 # ---------------------------------------------------------------------------
 # decode-step operations
 # ---------------------------------------------------------------------------

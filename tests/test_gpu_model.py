@@ -212,14 +212,16 @@ def _run(ctx, seed, n_gen=32):
     prompt = np.concatenate([[1], rng.integers(0, hp.n_vocab, 7)]).astype(np.int32)
 
     g = LlamaHip(ctx, m)
-    graph = g.generate(prompt, n_gen, use_graph=True)
+    graph = g.generate(prompt, n_gen, use_graph=True)  # batched prefill
     eager = g.generate(prompt, n_gen, use_graph=False)
     graph2 = g.generate(prompt, n_gen, use_graph=True)  # replays are repeatable
+    tbt = g.generate(prompt, n_gen, use_graph=True, batched_prefill=False)
     g.forward_token(int(prompt[0]), 0)
     gl = g.logits()
     g.close()
     assert np.array_equal(graph, eager), "graph replay and eager launches disagree"
     assert np.array_equal(graph, graph2), "second graph generation differs"
+    assert np.array_equal(graph, tbt), "batched and token-by-token prefill disagree"
 
     om = O.OracleModel(hp, m.tensors)
     seq = om.generate(prompt, n_gen, batched_prefill=False)
@@ -299,4 +301,88 @@ def test_generate_rejects_bad_input(ctx):
         g.generate(np.array([1, 5000], np.int32), 4)  # token id beyond the vocabulary
     with pytest.raises(AxfError):
         g.generate(np.arange(60, dtype=np.int32), 10)  # exceeds n_ctx
+    g.close()
+
+
+# ---------------------------------------------------------------------------
+# batched prefill (llama_forward_batch)
+# ---------------------------------------------------------------------------
+
+def _prefill_case(ctx, hp_kwargs, seed, T, splits=(), with_bias=False):
+    """Last-row logits and residual after a batched prefill of T tokens (run as
+    the given chunk boundaries on the GPU), against the oracle's single batch."""
+    from llm_core_amd.model import Hparams, LlamaHip, SynthLlama
+
+    hp = Hparams(**hp_kwargs)
+    m = SynthLlama(hp, seed=seed, norm_std=0.1, with_bias=with_bias)
+    rng = np.random.default_rng(seed)
+    toks = np.concatenate([[1], rng.integers(0, hp.n_vocab, T - 1)]).astype(np.int32)
+    om = O.OracleModel(hp, m.tensors)
+    om.forward_batch(toks, 0)
+    ol, ox = om.logits(), om.x_view().copy()
+    # the oracle's own token-by-token path: its distance to the batch measures
+    # how far fp32 reordering moves these logits on this input (a Q8_0 rounding
+    # flip of one activation moves them by ~1e-2 on the small models)
+    om.reset()
+    for t, tok in enumerate(toks):
+        om.forward_token(int(tok), t)
+    noise = float(np.max(np.abs(om.logits().astype(np.float64) - ol)))
+    om.close()
+    g = LlamaHip(ctx, m)
+    bounds = [0, *splits, T]
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        g.forward_batch(toks[a:b], a)
+    gl, gx = g.logits(), g.get_x()
+    g.close()
+    return gl, ol, gx, ox, noise
+
+
+def _check_prefill(gl, ol, noise):
+    """Logits within the tolerance, or within twice the oracle's own reorder
+    noise on this input; the greedy pick agrees wherever the oracle's
+    top-1/top-2 margin exceeds the observed difference."""
+    err = float(np.max(np.abs(gl.astype(np.float64) - ol)))
+    ok, _ = within(gl, ol)
+    assert ok or err <= 2 * noise + 1e-4, f"logits max abs err {err}, oracle noise {noise}"
+    if O.top2_margin(ol) > 2 * err:
+        assert int(np.argmax(gl)) == O.argmax(ol)
+
+
+@pytest.mark.parametrize("seed,T", [(3, 24), (8, 9), (21, 64)])
+def test_forward_batch_small(ctx, seed, T):
+    gl, ol, gx, ox, noise = _prefill_case(ctx, SMALL, seed, T)
+    _check_prefill(gl, ol, noise)
+    rel = np.linalg.norm(gx.astype(np.float64) - ox) / np.linalg.norm(ox)
+    assert rel < 1e-3 or noise > 1e-3, f"final-norm row relative error {rel}"
+
+
+def test_forward_batch_in_chunks(ctx):
+    """Prefill as three calls (positions 0, 5, 30) equals the single batch."""
+    gl, ol, gx, ox, noise = _prefill_case(ctx, SMALL, 11, 40, splits=(5, 30))
+    _check_prefill(gl, ol, noise)
+
+
+def test_forward_batch_qwen25_3b_layer(ctx):
+    """One Qwen2.5-3B-like layer (hidden 2048, 16/2 heads, FFN 11008, q/k/v
+    biases) prefilling 48 tokens: last-row logits and residual."""
+    cfg = dict(n_layer=1, n_embd=2048, n_heads=16, n_kv_heads=2, ffn_dim=11008, n_vocab=512,
+               n_ctx=64, rms_eps=1e-6, rope_theta=1e6)
+    gl, ol, gx, ox, noise = _prefill_case(ctx, cfg, 4, 48, with_bias=True)
+    # four Q8_0 re-quantisations per layer: the final-norm row norm-wise as in
+    # the decode layer test, the logits against the oracle's own reorder noise
+    rel = np.linalg.norm(gx.astype(np.float64) - ox) / np.linalg.norm(ox)
+    assert rel < 1e-3, f"final-norm row relative error {rel}"
+    _check_prefill(gl, ol, max(noise, 1e-3))
+
+
+def test_forward_batch_rejects_bad_input(ctx):
+    from llm_core_amd._ffi import AxfError
+    from llm_core_amd.model import Hparams, LlamaHip, SynthLlama
+
+    hp = Hparams(**SMALL)
+    g = LlamaHip(ctx, SynthLlama(hp, seed=1))
+    with pytest.raises(AxfError):
+        g.forward_batch(np.array([1, hp.n_vocab], np.int32))  # token out of range
+    with pytest.raises(AxfError):
+        g.forward_batch(np.ones(hp.n_ctx, np.int32), 1)  # past the context
     g.close()
