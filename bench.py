@@ -74,6 +74,28 @@ def gemv_case(ctx, kind, qtype, rows, cols, reps, seed, min_bytes=2 * MALL_BYTES
     return res, W, x
 
 
+def c5_run(gpu, hp, e2e_too=True):
+    """Config 5 end to end on a loaded model: batched prefill of a 512-token
+    prompt (mean of 3 after one untimed), then 512 + 128 greedy tokens timed on
+    the host clock (decode from position 512; cache rows re-written)."""
+    pf_ms = gpu.bench_prefill(512, reps=3)
+    if not e2e_too:
+        log(f"prefill 512 tokens: {pf_ms:.1f} ms ({512 / pf_ms * 1e3:.0f} tok/s)")
+        return {"prefill_512_ms": round(pf_ms, 2), "prefill_tok_s": round(512 / pf_ms * 1e3, 1)}
+    prompt = (1 + 7 * np.arange(512)) % hp.n_vocab
+    gpu.generate(prompt[:8], 2)  # captures the decode graph
+    t0 = time.perf_counter()
+    gen = gpu.generate(prompt, 128)
+    e2e = time.perf_counter() - t0
+    log(f"prefill 512 tokens: {pf_ms:.1f} ms ({512 / pf_ms * 1e3:.0f} tok/s); "
+        f"512 + 128 greedy end to end: {e2e * 1e3:.1f} ms")
+    return {"prefill_512_ms": round(pf_ms, 2),
+            "prefill_tok_s": round(512 / pf_ms * 1e3, 1),
+            "e2e_512_plus_128_ms": round(e2e * 1e3, 1),
+            "decode_tok_s_after_prefill": round(127 / max(e2e - pf_ms * 1e-3, 1e-9), 1),
+            "generated_head": [int(t) for t in gen[:8]]}
+
+
 def c4_sweep(ctx, Ms=(1, 2, 4, 8, 16, 32, 64)):
     res = [gemm_case(ctx, M) for M in Ms]
     for g4 in res:
@@ -217,7 +239,13 @@ def main() -> int:
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="approximate CPU seconds spent on the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm"], default="all")
+    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill"], default="all")
+    ap.add_argument("--skip-c4", action="store_true",
+                    help="leave out the config-4 GEMM sweep (shorter profiling runs)")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="--only prefill: time the prefill alone (no graph-replayed generation)")
+    ap.add_argument("--skip-c5", action="store_true",
+                    help="leave out the config-5 prefill and end-to-end timing")
     ap.add_argument("--mall-warm", action="store_true",
                     help="also time the roofline GEMV on one weight copy (Infinity-Cache warm)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
@@ -249,6 +277,13 @@ def main() -> int:
 
     if args.only == "gemm":  # config 4 sweep alone (not a bench line)
         print(json.dumps({"c4_q4k_q8_gemm_11008x4096": c4_sweep(ctx)}))
+        return 0
+    if args.only == "prefill":  # config 5 prefill + end to end alone (not a bench line)
+        hp = Hparams(n_ctx=args.ctx, **LLAMA2_7B)
+        gpu = LlamaHip(ctx, SynthLlama(hp, seed=5))
+        print(json.dumps({"c5_prefill_and_e2e": c5_run(gpu, hp, e2e_too=not args.no_e2e)}))
+        gpu.close()
+        ctx.close()
         return 0
 
     # ---- dominant kernel: Q4_K x Q8_0 GEMV, 11008 x 4096, M = 1 ----------------
@@ -282,7 +317,7 @@ def main() -> int:
             "weight_copies": g["n_copies"],
             "mall_warm_us_per_launch": round(warm["us_per_launch"], 3) if warm else None,
         }
-        c4 = c4_sweep(ctx)
+        c4 = None if args.skip_c4 else c4_sweep(ctx)
         out["kernels"] = {
             "copy_256MiB_d2d": cp,
             "c4_q4k_q8_gemm_11008x4096": c4,
@@ -322,6 +357,10 @@ def main() -> int:
         log(f"decode step @ctx {n_ctx}: {ms_step:.3f} ms -> {tok_s:.1f} tok/s; "
             f"{(w_bytes + kv_bytes) / (ms_step * 1e-3) / 1e9:.0f} GB/s over {(w_bytes + kv_bytes) / 1e9:.2f} GB")
         result = dict(ms_step=ms_step, tok_s=tok_s, w_bytes=w_bytes, kv_bytes=kv_bytes)
+        # config 5 end to end: batched prefill of a 512-token prompt, then 128
+        # greedy tokens (decode from position 512; rows of the cache re-written)
+        if not args.skip_c5:
+            result["c5"] = c5_run(gpu, hp)
         gpu.close()
 
         cpu = None
@@ -381,6 +420,7 @@ def main() -> int:
             },
             "roofline": roof,
             "cpu_baseline": result.get("cpu"),
+            "c5_prefill_and_e2e": result.get("c5"),
         }
         line.update(out)
     else:

@@ -234,7 +234,7 @@ private:
     // inputs[0] weight, inputs[1] activation, outputs[0] y, rows = y.numel(),
     // cols = x.numel(), attribute "row_bytes".  Extensions: Q6_K weights, Q8_0
     // activations, "accumulate" (y += W x), and 2-D activations [T, cols] with
-    // y [T, rows] for the batched Q4_K x Q8_0 path.
+    // y [T, rows] for the batched Q4_K / Q6_K x Q8_0 paths.
     void matmul(const Tensor& w, const Tensor& x, Tensor& y, const AttributeMap& attrs) {
         const int qt = qtype(w.dtype());
         const bool batched = x.shape().size() == 2 && x.shape()[0] > 1;
@@ -255,11 +255,15 @@ private:
                       "HIP MATMUL");
         } else if (x.dtype() == DType::Q8_0) {
             if (batched) {
-                if (qt != AXF_TYPE_Q4_K || acc)
-                    throw std::runtime_error("HIP MATMUL: batched path is Q4_K x Q8_0 only");
-                check(axf_hip_gemm_q4k_q8(ctx_, yp, w.raw_data(), x.raw_data(), rows, T, cols,
-                                          row_bytes),
-                      "HIP MATMUL");
+                if (acc) throw std::runtime_error("HIP MATMUL: batched path does not accumulate");
+                if (qt == AXF_TYPE_Q4_K)
+                    check(axf_hip_gemm_q4k_q8(ctx_, yp, w.raw_data(), x.raw_data(), rows, T, cols,
+                                              row_bytes),
+                          "HIP MATMUL");
+                else
+                    check(axf_hip_gemm_q6k_q8(ctx_, yp, w.raw_data(), x.raw_data(), rows, T, cols,
+                                              row_bytes),
+                          "HIP MATMUL");
             } else if (qt == AXF_TYPE_Q4_K) {
                 check(axf_hip_gemv_q4k_q8(ctx_, yp, w.raw_data(), x.raw_data(), rows, cols,
                                           row_bytes, acc),
