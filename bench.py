@@ -105,13 +105,27 @@ def c4_sweep(ctx, Ms=(1, 2, 4, 8, 16, 32, 64)):
     return res
 
 
-def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL_BYTES + (96 << 20)):
-    """The T-token Q4_K x Q8_0 GEMM (config 4: 11008x4096, M tokens), weights
-    rotated like gemv_case; X = M x cols fp32 N(0,1) quantized to Q8_0 on the GPU."""
+def q6k_sweep(ctx, Ms=(1, 8, 16, 64)):
+    """The Q6_K GEMM of the prefill's ffn_down (4096 x 11008 for the 7B shape)."""
+    from llm_core_amd import hip
+    res = [gemm_case(ctx, M, rows=4096, cols=11008, qtype=hip.AXF_TYPE_Q6_K) for M in Ms]
+    for g6 in res:
+        log(f"gemm q6k 4096x11008 M={g6['M']}: dot4 {g6['dot4_us']:.2f} us, "
+            f"mfma {g6['mfma_us']:.2f} us, auto {g6['auto_us']:.2f} us = {g6['GBs']:.0f} GB/s, "
+            f"{g6['TOPs']:.2f} TOP/s")
+    return res
+
+
+def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL_BYTES + (96 << 20),
+              qtype=None):
+    """The T-token Q4_K (or Q6_K) x Q8_0 GEMM (config 4: Q4_K 11008x4096, M
+    tokens), weights rotated like gemv_case; X = M x cols fp32 N(0,1) quantized
+    to Q8_0 on the GPU."""
     from llm_core_amd import hip
 
-    W = hip.synth_weight(hip.AXF_TYPE_Q4_K, rows, cols, seed)
-    rb = hip.row_bytes(hip.AXF_TYPE_Q4_K, cols)
+    qtype = hip.AXF_TYPE_Q4_K if qtype is None else qtype
+    W = hip.synth_weight(qtype, rows, cols, seed)
+    rb = hip.row_bytes(qtype, cols)
     n_copies = max(1, math.ceil(min_bytes / W.nbytes))
     bufs = [ctx.upload(W) for _ in range(n_copies)]
     X = hip.synth_normal(M * cols, seed + 7)
@@ -122,8 +136,8 @@ def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL
     alg = W.nbytes + M * (cols // 32 * 36) + 4 * M * rows
     res = {"M": M}
     for name, path in (("dot4", 1), ("mfma", 2), ("auto", 0)):
-        ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2, path)
-        ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps, path)
+        ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2, path, qtype)
+        ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps, path, qtype)
         res[f"{name}_us"] = round(ms * 1000.0 / (reps * n_copies), 3)
     us = res["auto_us"]
     for b in bufs:
@@ -276,7 +290,8 @@ def main() -> int:
     out: dict = {}
 
     if args.only == "gemm":  # config 4 sweep alone (not a bench line)
-        print(json.dumps({"c4_q4k_q8_gemm_11008x4096": c4_sweep(ctx)}))
+        print(json.dumps({"c4_q4k_q8_gemm_11008x4096": c4_sweep(ctx),
+                          "q6k_q8_gemm_4096x11008": q6k_sweep(ctx)}))
         return 0
     if args.only == "prefill":  # config 5 prefill + end to end alone (not a bench line)
         hp = Hparams(n_ctx=args.ctx, **LLAMA2_7B)
@@ -318,9 +333,11 @@ def main() -> int:
             "mall_warm_us_per_launch": round(warm["us_per_launch"], 3) if warm else None,
         }
         c4 = None if args.skip_c4 else c4_sweep(ctx)
+        g6 = None if args.skip_c4 else q6k_sweep(ctx)
         out["kernels"] = {
             "copy_256MiB_d2d": cp,
             "c4_q4k_q8_gemm_11008x4096": c4,
+            "q6k_q8_gemm_4096x11008": g6,
             "c1_q4k_f32_4096x4096": {"us": round(c1["us_per_launch"], 3), "GBs": round(c1["gbs"], 1)},
             "c2_q6k_q8_151936x2048": {"us": round(c2["us_per_launch"], 3), "GBs": round(c2["gbs"], 1)},
         }

@@ -112,11 +112,17 @@ int axf_hip_gemm_q4k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, 
  * (llama_model.cpp:860-873). */
 int axf_hip_gemm_q6k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
                         int T, int cols, size_t row_bytes);
-/* The same GEMM with the kernel chosen explicitly (no reference counterpart;
+/* The same GEMMs with the kernel chosen explicitly (no reference counterpart;
  * for tests and measurement): path 0 automatic (matrix cores from 8 tokens up),
  * 1 the dot4 kernel, 2 the matrix-core (int8 MFMA) kernel.  Results of the two
- * kernels differ only in float summation order. */
+ * kernels differ only in float summation order.  Q6_K takes the matrix cores
+ * only where the last row's last block ends on a 16-byte boundary, under 2 GiB
+ * from W (true of a 16-byte aligned W with row_bytes = cols / 256 * 210 and
+ * rows * cols / 256 a multiple of 8); other Q6_K matrices take the dot4 kernel
+ * on every path. */
 int axf_hip_gemm_q4k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
+                             int T, int cols, size_t row_bytes, int path);
+int axf_hip_gemm_q6k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
                              int T, int cols, size_t row_bytes, int path);
 
 /* Greedy pick: *idx_dev = first index of the maximum of x[0..n), the
@@ -172,9 +178,9 @@ int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_li
                        const void* x, int rows, int cols, size_t row_bytes, int reps, float* ms);
 
 /* Benchmark helper (no reference counterpart): as axf_hip_bench_gemv for the
- * T-token GEMM of axf_hip_gemm_q4k_q8 (Q4_K weights, Q8_0 activations); path as for
- * axf_hip_gemm_q4k_q8_path. */
-int axf_hip_bench_gemm(axf_ctx* ctx, float* Y, const void* const* W_list, int n_w,
+ * T-token GEMM of axf_hip_gemm_q4k_q8 / axf_hip_gemm_q6k_q8 (qtype AXF_TYPE_Q4_K or
+ * AXF_TYPE_Q6_K weights, Q8_0 activations); path as for axf_hip_gemm_q4k_q8_path. */
+int axf_hip_bench_gemm(axf_ctx* ctx, int qtype, float* Y, const void* const* W_list, int n_w,
                        const void* XQ8, int rows, int T, int cols, size_t row_bytes, int path,
                        int reps, float* ms);
 

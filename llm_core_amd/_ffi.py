@@ -74,6 +74,7 @@ SIGNATURES: dict[str, list] = {
     "axf_hip_gemm_q4k_q8": [vp, vp, vp, vp, i32, i32, i32, sz],
     "axf_hip_gemm_q4k_q8_path": [vp, vp, vp, vp, i32, i32, i32, sz, i32],
     "axf_hip_gemm_q6k_q8": [vp, vp, vp, vp, i32, i32, i32, sz],
+    "axf_hip_gemm_q6k_q8_path": [vp, vp, vp, vp, i32, i32, i32, sz, i32],
     "axf_hip_argmax_f32": [vp, vp, vp, i32],
     "axf_hip_rmsnorm": [vp, vp, vp, vp, vp, i32, f32],
     "axf_rope_table": [vp, vp, i32, f32, i32],
@@ -85,7 +86,7 @@ SIGNATURES: dict[str, list] = {
     "axf_hip_timer_start": [vp],
     "axf_hip_timer_stop": [vp, C.POINTER(f32)],
     "axf_hip_bench_gemv": [vp, i32, vp, C.POINTER(vp), i32, vp, i32, i32, sz, i32, C.POINTER(f32)],
-    "axf_hip_bench_gemm": [vp, vp, C.POINTER(vp), i32, vp, i32, i32, i32, sz, i32, i32,
+    "axf_hip_bench_gemm": [vp, i32, vp, C.POINTER(vp), i32, vp, i32, i32, i32, sz, i32, i32,
                            C.POINTER(f32)],
     "axf_synth_normal": [vp, i64, u64, f32, f32],
     "axf_synth_quantize": [i32, vp, vp, i64],

@@ -258,44 +258,47 @@ int axf_hip_gemv_q6k_q8(axf_ctx* ctx, float* y, const void* W, const void* xq8, 
                    row_bytes, accumulate);
 }
 
-static int do_gemm(axf_ctx* ctx, const char* fn, float* Y, const void* W, const void* XQ8,
-                   int rows, int T, int cols, size_t row_bytes, int path) {
+static int do_gemm(axf_ctx* ctx, const char* fn, int qtype, float* Y, const void* W,
+                   const void* XQ8, int rows, int T, int cols, size_t row_bytes, int path) {
     AXF_CHECK_CTX(ctx);
     AXF_REQUIRE(T >= 0, "negative T");
     AXF_REQUIRE(path >= 0 && path <= 2, "path must be 0 (auto), 1 (dot4) or 2 (matrix cores)");
-    int rc = check_gemv(fn, AXF_TYPE_Q4_K, W, XQ8, Y, rows, cols, row_bytes, false);
+    int rc = check_gemv(fn, qtype, W, XQ8, Y, rows, cols, row_bytes, false);
     if (rc) return rc;
     if (rows == 0 || cols == 0 || T == 0) return AXF_OK;
-    const size_t sb = gemm_scratch_bytes((GemmPath)path, T, cols / QK_K);
+    const size_t sb = gemm_scratch_bytes(qtype, (GemmPath)path, T, cols / QK_K);
     void* scratch = nullptr;
     if (sb) {
         rc = ctx_scratch(ctx, sb, &scratch);
         if (rc) return rc;
     }
-    AXF_HIP(launch_gemm_q4k_q8(Y, W, XQ8, rows, T, cols / QK_K, (long)row_bytes, (GemmPath)path,
-                               scratch, ctx->stream));
+    if (qtype == AXF_TYPE_Q6_K)
+        AXF_HIP(launch_gemm_q6k_q8(Y, W, XQ8, rows, T, cols / QK_K, (long)row_bytes,
+                                   (GemmPath)path, scratch, ctx->stream));
+    else
+        AXF_HIP(launch_gemm_q4k_q8(Y, W, XQ8, rows, T, cols / QK_K, (long)row_bytes,
+                                   (GemmPath)path, scratch, ctx->stream));
     return AXF_OK;
 }
 
 int axf_hip_gemm_q4k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows, int T,
                         int cols, size_t row_bytes) {
-    return do_gemm(ctx, __func__, Y, W, XQ8, rows, T, cols, row_bytes, 0);
+    return do_gemm(ctx, __func__, AXF_TYPE_Q4_K, Y, W, XQ8, rows, T, cols, row_bytes, 0);
 }
 
 int axf_hip_gemm_q6k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows, int T,
                         int cols, size_t row_bytes) {
-    AXF_CHECK_CTX(ctx);
-    AXF_REQUIRE(T >= 0, "negative T");
-    int rc = check_gemv(__func__, AXF_TYPE_Q6_K, W, XQ8, Y, rows, cols, row_bytes, false);
-    if (rc) return rc;
-    if (rows == 0 || cols == 0 || T == 0) return AXF_OK;
-    AXF_HIP(launch_gemm_q6k_q8(Y, W, XQ8, rows, T, cols / QK_K, (long)row_bytes, ctx->stream));
-    return AXF_OK;
+    return do_gemm(ctx, __func__, AXF_TYPE_Q6_K, Y, W, XQ8, rows, T, cols, row_bytes, 0);
+}
+
+int axf_hip_gemm_q6k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
+                             int T, int cols, size_t row_bytes, int path) {
+    return do_gemm(ctx, __func__, AXF_TYPE_Q6_K, Y, W, XQ8, rows, T, cols, row_bytes, path);
 }
 
 int axf_hip_gemm_q4k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
                              int T, int cols, size_t row_bytes, int path) {
-    return do_gemm(ctx, __func__, Y, W, XQ8, rows, T, cols, row_bytes, path);
+    return do_gemm(ctx, __func__, AXF_TYPE_Q4_K, Y, W, XQ8, rows, T, cols, row_bytes, path);
 }
 
 int axf_hip_argmax_f32(axf_ctx* ctx, int* idx_dev, const float* x, int n) {
@@ -462,24 +465,28 @@ int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_li
     });
 }
 
-int axf_hip_bench_gemm(axf_ctx* ctx, float* Y, const void* const* W_list, int n_w,
+int axf_hip_bench_gemm(axf_ctx* ctx, int qtype, float* Y, const void* const* W_list, int n_w,
                        const void* XQ8, int rows, int T, int cols, size_t row_bytes, int path,
                        int reps, float* ms) {
     AXF_CHECK_CTX(ctx);
     AXF_REQUIRE(W_list && n_w > 0 && reps > 0 && ms && T > 0 && rows > 0 && cols > 0,
                 "bad arguments");
+    AXF_REQUIRE(qtype == AXF_TYPE_Q4_K || qtype == AXF_TYPE_Q6_K, "qtype must be Q4_K or Q6_K");
     AXF_REQUIRE(path >= 0 && path <= 2, "path must be 0 (auto), 1 (dot4) or 2 (matrix cores)");
     for (int i = 0; i < n_w; i++) {
-        int rc = check_gemv(__func__, AXF_TYPE_Q4_K, W_list[i], XQ8, Y, rows, cols, row_bytes, false);
+        int rc = check_gemv(__func__, qtype, W_list[i], XQ8, Y, rows, cols, row_bytes, false);
         if (rc) return rc;
     }
-    const size_t sb = gemm_scratch_bytes((GemmPath)path, T, cols / QK_K);
+    const size_t sb = gemm_scratch_bytes(qtype, (GemmPath)path, T, cols / QK_K);
     void* scratch = nullptr;
     if (sb) {  // allocated before capture
         int rc = ctx_scratch(ctx, sb, &scratch);
         if (rc) return rc;
     }
     return bench_graph(ctx, __func__, n_w, reps, ms, [&](int i, hipStream_t st) {
+        if (qtype == AXF_TYPE_Q6_K)
+            return launch_gemm_q6k_q8(Y, W_list[i], XQ8, rows, T, cols / QK_K, (long)row_bytes,
+                                      (GemmPath)path, scratch, st);
         return launch_gemm_q4k_q8(Y, W_list[i], XQ8, rows, T, cols / QK_K, (long)row_bytes,
                                   (GemmPath)path, scratch, st);
     });

@@ -61,20 +61,27 @@ hipError_t launch_qgemv2(QAct act, QGemvArgs a, int threads, hipStream_t st);
 int qgemv_threads(QAct act, int nb);  // default workgroup size for launch_qgemv
 bool qgemv_threads_ok(QAct act, int nb, int threads);
 int qgemv_rows_per_wg(int nb, int threads);
-// Q4_K x Q8_0 GEMM, Y token-major.  Auto picks the matrix-core kernel from
-// kGemmMfmaMinT tokens up, the dot4 kernel below.  The matrix-core path needs
-// gemm_scratch_bytes() of device scratch (activation re-layout).
+// Q4_K / Q6_K x Q8_0 GEMM, Y token-major.  Auto picks the matrix-core kernel
+// from kGemmMfmaMinT tokens up, the dot4 kernel below.  The matrix-core path
+// needs gemm_scratch_bytes() of device scratch (activation re-layout).
 enum class GemmPath { Auto = 0, Dot4 = 1, Mfma = 2 };
 constexpr int kGemmMfmaMinT = 8;
 GemmPath gemm_resolve(GemmPath path, int T);
-size_t gemm_scratch_bytes(GemmPath path, int T, int nb);
+size_t gemm_scratch_bytes(int qtype, GemmPath path, int T, int nb);
 hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
                               long row_bytes, GemmPath path, void* scratch, hipStream_t st);
-size_t gemm_mfma_scratch_bytes(int T, int nb);
-// Q6_K x Q8_0 for T tokens (dot4; weights decoded once per token tile), Y token-major.
+// Q6_K: the matrix-core kernel runs only when gemm_mfma_q6k_ok (the last
+// row's last block ends on a 16-byte boundary, under 2 GiB from W); otherwise
+// the dot4 kernel.
 hipError_t launch_gemm_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
-                              long row_bytes, hipStream_t st);
+                              long row_bytes, GemmPath path, void* scratch, hipStream_t st);
+// the matrix-core kernels (kernels/gemm_mfma.hip)
+size_t gemm_mfma_scratch_bytes(int T, int nb);
 hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
+                                   int nb, long row_bytes, void* scratch, hipStream_t st);
+size_t gemm_mfma_q6k_scratch_bytes(int T, int nb);
+bool gemm_mfma_q6k_ok(const void* W, int rows, int nb, long row_bytes);
+hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
                                    int nb, long row_bytes, void* scratch, hipStream_t st);
 hipError_t launch_dequant_q4k(float* y, const void* W, long nblocks, hipStream_t st);
 hipError_t launch_dequant_q6k(float* y, const void* W, long nblocks, hipStream_t st);

@@ -404,7 +404,9 @@ int prefill_alloc(axf_llama* m) {
     m->pf_part = static_cast<float*>(p);
     LL_TRY(dalloc(m, C * (kmax > qo ? kmax : qo) / 32 * Q8_0_BYTES, &p));
     m->pf_q8 = static_cast<uint8_t*>(p);
-    const size_t gs = gemm_scratch_bytes(GemmPath::Auto, cap, kmax / QK_K);
+    const size_t g4 = gemm_scratch_bytes(AXF_TYPE_Q4_K, GemmPath::Auto, cap, kmax / QK_K);
+    const size_t g6 = gemm_scratch_bytes(AXF_TYPE_Q6_K, GemmPath::Auto, cap, kmax / QK_K);
+    const size_t gs = g4 > g6 ? g4 : g6;
     LL_TRY(dalloc(m, gs > 16 ? gs : 16, &p));
     m->pf_gemm = static_cast<uint8_t*>(p);
     m->pf_cap = cap;
@@ -417,7 +419,8 @@ hipError_t gemm_rows(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, 
     if (w.qtype == AXF_TYPE_Q4_K)
         return launch_gemm_q4k_q8(Y, w.d, xq8, rows, T, cols / QK_K, (long)w.row_bytes,
                                   GemmPath::Auto, m->pf_gemm, st);
-    return launch_gemm_q6k_q8(Y, w.d, xq8, rows, T, cols / QK_K, (long)w.row_bytes, st);
+    return launch_gemm_q6k_q8(Y, w.d, xq8, rows, T, cols / QK_K, (long)w.row_bytes,
+                              GemmPath::Auto, m->pf_gemm, st);
 }
 
 hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {

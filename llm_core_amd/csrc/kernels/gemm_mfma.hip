@@ -1,4 +1,5 @@
-// gemm_mfma.hip — Q4_K x Q8_0 small-M GEMM on the CDNA4 matrix cores.
+// gemm_mfma.hip — Q4_K x Q8_0 and Q6_K x Q8_0 small-M GEMMs on the CDNA4 matrix
+// cores (the Q6_K kernel is described where it starts, below).
 //
 //   Y[t*rows + o] = sum_b sum_s ( d[o,b]*sc[o,b,s]*dx[t,b,s]*S[o,t,b,s]
 //                                 - dmin[o,b]*m[o,b,s]*dx[t,b,s]*bsum[t,b,s] )
@@ -61,7 +62,7 @@ __global__ __launch_bounds__(256) void k_gemm_prep(const uint8_t* __restrict__ X
     const int t = (int)(i % Tp), kb = (int)(i / Tp);
     uint4 q0 = make_uint4(0u, 0u, 0u, 0u), q1 = q0;
     float d = 0.f;
-    int bs = 0;
+    int b0 = 0, b1 = 0;
     if (t < T) {
         const uint8_t* p = XQ8 + ((size_t)t * nkb + kb) * Q8_0_BYTES;
         d = __uint_as_float(ld4(p));
@@ -69,13 +70,16 @@ __global__ __launch_bounds__(256) void k_gemm_prep(const uint8_t* __restrict__ X
         q1 = make_uint4(ld4(p + 20), ld4(p + 24), ld4(p + 28), ld4(p + 32));
         const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-        for (int k = 0; k < 8; k++) bs = dot4((int)w[k], 0x01010101, bs);
+        for (int k = 0; k < 4; k++) {
+            b0 = dot4((int)w[k], 0x01010101, b0);
+            b1 = dot4((int)w[k + 4], 0x01010101, b1);
+        }
     }
     uint4* o = reinterpret_cast<uint4*>(xs + (size_t)i * 32);
     o[0] = q0;
     o[1] = q1;
     dxs[i] = d;
-    gxs[i] = d * (float)bs;
+    gxs[i] = d * (float)(b0 + b1);
 }
 
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
@@ -347,6 +351,311 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_mfma_q4k(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q6_K x Q8_0 on the matrix cores.  Per (token t, row o):
+//   Y = sum_b d * sum_s sc_s * dx_s * sum_k (q_k - 32) x_k
+// over the 16-weight sub-blocks s (the per-token dot of
+// gemv_q6k_q8_avx2_range, gemv_q6k_q8_avx2.cpp:104-205, which gemm_wt_q8 runs
+// per token for Q6_K weights, llama_model.cpp:860-873).
+//   * B = the signed 6-bit weights q - 32 in [-32, 31] as int8: low nibble from
+//     ql, high nibble (h - 2) mod 16 from the two qh bits h, which is exact;
+//   * one Q8_0 block (32 k) covers two sub-blocks with their own int8 scales,
+//     so it takes two v_mfma_i32_16x16x32_i8 whose B has the other
+//     sub-block's k-groups zeroed; sc is applied by 24-bit integer
+//     multiply-adds (exact in int32), dx by an fp32 FMA, d once per block.
+// Stage layout: KS super-blocks, each RW rows x 224-byte slots holding the
+// 16-byte-aligned span that covers the row's 210-byte block (blocks are 2-byte
+// aligned), then the KS super-blocks' int8 activations and dx (as for Q4_K).
+// A span starts up to 14 bytes before its block and ends up to 14 bytes after
+// it; the launcher takes this kernel only when the matrix's last block ends on
+// a 16-byte boundary, so every span lies in [W rounded down to 16 bytes, end
+// of the last block).  The spans are copied by buffer loads whose resource is
+// exactly that range.
+// Waves: KS groups (one super-block of the stage each) x RT row tiles x TS
+// token splits; the KS partial sums are added in a fixed order through LDS.
+// ---------------------------------------------------------------------------
+template <int RT, int TT, int KS, int TS, int S>
+struct Stage6 {
+    static constexpr int RW = kTile * RT, TW = kTile * TT;
+    static constexpr int NW = KS * RT * TS;
+    static constexpr int SLOT = 224;
+    static constexpr int WSB = RW * SLOT;     // weights of one super-block
+    static constexpr int XSB = 8 * TW * 32;   // int8 activations of one super-block
+    static constexpr int DSB = 8 * TW * 4;    // dx of one super-block
+    static constexpr int WB = KS * WSB, XB = KS * XSB, DB = KS * DSB;
+    static constexpr int BYTES = WB + XB + DB;
+    static constexpr int PIECES = (BYTES + 1023) / 1024;
+    static constexpr int ALLOC = PIECES * 1024;
+    static constexpr int PMAX = (PIECES + NW - 1) / NW;
+    static constexpr int PMIN = PIECES / NW;
+    static constexpr int WP = WB / 1024;  // pieces 0..WP-1 hold weights
+    static constexpr int WT = TT / TS;    // token tiles per wave
+    static_assert(TT % TS == 0, "token split");
+    static_assert(WB % 1024 == 0 && XSB % 16 == 0 && DSB % 16 == 0, "piece alignment");
+    static_assert(NW <= 16, "workgroup size");
+};
+
+// N dwords of LDS bytes at p0 + off, p0 4-byte aligned, off any byte offset
+// (the address stays an LDS pointer: aligned ds_read_b32 + v_alignbyte)
+template <int N>
+__device__ __forceinline__ void lds_bytes(const uint8_t* p0, uint32_t off, uint32_t (&out)[N]) {
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(p0 + (off & ~3u));
+    const uint32_t sh = off & 3u;
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int k = 0; k <= N; k++) w[k] = base[k];
+#pragma unroll
+    for (int k = 0; k < N; k++) out[k] = __builtin_amdgcn_alignbyte(w[k + 1], w[k], sh);
+}
+
+// Per copy piece of this lane: weights — base = the row's offset in the
+// buffer resource, aux = the lane's offset in the slot; activations — base =
+// the address for super-block 0, aux = bytes per super-block.  ks = the
+// piece's super-block within the stage.
+template <int RT, int TT, int KS, int TS, int S>
+struct Plan6 {
+    uint64_t base[Stage6<RT, TT, KS, TS, S>::PMAX];
+    uint32_t aux[Stage6<RT, TT, KS, TS, S>::PMAX];
+    uint32_t ks[Stage6<RT, TT, KS, TS, S>::PMAX];
+};
+
+template <int RT, int TT, int KS, int TS, int S>
+__device__ __forceinline__ void gemm6_step(
+    const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt, bool do_copy, int snext, int i,
+    int nst, int nb, const Plan6<RT, TT, KS, TS, S>& pl, __amdgpu_buffer_rsrc_t wrsrc, int wave, int col, int g, int ksw, int rt, int tt0,
+    uint32_t wlo, v4f_t (&acc)[Stage6<RT, TT, KS, TS, S>::WT]) {
+    using G = Stage6<RT, TT, KS, TS, S>;
+    constexpr int TW = G::TW, NW = G::NW;
+    if (do_copy) {
+#pragma unroll
+        for (int j = 0; j < G::PMAX; j++) {
+            const int piece = wave + NW * j;
+            // super-block of this piece (past the end: the last one again, unused)
+            const uint32_t b = min((uint32_t)(snext * KS) + pl.ks[j], (uint32_t)(nb - 1));
+            if (piece < G::WP) {
+                // the aligned span of the row's block b; this lane's 16 bytes sit
+                // aux[j] bytes into the slot
+                const uint32_t o =
+                    (((uint32_t)pl.base[j] + b * (uint32_t)Q6K_BYTES) & ~15u) + pl.aux[j];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, (lmem_t*)(nxt + piece * 1024), 16,
+                                                         o, 0, 0, 0);
+            } else if (piece < G::PIECES) {
+                const uint8_t* a =
+                    reinterpret_cast<const uint8_t*>(pl.base[j]) + (size_t)b * pl.aux[j];
+                __builtin_amdgcn_global_load_lds((gmem_t*)a, (lmem_t*)(nxt + piece * 1024), 16,
+                                                 0, 0);
+            }
+        }
+    }
+    if (i < 0) return;
+    const int later = min(S - 1, nst - 1 - i);
+    if constexpr (S >= 4) {
+        if (later >= 3) wait_vmcnt<3 * G::PMIN>();
+        else if (later == 2) wait_vmcnt<2 * G::PMIN>();
+        else if (later == 1) wait_vmcnt<G::PMIN>();
+        else wait_vmcnt<0>();
+    } else if constexpr (S == 3) {
+        if (later >= 2) wait_vmcnt<2 * G::PMIN>();
+        else if (later == 1) wait_vmcnt<G::PMIN>();
+        else wait_vmcnt<0>();
+    } else {
+        if (later >= 1) wait_vmcnt<G::PMIN>();
+        else wait_vmcnt<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+
+    const int b = i * KS + ksw;  // this wave's super-block
+    if (b < nb) {
+        // this lane's weight row: its block starts (wlo + 2b) & 15 bytes into the slot
+        const uint8_t* wl = cur + ksw * G::WSB + (kTile * rt + col) * G::SLOT;
+        const uint32_t wo = (wlo + 2u * (uint32_t)b) & 15u;
+        const uint8_t* xl = cur + G::WB + ksw * G::XSB;
+        const float* dl = reinterpret_cast<const float*>(cur + G::WB + G::XB + ksw * G::DSB);
+        uint32_t ql[2][2][2], qh[2][2], sc[4], dw[1];
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) lds_bytes<2>(wl, wo + 64 * n + 32 * h + 8 * g, ql[n][h]);
+            lds_bytes<2>(wl, wo + 128 + 32 * n + 8 * g, qh[n]);
+        }
+        lds_bytes<4>(wl, wo + 192, sc);
+        lds_bytes<1>(wl, wo + 208, dw);
+        const float d = h2f(dw[0] & 0xffffu);
+        const v4i_t zi = {0, 0, 0, 0};
+        // k-groups 0,1 are the block's first sub-block, k-groups 2,3 its second
+        const uint64_t m1 = g < 2 ? ~0ull : 0ull;
+        v4f_t accb[G::WT];
+#pragma unroll
+        for (int w = 0; w < G::WT; w++) accb[w] = v4f_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 8; kb++) {
+            const int n = kb >> 2, q = kb & 3, h = q & 1, nib = q >> 1;
+            uint32_t v[2];
+#pragma unroll
+            for (int x = 0; x < 2; x++) {
+                // bytes q - 32: low nibble | ((hi2 + 14) mod 16) << 4
+                const uint32_t lo = (ql[n][h][x] >> (4 * nib)) & 0x0f0f0f0fu;
+                const uint32_t hi = (((qh[n][x] >> (2 * q)) & 0x03030303u) + 0x0e0e0e0eu) &
+                                    0x0f0f0f0fu;
+                v[x] = lo | (hi << 4);
+            }
+            const uint64_t bw = ((uint64_t)v[1] << 32) | v[0];
+            const long b1 = (long)(bw & m1), b2 = (long)(bw & ~m1);
+            const int s1 = (int)(int8_t)(sc[kb >> 1] >> (16 * (kb & 1)));
+            const int s2 = (int)(int8_t)(sc[kb >> 1] >> (16 * (kb & 1) + 8));
+#pragma unroll
+            for (int w = 0; w < G::WT; w++) {
+                const int tok = kTile * (tt0 + w);
+                // (a scalar 64-bit read: its LDS access keeps the noalias scope
+                // that lets the copies into the other stage buffers stay in flight)
+                const long a =
+                    *reinterpret_cast<const long*>(xl + (kb * TW + tok + col) * 32 + 8 * g);
+                const float4 dx = *reinterpret_cast<const float4*>(dl + kb * TW + tok + 4 * g);
+                const v4i_t c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zi, 0, 0, 0);
+                const v4i_t c2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b2, zi, 0, 0, 0);
+                // |c| <= 16 * 128 * 32 and |sc| <= 128: the 24-bit products are exact
+                accb[w][0] = fmaf((float)(__mul24(c2[0], s2) + __mul24(c1[0], s1)), dx.x, accb[w][0]);
+                accb[w][1] = fmaf((float)(__mul24(c2[1], s2) + __mul24(c1[1], s1)), dx.y, accb[w][1]);
+                accb[w][2] = fmaf((float)(__mul24(c2[2], s2) + __mul24(c1[2], s1)), dx.z, accb[w][2]);
+                accb[w][3] = fmaf((float)(__mul24(c2[3], s2) + __mul24(c1[3], s1)), dx.w, accb[w][3]);
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < G::WT; w++)
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) acc[w][ii] = fmaf(d, accb[w][ii], acc[w][ii]);
+    }
+    __builtin_amdgcn_s_barrier();
+}
+
+// Workgroup = NW waves on a (16*RT rows) x (16*TT tokens) tile; stage i holds
+// super-blocks i*KS .. i*KS + KS - 1.
+template <int RT, int TT, int KS, int TS, int S>
+__global__ __launch_bounds__(KS * RT * TS * 64) void k_gemm_mfma_q6k(
+    float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ xs,
+    const float* __restrict__ dxs, int rows, int nb, long row_bytes, int T, int Tp) {
+    using G = Stage6<RT, TT, KS, TS, S>;
+    constexpr int RW = G::RW, TW = G::TW, NW = G::NW;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[S * G::ALLOC];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, g = lane >> 4;
+    const int row_base = blockIdx.x * RW;
+    const int tok_base = blockIdx.y * TW;
+
+    // weights through a buffer resource from W rounded down to 16 bytes to the
+    // end of the last block (the host checks that this is under 2 GiB)
+    const uint32_t w0 = (uint32_t)(reinterpret_cast<uintptr_t>(W) & 15);
+    const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(W - w0), 0,
+        (int)(w0 + (uint32_t)(rows - 1) * (uint32_t)row_bytes + (uint32_t)nb * Q6K_BYTES),
+        0x00020000);
+    // activations: xs [8b + k][Tp][32] and dxs [8b + k][Tp] for super-block b
+    Plan6<RT, TT, KS, TS, S> pl;
+#pragma unroll
+    for (int j = 0; j < G::PMAX; j++) {
+        int o = (wave + NW * j) * 1024 + lane * 16;
+        if (o >= G::BYTES) o = G::WB;  // tail of the last piece: a harmless duplicate
+        if (o < G::WB) {
+            const int ks = o / G::WSB, y = o - ks * G::WSB, r = y / G::SLOT;
+            pl.ks[j] = (uint32_t)ks;
+            pl.base[j] = w0 + (uint32_t)min(row_base + r, rows - 1) * (uint32_t)row_bytes;
+            pl.aux[j] = (uint32_t)(y - r * G::SLOT);
+        } else if (o < G::WB + G::XB) {
+            const int x = o - G::WB, ks = x / G::XSB, y = x - ks * G::XSB, k = y / (TW * 32);
+            pl.ks[j] = (uint32_t)ks;
+            pl.base[j] = reinterpret_cast<uint64_t>(xs + ((size_t)k * Tp + tok_base) * 32 +
+                                                    (y - k * TW * 32));
+            pl.aux[j] = 8u * (uint32_t)Tp * 32u;
+        } else {
+            const int x = o - G::WB - G::XB, ks = x / G::DSB, y = x - ks * G::DSB,
+                      k = y / (TW * 4);
+            pl.ks[j] = (uint32_t)ks;
+            pl.base[j] = reinterpret_cast<uint64_t>(
+                reinterpret_cast<const uint8_t*>(dxs + (size_t)k * Tp + tok_base) +
+                (y - k * TW * 4));
+            pl.aux[j] = 8u * (uint32_t)Tp * 4u;
+        }
+    }
+    const int ksw = wave / (RT * TS), rr = wave % (RT * TS);
+    const int rt = rr % RT, tt0 = (rr / RT) * G::WT;
+    const uint32_t wlo =
+        (w0 + (uint32_t)min(row_base + kTile * rt + col, rows - 1) * (uint32_t)row_bytes) & 15u;
+    v4f_t acc[G::WT];
+#pragma unroll
+    for (int w = 0; w < G::WT; w++) acc[w] = v4f_t{0.f, 0.f, 0.f, 0.f};
+    const int nst = (nb + KS - 1) / KS;
+    for (int i = 1 - S; i < nst; i++) {
+        const int inext = i + S - 1;
+        gemm6_step<RT, TT, KS, TS, S>(smem + ((i + S) % S) * G::ALLOC,
+                                      smem + (inext % S) * G::ALLOC, inext < nst, inext, i, nst,
+                                      nb, pl, wrsrc, wave, col, g, ksw, rt, tt0, wlo, acc);
+    }
+    // sum the KS partial tiles in a fixed order (group 0 + 1 + ... + KS-1)
+    if constexpr (KS > 1) {
+        float* red = reinterpret_cast<float*>(smem);
+        static_assert((KS - 1) * RT * TT * 64 * 16 <= S * G::ALLOC, "reduction space");
+        if (ksw > 0) {
+#pragma unroll
+            for (int w = 0; w < G::WT; w++)
+                *reinterpret_cast<float4*>(
+                    red + ((((ksw - 1) * RT + rt) * TT + tt0 + w) * 64 + lane) * 4) =
+                    make_float4(acc[w][0], acc[w][1], acc[w][2], acc[w][3]);
+        }
+        __syncthreads();
+        if (ksw > 0) return;
+#pragma unroll
+        for (int k = 1; k < KS; k++)
+#pragma unroll
+            for (int w = 0; w < G::WT; w++) {
+                const float4 p = *reinterpret_cast<const float4*>(
+                    red + ((((k - 1) * RT + rt) * TT + tt0 + w) * 64 + lane) * 4);
+                acc[w][0] += p.x;
+                acc[w][1] += p.y;
+                acc[w][2] += p.z;
+                acc[w][3] += p.w;
+            }
+    }
+    const int o = row_base + kTile * rt + col;
+    if (o < rows) {
+#pragma unroll
+        for (int w = 0; w < G::WT; w++) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) {
+                const int tok = tok_base + kTile * (tt0 + w) + 4 * g + ii;
+                if (tok < T) Y[(size_t)tok * rows + o] = acc[w][ii];
+            }
+        }
+    }
+}
+
+template <int RT, int TT, int KS, int TS, int S>
+void launch6_cfg(float* Y, const uint8_t* W, const uint8_t* xs, const float* dxs, int rows,
+                 int nb, long row_bytes, int T, int Tp, hipStream_t st) {
+    using G = Stage6<RT, TT, KS, TS, S>;
+    const dim3 grid((unsigned)((rows + G::RW - 1) / G::RW), (unsigned)(Tp / G::TW));
+    hipLaunchKernelGGL((k_gemm_mfma_q6k<RT, TT, KS, TS, S>), grid, dim3(G::NW * 64), 0, st, Y,
+                       W, xs, dxs, rows, nb, row_bytes, T, Tp);
+}
+
+// Tile choice: the largest of 64x64, 32x32, 16x16 (rows x tokens) whose grid
+// still has one workgroup per CU; below that the 16x16 tile with the widest
+// K split.  (Measured on 4096 x 11008 and 2048 x 11008 matrices, T = 8..256.)
+enum class Tile6 { R64T64, R32T32, R16T16, R16T16K8 };
+
+Tile6 pick6(int rows, int T) {
+    auto grid = [&](int rw, int tw) {
+        return (long)((rows + rw - 1) / rw) * (long)((T + tw - 1) / tw);
+    };
+    constexpr long kFill = 256;
+    if (T <= 16) return Tile6::R16T16K8;
+    if (grid(64, 64) >= kFill) return Tile6::R64T64;
+    if (grid(32, 32) >= kFill) return Tile6::R32T32;
+    if (grid(16, 16) >= kFill) return Tile6::R16T16;
+    return Tile6::R16T16K8;
+}
+
+int tokens6(Tile6 t) { return t == Tile6::R64T64 ? 64 : (t == Tile6::R32T32 ? 32 : 16); }
+
 struct MfmaCfg {
     int rt, tt;
 };
@@ -373,6 +682,56 @@ void launch_cfg(float* Y, const uint8_t* W, const uint8_t* xs, const float* dxs,
 }
 
 }  // namespace
+
+// bytes from W to the end of the last row's last block
+static uint64_t q6k_span(int rows, int nb, long row_bytes) {
+    return (uint64_t)(rows - 1) * (uint64_t)row_bytes + (uint64_t)nb * Q6K_BYTES;
+}
+
+bool gemm_mfma_q6k_ok(const void* W, int rows, int nb, long row_bytes) {
+    if (rows <= 0 || nb <= 0) return false;
+    const uint64_t bytes = q6k_span(rows, nb, row_bytes);
+    return bytes + 16 < (1ull << 31) && ((reinterpret_cast<uintptr_t>(W) + bytes) & 15) == 0;
+}
+
+size_t gemm_mfma_q6k_scratch_bytes(int T, int nb) {
+    if (T <= 0 || nb <= 0) return 0;
+    const size_t tp = (size_t)((T + 63) / 64 * 64);  // the widest token tile's padding
+    return (size_t)nb * 8 * tp * (32 + 4 + 4);
+}
+
+hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
+                                   int nb, long row_bytes, void* scratch, hipStream_t st) {
+    if (rows <= 0 || T <= 0 || nb <= 0 || scratch == nullptr) return hipErrorInvalidValue;
+    if (!gemm_mfma_q6k_ok(W, rows, nb, row_bytes)) return hipErrorInvalidValue;
+    const Tile6 tile = pick6(rows, T);
+    const int q = tokens6(tile);
+    const int Tp = (T + q - 1) / q * q;
+    const int nkb = nb * 8;
+    if ((uint64_t)nkb * Tp * 32 >= (1ull << 32)) return hipErrorInvalidValue;
+    auto* xs = static_cast<uint8_t*>(scratch);
+    auto* dxs = reinterpret_cast<float*>(xs + (size_t)nkb * Tp * 32);
+    auto* gxs = dxs + (size_t)nkb * Tp;  // written by the shared prep, unused here
+    const long n = (long)nkb * Tp;
+    hipLaunchKernelGGL(k_gemm_prep, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const uint8_t*>(XQ8), T, Tp, nkb, xs, dxs, gxs);
+    const auto* w = static_cast<const uint8_t*>(W);
+    switch (tile) {
+    case Tile6::R64T64:
+        launch6_cfg<4, 4, 2, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st);
+        break;
+    case Tile6::R32T32:
+        launch6_cfg<2, 2, 4, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st);
+        break;
+    case Tile6::R16T16:
+        launch6_cfg<1, 1, 4, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st);
+        break;
+    default:
+        launch6_cfg<1, 1, 8, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st);
+        break;
+    }
+    return hipGetLastError();
+}
 
 size_t gemm_mfma_scratch_bytes(int T, int nb) {
     if (T <= 0 || nb <= 0) return 0;

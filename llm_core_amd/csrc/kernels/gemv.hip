@@ -1128,8 +1128,8 @@ static hipError_t launch_gemm6_tt(float* Y, const void* W, const void* XQ8, int 
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
-                              long row_bytes, hipStream_t st) {
+static hipError_t launch_gemm6_dot4(float* Y, const void* W, const void* XQ8, int rows, int T,
+                                    int nb, long row_bytes, hipStream_t st) {
     // token tile: as many tokens as fit 64 KiB of LDS records (80 B per chunk),
     // and few enough that the decoded chunks and accumulators stay in VGPRs
     const size_t per_tok = (size_t)4 * nb * 80;
@@ -1148,8 +1148,10 @@ GemmPath gemm_resolve(GemmPath path, int T) {
     return T >= kGemmMfmaMinT ? GemmPath::Mfma : GemmPath::Dot4;
 }
 
-size_t gemm_scratch_bytes(GemmPath path, int T, int nb) {
-    return gemm_resolve(path, T) == GemmPath::Mfma ? gemm_mfma_scratch_bytes(T, nb) : 0;
+size_t gemm_scratch_bytes(int qtype, GemmPath path, int T, int nb) {
+    if (gemm_resolve(path, T) != GemmPath::Mfma) return 0;
+    return qtype == AXF_TYPE_Q6_K ? gemm_mfma_q6k_scratch_bytes(T, nb)
+                                  : gemm_mfma_scratch_bytes(T, nb);
 }
 
 hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
@@ -1157,6 +1159,15 @@ hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows
     if (gemm_resolve(path, T) == GemmPath::Mfma)
         return launch_gemm_mfma_q4k_q8(Y, W, XQ8, rows, T, nb, row_bytes, scratch, st);
     return launch_gemm_dot4(Y, W, XQ8, rows, T, nb, row_bytes, st);
+}
+
+hipError_t launch_gemm_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
+                              long row_bytes, GemmPath path, void* scratch, hipStream_t st) {
+    // the matrix-core kernel copies 16-byte-aligned spans of the 2-byte-aligned
+    // blocks: it needs a last block that ends on a 16-byte boundary (and < 2 GiB)
+    if (gemm_resolve(path, T) == GemmPath::Mfma && gemm_mfma_q6k_ok(W, rows, nb, row_bytes))
+        return launch_gemm_mfma_q6k_q8(Y, W, XQ8, rows, T, nb, row_bytes, scratch, st);
+    return launch_gemm6_dot4(Y, W, XQ8, rows, T, nb, row_bytes, st);
 }
 
 }  // namespace axf

@@ -135,9 +135,15 @@ class Context:
             call("axf_hip_gemm_q4k_q8_path", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
                  C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb), int(path))
 
-    def gemm_q6k_q8(self, Y: int, W: int, XQ8: int, rows: int, T: int, cols: int, rb: int) -> None:
-        call("axf_hip_gemm_q6k_q8", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
-             C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb))
+    def gemm_q6k_q8(self, Y: int, W: int, XQ8: int, rows: int, T: int, cols: int, rb: int,
+                    path: int | None = None) -> None:
+        """Token-major Q6_K x Q8_0 GEMM; path None = automatic, 1 dot4, 2 matrix cores."""
+        if path is None:
+            call("axf_hip_gemm_q6k_q8", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
+                 C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb))
+        else:
+            call("axf_hip_gemm_q6k_q8_path", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
+                 C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb), int(path))
 
     def argmax(self, idx: int, x: int, n: int) -> None:
         call("axf_hip_argmax_f32", self.handle, C.c_void_p(int(idx)), C.c_void_p(int(x)), n)
@@ -188,12 +194,12 @@ class Context:
         return ms.value
 
     def bench_gemm(self, Y: int, W_list, XQ8: int, rows: int, T: int, cols: int, rb: int,
-                   reps: int, path: int = 0) -> float:
-        """Milliseconds for reps*len(W_list) graph-replayed Q4_K x Q8_0 GEMM
-        launches of T tokens (path 0 automatic, 1 dot4, 2 matrix cores)."""
+                   reps: int, path: int = 0, qtype: int = AXF_TYPE_Q4_K) -> float:
+        """Milliseconds for reps*len(W_list) graph-replayed Q4_K (or Q6_K) x Q8_0
+        GEMM launches of T tokens (path 0 automatic, 1 dot4, 2 matrix cores)."""
         arr = (C.c_void_p * len(W_list))(*[int(w) for w in W_list])
         ms = C.c_float(0)
-        call("axf_hip_bench_gemm", self.handle, C.c_void_p(int(Y)), arr, len(W_list),
+        call("axf_hip_bench_gemm", self.handle, int(qtype), C.c_void_p(int(Y)), arr, len(W_list),
              C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb), int(path), reps, C.byref(ms))
         return ms.value
 

@@ -201,22 +201,63 @@ def test_gemm_q4k_q8(ctx, rows, cols, T, path):
     assert ok, err
 
 
-@pytest.mark.parametrize("rows,cols,T", [(4096, 4096, 1), (4096, 11008, 4), (512, 11008, 9),
-                                         (2048, 2048, 17), (40, 512, 8), (300, 1024, 33)])
-def test_gemm_q6k_q8(ctx, rows, cols, T):
+GEMM6_CASES = [(4096, 4096, 1), (4096, 11008, 4), (512, 11008, 9), (2048, 2048, 17),
+               (40, 512, 8), (300, 1024, 33), (256, 2048, 64), (64, 768, 130), (75, 512, 12),
+               (90, 768, 24), (6, 256, 8),
+               # the wider tiles: 64x64 (ragged rows and tokens), 32x32, 16x16
+               (4096, 768, 256), (4100, 768, 250), (2048, 1280, 128), (2040, 1280, 120)]
+
+
+def _gemm6_want(W, XQ, rows, cols, T):
+    bpt = cols // 32 * 36
+    return np.stack([O.gemv_q8(Q6K, W, XQ[t * bpt:(t + 1) * bpt], rows, cols) for t in range(T)])
+
+
+@pytest.mark.parametrize("path", [None, 1, 2], ids=["auto", "dot4", "mfma"])
+@pytest.mark.parametrize("rows,cols,T", GEMM6_CASES)
+def test_gemm_q6k_q8(ctx, rows, cols, T, path):
     """Batched Q6_K: row t equals the oracle's per-token GEMV of token t (the
-    reference's gemm_wt_q8 runs gemv_q6k_q8 per token for Q6_K weights)."""
+    reference's gemm_wt_q8 runs gemv_q6k_q8 per token for Q6_K weights).  The
+    matrix sits at the 4-byte-aligned offset that makes it end on a 16-byte
+    boundary, so the matrix-core kernel runs for path 2 (and auto from 8 tokens)
+    also where W itself is not 16-byte aligned."""
     W = weights(Q6K, rows, cols, 6)
     X = np.random.default_rng(T + 1).standard_normal(T * cols).astype(np.float32)
     XQ = O.quantize_q8_0(X)
-    bpt = cols // 32 * 36
-    want = np.stack([O.gemv_q8(Q6K, W, XQ[t * bpt:(t + 1) * bpt], rows, cols) for t in range(T)])
-    dW, dX, dY = ctx.upload(W), ctx.upload(XQ), ctx.alloc(T * rows * 4)
+    want = _gemm6_want(W, XQ, rows, cols, T)
+    off = -W.size % 16
+    assert off % 4 == 0
+    dW = ctx.alloc(off + W.size)
+    ctx.write(dW.at(off), W)
+    dX, dY = ctx.upload(XQ), ctx.alloc(T * rows * 4)
     ctx.write(dY, np.full(T * rows, np.nan, np.float32))  # every output must be written
-    ctx.gemm_q6k_q8(dY, dW, dX, rows, T, cols, O.row_bytes(Q6K, cols))
+    ctx.gemm_q6k_q8(dY, dW.at(off), dX, rows, T, cols, O.row_bytes(Q6K, cols), path=path)
     got = ctx.download(dY, np.float32, T * rows).reshape(T, rows)
     ok, err = close(got, want)
     assert ok, err
+
+
+@pytest.mark.parametrize("lead", [0, 8, 12])
+def test_gemm_q6k_q8_unaligned_end(ctx, lead):
+    """A Q6_K matrix whose end is not 16-byte aligned takes the dot4 kernel on
+    every path (the matrix-core kernel's aligned spans would read past it):
+    still exact against the oracle, with the matrix ending at its allocation's
+    last byte."""
+    rows, cols, T = 75, 512, 16   # 75 rows x 420 B: 31500 B, 12 mod 16
+    W = weights(Q6K, rows, cols, 7)
+    assert (lead + W.size) % 16 != 0
+    X = np.random.default_rng(3).standard_normal(T * cols).astype(np.float32)
+    XQ = O.quantize_q8_0(X)
+    want = _gemm6_want(W, XQ, rows, cols, T)
+    dW = ctx.alloc(lead + W.size)
+    ctx.write(dW.at(lead), W)
+    dX, dY = ctx.upload(XQ), ctx.alloc(T * rows * 4)
+    for path in (None, 2):
+        ctx.write(dY, np.full(T * rows, np.nan, np.float32))
+        ctx.gemm_q6k_q8(dY, dW.at(lead), dX, rows, T, cols, O.row_bytes(Q6K, cols), path=path)
+        got = ctx.download(dY, np.float32, T * rows).reshape(T, rows)
+        ok, err = close(got, want)
+        assert ok, (path, err)
 
 
 # ---------------------------------------------------------------------------

@@ -322,7 +322,8 @@ def _prefill_case(ctx, hp_kwargs, seed, T, splits=(), with_bias=False):
     ol, ox = om.logits(), om.x_view().copy()
     # the oracle's own token-by-token path: its distance to the batch measures
     # how far fp32 reordering moves these logits on this input (a Q8_0 rounding
-    # flip of one activation moves them by ~1e-2 on the small models)
+    # flip of one activation moves them by ~1e-2 on the small models; about one
+    # input in three has such a near-tie somewhere)
     om.reset()
     for t, tok in enumerate(toks):
         om.forward_token(int(tok), t)
@@ -333,6 +334,13 @@ def _prefill_case(ctx, hp_kwargs, seed, T, splits=(), with_bias=False):
     for a, b in zip(bounds[:-1], bounds[1:]):
         g.forward_batch(toks[a:b], a)
     gl, gx = g.logits(), g.get_x()
+    # the GPU's decode path over the same tokens (the per-token GEMVs, checked
+    # against the oracle by the decode tests) sums in a third order: its
+    # distance to the oracle's batch is another sample of the same noise (each
+    # step rewrites cache row t before attending to rows 0..t)
+    for t, tok in enumerate(toks):
+        g.forward_token(int(tok), t)
+    noise = max(noise, float(np.max(np.abs(g.logits().astype(np.float64) - ol))))
     g.close()
     return gl, ol, gx, ox, noise
 
