@@ -196,6 +196,73 @@ int axf_synth_weight(int qtype, uint8_t* dst, int64_t rows, int64_t cols, uint64
                      float stddev);
 size_t axf_row_bytes(int qtype, int64_t cols);
 
+/* ---- GGUF v2/v3 files (GgufReader, src/loader/gguf_reader.hpp and
+ *      gguf_loader.cpp:49-335; host code, no GPU needed) --------------------- */
+typedef struct axf_gguf axf_gguf;
+
+/* Replaces GgufReader::open + parse (gguf_loader.cpp:49-163): mmap the file and
+ * parse header, KV pairs and tensor infos.  Format errors return
+ * AXF_ERR_INVALID_ARG with the reference's runtime_error message ("GgufReader:
+ * invalid magic (not a GGUF file)", "... unsupported GGUF version N (supported:
+ * 2, 3)", "... unexpected end of file (truncated)", ...). */
+int axf_gguf_open(const char* path, axf_gguf** out);
+int axf_gguf_close(axf_gguf* g);
+uint32_t axf_gguf_version(const axf_gguf* g);      /* GgufReader::version */
+uint64_t axf_gguf_alignment(const axf_gguf* g);    /* general.alignment (u32) or 32 */
+uint64_t axf_gguf_data_offset(const axf_gguf* g);  /* tensor_data_offset */
+uint64_t axf_gguf_file_size(const axf_gguf* g);
+int64_t axf_gguf_n_kv(const axf_gguf* g);
+int64_t axf_gguf_n_tensors(const axf_gguf* g);
+/* KV access with the reference's typed accessors and coercions
+ * (gguf_loader.cpp:222-296): a missing key, or a stored type that the
+ * accessor does not convert, returns def.  axf_gguf_kv_type gives the value
+ * type tag (0 u8 .. 12 f64, 8 string, 9 array) or -1. */
+int axf_gguf_kv_type(const axf_gguf* g, const char* key);
+uint64_t axf_gguf_get_u64(const axf_gguf* g, const char* key, uint64_t def);
+uint32_t axf_gguf_get_u32(const axf_gguf* g, const char* key, uint32_t def);
+int32_t axf_gguf_get_i32(const axf_gguf* g, const char* key, int32_t def);
+float axf_gguf_get_f32(const axf_gguf* g, const char* key, float def);
+int axf_gguf_get_bool(const axf_gguf* g, const char* key, int def);
+/* string value; *s stays valid until axf_gguf_close */
+int axf_gguf_get_str(const axf_gguf* g, const char* key, const char** s, size_t* len);
+uint64_t axf_gguf_get_array_count(const axf_gguf* g, const char* key);
+int axf_gguf_get_array_type(const axf_gguf* g, const char* key); /* element tag or -1 */
+int axf_gguf_get_array_str(const axf_gguf* g, const char* key, uint64_t i, const char** s,
+                           size_t* len);
+int axf_gguf_get_array_data(const axf_gguf* g, const char* key, const void** data,
+                            size_t* bytes);
+
+typedef struct {
+    const char* name;   /* valid until axf_gguf_close */
+    int n_dims;
+    int64_t shape[4];   /* GGML order: shape[0] is the innermost (columns) */
+    int ggml_type;      /* 0 F32, 12 Q4_K, 14 Q6_K, ... (the AXF_TYPE_* values) */
+    uint64_t offset;    /* within the data blob */
+    uint64_t nbytes;    /* gguf_tensor_nbytes; 0 for types the reference does not size */
+    const void* data;   /* into the mapping; NULL when the range leaves the file */
+} axf_gguf_tensor;
+/* GgufReader::tensor_info / weight_tensor (zero-copy view). */
+int axf_gguf_tensor_info(const axf_gguf* g, int64_t i, axf_gguf_tensor* out);
+int64_t axf_gguf_find_tensor(const axf_gguf* g, const char* name); /* index or -1 */
+/* gguf_tensor_nbytes over ggml_type_to_dtype (include/axonforge/dtype.hpp:107-155)
+ * and gguf_type_pod_size (:87-104). */
+size_t axf_gguf_type_nbytes(int ggml_type, int64_t numel);
+size_t axf_gguf_pod_size(int type_tag);
+
+/* ModelConfig of Engine::from_gguf (src/engine.cpp:79-118): <arch>.block_count,
+ * .embedding_length, .feed_forward_length, .attention.head_count(_kv),
+ * .context_length (default 4096), .attention.layer_norm_rms_epsilon (1e-5),
+ * .rope.freq_base (10000), .rope.scaling.alpha (hunyuan-dense theta scaling),
+ * vocabulary = length of tokenizer.ggml.tokens, BOS/EOS ids (defaults 1 / 2). */
+typedef struct {
+    char arch[64];
+    int n_layer, n_embd, ffn_dim, n_heads, n_kv_heads, head_dim, max_seq_len, n_vocab;
+    float rms_eps, rope_theta, rope_scaling_alpha;
+    int weight_type; /* GGML type of the file's first tensor, -1 if none */
+    int32_t bos_id, eos_id;
+} axf_gguf_model_config;
+int axf_gguf_read_model_config(const axf_gguf* g, axf_gguf_model_config* out);
+
 /* ---- LLaMA-family decoder on the device (llama_generate's `-b hip` hook,
  *      the model-level branch of llama_model.cpp:1633-1642) ----------------- */
 typedef struct axf_llama axf_llama;
@@ -215,7 +282,21 @@ int axf_llama_set_tensor(axf_llama* m, const char* name, int qtype, const void* 
                          size_t bytes);
 /* Upload all registered tensors once and allocate the KV cache and buffers. */
 int axf_llama_load(axf_llama* m);
+/* Register every model tensor of an open GGUF file (the names build_weights
+ * reads, llama_model.cpp:975-1006) straight from the mapping and load.  F32,
+ * Q4_K and Q6_K tensors; per-head q/k norms (attn_q_norm / attn_k_norm) are
+ * AXF_ERR_UNSUPPORTED. */
+int axf_llama_load_gguf(axf_llama* m, const axf_gguf* g);
+/* Engine::from_gguf + the model construction of llama_generate_cpu_impl
+ * (llama_model.cpp:1508-1518): hyperparameters from the file's metadata with
+ * the reference's defaults, context = min(context_length, max_context_len)
+ * (max_context_len <= 0: 4096, LlamaConfig's default), weights uploaded from
+ * the mapping.  The file is closed before returning. */
+int axf_llama_from_gguf(axf_ctx* ctx, const char* path, int max_context_len, axf_llama** out);
 size_t axf_llama_device_bytes(axf_llama* m);
+/* The hyperparameters the model was created with (no reference counterpart;
+ * for callers of axf_llama_from_gguf). */
+int axf_llama_get_hparams(const axf_llama* m, axf_llama_hparams* hp);
 /* Residual stream / KV access (host buffers). */
 int axf_llama_set_x(axf_llama* m, const float* x);
 int axf_llama_get_x(axf_llama* m, float* x);
@@ -228,8 +309,8 @@ int axf_llama_forward_layer(axf_llama* m, int layer, int pos);
 int axf_llama_forward_token(axf_llama* m, int token, int pos);
 /* Batched prefill: replaces llama_forward_batch (llama_model.cpp:1339-1462).
  * Runs tokens[0..T) at positions pos_start..pos_start+T-1 (K/V rows written),
- * Q4_K projections as T-token GEMMs, Q6_K ones with the multi-token kernel,
- * causal attention per row; leaves the last row's logits (get_logits) and,
+ * the projections as T-token GEMMs (matrix cores from 8 tokens up), causal
+ * attention per row; leaves the last row's logits (get_logits) and,
  * as the reference leaves s.x, that row after the final RMSNorm (get_x).
  * Long prompts run in chunks of up to 256 tokens. */
 int axf_llama_forward_batch(axf_llama* m, const int32_t* tokens, int T, int pos_start);

@@ -42,6 +42,38 @@ class LlamaHparams(C.Structure):
     ]
 
 
+class GgufTensor(C.Structure):
+    _fields_ = [
+        ("name", C.c_char_p),
+        ("n_dims", C.c_int),
+        ("shape", C.c_int64 * 4),
+        ("ggml_type", C.c_int),
+        ("offset", C.c_uint64),
+        ("nbytes", C.c_uint64),
+        ("data", C.c_void_p),
+    ]
+
+
+class GgufModelConfig(C.Structure):
+    _fields_ = [
+        ("arch", C.c_char * 64),
+        ("n_layer", C.c_int),
+        ("n_embd", C.c_int),
+        ("ffn_dim", C.c_int),
+        ("n_heads", C.c_int),
+        ("n_kv_heads", C.c_int),
+        ("head_dim", C.c_int),
+        ("max_seq_len", C.c_int),
+        ("n_vocab", C.c_int),
+        ("rms_eps", C.c_float),
+        ("rope_theta", C.c_float),
+        ("rope_scaling_alpha", C.c_float),
+        ("weight_type", C.c_int),
+        ("bos_id", C.c_int32),
+        ("eos_id", C.c_int32),
+    ]
+
+
 vp = C.c_void_p
 i32 = C.c_int
 i64 = C.c_int64
@@ -96,6 +128,33 @@ SIGNATURES: dict[str, list] = {
     "axf_llama_destroy": [vp],
     "axf_llama_set_tensor": [vp, C.c_char_p, i32, vp, sz],
     "axf_llama_load": [vp],
+    "axf_llama_load_gguf": [vp, vp],
+    "axf_llama_get_hparams": [vp, C.POINTER(LlamaHparams)],
+    "axf_llama_from_gguf": [vp, C.c_char_p, i32, C.POINTER(vp)],
+    "axf_gguf_open": [C.c_char_p, C.POINTER(vp)],
+    "axf_gguf_close": [vp],
+    "axf_gguf_version": [vp],
+    "axf_gguf_alignment": [vp],
+    "axf_gguf_data_offset": [vp],
+    "axf_gguf_file_size": [vp],
+    "axf_gguf_n_kv": [vp],
+    "axf_gguf_n_tensors": [vp],
+    "axf_gguf_kv_type": [vp, C.c_char_p],
+    "axf_gguf_get_u64": [vp, C.c_char_p, u64],
+    "axf_gguf_get_u32": [vp, C.c_char_p, C.c_uint32],
+    "axf_gguf_get_i32": [vp, C.c_char_p, C.c_int32],
+    "axf_gguf_get_f32": [vp, C.c_char_p, f32],
+    "axf_gguf_get_bool": [vp, C.c_char_p, i32],
+    "axf_gguf_get_str": [vp, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(sz)],
+    "axf_gguf_get_array_count": [vp, C.c_char_p],
+    "axf_gguf_get_array_type": [vp, C.c_char_p],
+    "axf_gguf_get_array_str": [vp, C.c_char_p, u64, C.POINTER(C.c_char_p), C.POINTER(sz)],
+    "axf_gguf_get_array_data": [vp, C.c_char_p, C.POINTER(vp), C.POINTER(sz)],
+    "axf_gguf_tensor_info": [vp, i64, C.POINTER(GgufTensor)],
+    "axf_gguf_find_tensor": [vp, C.c_char_p],
+    "axf_gguf_type_nbytes": [i32, i64],
+    "axf_gguf_pod_size": [i32],
+    "axf_gguf_read_model_config": [vp, C.POINTER(GgufModelConfig)],
     "axf_llama_device_bytes": [vp],
     "axf_llama_set_x": [vp, vp],
     "axf_llama_get_x": [vp, vp],
@@ -115,6 +174,20 @@ _RESTYPES = {
     "axf_hip_last_error": C.c_char_p,
     "axf_row_bytes": sz,
     "axf_llama_device_bytes": sz,
+    "axf_gguf_version": C.c_uint32,
+    "axf_gguf_alignment": u64,
+    "axf_gguf_data_offset": u64,
+    "axf_gguf_file_size": u64,
+    "axf_gguf_n_kv": i64,
+    "axf_gguf_n_tensors": i64,
+    "axf_gguf_get_u64": u64,
+    "axf_gguf_get_u32": C.c_uint32,
+    "axf_gguf_get_i32": C.c_int32,
+    "axf_gguf_get_f32": f32,
+    "axf_gguf_get_array_count": u64,
+    "axf_gguf_find_tensor": i64,
+    "axf_gguf_type_nbytes": sz,
+    "axf_gguf_pod_size": sz,
 }
 
 

@@ -37,6 +37,7 @@ SOURCES = [
     "capi.cpp",
     "host/synth.cpp",
     "host/llama_hip.cpp",
+    "host/gguf.cpp",
     "host/hip_backend.cpp",
 ]
 

@@ -690,6 +690,12 @@ int axf_llama_load(axf_llama* m) {
 
 size_t axf_llama_device_bytes(axf_llama* m) { return m ? m->dev_bytes : 0; }
 
+int axf_llama_get_hparams(const axf_llama* m, axf_llama_hparams* hp) {
+    if (!m || !hp) return fail(AXF_ERR_INVALID_ARG, "axf_llama_get_hparams: null argument");
+    *hp = m->hp;
+    return AXF_OK;
+}
+
 #define LL_LOADED(m)                                                                       \
     if (!(m)) return fail(AXF_ERR_INVALID_ARG, std::string(__func__) + ": null model");     \
     if (!(m)->loaded) return fail(AXF_ERR_STATE, std::string(__func__) + ": model not loaded")

@@ -132,6 +132,22 @@ class LlamaHip:
         call("axf_llama_load", self.handle)
         del keep
 
+    @classmethod
+    def from_gguf(cls, ctx: hip.Context, path, max_context_len: int = 0) -> "LlamaHip":
+        """Load a GGUF file onto the device (axf_llama_from_gguf): hyperparameters
+        from its metadata, weights uploaded from the file mapping."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        h = C.c_void_p()
+        call("axf_llama_from_gguf", ctx.handle, str(path).encode(), int(max_context_len),
+             C.byref(h))
+        self.handle = h
+        c = LlamaHparams()
+        call("axf_llama_get_hparams", self.handle, C.byref(c))
+        self.hp = Hparams(c.n_layer, c.n_embd, c.n_heads, c.n_kv_heads, c.ffn_dim, c.n_vocab,
+                          c.n_ctx, c.rms_eps, c.rope_theta)
+        return self
+
     def close(self) -> None:
         if self.handle:
             call("axf_llama_destroy", self.handle)
