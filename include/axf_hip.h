@@ -130,6 +130,33 @@ int axf_hip_gemm_q6k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* 
  * device int. */
 int axf_hip_argmax_f32(axf_ctx* ctx, int* idx_dev, const float* x, int n);
 
+/* Sampling parameters of LlamaConfig (include/axonforge/models/llama.hpp:18-33). */
+typedef struct {
+    float temperature;      /* <= 0: greedy (std::max_element) */
+    int top_k;              /* <= 0 or >= n_vocab: the whole vocabulary */
+    float top_p;            /* 1: no nucleus cut */
+    float rep_penalty;      /* 1: no repetition penalty */
+    int rep_penalty_last_n; /* window of the penalty */
+    uint32_t seed;          /* std::mt19937 seed; the reference uses 42 */
+    int32_t eos_id;         /* generation stops before this token; -1: none */
+} axf_sampling;
+
+/* One token choice: the reference's apply_rep_penalty over the last
+ * rep_penalty_last_n of hist[0..n_hist) (llama_model.cpp:1595-1605; applied to
+ * logits_dev in place, as the reference does to state.logits), then sample()
+ * (:1466-1498) with the uniform draw r.  *token (host) receives the id.  The
+ * device path sorts at most 16384 candidates: ceil(n_vocab / 4096) *
+ * min(k, 4096) must not exceed it (AXF_ERR_UNSUPPORTED otherwise; e.g. top_k
+ * up to 431 at n_vocab 151936, 2048 at 32000, any k at n_vocab <= 16384).
+ * Among exactly equal scores the lower index ranks first. */
+int axf_hip_sample(axf_ctx* ctx, float* logits_dev, int n_vocab, const axf_sampling* s,
+                   const int32_t* hist, int n_hist, float r, int32_t* token);
+/* The reference's random stream: the first n outputs of std::mt19937(seed), and
+ * the first n std::uniform_real_distribution<float>(0, 1) draws from it as
+ * libstdc++ computes them (one 32-bit output each). */
+int axf_mt19937(uint32_t seed, uint32_t* out, int n);
+int axf_sampling_uniforms(uint32_t seed, float* out, int n);
+
 /* ---- decode-step operations (llama_forward_token, llama_model.cpp:1207-1333) */
 
 /* y = w*(x*s), s = 1/sqrt(mean(x^2)+eps): rms_norm_out (llama_model.cpp:396-419).
@@ -324,6 +351,18 @@ int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_
  * llama_forward_token path) instead. */
 int axf_llama_generate_ex(axf_llama* m, const int32_t* prompt, int n_prompt, int n_gen,
                           int32_t* out_tokens, int use_graph, int batched_prefill);
+/* The generation loop of llama_generate_cpu_impl (llama_model.cpp:1590-1624)
+ * with sampling on the device: the prompt (BOS already in place: the caller
+ * prepends it as :1563-1566 does) is prefilled (one batch when n_prompt > 1),
+ * then each step applies the repetition penalty over the prompt and the tokens
+ * so far, samples (temperature / top-k / top-p, the uniform draws of
+ * std::mt19937(s->seed) precomputed on the host) and decodes the token, one
+ * captured HIP graph per step when use_graph != 0.  Stops before s->eos_id
+ * (not emitted) and when the context is full; *n_out = tokens written to out
+ * (at most max_new_tokens). */
+int axf_llama_generate_sampled(axf_llama* m, const int32_t* prompt, int n_prompt,
+                               int max_new_tokens, const axf_sampling* s, int32_t* out,
+                               int* n_out, int use_graph);
 /* Benchmark helper (no reference counterpart): mean milliseconds of `reps`
  * axf_llama_forward_batch calls on T synthetic tokens at positions 0..T-1,
  * after one untimed call (HIP events on the context stream). */

@@ -42,6 +42,18 @@ class LlamaHparams(C.Structure):
     ]
 
 
+class Sampling(C.Structure):
+    _fields_ = [
+        ("temperature", C.c_float),
+        ("top_k", C.c_int),
+        ("top_p", C.c_float),
+        ("rep_penalty", C.c_float),
+        ("rep_penalty_last_n", C.c_int),
+        ("seed", C.c_uint32),
+        ("eos_id", C.c_int32),
+    ]
+
+
 class GgufTensor(C.Structure):
     _fields_ = [
         ("name", C.c_char_p),
@@ -108,6 +120,9 @@ SIGNATURES: dict[str, list] = {
     "axf_hip_gemm_q6k_q8": [vp, vp, vp, vp, i32, i32, i32, sz],
     "axf_hip_gemm_q6k_q8_path": [vp, vp, vp, vp, i32, i32, i32, sz, i32],
     "axf_hip_argmax_f32": [vp, vp, vp, i32],
+    "axf_hip_sample": [vp, vp, i32, C.POINTER(Sampling), vp, i32, f32, C.POINTER(C.c_int32)],
+    "axf_mt19937": [C.c_uint32, vp, i32],
+    "axf_sampling_uniforms": [C.c_uint32, vp, i32],
     "axf_hip_rmsnorm": [vp, vp, vp, vp, vp, i32, f32],
     "axf_rope_table": [vp, vp, i32, f32, i32],
     "axf_hip_rope": [vp, vp, vp, i32, i32, i32, vp, vp],
@@ -165,6 +180,8 @@ SIGNATURES: dict[str, list] = {
     "axf_llama_forward_token": [vp, i32, i32],
     "axf_llama_generate": [vp, vp, i32, i32, vp, i32],
     "axf_llama_generate_ex": [vp, vp, i32, i32, vp, i32, i32],
+    "axf_llama_generate_sampled": [vp, vp, i32, i32, C.POINTER(Sampling), vp, C.POINTER(i32),
+                                   i32],
     "axf_llama_forward_batch": [vp, vp, i32, i32],
     "axf_llama_bench_prefill": [vp, i32, i32, C.POINTER(f32)],
     "axf_llama_bench_decode": [vp, i32, i32, i32, C.POINTER(f32)],

@@ -34,10 +34,12 @@ SOURCES = [
     "kernels/gemm_mfma.hip",
     "kernels/ops.hip",
     "kernels/attention.hip",
+    "kernels/sample.hip",
     "capi.cpp",
     "host/synth.cpp",
     "host/llama_hip.cpp",
     "host/gguf.cpp",
+    "host/sampling.cpp",
     "host/hip_backend.cpp",
 ]
 

@@ -314,6 +314,38 @@ int axf_hip_argmax_f32(axf_ctx* ctx, int* idx_dev, const float* x, int n) {
     return AXF_OK;
 }
 
+int axf_hip_sample(axf_ctx* ctx, float* logits_dev, int n_vocab, const axf_sampling* s,
+                   const int32_t* hist, int n_hist, float r, int32_t* token) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(logits_dev && s && token && n_vocab > 0 && n_hist >= 0 && (n_hist == 0 || hist),
+                "bad arguments");
+    const int n_cand = sample_candidates(n_vocab, sample_k(*s, n_vocab));
+    if (n_cand == 0)
+        return fail(AXF_ERR_UNSUPPORTED, "axf_hip_sample: top_k too large for the device sampler");
+    // scratch: candidates | history | history count | token
+    const size_t hist_off = (size_t)n_cand * 8;
+    const size_t bytes = hist_off + (size_t)(n_hist + 2) * 4;
+    void* scratch = nullptr;
+    int rc = ctx_scratch(ctx, bytes, &scratch);
+    if (rc) return rc;
+    auto* cand = static_cast<uint64_t*>(scratch);
+    int* d_hist = reinterpret_cast<int*>(static_cast<uint8_t*>(scratch) + hist_off);
+    int* d_hist_n = d_hist + n_hist;
+    int* d_tok = d_hist_n + 1;
+    if (s->rep_penalty != 1.0f && n_hist > 0) {
+        AXF_HIP(hipMemcpyAsync(d_hist, hist, (size_t)n_hist * 4, hipMemcpyHostToDevice,
+                               ctx->stream));
+        AXF_HIP(hipMemcpyAsync(d_hist_n, &n_hist, 4, hipMemcpyHostToDevice, ctx->stream));
+        AXF_HIP(launch_rep_penalty(logits_dev, d_hist, d_hist_n, s->rep_penalty_last_n,
+                                   s->rep_penalty, n_vocab, ctx->stream));
+    }
+    AXF_HIP(launch_sample(d_tok, cand, logits_dev, n_vocab, s->temperature, s->top_k, s->top_p,
+                          nullptr, r, nullptr, nullptr, nullptr, nullptr, nullptr, ctx->stream));
+    AXF_HIP(hipMemcpyAsync(token, d_tok, 4, hipMemcpyDeviceToHost, ctx->stream));
+    AXF_HIP(hipStreamSynchronize(ctx->stream));
+    return AXF_OK;
+}
+
 int axf_hip_rmsnorm(axf_ctx* ctx, float* y, void* yq8, const float* x, const float* w, int n,
                     float eps) {
     AXF_CHECK_CTX(ctx);

@@ -141,5 +141,21 @@ hipError_t launch_silu(float* y, const float* x, int n, hipStream_t st);
 hipError_t launch_mul(float* y, const float* a, const float* b, int n, hipStream_t st);
 hipError_t launch_set_int(int* p, int v, hipStream_t st);
 hipError_t launch_push_token(int* tokens, int* step, const int* tok, hipStream_t st);
+// Device sampler (kernels/sample.hip).  sample_candidates returns the number of
+// candidate keys (uint64) launch_sample needs in `cand`, 0 when k is beyond
+// the device path.
+int sample_candidates(int n_vocab, int k);
+hipError_t launch_rep_penalty(float* logits, const int* hist, const int* hist_n, int last_n,
+                              float penalty, int n_vocab, hipStream_t st);
+hipError_t launch_sample(int* out, uint64_t* cand, const float* logits, int n_vocab,
+                         float temperature, int top_k, float top_p, const float* r_table,
+                         float r_fixed, int* tokens, int* step, int* pos, int* hist, int* hist_n,
+                         hipStream_t st);
+void sampling_uniforms(uint32_t seed, float* out, int n);
+// effective k of sample() (llama_model.cpp:1473): 1 for greedy
+inline int sample_k(const axf_sampling& s, int n_vocab) {
+    if (!(s.temperature > 0.f)) return 1;
+    return (s.top_k > 0 && s.top_k < n_vocab) ? s.top_k : n_vocab;
+}
 
 }  // namespace axf

@@ -92,10 +92,19 @@ struct axf_llama {
           *pf_gu = nullptr, *pf_part = nullptr;
     uint8_t *pf_q8 = nullptr, *pf_gemm = nullptr;
 
-    // graph[0]: generation step (records the token, advances the position);
-    // graph[1]: fixed-position step used to time decode at a given context
-    hipGraph_t graph[2] = {nullptr, nullptr};
-    hipGraphExec_t exec[2] = {nullptr, nullptr};
+    // sampled generation (allocated on first use): penalty history (prompt and
+    // generated tokens) and its length, the step's uniform draws, sort keys
+    int *d_hist = nullptr, *d_hist_n = nullptr;
+    float* d_r = nullptr;
+    uint64_t* d_cand = nullptr;
+    int cand_cap = 0;
+
+    // graph[0]: greedy generation step (records the token, advances the position);
+    // graph[1]: fixed-position step used to time decode at a given context;
+    // graph[2]: sampled generation step, captured for the parameters in graph_smp
+    hipGraph_t graph[3] = {nullptr, nullptr, nullptr};
+    hipGraphExec_t exec[3] = {nullptr, nullptr, nullptr};
+    axf_sampling graph_smp{};
 };
 
 namespace {
@@ -343,7 +352,28 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
 
 // Whole step: embedding of *d_token (or `token`), layers, final norm, head,
 // argmax into d_token (+ tokens[step++] and pos++ when record != 0).
-hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, bool record) {
+// The step's token choice: greedy argmax, or penalty + sampler (smp) with the
+// draw r_table[*step] and the token appended to the penalty history.
+hipError_t enqueue_pick(axf_llama* m, bool record, bool advance_pos, const axf_sampling* smp) {
+    const auto& hp = m->hp;
+    hipStream_t st = m->ctx->stream;
+    if (!smp)
+        return launch_argmax(m->d_token, m->arg_v, m->arg_i, m->logits, hp.n_vocab,
+                             record ? m->d_tokens : nullptr, record ? m->d_step : nullptr,
+                             advance_pos ? m->d_pos : nullptr, st);
+    if (smp->rep_penalty != 1.0f) {
+        hipError_t e = launch_rep_penalty(m->logits, m->d_hist, m->d_hist_n,
+                                          smp->rep_penalty_last_n, smp->rep_penalty, hp.n_vocab, st);
+        if (e != hipSuccess) return e;
+    }
+    return launch_sample(m->d_token, m->d_cand, m->logits, hp.n_vocab, smp->temperature,
+                         smp->top_k, smp->top_p, m->d_r, 0.f, record ? m->d_tokens : nullptr,
+                         record ? m->d_step : nullptr, advance_pos ? m->d_pos : nullptr,
+                         m->d_hist, m->d_hist_n, st);
+}
+
+hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, bool record,
+                        const axf_sampling* smp = nullptr) {
     const auto& hp = m->hp;
     hipStream_t st = m->ctx->stream;
     const int* pd = device_state ? m->d_pos : nullptr;
@@ -356,9 +386,7 @@ hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, boo
     if ((e = gemv_norm(m->output, m->logits, m->x, m->output_norm, hp.rms_eps, hp.n_vocab,
                        hp.n_embd, false, st)) != hipSuccess)
         return e;
-    return launch_argmax(m->d_token, m->arg_v, m->arg_i, m->logits, hp.n_vocab,
-                         record ? m->d_tokens : nullptr, record ? m->d_step : nullptr,
-                         (device_state && record) ? m->d_pos : nullptr, st);
+    return enqueue_pick(m, record, device_state && record, smp);
 }
 
 // ---------------------------------------------------------------------------
@@ -527,17 +555,55 @@ int forward_batch(axf_llama* m, const int32_t* tokens, int T, int pos0) {
 }
 
 // kind 0: generation step; kind 1: fixed-position step (no token record, no pos advance)
-int ensure_graph(axf_llama* m, int kind) {
+bool same_sampling(const axf_sampling& a, const axf_sampling& b) {
+    return a.temperature == b.temperature && a.top_k == b.top_k && a.top_p == b.top_p &&
+           a.rep_penalty == b.rep_penalty && a.rep_penalty_last_n == b.rep_penalty_last_n;
+}
+
+int ensure_graph(axf_llama* m, int kind, const axf_sampling* smp = nullptr) {
+    if (kind == 2 && m->exec[2] && !same_sampling(m->graph_smp, *smp)) {
+        LL_HIP(hipGraphExecDestroy(m->exec[2]));
+        LL_HIP(hipGraphDestroy(m->graph[2]));
+        m->exec[2] = nullptr;
+        m->graph[2] = nullptr;
+    }
     if (m->exec[kind]) return AXF_OK;
     hipStream_t st = m->ctx->stream;
     LL_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    hipError_t e = enqueue_step(m, true, 0, 0, kind == 0);
+    hipError_t e = enqueue_step(m, true, 0, 0, kind != 1, kind == 2 ? smp : nullptr);
     hipGraph_t g = nullptr;
     hipError_t e2 = hipStreamEndCapture(st, &g);
     if (e != hipSuccess) return hip_fail(e, "axf_llama: capture");
     if (e2 != hipSuccess) return hip_fail(e2, "axf_llama: hipStreamEndCapture");
     m->graph[kind] = g;
     LL_HIP(hipGraphInstantiate(&m->exec[kind], g, nullptr, nullptr, 0));
+    if (kind == 2) m->graph_smp = *smp;
+    return AXF_OK;
+}
+
+int sampler_alloc(axf_llama* m, int n_cand) {
+    void* p;
+    if (!m->d_hist) {
+        const size_t n = (size_t)m->hp.n_ctx + 2;
+        LL_TRY(dalloc(m, n * 4, &p));
+        m->d_hist = static_cast<int*>(p);
+        LL_TRY(dalloc(m, 16, &p));
+        m->d_hist_n = static_cast<int*>(p);
+        LL_TRY(dalloc(m, n * 4, &p));
+        m->d_r = static_cast<float*>(p);
+    }
+    if (n_cand > m->cand_cap) {
+        // the sampled graph holds the old pointer: it is recaptured below
+        LL_TRY(dalloc(m, (size_t)n_cand * 8, &p));
+        m->d_cand = static_cast<uint64_t*>(p);
+        m->cand_cap = n_cand;
+        if (m->exec[2]) {
+            LL_HIP(hipGraphExecDestroy(m->exec[2]));
+            LL_HIP(hipGraphDestroy(m->graph[2]));
+            m->exec[2] = nullptr;
+            m->graph[2] = nullptr;
+        }
+    }
     return AXF_OK;
 }
 
@@ -579,7 +645,7 @@ int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out)
 int axf_llama_destroy(axf_llama* m) {
     if (!m) return AXF_OK;
     (void)hipStreamSynchronize(m->ctx->stream);
-    for (int k = 0; k < 2; k++) {
+    for (int k = 0; k < 3; k++) {
         if (m->exec[k]) (void)hipGraphExecDestroy(m->exec[k]);
         if (m->graph[k]) (void)hipGraphDestroy(m->graph[k]);
     }
@@ -847,6 +913,65 @@ int axf_llama_generate_ex(axf_llama* m, const int32_t* prompt, int n_prompt, int
         LL_HIP(hipMemcpyAsync(out_tokens, m->d_tokens, (size_t)n_gen * 4, hipMemcpyDeviceToHost,
                               st));
     LL_HIP(hipStreamSynchronize(st));
+    return AXF_OK;
+}
+
+int axf_llama_generate_sampled(axf_llama* m, const int32_t* prompt, int n_prompt,
+                               int max_new_tokens, const axf_sampling* s, int32_t* out,
+                               int* n_out, int use_graph) {
+    LL_LOADED(m);
+    if (!prompt || n_prompt <= 0 || max_new_tokens < 0 || !s || !n_out ||
+        (max_new_tokens && !out))
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_generate_sampled: bad arguments");
+    *n_out = 0;
+    const auto& hp = m->hp;
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= hp.n_vocab)
+            return fail(AXF_ERR_INVALID_ARG, "axf_llama_generate_sampled: prompt token out of range");
+    if (n_prompt > hp.n_ctx)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_generate_sampled: prompt longer than the context");
+    const int n_cand = sample_candidates(hp.n_vocab, sample_k(*s, hp.n_vocab));
+    if (n_cand == 0)
+        return fail(AXF_ERR_UNSUPPORTED,
+                    "axf_llama_generate_sampled: top_k too large for the device sampler");
+    // tokens are emitted while n_past < n_ctx (llama_model.cpp:1613); n_past
+    // starts at n_prompt
+    int n_gen = hp.n_ctx - n_prompt;
+    if (n_gen > max_new_tokens) n_gen = max_new_tokens;
+    if (n_gen <= 0) return AXF_OK;
+    LL_TRY(sampler_alloc(m, n_cand));
+    hipStream_t st = m->ctx->stream;
+    std::vector<float> r((size_t)n_gen, 0.f);
+    if (s->temperature > 0.f) sampling_uniforms(s->seed, r.data(), n_gen);
+    LL_HIP(hipMemcpyAsync(m->d_r, r.data(), r.size() * 4, hipMemcpyHostToDevice, st));
+    LL_HIP(hipMemcpyAsync(m->d_hist, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, st));
+    LL_HIP(launch_set_int(m->d_hist_n, n_prompt, st));
+    LL_HIP(launch_set_int(m->d_step, 0, st));
+    if (use_graph) LL_TRY(ensure_graph(m, 2, s));
+    // prefill: one batch for a multi-token prompt (:1568-1576), else the
+    // single-token forward (its greedy pick is overwritten below)
+    if (n_prompt > 1)
+        LL_TRY(forward_batch(m, prompt, n_prompt, 0));
+    else
+        LL_HIP(enqueue_step(m, false, prompt[0], 0, false));
+    LL_HIP(launch_set_int(m->d_pos, n_prompt, st));
+    // token 0: penalty over the prompt, sample with draw 0 (:1607-1609)
+    LL_HIP(enqueue_pick(m, true, false, s));
+    for (int i = 1; i < n_gen; i++) {
+        if (use_graph)
+            LL_HIP(hipGraphLaunch(m->exec[2], st));
+        else
+            LL_HIP(enqueue_step(m, true, 0, 0, true, s));
+    }
+    LL_HIP(hipMemcpyAsync(out, m->d_tokens, (size_t)n_gen * 4, hipMemcpyDeviceToHost, st));
+    LL_HIP(hipStreamSynchronize(st));
+    int n = n_gen;
+    for (int i = 0; i < n_gen; i++)
+        if (out[i] == s->eos_id) {  // stops before EOS; EOS is not emitted (:1612)
+            n = i;
+            break;
+        }
+    *n_out = n;
     return AXF_OK;
 }
 

@@ -145,6 +145,19 @@ class Context:
             call("axf_hip_gemm_q6k_q8_path", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
                  C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb), int(path))
 
+    def sample(self, logits: int, n_vocab: int, temperature: float = 1.0, top_k: int = 40,
+               top_p: float = 1.0, rep_penalty: float = 1.0, rep_penalty_last_n: int = 64,
+               hist=(), r: float = 0.0) -> int:
+        """One token choice (axf_hip_sample); the penalty is applied to the device
+        logits in place."""
+        s = sampling(temperature, top_k, top_p, rep_penalty, rep_penalty_last_n)
+        h = np.ascontiguousarray(hist, np.int32)
+        tok = C.c_int32()
+        call("axf_hip_sample", self.handle, C.c_void_p(int(logits)), n_vocab, C.byref(s),
+             h.ctypes.data_as(C.c_void_p) if h.size else None, int(h.size), float(r),
+             C.byref(tok))
+        return int(tok.value)
+
     def argmax(self, idx: int, x: int, n: int) -> None:
         call("axf_hip_argmax_f32", self.handle, C.c_void_p(int(idx)), C.c_void_p(int(x)), n)
 
@@ -225,6 +238,27 @@ def synth_quantize(qtype: int, x: np.ndarray) -> np.ndarray:
     out = np.empty(x.size // 256 * bb, np.uint8)
     call("axf_synth_quantize", qtype, out.ctypes.data_as(C.c_void_p), x.ctypes.data_as(C.c_void_p),
          C.c_int64(x.size))
+    return out
+
+
+def sampling(temperature: float = 1.0, top_k: int = 40, top_p: float = 1.0,
+             rep_penalty: float = 1.0, rep_penalty_last_n: int = 64, seed: int = 42,
+             eos_id: int = -1) -> _ffi.Sampling:
+    """axf_sampling with LlamaConfig's defaults (models/llama.hpp:18-33) and the
+    reference's fixed seed 42."""
+    return _ffi.Sampling(float(temperature), int(top_k), float(top_p), float(rep_penalty),
+                         int(rep_penalty_last_n), int(seed), int(eos_id))
+
+
+def mt19937(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint32)
+    call("axf_mt19937", int(seed), out.ctypes.data_as(C.c_void_p), int(n))
+    return out
+
+
+def sampling_uniforms(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    call("axf_sampling_uniforms", int(seed), out.ctypes.data_as(C.c_void_p), int(n))
     return out
 
 

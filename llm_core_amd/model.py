@@ -197,6 +197,19 @@ class LlamaHip:
         call("axf_llama_forward_batch", self.handle, t.ctypes.data_as(C.c_void_p), int(t.size),
              pos_start)
 
+    def generate_sampled(self, prompt, max_new_tokens: int, use_graph: bool = True,
+                         **sampling) -> np.ndarray:
+        """llama_generate_cpu_impl's loop with the device sampler
+        (axf_llama_generate_sampled); keyword arguments as hip.sampling()."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        s = hip.sampling(**sampling)
+        out = np.zeros(max(1, max_new_tokens), np.int32)
+        n = C.c_int()
+        call("axf_llama_generate_sampled", self.handle, p.ctypes.data_as(C.c_void_p), p.size,
+             int(max_new_tokens), C.byref(s), out.ctypes.data_as(C.c_void_p), C.byref(n),
+             1 if use_graph else 0)
+        return out[:n.value].copy()
+
     def generate(self, prompt, n_gen: int, use_graph: bool = True,
                  batched_prefill: bool = True) -> np.ndarray:
         p = np.ascontiguousarray(prompt, np.int32)

@@ -7,6 +7,7 @@
  */
 #include "axf_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -634,6 +635,99 @@ float orc_top2_margin(const float* x, int n) {
     for (int i = 0; i < n; i++)
         if (i != b && x[i] > second) second = x[i];
     return x[b] - second;
+}
+
+/* ------------------------------------------------------------------------ */
+/* sampling (llama_generate_cpu_impl)                                        */
+/* ------------------------------------------------------------------------ */
+
+/* apply_rep_penalty (llama_model.cpp:1595-1605): the last min(last_n, n_hist)
+ * history ids in order, each occurrence dividing a positive logit by the
+ * penalty or multiplying a non-positive one. */
+void orc_rep_penalty(float* logits, int n_vocab, const int32_t* hist, int n_hist, int last_n,
+                     float penalty) {
+    if (penalty == 1.0f) return;
+    const int win = last_n < n_hist ? last_n : n_hist;
+    for (int i = n_hist - win; i < n_hist; i++) {
+        const int32_t id = hist[i];
+        if (id < 0 || id >= n_vocab) continue;
+        logits[id] = logits[id] > 0.f ? logits[id] / penalty : logits[id] * penalty;
+    }
+}
+
+typedef struct {
+    float v;
+    int32_t i;
+} orc_scored;
+
+/* value descending; equal values by index ascending (the reference's
+ * partial_sort leaves their order unspecified) */
+static int scored_cmp(const void* pa, const void* pb) {
+    const orc_scored* a = (const orc_scored*)pa;
+    const orc_scored* b = (const orc_scored*)pb;
+    if (a->v > b->v) return -1;
+    if (a->v < b->v) return 1;
+    return (a->i > b->i) - (a->i < b->i);
+}
+
+static float fminabs(float m, float d) {
+    d = fabsf(d);
+    return d < m ? d : m;
+}
+
+/* sample() (llama_model.cpp:1466-1498) with the uniform draw r.  *margin is
+ * the distance of the decision from flipping: |r - cum| at the chosen entry
+ * and the one before it, and |cum - top_p| at the nucleus cut (FLT_MAX for
+ * greedy). */
+int orc_sample(const float* logits, int n_vocab, int top_k, float top_p, float temperature,
+               float r, float* margin) {
+    if (margin) *margin = FLT_MAX;
+    if (temperature <= 0.f) return orc_argmax(logits, n_vocab);
+    int k = (top_k > 0 && top_k < n_vocab) ? top_k : n_vocab;
+    orc_scored* sc = (orc_scored*)malloc(sizeof(orc_scored) * (size_t)n_vocab);
+    float* probs = (float*)malloc(sizeof(float) * (size_t)n_vocab);
+    for (int i = 0; i < n_vocab; i++) {
+        sc[i].v = logits[i] / temperature;
+        sc[i].i = i;
+    }
+    qsort(sc, (size_t)n_vocab, sizeof(orc_scored), scored_cmp);
+    const float mx = sc[0].v;
+    float sum = 0.f, m = FLT_MAX;
+    for (int i = 0; i < k; i++) {
+        probs[i] = expf(sc[i].v - mx);
+        sum += probs[i];
+    }
+    for (int i = 0; i < k; i++) probs[i] /= sum;
+    if (top_p < 1.0f) {
+        float cum = 0.f;
+        int cut = k;
+        for (int i = 0; i < k; i++) {
+            cum += probs[i];
+            m = fminabs(m, cum - top_p);
+            if (cum >= top_p) {
+                cut = i + 1;
+                break;
+            }
+        }
+        sum = 0.f;
+        for (int i = 0; i < cut; i++) sum += probs[i];
+        for (int i = 0; i < cut; i++) probs[i] /= sum;
+        k = cut;
+    }
+    float cum = 0.f;
+    int chosen = sc[k - 1].i;
+    for (int i = 0; i < k; i++) {
+        cum += probs[i];
+        m = fminabs(m, r - cum);
+        if (r < cum) {
+            chosen = sc[i].i;
+            break;
+        }
+    }
+    free(sc);
+    free(probs);
+    if (margin) *margin = m;
+    return chosen;
 }
 
 /* ------------------------------------------------------------------------ */

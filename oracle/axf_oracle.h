@@ -76,6 +76,10 @@ float orc_exp_cephes(float x);
 void orc_swiglu(float* gate, const float* up, int n);
 int orc_argmax(const float* x, int n);
 float orc_top2_margin(const float* x, int n);
+void orc_rep_penalty(float* logits, int n_vocab, const int32_t* hist, int n_hist, int last_n,
+                     float penalty);
+int orc_sample(const float* logits, int n_vocab, int top_k, float top_p, float temperature,
+               float r, float* margin);
 
 /* ---- decoder ------------------------------------------------------------- */
 typedef struct {

@@ -54,6 +54,8 @@ def _load_orc() -> C.CDLL:
         "orc_swiglu": ([vp, vp, i32], None),
         "orc_argmax": ([vp, i32], i32),
         "orc_top2_margin": ([vp, i32], f32),
+        "orc_rep_penalty": ([vp, i32, vp, i32, i32, f32], None),
+        "orc_sample": ([vp, i32, i32, f32, f32, f32, C.POINTER(f32)], i32),
         "orc_state_new": ([vp], vp),
         "orc_state_free": ([vp], None),
         "orc_state_logits": ([vp], C.POINTER(C.c_float)),
@@ -223,6 +225,25 @@ def ref_time_decode_step(model: "OracleModel", kv_k: np.ndarray, kv_v: np.ndarra
     t = ref.ref_time_decode_step(C.byref(model.m), _ptr(kv_k), _ptr(kv_v), pos, warmup, steps,
                                  n_threads, C.byref(used), C.byref(last))
     return t, used.value, last.value
+
+
+def rep_penalty(logits: np.ndarray, hist, last_n: int, penalty: float) -> np.ndarray:
+    """apply_rep_penalty (llama_model.cpp:1595-1605) on a copy."""
+    y = np.ascontiguousarray(logits, np.float32).copy()
+    h = np.ascontiguousarray(hist, np.int32)
+    orc.orc_rep_penalty(_ptr(y), y.size, _ptr(h), h.size, int(last_n), float(penalty))
+    return y
+
+
+def sample(logits: np.ndarray, top_k: int, top_p: float, temperature: float,
+           r: float) -> tuple[int, float]:
+    """sample() (llama_model.cpp:1466-1498) with the uniform draw r: (token,
+    distance of the decision from flipping)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    m = C.c_float()
+    tok = orc.orc_sample(_ptr(x), x.size, int(top_k), float(top_p), float(temperature),
+                         float(r), C.byref(m))
+    return int(tok), float(m.value)
 
 
 def top2_margin(x: np.ndarray) -> float:
