@@ -42,6 +42,9 @@ extern "C" {
 
 /* GGML tensor type ids (reference dtype.hpp:107-124: 12 -> Q4_K_M, 14 -> Q6_K). */
 #define AXF_TYPE_F32 0
+#define AXF_TYPE_F16 1
+#define AXF_TYPE_Q5_0 6
+#define AXF_TYPE_Q8_0 8
 #define AXF_TYPE_Q4_K 12
 #define AXF_TYPE_Q6_K 14
 
@@ -124,6 +127,25 @@ int axf_hip_gemm_q4k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* 
                              int T, int cols, size_t row_bytes, int path);
 int axf_hip_gemm_q6k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
                              int T, int cols, size_t row_bytes, int path);
+
+/* Other GGUF weight types of the decode path (LM heads of Qwen / DeepSeek files,
+ * F16 models).  cols is a multiple of 32 for the block types, rows of
+ * cols/32 blocks (34 B Q8_0: fp16 d + 32 int8; 22 B Q5_0: fp16 d, u32 high
+ * bits, 16 B nibbles), 2-byte aligned.
+ * Q8_0 x Q8_0: replaces gemv_q8_0_weight_q8 / q8_0_weight_dot_q8_row
+ * (llama_model.cpp:171-228), the q8_fast branch of gemv_wt_q8 (:825-828). */
+int axf_hip_gemv_q8_0w_q8(axf_ctx* ctx, float* y, const void* W, const void* xq8, int rows,
+                          int cols, size_t row_bytes, int accumulate);
+/* Q8_0 x fp32: q8_0_weight_dot_row (:154-169) in gemv_wt (:701-712); x 16-byte aligned. */
+int axf_hip_gemv_q8_0w_f32(axf_ctx* ctx, float* y, const void* W, const float* x, int rows,
+                           int cols, size_t row_bytes);
+/* Q5_0 x fp32: q5_0_dot_row (:245-267) in gemv_wt (:713-724). */
+int axf_hip_gemv_q5_0_f32(axf_ctx* ctx, float* y, const void* W, const float* x, int rows,
+                          int cols, size_t row_bytes);
+/* F16 x fp32 (+ bias b, may be NULL): gemv_f16_avx2_range (gemv_f16_avx2.cpp:138-153);
+ * W rows of cols halfs, W and x 16-byte aligned, cols % 8 == 0. */
+int axf_hip_gemv_f16_f32(axf_ctx* ctx, float* y, const void* W, const float* x, const float* b,
+                         int rows, int cols);
 
 /* Greedy pick: *idx_dev = first index of the maximum of x[0..n), the
  * std::max_element of sample() (llama_model.cpp:1470-1471).  idx_dev is a

@@ -18,6 +18,9 @@ AXF_ERR_NO_DEVICE = -4
 AXF_ERR_STATE = -5
 
 AXF_TYPE_F32 = 0
+AXF_TYPE_F16 = 1
+AXF_TYPE_Q5_0 = 6
+AXF_TYPE_Q8_0 = 8
 AXF_TYPE_Q4_K = 12
 AXF_TYPE_Q6_K = 14
 
@@ -120,6 +123,10 @@ SIGNATURES: dict[str, list] = {
     "axf_hip_gemm_q6k_q8": [vp, vp, vp, vp, i32, i32, i32, sz],
     "axf_hip_gemm_q6k_q8_path": [vp, vp, vp, vp, i32, i32, i32, sz, i32],
     "axf_hip_argmax_f32": [vp, vp, vp, i32],
+    "axf_hip_gemv_q8_0w_q8": [vp, vp, vp, vp, i32, i32, sz, i32],
+    "axf_hip_gemv_q8_0w_f32": [vp, vp, vp, vp, i32, i32, sz],
+    "axf_hip_gemv_q5_0_f32": [vp, vp, vp, vp, i32, i32, sz],
+    "axf_hip_gemv_f16_f32": [vp, vp, vp, vp, vp, i32, i32],
     "axf_hip_sample": [vp, vp, i32, C.POINTER(Sampling), vp, i32, f32, C.POINTER(C.c_int32)],
     "axf_mt19937": [C.c_uint32, vp, i32],
     "axf_sampling_uniforms": [C.c_uint32, vp, i32],

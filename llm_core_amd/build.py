@@ -35,6 +35,7 @@ SOURCES = [
     "kernels/ops.hip",
     "kernels/attention.hip",
     "kernels/sample.hip",
+    "kernels/gemv_misc.hip",
     "capi.cpp",
     "host/synth.cpp",
     "host/llama_hip.cpp",

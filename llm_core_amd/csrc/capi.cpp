@@ -423,13 +423,83 @@ int axf_hip_add(axf_ctx* ctx, float* y, const float* a, const float* b, int n) {
 int axf_hip_embed(axf_ctx* ctx, float* out, int qtype, const void* W, int token, int rows,
                   int cols) {
     AXF_CHECK_CTX(ctx);
-    AXF_REQUIRE(out && W && cols > 0 && cols % QK_K == 0, "bad arguments");
+    AXF_REQUIRE(out && W && cols > 0, "bad arguments");
     AXF_REQUIRE(token >= 0 && token < rows, "token out of range");
-    AXF_REQUIRE(qtype == AXF_TYPE_Q4_K || qtype == AXF_TYPE_Q6_K, "qtype must be Q4_K or Q6_K");
+    if (qtype == AXF_TYPE_Q8_0 || qtype == AXF_TYPE_Q5_0 || qtype == AXF_TYPE_F16) {
+        AXF_REQUIRE(cols % 32 == 0, "cols must be a multiple of 32");
+        AXF_REQUIRE(aligned(W, 2), "W misaligned");
+        AXF_HIP(launch_embed_misc(qtype, out, W, nullptr, token, 1, cols,
+                                  (long)axf_row_bytes(qtype, cols), ctx->stream));
+        return AXF_OK;
+    }
+    AXF_REQUIRE(cols % QK_K == 0, "cols must be a multiple of 256");
+    AXF_REQUIRE(qtype == AXF_TYPE_Q4_K || qtype == AXF_TYPE_Q6_K,
+                "qtype must be Q4_K, Q6_K, Q8_0, Q5_0 or F16");
     AXF_REQUIRE(qtype == AXF_TYPE_Q6_K ? aligned(W, 2) : aligned(W, 16), "W misaligned");
     const int nb = cols / QK_K;
     AXF_HIP(launch_embed(qtype, out, W, nullptr, token, nb,
                          (long)axf_row_bytes(qtype, cols), ctx->stream));
+    return AXF_OK;
+}
+
+// The other weight types: rows of cols/32 blocks (2-byte aligned) or halfs.
+static int check_misc(const char* fn, int qtype, const void* W, const void* x, const float* y,
+                      int rows, int cols, size_t row_bytes, bool x16) {
+    const std::string f(fn);
+    if (!W || !x || !y) return fail(AXF_ERR_INVALID_ARG, f + ": null pointer");
+    if (rows < 0 || cols < 0) return fail(AXF_ERR_INVALID_ARG, f + ": negative size");
+    if (qtype == AXF_TYPE_F16) {
+        if (cols % 8) return fail(AXF_ERR_INVALID_ARG, f + ": cols must be a multiple of 8");
+        if (!aligned(W, 16)) return fail(AXF_ERR_INVALID_ARG, f + ": W must be 16-byte aligned");
+    } else {
+        if (cols % 32) return fail(AXF_ERR_INVALID_ARG, f + ": cols must be a multiple of 32");
+        if (row_bytes < axf_row_bytes(qtype, cols) || row_bytes % 2)
+            return fail(AXF_ERR_INVALID_ARG, f + ": row_bytes smaller than one row or odd");
+        if (!aligned(W, 2)) return fail(AXF_ERR_INVALID_ARG, f + ": W must be 2-byte aligned");
+    }
+    if (!aligned(x, x16 ? 16 : 4) || !aligned(y, 4))
+        return fail(AXF_ERR_INVALID_ARG, f + ": x or y misaligned");
+    return AXF_OK;
+}
+
+int axf_hip_gemv_q8_0w_q8(axf_ctx* ctx, float* y, const void* W, const void* xq8, int rows,
+                          int cols, size_t row_bytes, int accumulate) {
+    AXF_CHECK_CTX(ctx);
+    int rc = check_misc(__func__, AXF_TYPE_Q8_0, W, xq8, y, rows, cols, row_bytes, false);
+    if (rc) return rc;
+    if (!rows || !cols) return AXF_OK;
+    AXF_HIP(launch_gemv_q8w_q8(y, W, xq8, rows, cols / 32, (long)row_bytes, accumulate,
+                               ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_gemv_q8_0w_f32(axf_ctx* ctx, float* y, const void* W, const float* x, int rows,
+                           int cols, size_t row_bytes) {
+    AXF_CHECK_CTX(ctx);
+    int rc = check_misc(__func__, AXF_TYPE_Q8_0, W, x, y, rows, cols, row_bytes, true);
+    if (rc) return rc;
+    if (!rows || !cols) return AXF_OK;
+    AXF_HIP(launch_gemv_q8w_f32(y, W, x, rows, cols / 32, (long)row_bytes, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_gemv_q5_0_f32(axf_ctx* ctx, float* y, const void* W, const float* x, int rows,
+                          int cols, size_t row_bytes) {
+    AXF_CHECK_CTX(ctx);
+    int rc = check_misc(__func__, AXF_TYPE_Q5_0, W, x, y, rows, cols, row_bytes, false);
+    if (rc) return rc;
+    if (!rows || !cols) return AXF_OK;
+    AXF_HIP(launch_gemv_q5_0_f32(y, W, x, rows, cols / 32, (long)row_bytes, ctx->stream));
+    return AXF_OK;
+}
+
+int axf_hip_gemv_f16_f32(axf_ctx* ctx, float* y, const void* W, const float* x, const float* b,
+                         int rows, int cols) {
+    AXF_CHECK_CTX(ctx);
+    int rc = check_misc(__func__, AXF_TYPE_F16, W, x, y, rows, cols, (size_t)cols * 2, true);
+    if (rc) return rc;
+    if (!rows || !cols) return AXF_OK;
+    AXF_HIP(launch_gemv_f16_f32(y, W, x, b, rows, cols, ctx->stream));
     return AXF_OK;
 }
 
@@ -529,6 +599,9 @@ size_t axf_row_bytes(int qtype, int64_t cols) {
     if (qtype == AXF_TYPE_Q4_K) return (size_t)nb * Q4K_BYTES;
     if (qtype == AXF_TYPE_Q6_K) return (size_t)nb * Q6K_BYTES;
     if (qtype == AXF_TYPE_F32) return (size_t)cols * 4;
+    if (qtype == AXF_TYPE_F16) return (size_t)cols * 2;
+    if (qtype == AXF_TYPE_Q8_0) return (size_t)(cols / 32) * 34;
+    if (qtype == AXF_TYPE_Q5_0) return (size_t)(cols / 32) * 22;
     return 0;
 }
 

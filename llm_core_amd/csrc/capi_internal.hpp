@@ -83,6 +83,17 @@ size_t gemm_mfma_q6k_scratch_bytes(int T, int nb);
 bool gemm_mfma_q6k_ok(const void* W, int rows, int nb, long row_bytes);
 hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
                                    int nb, long row_bytes, void* scratch, hipStream_t st);
+// Other weight types (kernels/gemv_misc.hip): nb = 32-element blocks per row.
+hipError_t launch_gemv_q8w_q8(float* y, const void* W, const void* xq8, int rows, int nb,
+                              long row_bytes, int accumulate, hipStream_t st);
+hipError_t launch_gemv_q8w_f32(float* y, const void* W, const float* x, int rows, int nb,
+                               long row_bytes, hipStream_t st);
+hipError_t launch_gemv_q5_0_f32(float* y, const void* W, const float* x, int rows, int nb,
+                                long row_bytes, hipStream_t st);
+hipError_t launch_gemv_f16_f32(float* y, const void* W, const float* x, const float* bias,
+                               int rows, int cols, hipStream_t st);
+hipError_t launch_embed_misc(int qtype, float* out, const void* W, const int* tok_dev, int tok,
+                             int T, int cols, long row_bytes, hipStream_t st);
 hipError_t launch_dequant_q4k(float* y, const void* W, long nblocks, hipStream_t st);
 hipError_t launch_dequant_q6k(float* y, const void* W, long nblocks, hipStream_t st);
 hipError_t launch_quantize_q8_0(void* y, const float* x, int n, hipStream_t st);

@@ -483,11 +483,17 @@ int axf_llama_load_gguf(axf_llama* m, const axf_gguf* g) {
             t.name.find("attn_k_norm") != std::string::npos)
             return fail(AXF_ERR_UNSUPPORTED,
                         "axf_llama_load_gguf: per-head q/k norms (" + t.name + ") are not supported");
+        // Q8_0 / Q5_0 / F16 only for the embedding and the head (the layer
+        // matrices run the fused Q4_K / Q6_K kernels)
+        const bool head = t.name == "token_embd.weight" || t.name == "output.weight";
+        const bool other = t.ggml_type == AXF_TYPE_Q8_0 || t.ggml_type == AXF_TYPE_Q5_0 ||
+                           t.ggml_type == AXF_TYPE_F16;
         if (t.ggml_type != AXF_TYPE_F32 && t.ggml_type != AXF_TYPE_Q4_K &&
-            t.ggml_type != AXF_TYPE_Q6_K)
+            t.ggml_type != AXF_TYPE_Q6_K && !(head && other))
             return fail(AXF_ERR_UNSUPPORTED, "axf_llama_load_gguf: " + t.name + " has GGML type " +
                                                  std::to_string(t.ggml_type) +
-                                                 " (supported: F32, Q4_K, Q6_K)");
+                                                 (head ? " (supported: Q4_K, Q6_K, Q8_0, Q5_0, F16)"
+                                                       : " (supported: F32, Q4_K, Q6_K)"));
         const uint8_t* p = g->data(t);
         if (!p || t.nbytes == 0)
             return fail(AXF_ERR_INVALID_ARG,

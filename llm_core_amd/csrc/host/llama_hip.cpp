@@ -109,6 +109,10 @@ struct axf_llama {
 
 namespace {
 
+bool misc_type(int qtype) {
+    return qtype == AXF_TYPE_Q8_0 || qtype == AXF_TYPE_Q5_0 || qtype == AXF_TYPE_F16;
+}
+
 int dalloc(axf_llama* m, size_t bytes, void** p) {
     *p = nullptr;
     if (!bytes) return AXF_OK;
@@ -160,6 +164,24 @@ int upload_f32(axf_llama* m, const std::string& name, int n, float** out, bool r
     LL_TRY(dalloc(m, t->bytes, &p));
     LL_TRY(upload(m, p, t->host, t->bytes));
     *out = static_cast<float*>(p);
+    return AXF_OK;
+}
+
+// token_embd / output: also the other GGUF weight types of the reference's
+// head and embedding paths (Q8_0, Q5_0, F16)
+int upload_head(axf_llama* m, const std::string& name, int rows, int cols, DevW* w) {
+    const HostTensor* t;
+    LL_TRY(need(m, name, &t));
+    if (t->qtype != AXF_TYPE_Q4_K && t->qtype != AXF_TYPE_Q6_K && !misc_type(t->qtype))
+        return fail(AXF_ERR_UNSUPPORTED,
+                    "axf_llama_load: " + name + " must be Q4_K, Q6_K, Q8_0, Q5_0 or F16");
+    const size_t rb = axf_row_bytes(t->qtype, cols);
+    if (t->bytes != (size_t)rows * rb)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_load: " + name + " has wrong byte size");
+    void* p;
+    LL_TRY(dalloc(m, t->bytes, &p));
+    LL_TRY(upload(m, p, t->host, t->bytes));
+    *w = DevW{t->qtype, static_cast<uint8_t*>(p), rb};
     return AXF_OK;
 }
 
@@ -271,6 +293,43 @@ hipError_t gemv_norm(const DevW& w, float* y, const float* x, const float* nw, f
     return launch_qgemv(w.qtype, QAct::Norm, swiglu, a, threads, st);
 }
 
+// logits = output * RMSNorm(x) * output_norm.  Q4_K / Q6_K heads fuse the norm
+// into the GEMV prologue; the other types (gemv_wt_q8 / gemv_wt of the
+// reference, llama_model.cpp:767-831) take the normalised row from k_rmsnorm:
+// as Q8_0 activations for Q8_0 weights, fp32 for Q5_0 and F16.  `scratch`
+// holds n_embd floats.
+hipError_t head_logits(axf_llama* m, const float* x, float* scratch, hipStream_t st) {
+    const auto& hp = m->hp;
+    const DevW& w = m->output;
+    if (!misc_type(w.qtype))
+        return gemv_norm(w, m->logits, x, m->output_norm, hp.rms_eps, hp.n_vocab, hp.n_embd,
+                         false, st);
+    const bool q8 = w.qtype == AXF_TYPE_Q8_0;
+    hipError_t e = launch_rmsnorm(scratch, q8 ? m->xq8 : nullptr, x, m->output_norm, hp.n_embd,
+                                  hp.rms_eps, st);
+    if (e != hipSuccess) return e;
+    if (q8)
+        return launch_gemv_q8w_q8(m->logits, w.d, m->xq8, hp.n_vocab, hp.n_embd / 32,
+                                  (long)w.row_bytes, 0, st);
+    if (w.qtype == AXF_TYPE_Q5_0)
+        return launch_gemv_q5_0_f32(m->logits, w.d, scratch, hp.n_vocab, hp.n_embd / 32,
+                                    (long)w.row_bytes, st);
+    return launch_gemv_f16_f32(m->logits, w.d, scratch, nullptr, hp.n_vocab, hp.n_embd, st);
+}
+
+// Embedding rows of T tokens (token ids on the device) or one token.
+hipError_t embed(axf_llama* m, float* out, const int* tok_dev, int tok, int T, hipStream_t st) {
+    const auto& hp = m->hp;
+    const DevW& w = m->tok_embd;
+    if (misc_type(w.qtype))
+        return launch_embed_misc(w.qtype, out, w.d, tok_dev, tok, T, hp.n_embd, (long)w.row_bytes,
+                                 st);
+    if (T == 1 && (!tok_dev || tok_dev == m->d_token))
+        return launch_embed(w.qtype, out, w.d, tok_dev, tok, hp.n_embd / QK_K, (long)w.row_bytes,
+                            st);
+    return launch_embed_rows(w.qtype, out, w.d, tok_dev, T, hp.n_embd / QK_K, (long)w.row_bytes, st);
+}
+
 // Enqueue one decoder layer; pos from device memory when pos_dev != nullptr.
 hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
     const auto& hp = m->hp;
@@ -378,14 +437,11 @@ hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, boo
     hipStream_t st = m->ctx->stream;
     const int* pd = device_state ? m->d_pos : nullptr;
     const int* td = device_state ? m->d_token : nullptr;
-    hipError_t e = launch_embed(m->tok_embd.qtype, m->x, m->tok_embd.d, td, token,
-                                hp.n_embd / QK_K, (long)m->tok_embd.row_bytes, st);
+    hipError_t e = embed(m, m->x, td, token, 1, st);
     if (e != hipSuccess) return e;
     for (int l = 0; l < hp.n_layer; l++)
         if ((e = enqueue_layer(m, l, pd, pos)) != hipSuccess) return e;
-    if ((e = gemv_norm(m->output, m->logits, m->x, m->output_norm, hp.rms_eps, hp.n_vocab,
-                       hp.n_embd, false, st)) != hipSuccess)
-        return e;
+    if ((e = head_logits(m, m->x, m->attn_out, st)) != hipSuccess) return e;
     return enqueue_pick(m, record, device_state && record, smp);
 }
 
@@ -527,13 +583,11 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
 int enqueue_prefill_chunk(axf_llama* m, int T, int pos0, bool head) {
     const auto& hp = m->hp;
     hipStream_t st = m->ctx->stream;
-    LL_HIP(launch_embed_rows(m->tok_embd.qtype, m->pf_x, m->tok_embd.d, m->pf_tok, T,
-                             hp.n_embd / QK_K, (long)m->tok_embd.row_bytes, st));
+    LL_HIP(embed(m, m->pf_x, m->pf_tok, 0, T, st));
     for (int l = 0; l < hp.n_layer; l++) LL_HIP(enqueue_prefill_layer(m, l, T, pos0));
     if (head) {
         const float* xl = m->pf_x + (size_t)(T - 1) * hp.n_embd;
-        LL_HIP(gemv_norm(m->output, m->logits, xl, m->output_norm, hp.rms_eps, hp.n_vocab,
-                         hp.n_embd, false, st));
+        LL_HIP(head_logits(m, xl, m->attn_out, st));
         // x = the last row after the final norm, as llama_forward_batch leaves s.x
         // (its in-place rms_norm_avx2 before the copy, :1452-1461)
         LL_HIP(launch_rmsnorm(m->x, nullptr, xl, m->output_norm, hp.n_embd, hp.rms_eps, st));
@@ -670,15 +724,10 @@ int axf_llama_load(axf_llama* m) {
     const int E = hp.n_embd, FD = hp.ffn_dim, qo = hp.n_heads * m->hd, kvo = m->kv_embd;
     char nm[128];
     {
-        const HostTensor* t;
-        LL_TRY(need(m, "token_embd.weight", &t));
-        LL_TRY(check_q("token_embd.weight", t, hp.n_vocab, E));
-        LL_TRY(upload_pair(m, "token_embd.weight", hp.n_vocab, "", 0, E, &m->tok_embd, nullptr,
-                           nullptr));
+        LL_TRY(upload_head(m, "token_embd.weight", hp.n_vocab, E, &m->tok_embd));
         // output.weight falls back to token_embd (make_wt_opt, llama_model.cpp:660-667)
         if (find(m, "output.weight"))
-            LL_TRY(upload_pair(m, "output.weight", hp.n_vocab, "", 0, E, &m->output, nullptr,
-                               nullptr));
+            LL_TRY(upload_head(m, "output.weight", hp.n_vocab, E, &m->output));
         else
             m->output = m->tok_embd;
         LL_TRY(upload_f32(m, "output_norm.weight", E, &m->output_norm, true));

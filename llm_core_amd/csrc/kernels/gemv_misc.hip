@@ -1,0 +1,247 @@
+// gemv_misc.hip — GEMVs and embedding rows for the other GGUF weight types the
+// reference's decode path handles (LM heads of Qwen / DeepSeek files and F16
+// models), for gfx950:
+//   * Q8_0 weights (34-byte blocks: fp16 d, 32 int8) x Q8_0 activations —
+//     q8_0_weight_dot_q8_row (src/models/llama_model.cpp:171-211): per block
+//     (d_w * d_x) * isum, isum the exact int32 dot (v_dot4_i32_i8);
+//   * Q8_0 weights x fp32 activations — q8_0_weight_dot_row (:154-169);
+//   * Q5_0 weights (22-byte blocks: fp16 d, u32 high bits, 16 B nibbles) x fp32
+//     activations — q5_0_dot_row (:241-267): w = d * (q5 - 16);
+//   * F16 weights x fp32 activations (+ optional bias) — gemv_f16_avx2_range
+//     (src/backend/cpu_x86/kernels/gemv_f16_avx2.cpp:138-153);
+//   * embedding rows of the three types — emb_lookup (:882-898), exact.
+// These are HBM-bound streams.  LPR lanes share a row and stride over its
+// 32-element blocks (F16: 8-element groups); the lane partials are reduced with
+// shuffles, so the fp32 sums differ from the reference's sequential order
+// only by reassociation.  The 34- and 22-byte blocks are 2-byte aligned and
+// read as 16-bit words; F16 rows are read 16 bytes at a time (the entry points
+// require 16-byte aligned rows).
+#include "common.hpp"
+
+namespace axf {
+
+namespace {
+
+constexpr int kMiscThreads = 256;
+
+__device__ __forceinline__ uint32_t ld2(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// 2-byte-aligned 32-bit word
+__device__ __forceinline__ uint32_t ld2x2(const uint8_t* p) { return ld2(p) | (ld2(p + 2) << 16); }
+
+template <int LPR>
+__device__ __forceinline__ float lanes_sum(float v) {
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// One row per LPR lanes; blockIdx.x * (256 / LPR) + threadIdx.x / LPR is the row.
+template <int LPR>
+__device__ __forceinline__ long misc_row() {
+    return (long)blockIdx.x * (kMiscThreads / LPR) + threadIdx.x / LPR;
+}
+
+template <int LPR>
+__global__ __launch_bounds__(kMiscThreads) void k_gemv_q8w_q8(float* __restrict__ y,
+                                                              const uint8_t* __restrict__ W,
+                                                              const uint8_t* __restrict__ xq8,
+                                                              int rows, int nb, long row_bytes,
+                                                              int accumulate) {
+    const long row = misc_row<LPR>();
+    const int rl = threadIdx.x % LPR;
+    float acc = 0.f;
+    if (row < rows) {
+        const uint8_t* wr = W + row * row_bytes;
+        for (int b = rl; b < nb; b += LPR) {
+            const uint8_t* wb = wr + (long)b * 34;
+            const uint8_t* xb = xq8 + (long)b * Q8_0_BYTES;
+            const float scale = h2f(ld2(wb)) * __uint_as_float(ld4(xb));
+            int isum = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) isum = dot4((int)ld2x2(wb + 2 + 4 * k), (int)ld4(xb + 4 + 4 * k), isum);
+            acc = fmaf(scale, (float)isum, acc);
+        }
+    }
+    acc = lanes_sum<LPR>(acc);
+    if (row < rows && rl == 0) y[row] = accumulate ? y[row] + acc : acc;
+}
+
+template <int LPR>
+__global__ __launch_bounds__(kMiscThreads) void k_gemv_q8w_f32(float* __restrict__ y,
+                                                               const uint8_t* __restrict__ W,
+                                                               const float* __restrict__ x,
+                                                               int rows, int nb, long row_bytes) {
+    const long row = misc_row<LPR>();
+    const int rl = threadIdx.x % LPR;
+    float acc = 0.f;
+    if (row < rows) {
+        const uint8_t* wr = W + row * row_bytes;
+        for (int b = rl; b < nb; b += LPR) {
+            const uint8_t* wb = wr + (long)b * 34;
+            const float d = h2f(ld2(wb));
+            const float4* xb = reinterpret_cast<const float4*>(x + 32 * b);
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t q = ld2x2(wb + 2 + 4 * k);
+                const float4 xv = xb[k];
+                acc = fmaf(d * (float)(int8_t)(q & 0xff), xv.x, acc);
+                acc = fmaf(d * (float)(int8_t)((q >> 8) & 0xff), xv.y, acc);
+                acc = fmaf(d * (float)(int8_t)((q >> 16) & 0xff), xv.z, acc);
+                acc = fmaf(d * (float)(int8_t)(q >> 24), xv.w, acc);
+            }
+        }
+    }
+    acc = lanes_sum<LPR>(acc);
+    if (row < rows && rl == 0) y[row] = acc;
+}
+
+template <int LPR>
+__global__ __launch_bounds__(kMiscThreads) void k_gemv_q5_0_f32(float* __restrict__ y,
+                                                                const uint8_t* __restrict__ W,
+                                                                const float* __restrict__ x,
+                                                                int rows, int nb, long row_bytes) {
+    const long row = misc_row<LPR>();
+    const int rl = threadIdx.x % LPR;
+    float acc = 0.f;
+    if (row < rows) {
+        const uint8_t* wr = W + row * row_bytes;
+        for (int b = rl; b < nb; b += LPR) {
+            const uint8_t* wb = wr + (long)b * 22;
+            const float d = h2f(ld2(wb));
+            const uint32_t qh = ld2x2(wb + 2);
+            const float* xb = x + 32 * b;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t qs = ld2x2(wb + 6 + 4 * k);  // bytes 4k..4k+3 of the 16
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int i = 4 * k + j;  // low nibble: element i, high: element i + 16
+                    const uint32_t lo = (qs >> (8 * j)) & 0x0fu, hi = (qs >> (8 * j + 4)) & 0x0fu;
+                    const float w0 = d * ((float)(lo | (((qh >> i) & 1u) << 4)) - 16.f);
+                    const float w1 = d * ((float)(hi | (((qh >> (i + 16)) & 1u) << 4)) - 16.f);
+                    acc = fmaf(w0, xb[i], acc);
+                    acc = fmaf(w1, xb[i + 16], acc);
+                }
+            }
+        }
+    }
+    acc = lanes_sum<LPR>(acc);
+    if (row < rows && rl == 0) y[row] = acc;
+}
+
+template <int LPR>
+__global__ __launch_bounds__(kMiscThreads) void k_gemv_f16_f32(float* __restrict__ y,
+                                                               const uint16_t* __restrict__ W,
+                                                               const float* __restrict__ x,
+                                                               const float* __restrict__ bias,
+                                                               int rows, int cols) {
+    const long row = misc_row<LPR>();
+    const int rl = threadIdx.x % LPR;
+    float acc = 0.f;
+    if (row < rows) {
+        const uint4* wr = reinterpret_cast<const uint4*>(W + row * (long)cols);
+        const int ng = cols / 8;
+        for (int g = rl; g < ng; g += LPR) {
+            const uint4 w = wr[g];
+            const float4 x0 = reinterpret_cast<const float4*>(x)[2 * g];
+            const float4 x1 = reinterpret_cast<const float4*>(x)[2 * g + 1];
+            acc = fmaf(h2f(w.x & 0xffffu), x0.x, acc);
+            acc = fmaf(h2f(w.x >> 16), x0.y, acc);
+            acc = fmaf(h2f(w.y & 0xffffu), x0.z, acc);
+            acc = fmaf(h2f(w.y >> 16), x0.w, acc);
+            acc = fmaf(h2f(w.z & 0xffffu), x1.x, acc);
+            acc = fmaf(h2f(w.z >> 16), x1.y, acc);
+            acc = fmaf(h2f(w.w & 0xffffu), x1.z, acc);
+            acc = fmaf(h2f(w.w >> 16), x1.w, acc);
+        }
+    }
+    acc = lanes_sum<LPR>(acc);
+    if (row < rows && rl == 0) y[row] = acc + (bias ? bias[row] : 0.f);
+}
+
+// Embedding row (rows of T tokens when tok_dev lists them): exact dequant.
+__global__ __launch_bounds__(256) void k_embed_misc(float* __restrict__ out, int qtype,
+                                                    const uint8_t* __restrict__ W,
+                                                    const int* __restrict__ tok_dev, int tok,
+                                                    int cols, long row_bytes) {
+    const int id = tok_dev ? tok_dev[blockIdx.x] : tok;
+    const uint8_t* r = W + (long)id * row_bytes;
+    float* o = out + (long)blockIdx.x * cols;
+    for (int i = threadIdx.x; i < cols; i += 256) {
+        float v;
+        if (qtype == 1) {  // F16
+            v = h2f(ld2(r + 2 * i));
+        } else {
+            const int b = i >> 5, e = i & 31;
+            if (qtype == 8) {  // Q8_0: d * q (q8_0_weight_row_to_f32, :230-243)
+                const uint8_t* blk = r + (long)b * 34;
+                v = h2f(ld2(blk)) * (float)(int8_t)blk[2 + e];
+            } else {  // Q5_0: d * (q5 - 16) (q5_0_row_to_f32, :269-293)
+                const uint8_t* blk = r + (long)b * 22;
+                const uint32_t qh = ld2x2(blk + 2);
+                const uint32_t nib = e < 16 ? (blk[6 + e] & 0x0fu) : (blk[6 + e - 16] >> 4);
+                v = h2f(ld2(blk)) * ((float)(nib | (((qh >> e) & 1u) << 4)) - 16.f);
+            }
+        }
+        o[i] = v;
+    }
+}
+
+int misc_lpr(int units) { return units >= 64 ? 64 : (units >= 32 ? 32 : 16); }
+
+}  // namespace
+
+#define AXF_MISC_LAUNCH(KERNEL, LPR_, ROWS, ...)                                           \
+    do {                                                                                   \
+        const dim3 grid_((unsigned)(((long)(ROWS) + (kMiscThreads / LPR_) - 1) /           \
+                                    (kMiscThreads / LPR_)));                              \
+        hipLaunchKernelGGL((KERNEL<LPR_>), grid_, dim3(kMiscThreads), 0, st, __VA_ARGS__); \
+    } while (0)
+
+#define AXF_MISC_DISPATCH(KERNEL, UNITS, ROWS, ...)                                        \
+    do {                                                                                   \
+        const int l_ = misc_lpr(UNITS);                                                    \
+        if (l_ == 64) AXF_MISC_LAUNCH(KERNEL, 64, ROWS, __VA_ARGS__);                      \
+        else if (l_ == 32) AXF_MISC_LAUNCH(KERNEL, 32, ROWS, __VA_ARGS__);                 \
+        else AXF_MISC_LAUNCH(KERNEL, 16, ROWS, __VA_ARGS__);                               \
+    } while (0)
+
+hipError_t launch_gemv_q8w_q8(float* y, const void* W, const void* xq8, int rows, int nb,
+                              long row_bytes, int accumulate, hipStream_t st) {
+    AXF_MISC_DISPATCH(k_gemv_q8w_q8, nb, rows, y, static_cast<const uint8_t*>(W),
+                      static_cast<const uint8_t*>(xq8), rows, nb, row_bytes, accumulate);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_q8w_f32(float* y, const void* W, const float* x, int rows, int nb,
+                               long row_bytes, hipStream_t st) {
+    AXF_MISC_DISPATCH(k_gemv_q8w_f32, nb, rows, y, static_cast<const uint8_t*>(W), x, rows, nb,
+                      row_bytes);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_q5_0_f32(float* y, const void* W, const float* x, int rows, int nb,
+                                long row_bytes, hipStream_t st) {
+    AXF_MISC_DISPATCH(k_gemv_q5_0_f32, nb, rows, y, static_cast<const uint8_t*>(W), x, rows, nb,
+                      row_bytes);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_f16_f32(float* y, const void* W, const float* x, const float* bias,
+                               int rows, int cols, hipStream_t st) {
+    AXF_MISC_DISPATCH(k_gemv_f16_f32, cols / 8, rows, y, static_cast<const uint16_t*>(W), x, bias,
+                      rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_misc(int qtype, float* out, const void* W, const int* tok_dev, int tok,
+                             int T, int cols, long row_bytes, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed_misc, dim3((unsigned)T), dim3(256), 0, st, out, qtype,
+                       static_cast<const uint8_t*>(W), tok_dev, tok, cols, row_bytes);
+    return hipGetLastError();
+}
+
+}  // namespace axf

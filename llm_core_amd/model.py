@@ -14,7 +14,8 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import hip
-from ._ffi import AXF_TYPE_F32, AXF_TYPE_Q4_K, AXF_TYPE_Q6_K, LlamaHparams, call, lib
+from ._ffi import (AXF_TYPE_F16, AXF_TYPE_F32, AXF_TYPE_Q4_K, AXF_TYPE_Q5_0, AXF_TYPE_Q6_K,
+                   AXF_TYPE_Q8_0, LlamaHparams, call, lib)
 
 
 @dataclass
@@ -56,6 +57,36 @@ Q4K_M_TYPES = {
 }
 
 
+def synth_other(qtype: int, rows: int, cols: int, seed: int, std: float = 0.02) -> np.ndarray:
+    """N(0, std) rows in the other GGUF weight types (F16, Q8_0, Q5_0), quantised
+    with ggml's reference rounding: Q8_0 d = amax/127, q = round(x/d); Q5_0
+    d = m/-16 for the value m of largest magnitude, q = min(31, int(x/d + 16.5))."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, cols)) * std).astype(np.float32)
+    if qtype == AXF_TYPE_F16:
+        return x.astype(np.float16).reshape(-1).view(np.uint8)
+    b = x.reshape(rows, cols // 32, 32)
+    if qtype == AXF_TYPE_Q8_0:
+        d = (np.abs(b).max(axis=2) / 127.0).astype(np.float16)
+        df = d.astype(np.float32)[..., None]
+        q = np.clip(np.round(np.divide(b, df, out=np.zeros_like(b), where=df != 0)), -127, 127)
+        return np.concatenate([d.view(np.uint8).reshape(rows, -1, 2),
+                               q.astype(np.int8).view(np.uint8)], axis=2).reshape(-1)
+    idx = np.abs(b).argmax(axis=2)[..., None]
+    m = np.take_along_axis(b, idx, axis=2)[..., 0]
+    d = (m / -16.0).astype(np.float16)
+    inv = np.divide(1.0, d.astype(np.float32), out=np.zeros(d.shape, np.float32),
+                    where=d.astype(np.float32) != 0)[..., None]
+    q = np.minimum(31, (b * inv + 16.5).astype(np.int32)).astype(np.uint32)
+    lo, hi = q[..., :16], q[..., 16:]
+    qs = ((lo & 15) | ((hi & 15) << 4)).astype(np.uint8)
+    bits = np.arange(16, dtype=np.uint32)
+    qh = (((lo >> 4) & 1) << bits).sum(axis=2) + (((hi >> 4) & 1) << (bits + 16)).sum(axis=2)
+    return np.concatenate([d.view(np.uint8).reshape(rows, -1, 2),
+                           qh.astype(np.uint32).view(np.uint8).reshape(rows, -1, 4), qs],
+                          axis=2).reshape(-1)
+
+
 @dataclass
 class SynthLlama:
     hp: Hparams
@@ -63,6 +94,8 @@ class SynthLlama:
     std: float = 0.02
     norm_std: float = 0.0
     with_bias: bool = False
+    embd_type: int = AXF_TYPE_Q4_K   # token_embd.weight
+    head_type: int = AXF_TYPE_Q6_K   # output.weight
     tensors: dict = field(default_factory=dict)  # name -> (qtype, ndarray)
 
     def __post_init__(self) -> None:
@@ -77,7 +110,11 @@ class SynthLlama:
             return self.seed * 1000003 + k
 
         def qw(name: str, qtype: int, rows: int, cols: int) -> None:
-            self.tensors[name] = (qtype, hip.synth_weight(qtype, rows, cols, seed(), self.std))
+            if qtype in (AXF_TYPE_Q4_K, AXF_TYPE_Q6_K):
+                a = hip.synth_weight(qtype, rows, cols, seed(), self.std)
+            else:
+                a = synth_other(qtype, rows, cols, seed(), self.std)
+            self.tensors[name] = (qtype, a)
 
         def norm(name: str, n: int) -> None:
             if self.norm_std > 0:
@@ -86,8 +123,8 @@ class SynthLlama:
                 v = np.ones(n, np.float32)
             self.tensors[name] = (AXF_TYPE_F32, v)
 
-        qw("token_embd.weight", AXF_TYPE_Q4_K, hp.n_vocab, E)
-        qw("output.weight", AXF_TYPE_Q6_K, hp.n_vocab, E)
+        qw("token_embd.weight", self.embd_type, hp.n_vocab, E)
+        qw("output.weight", self.head_type, hp.n_vocab, E)
         norm("output_norm.weight", E)
         shapes = {"attn_q": (qo, E), "attn_k": (kvo, E), "attn_v": (kvo, E),
                   "attn_output": (E, qo), "ffn_gate": (FD, E), "ffn_up": (FD, E),

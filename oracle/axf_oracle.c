@@ -638,6 +638,121 @@ float orc_top2_margin(const float* x, int n) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* other weight types of the decode path                                    */
+/* ------------------------------------------------------------------------ */
+
+/* q8_0_weight_dot_q8_row (llama_model.cpp:171-211): per 34-byte block the
+ * scale f16(d_w) * d_x times the exact int32 dot, summed in block order. */
+void orc_gemv_q8_0w_q8(float* y, const uint8_t* W, const orc_block_q8_0* xq8, int o0, int o1,
+                       int in, size_t rb) {
+    const int nb = in / 32;
+    for (int o = o0; o < o1; o++) {
+        const uint8_t* row = W + (size_t)o * rb;
+        float acc = 0.f;
+        for (int b = 0; b < nb; b++) {
+            const float scale = orc_fp16_to_fp32(rd16(row + (size_t)b * 34)) * xq8[b].d;
+            const int8_t* q = (const int8_t*)(row + (size_t)b * 34 + 2);
+            int isum = 0;
+            for (int i = 0; i < 32; i++) isum += (int)q[i] * (int)xq8[b].qs[i];
+            acc += scale * (float)isum;
+        }
+        y[o] = acc;
+    }
+}
+
+/* q8_0_weight_dot_row (:154-169): acc += d * q * x element by element. */
+void orc_gemv_q8_0w_f32(float* y, const uint8_t* W, const float* x, int o0, int o1, int in,
+                        size_t rb) {
+    const int nb = (in + 31) / 32;
+    for (int o = o0; o < o1; o++) {
+        const uint8_t* row = W + (size_t)o * rb;
+        float acc = 0.f;
+        for (int b = 0; b < nb; b++) {
+            const float d = orc_fp16_to_fp32(rd16(row + (size_t)b * 34));
+            const int8_t* q = (const int8_t*)(row + (size_t)b * 34 + 2);
+            const int lim = in - b * 32 < 32 ? in - b * 32 : 32;
+            for (int i = 0; i < lim; i++) acc += d * (float)q[i] * x[b * 32 + i];
+        }
+        y[o] = acc;
+    }
+}
+
+/* Q5_0 element i of a block: low nibble of qs[i] (i < 16) or high nibble of
+ * qs[i - 16], bit i of qh as bit 4; w = d * (q - 16) (q5_0_dot_row :245-267). */
+static float q5_0_w(const uint8_t* blk, int i) {
+    const float d = orc_fp16_to_fp32(rd16(blk));
+    const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                        ((uint32_t)blk[5] << 24);
+    const uint8_t* qs = blk + 6;
+    const uint32_t nib = i < 16 ? (uint32_t)(qs[i] & 0x0f) : (uint32_t)(qs[i - 16] >> 4);
+    const uint32_t hi = (qh >> i) & 1u;
+    return d * ((float)(nib | (hi << 4)) - 16.f);
+}
+
+void orc_gemv_q5_0_f32(float* y, const uint8_t* W, const float* x, int o0, int o1, int in,
+                       size_t rb) {
+    const int nb = (in + 31) / 32;
+    for (int o = o0; o < o1; o++) {
+        const uint8_t* row = W + (size_t)o * rb;
+        float acc = 0.f;
+        for (int b = 0; b < nb; b++) {
+            const int lim = in - b * 32 < 32 ? in - b * 32 : 32;
+            for (int i = 0; i < lim; i++) acc += q5_0_w(row + (size_t)b * 22, i) * x[b * 32 + i];
+        }
+        y[o] = acc;
+    }
+}
+
+/* gemv_f16_avx2_range (gemv_f16_avx2.cpp:98-153) with an __m256 restated as
+ * float[8]: 4-row tiles (when no bias) with two 8-lane FMA accumulators per
+ * row over 16-element steps, then one over an 8-element step, lane-wise add,
+ * hsum8, scalar tail; remaining rows one at a time the same way (+ bias). */
+static float f16_hsum8(const float* v) {
+    float lo[4];
+    for (int i = 0; i < 4; i++) lo[i] = v[i] + v[i + 4];
+    const float h0 = lo[0] + lo[1], h1 = lo[2] + lo[3];
+    return h0 + h1;
+}
+
+static float f16_dot_row(const uint16_t* w, const float* x, int in) {
+    float a[8] = {0}, b[8] = {0};
+    int k = 0;
+    for (; k + 16 <= in; k += 16)
+        for (int l = 0; l < 8; l++) {
+            a[l] = fmaf(orc_fp16_to_fp32(w[k + l]), x[k + l], a[l]);
+            b[l] = fmaf(orc_fp16_to_fp32(w[k + 8 + l]), x[k + 8 + l], b[l]);
+        }
+    for (; k + 8 <= in; k += 8)
+        for (int l = 0; l < 8; l++) a[l] = fmaf(orc_fp16_to_fp32(w[k + l]), x[k + l], a[l]);
+    for (int l = 0; l < 8; l++) a[l] += b[l];
+    float sum = f16_hsum8(a);
+    for (; k < in; k++) sum = fmaf(orc_fp16_to_fp32(w[k]), x[k], sum);
+    return sum;
+}
+
+void orc_gemv_f16_f32(float* y, const uint16_t* W, const float* x, const float* bias, int o0,
+                      int o1, int in) {
+    for (int o = o0; o < o1; o++) {
+        const float s = f16_dot_row(W + (size_t)o * in, x, in);
+        y[o] = bias ? s + bias[o] : s;
+    }
+}
+
+/* emb_lookup rows of the other types (llama_model.cpp:882-898): exact. */
+void orc_dequant_row(float* out, int qtype, const uint8_t* row, int cols) {
+    for (int i = 0; i < cols; i++) {
+        if (qtype == 1) {
+            out[i] = orc_fp16_to_fp32(rd16(row + 2 * i));
+        } else if (qtype == 8) {
+            const uint8_t* blk = row + (size_t)(i / 32) * 34;
+            out[i] = orc_fp16_to_fp32(rd16(blk)) * (float)(int8_t)blk[2 + i % 32];
+        } else {
+            out[i] = q5_0_w(row + (size_t)(i / 32) * 22, i % 32);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* sampling (llama_generate_cpu_impl)                                        */
 /* ------------------------------------------------------------------------ */
 
@@ -782,8 +897,17 @@ float* orc_state_kv_k(orc_state* s) { return s->kv_k; }
 float* orc_state_kv_v(orc_state* s) { return s->kv_v; }
 
 static size_t wt_row_bytes(const orc_wt* w, int in) {
+    if (w->type == 8) return (size_t)((in + 31) / 32) * 34;  /* Q8_0 */
+    if (w->type == 6) return (size_t)((in + 31) / 32) * 22;  /* Q5_0 */
+    if (w->type == 1) return (size_t)in * 2;                 /* F16 */
     return (size_t)(in / ORC_QK_K) * (w->type == ORC_TYPE_Q6_K ? ORC_Q6K_BYTES : ORC_Q4K_BYTES);
 }
+
+/* The head's gemv_wt_q8 (llama_model.cpp:767-831): Q8_0 weights take the Q8_0
+ * activations (q8_fast branch), Q5_0 and F16 fall back to gemv_wt with the fp32
+ * row (:701-724, the F16 kernel at :660-680); Q4_K / Q6_K as in the layers. */
+static void head_gemv(float* y, const orc_wt* w, const orc_block_q8_0* xq8, const float* x,
+                      int out, int in);
 
 /* gemv_wt_q8, llama_model.cpp:767-831 (Q4_K and Q6_K branches). */
 static void gemv_wt_q8(float* y, const orc_wt* w, const orc_block_q8_0* xq8, int out, int in) {
@@ -804,11 +928,25 @@ static void gemm_wt_q8(float* Y, const orc_wt* w, const orc_block_q8_0* XQ8, int
     }
 }
 
-/* emb_lookup, llama_model.cpp:882-934 (Q4_K and Q6_K rows). */
+static void head_gemv(float* y, const orc_wt* w, const orc_block_q8_0* xq8, const float* x,
+                      int out, int in) {
+    if (w->type == 8)
+        orc_gemv_q8_0w_q8(y, w->data, xq8, 0, out, in, wt_row_bytes(w, in));
+    else if (w->type == 6)
+        orc_gemv_q5_0_f32(y, w->data, x, 0, out, in, wt_row_bytes(w, in));
+    else if (w->type == 1)
+        orc_gemv_f16_f32(y, (const uint16_t*)w->data, x, NULL, 0, out, in);
+    else
+        gemv_wt_q8(y, w, xq8, out, in);
+}
+
+/* emb_lookup, llama_model.cpp:882-934. */
 static void emb_lookup(float* out, const orc_wt* w, int row, int cols) {
     const int nb = cols / ORC_QK_K;
     const uint8_t* p = w->data + (size_t)row * wt_row_bytes(w, cols);
-    if (w->type == ORC_TYPE_Q6_K)
+    if (w->type == 8 || w->type == 6 || w->type == 1)
+        orc_dequant_row(out, w->type, p, cols);
+    else if (w->type == ORC_TYPE_Q6_K)
         orc_dequant_q6k(out, p, nb);
     else
         orc_dequant_q4k(out, p, nb);
@@ -863,7 +1001,7 @@ void orc_forward_token(const orc_model* m, orc_state* s, int token, int pos) {
     for (int l = 0; l < m->n_layer; l++) orc_forward_layer(m, s, l, pos);
     orc_rmsnorm(s->x, s->x, m->output_norm, E, m->rms_eps);
     orc_quantize_q8_0(s->xq8, s->x, E);
-    gemv_wt_q8(s->logits, &m->output, s->xq8, m->n_vocab, E);
+    head_gemv(s->logits, &m->output, s->xq8, s->x, m->n_vocab, E);
 }
 
 /* llama_forward_batch, llama_model.cpp:1339-1462: batched prefill with the
@@ -933,7 +1071,7 @@ void orc_forward_batch(const orc_model* m, orc_state* s, const int32_t* tokens, 
     float* xl = X + (size_t)(T - 1) * E;
     orc_rmsnorm(xl, xl, m->output_norm, E, m->rms_eps);
     orc_quantize_q8_0(XQE, xl, E);
-    gemv_wt_q8(s->logits, &m->output, XQE, m->n_vocab, E);
+    head_gemv(s->logits, &m->output, XQE, xl, m->n_vocab, E);
     memcpy(s->x, xl, sizeof(float) * (size_t)E);
     free(X); free(XB); free(Q); free(K); free(V); free(AO); free(GATE); free(UP); free(FFN);
     free(XQE); free(XQF);

@@ -76,6 +76,15 @@ float orc_exp_cephes(float x);
 void orc_swiglu(float* gate, const float* up, int n);
 int orc_argmax(const float* x, int n);
 float orc_top2_margin(const float* x, int n);
+void orc_gemv_q8_0w_q8(float* y, const uint8_t* W, const orc_block_q8_0* xq8, int o0, int o1,
+                       int in, size_t rb);
+void orc_gemv_q8_0w_f32(float* y, const uint8_t* W, const float* x, int o0, int o1, int in,
+                        size_t rb);
+void orc_gemv_q5_0_f32(float* y, const uint8_t* W, const float* x, int o0, int o1, int in,
+                       size_t rb);
+void orc_gemv_f16_f32(float* y, const uint16_t* W, const float* x, const float* bias, int o0,
+                      int o1, int in);
+void orc_dequant_row(float* out, int qtype, const uint8_t* row, int cols);
 void orc_rep_penalty(float* logits, int n_vocab, const int32_t* hist, int n_hist, int last_n,
                      float penalty);
 int orc_sample(const float* logits, int n_vocab, int top_k, float top_p, float temperature,

@@ -55,6 +55,11 @@ def _load_orc() -> C.CDLL:
         "orc_argmax": ([vp, i32], i32),
         "orc_top2_margin": ([vp, i32], f32),
         "orc_rep_penalty": ([vp, i32, vp, i32, i32, f32], None),
+        "orc_gemv_q8_0w_q8": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "orc_gemv_q8_0w_f32": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "orc_gemv_q5_0_f32": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "orc_gemv_f16_f32": ([vp, vp, vp, vp, i32, i32, i32], None),
+        "orc_dequant_row": ([vp, i32, vp, i32], None),
         "orc_sample": ([vp, i32, i32, f32, f32, f32, C.POINTER(f32)], i32),
         "orc_state_new": ([vp], vp),
         "orc_state_free": ([vp], None),
@@ -83,6 +88,7 @@ def _load_ref() -> C.CDLL | None:
         "ref_has_avx2": ([], i32),
         "ref_gemv_q4k_f32": ([vp, vp, vp, i32, i32, i32, sz], None),
         "ref_gemv_q6k_f32": ([vp, vp, vp, i32, i32, i32, sz], None),
+        "ref_gemv_f16_f32": ([vp, vp, vp, vp, i32, i32, i32], None),
         "ref_quantize_q8_0": ([vp, vp, i32], None),
         "ref_gemv_q4k_q8": ([vp, vp, vp, i32, i32, i32, sz, i32], None),
         "ref_repack_q4k_r8": ([vp, vp, i32, i32], None),
@@ -225,6 +231,46 @@ def ref_time_decode_step(model: "OracleModel", kv_k: np.ndarray, kv_v: np.ndarra
     t = ref.ref_time_decode_step(C.byref(model.m), _ptr(kv_k), _ptr(kv_v), pos, warmup, steps,
                                  n_threads, C.byref(used), C.byref(last))
     return t, used.value, last.value
+
+
+MISC_BLOCK = {8: 34, 6: 22}  # bytes per 32 elements: Q8_0, Q5_0
+
+
+def misc_row_bytes(qtype: int, cols: int) -> int:
+    return cols * 2 if qtype == 1 else (cols + 31) // 32 * MISC_BLOCK[qtype]
+
+
+def gemv_misc(qtype: int, W: np.ndarray, x: np.ndarray, rows: int, cols: int,
+              bias: np.ndarray | None = None) -> np.ndarray:
+    """Other weight types with fp32 activations: Q8_0 (q8_0_weight_dot_row),
+    Q5_0 (q5_0_dot_row), F16 (gemv_f16_avx2_range)."""
+    y = np.zeros(rows, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    W = np.ascontiguousarray(W)
+    if qtype == 1:
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        orc.orc_gemv_f16_f32(_ptr(y), _ptr(W), _ptr(x), None if b is None else _ptr(b), 0, rows, cols)
+    elif qtype == 8:
+        orc.orc_gemv_q8_0w_f32(_ptr(y), _ptr(W), _ptr(x), 0, rows, cols, misc_row_bytes(8, cols))
+    else:
+        orc.orc_gemv_q5_0_f32(_ptr(y), _ptr(W), _ptr(x), 0, rows, cols, misc_row_bytes(6, cols))
+    return y
+
+
+def gemv_q8_0w_q8(W: np.ndarray, xq8: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """q8_0_weight_dot_q8_row over rows (llama_model.cpp:171-228)."""
+    y = np.zeros(rows, np.float32)
+    W = np.ascontiguousarray(W)
+    xq8 = np.ascontiguousarray(xq8)
+    orc.orc_gemv_q8_0w_q8(_ptr(y), _ptr(W), _ptr(xq8), 0, rows, cols, misc_row_bytes(8, cols))
+    return y
+
+
+def dequant_row(qtype: int, row: np.ndarray, cols: int) -> np.ndarray:
+    out = np.zeros(cols, np.float32)
+    r = np.ascontiguousarray(row)
+    orc.orc_dequant_row(_ptr(out), qtype, _ptr(r), cols)
+    return out
 
 
 def rep_penalty(logits: np.ndarray, hist, last_n: int, penalty: float) -> np.ndarray:

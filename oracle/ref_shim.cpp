@@ -38,6 +38,8 @@ void gemm_q4k_q8_avxvnni_range(float* Y, const uint8_t* W, const block_q8_0* XQ8
 void gemv_q6k_q8_avx2_range(float* y, const uint8_t* W, const block_q8_0* xq8, int o_start,
                             int o_end, int in_dim, size_t row_bytes) noexcept;
 void repack_q4k_8rows(uint8_t* dst, const uint8_t* src, int nrows, int ncols) noexcept;
+void gemv_f16_avx2_range(float* y, const uint16_t* W, const float* x, const float* b,
+                         int o_start, int o_end, int in) noexcept;
 void gemv_q4k_r8_avx2_range(float* y, const uint8_t* R8, const block_q8_0* xq8, int o_start,
                             int o_end, int in_dim) noexcept;
 void gemv_q4k_r8_avxvnni_range(float* y, const uint8_t* R8, const block_q8_0* xq8, int o_start,
@@ -49,6 +51,11 @@ namespace cx = axonforge::cpu_x86;
 extern "C" {
 
 int ref_has_avxvnni(void) { return cx::cpu_features().avxvnni ? 1 : 0; }
+
+void ref_gemv_f16_f32(float* y, const uint16_t* W, const float* x, const float* b, int o0,
+                      int o1, int in_dim) {
+    cx::gemv_f16_avx2_range(y, W, x, b, o0, o1, in_dim);
+}
 int ref_has_avx2(void) { return cx::cpu_features().avx2 ? 1 : 0; }
 
 void ref_gemv_q4k_f32(float* y, const uint8_t* W, const float* x, int o0, int o1, int in_dim,

@@ -26,9 +26,12 @@ def _same_outputs(ctx, a: LlamaHip, b: LlamaHip, prompt, n_gen=12):
     assert np.array_equal(ta, tb), (ta, tb)
 
 
-def test_llama_file_matches_tensor_api(ctx, tmp_path):
+@pytest.mark.parametrize("embd,head", [(12, 14), (8, 6), (1, 8)])
+def test_llama_file_matches_tensor_api(ctx, tmp_path, embd, head):
+    """Q4_K embedding + Q6_K head (Q4_K_M), and the other types the reference's
+    embedding and head paths take (Q8_0 / Q5_0 / F16)."""
     hp = Hparams(**SMALL)
-    m = SynthLlama(hp, seed=4, norm_std=0.1)
+    m = SynthLlama(hp, seed=4, norm_std=0.1, embd_type=embd, head_type=head)
     path = G.llama_gguf(m).write(tmp_path / "llama.gguf")
     with LlamaHip.from_gguf(ctx, path) as g, LlamaHip(ctx, m) as ref:
         # context = min(context_length 64, 4096); eps and theta come back as fp32
