@@ -200,6 +200,19 @@ int axf_hip_rope(axf_ctx* ctx, float* dst, const float* src, int pos, int n_head
 int axf_hip_attn_decode(axf_ctx* ctx, float* out, void* outq8, const float* q,
                         const float* kcache, const float* vcache, int seq, int n_heads,
                         int n_kv_heads, int head_dim);
+/* Causal attention of T query rows at positions pos0 .. pos0+T-1, the
+ * multi-token attention of llama_forward_batch (llama_model.cpp:1410-1426):
+ * row t (at q + t*q_ld, n_heads*head_dim raw projections) gets the bias bq
+ * (may be NULL) and RoPE from the tables (cos_t/sin_t [n_pos][head_dim/2]),
+ * then attends to cache rows 0 .. pos0+t (K rows already RoPE'd).  out row t
+ * at out + t*n_heads*head_dim; outq8 (may be NULL) holds its Q8_0 blocks.
+ * path 0: the matrix-core kernel (what the decoder's prefill uses); 1: the
+ * decode split/combine kernels over a token grid (no reference counterpart;
+ * for comparison). */
+int axf_hip_attn_prefill(axf_ctx* ctx, float* out, void* outq8, const float* q, int q_ld,
+                         const float* bq, const float* kcache, const float* vcache, int pos0,
+                         int T, int n_heads, int n_kv_heads, int head_dim, const float* cos_t,
+                         const float* sin_t, int path);
 
 /* out = silu(gate)*up as swiglu_avx2 (llama_model.cpp:348-368); out may equal
  * gate; outq8 may be NULL.  n % 32 == 0. */
@@ -361,7 +374,7 @@ int axf_llama_forward_token(axf_llama* m, int token, int pos);
  * the projections as T-token GEMMs (matrix cores from 8 tokens up), causal
  * attention per row; leaves the last row's logits (get_logits) and,
  * as the reference leaves s.x, that row after the final RMSNorm (get_x).
- * Long prompts run in chunks of up to 256 tokens. */
+ * Long prompts run in chunks of up to 512 tokens. */
 int axf_llama_forward_batch(axf_llama* m, const int32_t* tokens, int T, int pos_start);
 /* Greedy generation (greedy loop of llama_generate_cpu_impl,
  * llama_model.cpp:1568-1624, without EOS): the prompt is prefilled as one batch

@@ -134,6 +134,8 @@ SIGNATURES: dict[str, list] = {
     "axf_rope_table": [vp, vp, i32, f32, i32],
     "axf_hip_rope": [vp, vp, vp, i32, i32, i32, vp, vp],
     "axf_hip_attn_decode": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32],
+    "axf_hip_attn_prefill": [vp, vp, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, vp, vp,
+                             i32],
     "axf_hip_swiglu": [vp, vp, vp, vp, vp, i32],
     "axf_hip_add": [vp, vp, vp, vp, i32],
     "axf_hip_embed": [vp, vp, i32, vp, i32, i32, i32],

@@ -401,6 +401,53 @@ int axf_hip_attn_decode(axf_ctx* ctx, float* out, void* outq8, const float* q,
     return AXF_OK;
 }
 
+int axf_hip_attn_prefill(axf_ctx* ctx, float* out, void* outq8, const float* q, int q_ld,
+                         const float* bq, const float* kcache, const float* vcache, int pos0,
+                         int T, int n_heads, int n_kv_heads, int head_dim, const float* cos_t,
+                         const float* sin_t, int path) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(out && q && kcache && vcache && cos_t && sin_t, "null pointer");
+    AXF_REQUIRE(T > 0 && pos0 >= 0 && n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                "bad shape");
+    AXF_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
+                "head_dim must be 64, 128 or 256");
+    AXF_REQUIRE(n_heads / n_kv_heads <= 8, "more than 8 query heads per kv head");
+    AXF_REQUIRE(q_ld >= n_heads * head_dim, "q_ld below one row");
+    AXF_REQUIRE(path == 0 || path == 1, "path must be 0 or 1");
+    AXF_REQUIRE(aligned(q, 4) && aligned(kcache, 16) && aligned(vcache, 16) && aligned(out, 4) &&
+                    aligned(outq8, 4),
+                "misaligned pointer");
+    const int nsplit = attn_nsplit(pos0 + T);
+    AXF_REQUIRE(nsplit <= 512, "positions above 32768");
+    AttnArgs a{};
+    a.q = q;
+    a.bq = bq;
+    a.cos_t = cos_t;
+    a.sin_t = sin_t;
+    a.kcache = const_cast<float*>(kcache);
+    a.vcache = const_cast<float*>(vcache);
+    a.pos = pos0;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.nsplit = nsplit;
+    a.store_kv = 0;
+    a.out = out;
+    a.outq8 = static_cast<uint8_t*>(outq8);
+    a.n_tok = T;
+    a.q_ld = q_ld;
+    a.out_ld = n_heads * head_dim;
+    if (path == 1) {
+        void* scratch = nullptr;
+        int rc = ctx_scratch(ctx, (size_t)T * n_heads * nsplit * (head_dim + 2) * 4, &scratch);
+        if (rc) return rc;
+        a.part = static_cast<float*>(scratch);
+        AXF_HIP(launch_attention_fused(a, head_dim, ctx->stream));
+    } else {
+        AXF_HIP(launch_attention_prefill(a, head_dim, ctx->stream));
+    }
+    return AXF_OK;
+}
+
 int axf_hip_swiglu(axf_ctx* ctx, float* out, void* outq8, const float* gate, const float* up,
                    int n) {
     AXF_CHECK_CTX(ctx);

@@ -140,6 +140,10 @@ struct AttnArgs {
 };
 int attn_nsplit(int max_seq);
 hipError_t launch_attention_fused(const AttnArgs& a, int head_dim, hipStream_t st);
+// Batched prefill attention on the matrix cores (n_tok query rows, K/V rows
+// already in the cache; q, bq, cos_t/sin_t, kcache, vcache, pos, n_heads,
+// n_kv_heads, out, outq8, n_tok, q_ld, out_ld are used).
+hipError_t launch_attention_prefill(const AttnArgs& a, int head_dim, hipStream_t st);
 hipError_t launch_swiglu(float* out, void* outq8, const float* gate, const float* up, int n,
                          hipStream_t st);
 hipError_t launch_embed(int qtype, float* out, const void* W, const int* tok_dev, int tok,

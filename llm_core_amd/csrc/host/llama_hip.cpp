@@ -91,6 +91,9 @@ struct axf_llama {
     float *pf_x = nullptr, *pf_qk = nullptr, *pf_v = nullptr, *pf_ao = nullptr, *pf_tmp = nullptr,
           *pf_gu = nullptr, *pf_part = nullptr;
     uint8_t *pf_q8 = nullptr, *pf_gemm = nullptr;
+    // prefill attention: the matrix-core kernel, or (testing) the decode
+    // split/combine kernels over a token grid
+    bool pf_attn_split = false;
 
     // sampled generation (allocated on first use): penalty history (prompt and
     // generated tokens) and its length, the step's uniform draws, sort keys
@@ -462,10 +465,12 @@ int prefill_alloc(axf_llama* m) {
     if (m->pf_cap) return AXF_OK;
     const auto& hp = m->hp;
     const int E = hp.n_embd, FD = hp.ffn_dim, qo = hp.n_heads * m->hd, kvo = m->kv_embd;
-    // chunk: up to 256 tokens, the attention partials within 256 MiB
+    // chunk: up to 512 tokens (the matrix-core attention keeps no partials);
+    // with the split/combine attention up to 256, its partials within 256 MiB
     const size_t part_per_tok = (size_t)hp.n_heads * m->nsplit * (m->hd + 2) * 4;
-    int cap = 256;
-    while (cap > 16 && (size_t)cap * part_per_tok > ((size_t)256 << 20)) cap /= 2;
+    int cap = m->pf_attn_split ? 256 : 512;
+    while (m->pf_attn_split && cap > 16 && (size_t)cap * part_per_tok > ((size_t)256 << 20))
+        cap /= 2;
     if (cap > hp.n_ctx) cap = hp.n_ctx;
     const size_t C = (size_t)cap;
     const int kmax = E > FD ? E : FD;
@@ -484,8 +489,10 @@ int prefill_alloc(axf_llama* m) {
     m->pf_tmp = static_cast<float*>(p);
     LL_TRY(dalloc(m, C * 2 * FD * 4, &p));
     m->pf_gu = static_cast<float*>(p);
-    LL_TRY(dalloc(m, C * part_per_tok, &p));
-    m->pf_part = static_cast<float*>(p);
+    if (m->pf_attn_split) {
+        LL_TRY(dalloc(m, C * part_per_tok, &p));
+        m->pf_part = static_cast<float*>(p);
+    }
     LL_TRY(dalloc(m, C * (kmax > qo ? kmax : qo) / 32 * Q8_0_BYTES, &p));
     m->pf_q8 = static_cast<uint8_t*>(p);
     const size_t g4 = gemm_scratch_bytes(AXF_TYPE_Q4_K, GemmPath::Auto, cap, kmax / QK_K);
@@ -556,7 +563,8 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
         a.n_tok = T;
         a.q_ld = q_ld;
         a.out_ld = qo;
-        ST(launch_attention_fused(a, HD, st));
+        ST(m->pf_attn_split ? launch_attention_fused(a, HD, st)
+                            : launch_attention_prefill(a, HD, st));
     }
     // x += o
     ST(gemm_rows(m, L.wo, m->pf_tmp, m->pf_q8, E, T, qo, st));

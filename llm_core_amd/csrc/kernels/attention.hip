@@ -342,7 +342,237 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(AttnArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Batched prefill attention on the matrix cores (llama_forward_batch's causal
+// attention, src/models/llama_model.cpp:1410-1426): a workgroup owns 64 query
+// rows of one kv head (QT = 64 / G tokens x the G query heads that share it)
+// and walks the keys 0 .. (its last token's position) in blocks of 32.  Each
+// K/V block is staged once in LDS and used by all 64 rows:
+//   S = Q K^T   v_mfma_f32_16x16x4_f32, A = the wave's 16 query rows (held in
+//               VGPRs, bias and RoPE applied), B = 16 keys from LDS;
+//   online softmax per row (running max m, sum l; O rescaled by e^(m_old - m));
+//   O += P V    v_mfma_f32_16x16x4_f32, A = P re-read from LDS, B = V from LDS.
+// fp32 throughout, as the reference; results differ from the per-token
+// softmax only in summation order.  Row stride padding makes the B reads of
+// K (16 rows x 2 columns per half-wave: stride = 2 mod 32 banks), of V (2 rows x
+// 16 columns: stride = 16 mod 32) and the A reads of P conflict-free.
+// Outputs as the split/combine path: out rows (fp32) and their Q8_0 blocks.
+// ---------------------------------------------------------------------------
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+constexpr int kPfRows = 64;
+constexpr int kPfKeys = 32;
+
+template <int HD>
+struct PfLayout {
+    static constexpr int QS = HD + 4;        // Q tile row stride (floats)
+    static constexpr int KS = HD + 2;        // K block row stride
+    static constexpr int VS = HD + 16;       // V block row stride
+    static constexpr int PS = kPfKeys + 2;   // P tile row stride
+};
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_prefill(AttnArgs a, int G, int QT) {
+    using Lay = PfLayout<HD>;
+    constexpr int KSTEP = HD / 4;  // MFMA k-steps over the head dimension
+    constexpr int DT = HD / 16;    // output column tiles
+    constexpr int HALF = HD / 2;
+    __shared__ __attribute__((aligned(16))) float qs[kPfRows * Lay::QS];
+    __shared__ __attribute__((aligned(16))) float ks[kPfKeys * Lay::KS];
+    __shared__ __attribute__((aligned(16))) float vs[kPfKeys * Lay::VS];
+    __shared__ __attribute__((aligned(16))) float ps[4][16 * Lay::PS];
+
+    const int kvh = blockIdx.x, qt0 = blockIdx.y * QT;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int pos0 = a.pos_dev ? *a.pos_dev : a.pos;
+    const int n_tok = a.n_tok > 1 ? a.n_tok : 1;
+    const int t_end = min(qt0 + QT, n_tok);  // tokens qt0 .. t_end-1
+    const int kmax = pos0 + t_end - 1;       // last key any row attends to
+    const size_t kve = (size_t)a.n_kv_heads * HD;
+
+    // 1. Q tile: row r = token qt0 + r / G, head kvh*G + r % G (+ bias, RoPE)
+    for (int idx = tid; idx < kPfRows * HD; idx += 256) {
+        const int r = idx / HD, d = idx % HD, tl = r / G;
+        float v = 0.f;
+        if (tl < QT && qt0 + tl < n_tok) {
+            const size_t e = (size_t)(kvh * G + r % G) * HD + d;
+            v = a.q[(size_t)(qt0 + tl) * a.q_ld + e];
+            if (a.bq) v += a.bq[e];
+        }
+        qs[r * Lay::QS + d] = v;
+    }
+    __syncthreads();
+    if (a.cos_t) {
+        for (int idx = tid; idx < kPfRows * HALF; idx += 256) {
+            const int r = idx / HALF, i = idx % HALF, tl = r / G;
+            if (tl < QT && qt0 + tl < n_tok) {
+                const size_t pr = (size_t)(pos0 + qt0 + tl) * HALF + i;
+                const float c = a.cos_t[pr], sn = a.sin_t[pr];
+                float* h = qs + r * Lay::QS;
+                const float x0 = h[i], x1 = h[i + HALF];
+                h[i] = fmaf(x0, c, -(x1 * sn));
+                h[i + HALF] = fmaf(x0, sn, x1 * c);
+            }
+        }
+        __syncthreads();
+    }
+    float qa[KSTEP];
+#pragma unroll
+    for (int k = 0; k < KSTEP; k++) qa[k] = qs[(16 * wave + col) * Lay::QS + 4 * k + grp];
+
+    // this lane's four result rows 4*grp + i of the wave's 16: their positions
+    int qpos[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 16 * wave + 4 * grp + i, tl = r / G;
+        qpos[i] = (tl < QT && qt0 + tl < n_tok) ? pos0 + qt0 + tl : -1;  // -1: no row
+    }
+    const float scale = 1.f / sqrtf((float)HD);
+    float m[4], l[4];
+    v4f_t o[DT];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        m[i] = -INFINITY;
+        l[i] = 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < DT; t++) o[t] = v4f_t{0.f, 0.f, 0.f, 0.f};
+
+    // K/V blocks stream through registers: block kb+32 is loaded while block kb
+    // is used from LDS.  Rows past kmax re-read row kmax (masked below).
+    constexpr int NLD = kPfKeys * HD / 4 / 256;  // float4 of K (and of V) per thread
+    float4 kreg[NLD], vreg[NLD];
+    auto load_block = [&](int kb) {
+#pragma unroll
+        for (int u = 0; u < NLD; u++) {
+            const int idx = tid + 256 * u, r = idx / (HD / 4), c4 = idx % (HD / 4);
+            const size_t off = (size_t)min(kb + r, kmax) * kve + (size_t)kvh * HD + 4 * c4;
+            kreg[u] = *reinterpret_cast<const float4*>(a.kcache + off);
+            vreg[u] = *reinterpret_cast<const float4*>(a.vcache + off);
+        }
+    };
+    load_block(0);
+    for (int kb = 0; kb <= kmax; kb += kPfKeys) {
+        // 2. this block into LDS, the next one into registers
+#pragma unroll
+        for (int u = 0; u < NLD; u++) {
+            const int idx = tid + 256 * u, r = idx / (HD / 4), c4 = idx % (HD / 4);
+            float2* kd = reinterpret_cast<float2*>(ks + r * Lay::KS + 4 * c4);
+            kd[0] = make_float2(kreg[u].x, kreg[u].y);
+            kd[1] = make_float2(kreg[u].z, kreg[u].w);
+            *reinterpret_cast<float4*>(vs + r * Lay::VS + 4 * c4) = vreg[u];
+        }
+        __syncthreads();
+        if (kb + kPfKeys <= kmax) load_block(kb + kPfKeys);
+
+        // 3. S for 16 rows x 32 keys (two 16-key tiles)
+        v4f_t sacc[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            sacc[ct] = v4f_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < KSTEP; k++)
+                sacc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                    qa[k], ks[(16 * ct + col) * Lay::KS + 4 * k + grp], sacc[ct], 0, 0, 0);
+        }
+        // 4. online softmax of the lane's rows (16 lanes per row group share them)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float sv[2];
+            float bm = -INFINITY;
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+                const int key = kb + 16 * ct + col;
+                sv[ct] = (qpos[i] >= 0 && key <= qpos[i]) ? sacc[ct][i] * scale : -INFINITY;
+                bm = fmaxf(bm, sv[ct]);
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 16));
+            const float mn = fmaxf(m[i], bm);
+            // a row with nothing to attend to yet keeps zero weights
+            const float alpha = mn == -INFINITY ? 1.f : expf(m[i] - mn);
+            float rs = 0.f;
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+                const float p = mn == -INFINITY ? 0.f : expf(sv[ct] - mn);
+                ps[wave][(4 * grp + i) * Lay::PS + 16 * ct + col] = p;
+                rs += p;
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) rs += __shfl_xor(rs, off, 16);
+            l[i] = fmaf(l[i], alpha, rs);
+            m[i] = mn;
+#pragma unroll
+            for (int t = 0; t < DT; t++) o[t][i] *= alpha;
+        }
+        __syncthreads();
+        // 5. O += P V
+        float pa[kPfKeys / 4];
+#pragma unroll
+        for (int k = 0; k < kPfKeys / 4; k++) pa[k] = ps[wave][col * Lay::PS + 4 * k + grp];
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int k = 0; k < kPfKeys / 4; k++)
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                    pa[k], vs[(4 * k + grp) * Lay::VS + 16 * t + col], o[t], 0, 0, 0);
+        __syncthreads();
+    }
+
+    // 6. normalise, write the rows (fp32, through the Q tile's LDS for the Q8_0 pass)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float inv = l[i] > 0.f ? 1.f / l[i] : 0.f;
+        const int r = 16 * wave + 4 * grp + i;
+#pragma unroll
+        for (int t = 0; t < DT; t++) qs[r * Lay::QS + 16 * t + col] = o[t][i] * inv;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < kPfRows * HD; idx += 256) {
+        const int r = idx / HD, d = idx % HD, tl = r / G;
+        if (tl < QT && qt0 + tl < n_tok)
+            a.out[(size_t)(qt0 + tl) * a.out_ld + (size_t)(kvh * G + r % G) * HD + d] =
+                qs[r * Lay::QS + d];
+    }
+    if (a.outq8) {
+        // one 32-value block per 8 lanes, as q8_store4 expects
+        for (int idx = tid; idx < kPfRows * HD / 4; idx += 256) {
+            const int r = idx / (HD / 4), c4 = idx % (HD / 4), tl = r / G;
+            const float4 v = *reinterpret_cast<const float4*>(qs + r * Lay::QS + 4 * c4);
+            const bool ok = tl < QT && qt0 + tl < n_tok;
+            const size_t e0 = (size_t)(qt0 + (ok ? tl : 0)) * a.out_ld +
+                              (size_t)(kvh * G + r % G) * HD + 4 * c4;
+            // the 8 lanes of a block are consecutive and share r: all store or none
+            if (ok) q8_store4(a.outq8 + (e0 >> 5) * Q8_0_BYTES, c4 & 7, v);
+        }
+    }
+}
+
 int attn_nsplit(int max_seq) { return (max_seq + kAttnSplit - 1) / kAttnSplit; }
+
+template <int HD>
+static hipError_t launch_prefill_hd(const AttnArgs& a, int G, hipStream_t st) {
+    const int QT = kPfRows / G;
+    const int nt = a.n_tok > 1 ? a.n_tok : 1;
+    const dim3 grid((unsigned)a.n_kv_heads, (unsigned)((nt + QT - 1) / QT));
+    hipLaunchKernelGGL((k_attn_prefill<HD>), grid, dim3(256), 0, st, a, G, QT);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_prefill(const AttnArgs& a, int head_dim, hipStream_t st) {
+    if (a.n_kv_heads <= 0 || a.n_heads % a.n_kv_heads) return hipErrorInvalidValue;
+    const int G = a.n_heads / a.n_kv_heads;
+    if (G > 8 || a.store_kv || a.q_ld < a.n_heads * head_dim || a.out_ld < a.n_heads * head_dim ||
+        (a.outq8 && a.out_ld % 32))
+        return hipErrorInvalidValue;
+    switch (head_dim) {
+        case 64: return launch_prefill_hd<64>(a, G, st);
+        case 128: return launch_prefill_hd<128>(a, G, st);
+        case 256: return launch_prefill_hd<256>(a, G, st);
+        default: return hipErrorInvalidValue;
+    }
+}
 
 template <int HD>
 static hipError_t launch_attn_hd(const AttnArgs& a, int G, hipStream_t st) {

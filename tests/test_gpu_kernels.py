@@ -8,6 +8,8 @@ import ctypes as C
 import numpy as np
 import pytest
 
+from llm_core_amd._ffi import call
+
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -342,6 +344,37 @@ def test_attention(ctx, seq, H, KVH, hd):
     if seq == 1:  # a single position returns V of its kv head exactly
         assert np.array_equal(got.reshape(H, hd), np.repeat(vc.reshape(KVH, hd), H // KVH, 0))
     assert np.array_equal(ctx.download(dq8, np.uint8, H * hd // 32 * 36), O.quantize_q8_0(got))
+
+
+@pytest.mark.parametrize("hd,H,KVH,T,pos0", [(128, 32, 32, 64, 0), (128, 16, 2, 48, 100),
+                                             (64, 8, 4, 37, 5), (256, 8, 8, 20, 40),
+                                             (128, 14, 2, 70, 0), (128, 32, 32, 256, 256),
+                                             (64, 8, 2, 1, 0), (128, 16, 2, 9, 3000)])
+def test_attn_prefill(ctx, hd, H, KVH, T, pos0):
+    """Causal multi-row attention (bias and RoPE of q inside): the matrix-core
+    kernel and the split/combine token grid against the oracle's per-row
+    attention; Q8_0 blocks bit-exact against the oracle's quantiser."""
+    n = pos0 + T
+    rng = np.random.default_rng(T * 7 + pos0 + hd)
+    q = rng.standard_normal((T, H * hd)).astype(np.float32)
+    bq = (rng.standard_normal(H * hd) * 0.1).astype(np.float32)
+    kc = rng.standard_normal(n * KVH * hd).astype(np.float32)
+    vc = rng.standard_normal(n * KVH * hd).astype(np.float32)
+    cos_t, sin_t = O.rope_table(hd, 10000.0, n)
+    want = np.stack([O.attention(O.rope(q[t] + bq, pos0 + t, H, hd, cos_t, sin_t), kc, vc,
+                                 pos0 + t + 1, H, KVH, hd) for t in range(T)])
+    dq, dbq, dk, dv = ctx.upload(q), ctx.upload(bq), ctx.upload(kc), ctx.upload(vc)
+    dc, ds = ctx.upload(cos_t), ctx.upload(sin_t)
+    do, dq8 = ctx.alloc(T * H * hd * 4), ctx.alloc(T * H * hd // 32 * 36)
+    for path in (0, 1):
+        ctx.write(do, np.full(T * H * hd, np.nan, np.float32))
+        call("axf_hip_attn_prefill", ctx.handle, do.ptr, dq8.ptr, dq.ptr, H * hd, dbq.ptr, dk.ptr,
+             dv.ptr, pos0, T, H, KVH, hd, dc.ptr, ds.ptr, path)
+        got = ctx.download(do, np.float32, T * H * hd).reshape(T, H * hd)
+        ok, err = close(got, want, rtol=1e-5, atol=1e-6)
+        assert ok, (path, err)
+        assert np.array_equal(ctx.download(dq8, np.uint8, T * H * hd // 32 * 36),
+                              O.quantize_q8_0(got.reshape(-1))), path
 
 
 @pytest.mark.parametrize("n", [32, 11008])
