@@ -34,6 +34,14 @@ __device__ __forceinline__ uint32_t ld4(const uint8_t* p) {  // 4-byte aligned
 __device__ __forceinline__ uint32_t ld2(const uint8_t* p) {  // 2-byte aligned
     return *reinterpret_cast<const uint16_t*>(p);
 }
+// 16 bytes from a 2-byte aligned address: one global_load_dwordx4 (gfx9 global
+// loads take unaligned addresses; a load that straddles a cache line costs a
+// second line access, nothing else)
+typedef uint32_t u32x4_a2_t __attribute__((ext_vector_type(4), aligned(2)));
+__device__ __forceinline__ uint4 ld16_a2(const uint8_t* p) {
+    const u32x4_a2_t v = *reinterpret_cast<const u32x4_a2_t*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // Sum over groups of `width` consecutive lanes (width a power of two <= 64);
 // every lane of the group receives the group sum.

@@ -96,41 +96,43 @@ __device__ __forceinline__ void stage_f32(float* xs, const float* x, int K) {
 }
 
 // ---------------------------------------------------------------------------
-// Q6_K byte fetch: 2-byte aligned sources read as aligned dwords + alignbyte.
+// High nibbles of four Q4_K bytes for v_dot4_i32_i8 without a shift: byte
+// (q & 0xf0) ^ 0x80 read as int8 is 16*(h - 8) (one v_bitop3_b32), so a dot4
+// chain over a 32-value sub-block gives 16*sum(h*x) - 128*sum(x).
+// hi_dot_fix adds 128*sum(x) (the block's integer sum, which the min term
+// needs anyway) and divides by 16, exactly: the result is sum(h*x).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int hi_nibbles_x16(uint32_t q) {
+    return (int)((q & 0xf0f0f0f0u) ^ 0x80808080u);
+}
+__device__ __forceinline__ int hi_dot_fix(int dot16, int xsum) {
+    return (dot16 + xsum * 128) >> 4;
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K byte fetch: 2-byte aligned sources read as 16-byte vectors.
 // ---------------------------------------------------------------------------
 template <int N>
 __device__ __forceinline__ void load_u2(const uint8_t* p, uint32_t (&out)[N]) {
-    // p is 2-byte aligned; reads [p & ~3, (p & ~3) + 4*(N+1)) which stays inside
-    // the 210-byte block for the ql/qh fields (N = 8).
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-    const uint32_t sh = (uint32_t)(a & 3);
-    uint32_t w[N + 1];
+    static_assert(N % 4 == 0, "whole 16-byte vectors");
 #pragma unroll
-    for (int k = 0; k <= N; k++) w[k] = ld4(base + 4 * k);
-#pragma unroll
-    for (int k = 0; k < N; k++) out[k] = alignbyte(w[k + 1], w[k], sh);
+    for (int k = 0; k < N / 4; k++) {
+        const uint4 v = ld16_a2(p + 16 * k);
+        out[4 * k] = v.x;
+        out[4 * k + 1] = v.y;
+        out[4 * k + 2] = v.z;
+        out[4 * k + 3] = v.w;
+    }
 }
 
-// Scales (16 bytes at blk+192) and d (2 bytes at blk+208) without touching
-// bytes past blk+210.
+// Scales (16 bytes at blk+192) and d (2 bytes at blk+208).
 __device__ __forceinline__ void load_q6_tail(const uint8_t* blk, uint32_t (&sc)[4], uint32_t& dbits) {
-    const uint8_t* p = blk + 192;
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-    const uint32_t sh = (uint32_t)(a & 3);
-    uint32_t w[5];
-#pragma unroll
-    for (int k = 0; k < 4; k++) w[k] = ld4(base + 4 * k);
-    if (sh) {
-        w[4] = ld4(base + 16);  // bytes p+14..p+17: inside the block
-        dbits = w[4] >> 16;
-    } else {
-        w[4] = 0;
-        dbits = ld2(p + 16);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) sc[k] = alignbyte(w[k + 1], w[k], sh);
+    const uint4 v = ld16_a2(blk + 192);
+    sc[0] = v.x;
+    sc[1] = v.y;
+    sc[2] = v.z;
+    sc[3] = v.w;
+    dbits = ld2(blk + 208);
 }
 
 // ---------------------------------------------------------------------------
@@ -482,8 +484,9 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
 #pragma unroll
                     for (int k = 0; k < 8; k++) {
                         dlo = dot4((int)(q[k] & 0x0f0f0f0fu), (int)xa[k], dlo);
-                        dhi = dot4((int)((q[k] >> 4) & 0x0f0f0f0fu), (int)xb[k], dhi);
+                        dhi = dot4(hi_nibbles_x16(q[k]), (int)xb[k], dhi);
                     }
+                    dhi = hi_dot_fix(dhi, (int)meta.w);
                     const float s0 = ((float)sc0 * d) * dx0, mm0 = ((float)m0 * dmin) * dx0;
                     const float s1 = ((float)sc1 * d) * dx1, mm1 = ((float)m1 * dmin) * dx1;
                     float v = acc[n];
@@ -778,8 +781,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k_q8(float* __restrict__ Y,
 #pragma unroll
                         for (int k = 0; k < 8; k++) {
                             dlo = dot4((int)(q[k] & 0x0f0f0f0fu), (int)xa[k], dlo);
-                            dhi = dot4((int)((q[k] >> 4) & 0x0f0f0f0fu), (int)xb[k], dhi);
+                            dhi = dot4(hi_nibbles_x16(q[k]), (int)xb[k], dhi);
                         }
+                        dhi = hi_dot_fix(dhi, (int)meta.w);
                         const float dx0 = __uint_as_float(meta.x), dx1 = __uint_as_float(meta.y);
                         float a = acc[n][t];
                         a = fmaf(ds0 * dx0, (float)dlo, a);
