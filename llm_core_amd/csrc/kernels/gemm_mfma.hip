@@ -97,6 +97,18 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Wait until at most `later` chunks of P copies each are still in flight
+// (later <= L): s_waitcnt vmcnt(later * P) with the count a constant.
+template <int P, int L>
+__device__ __forceinline__ void wait_later(int later) {
+    if constexpr (L == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (later >= L) wait_vmcnt<L * P>();
+        else wait_later<P, L - 1>(later);
+    }
+}
+
 // One K-chunk (one Q4_K block, 256 weights per row) as staged in LDS:
 //   [RW rows][144 B] weights | [8 records][TW tokens][32 B] int8 activations |
 //   [8][TW] dx | [8][TW] dx*bsum.
@@ -119,6 +131,7 @@ struct Stage {
     static_assert(WB % 16 == 0 && XB % 1024 == 0 && DB % 16 == 0, "piece alignment");
     static_assert(NTILE % NW == 0 || NW % NTILE == 0, "tile split");
     static_assert(TT % WT == 0 && 8 % KS == 0, "tile split");
+    static_assert((KS - 1) * (NW / KS) * WT * 64 * 16 <= S * ALLOC, "reduction space");
 };
 
 // The sub-blocks s = KPH, KPH+KS, ... of one staged chunk for this wave's
@@ -197,16 +210,7 @@ __device__ __forceinline__ void gemm_step(
     if (i < 0) return;
         // own copies of chunk i done (at most min(S-1, nb-1-i) later chunks in flight)
         const int later = min(S - 1, nb - 1 - i);
-        if constexpr (S >= 4) {
-            if (later >= 3) wait_vmcnt<3 * G::PMIN>();
-            else if (later == 2) wait_vmcnt<2 * G::PMIN>();
-            else if (later == 1) wait_vmcnt<G::PMIN>();
-            else wait_vmcnt<0>();
-        } else {
-            if (later >= 2) wait_vmcnt<2 * G::PMIN>();
-            else if (later == 1) wait_vmcnt<G::PMIN>();
-            else wait_vmcnt<0>();
-        }
+        wait_later<G::PMIN, S - 1>(later);
         // every wave's copies of chunk i are in LDS (a bare barrier: the
         // fence of __syncthreads would also wait for the later chunks)
         __builtin_amdgcn_s_barrier();
@@ -233,6 +237,12 @@ __device__ __forceinline__ void gemm_step(
         if constexpr (G::KS > 2) {
             if (kph == 2) mfma_sub_blocks<G, 2>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
             if (kph == 3) mfma_sub_blocks<G, 3>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
+        }
+        if constexpr (G::KS > 4) {
+            if (kph == 4) mfma_sub_blocks<G, 4>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
+            if (kph == 5) mfma_sub_blocks<G, 5>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
+            if (kph == 6) mfma_sub_blocks<G, 6>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
+            if (kph == 7) mfma_sub_blocks<G, 7>(wl, xl, dl, g, col, tt0, sc03, sc47, accb);
         }
 #pragma unroll
         for (int w = 0; w < G::WT; w++) {
@@ -449,19 +459,7 @@ __device__ __forceinline__ void gemm6_step(
     }
     if (i < 0) return;
     const int later = min(S - 1, nst - 1 - i);
-    if constexpr (S >= 4) {
-        if (later >= 3) wait_vmcnt<3 * G::PMIN>();
-        else if (later == 2) wait_vmcnt<2 * G::PMIN>();
-        else if (later == 1) wait_vmcnt<G::PMIN>();
-        else wait_vmcnt<0>();
-    } else if constexpr (S == 3) {
-        if (later >= 2) wait_vmcnt<2 * G::PMIN>();
-        else if (later == 1) wait_vmcnt<G::PMIN>();
-        else wait_vmcnt<0>();
-    } else {
-        if (later >= 1) wait_vmcnt<G::PMIN>();
-        else wait_vmcnt<0>();
-    }
+    wait_later<G::PMIN, S - 1>(later);
     __builtin_amdgcn_s_barrier();
 
     const int b = i * KS + ksw;  // this wave's super-block
@@ -660,10 +658,15 @@ struct MfmaCfg {
     int rt, tt;
 };
 
+// Tile choice (measured on 11008 x 4096, T = 1..64, and the 512-token
+// prefill): up to 64 tokens one 16-row tile per workgroup (more workgroups in
+// flight; up to 16 tokens 4 waves split the tile's sub-blocks over a 3-deep
+// ring), beyond that 32 x 64 tiles.
 MfmaCfg pick_mfma(int T, int nb) {
     (void)nb;
-    if (T <= 16) return {2, 1};
-    return {2, T > 32 ? 4 : 2};
+    if (T <= 16) return {1, 1};
+    if (T <= 32) return {1, 2};
+    return {T <= 64 ? 1 : 2, 4};
 }
 
 int padded_tokens(int T, const MfmaCfg& c) {
@@ -761,8 +764,9 @@ hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int
     if (c.rt == RT && c.tt == TT)                                                          \
         launch_cfg<RT, TT, NW, S>(Y, w, xs, dxs, gxs, rows, nb, row_bytes, T, Tp, st);     \
     else
-    AXF_MFMA_CASE(2, 1, 4, 4)
-    AXF_MFMA_CASE(2, 2, 4, 4)
+    AXF_MFMA_CASE(1, 1, 4, 3)
+    AXF_MFMA_CASE(1, 2, 8, 3)
+    AXF_MFMA_CASE(1, 4, 8, 3)
     AXF_MFMA_CASE(2, 4, 8, 3)
     return hipErrorInvalidValue;
 #undef AXF_MFMA_CASE
