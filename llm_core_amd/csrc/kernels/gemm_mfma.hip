@@ -1,5 +1,6 @@
 // gemm_mfma.hip — Q4_K x Q8_0 and Q6_K x Q8_0 small-M GEMMs on the CDNA4 matrix
-// cores (the Q6_K kernel is described where it starts, below).
+// cores (the fp16 Q4_K kernel for 65+ tokens and the Q6_K kernel are described
+// where they start, below).
 //
 //   Y[t*rows + o] = sum_b sum_s ( d[o,b]*sc[o,b,s]*dx[t,b,s]*S[o,t,b,s]
 //                                 - dmin[o,b]*m[o,b,s]*dx[t,b,s]*bsum[t,b,s] )
@@ -359,6 +360,287 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_mfma_q4k(
             }
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K x Q8_0 for wide token tiles on the fp16 matrix cores, the same sums
+// with the 6-bit sub-block scale folded into the weight operand:
+//   A (weight rows) = q*sc as fp16, B (tokens) = the int8 values as fp16.
+// q <= 15 and sc <= 63 make q*sc <= 945, and |x| <= 128, so every operand,
+// product and partial sum of one 32-value sub-block is an integer below 2^24:
+// v_mfma_f32_16x16x32_f16 returns sc*S exactly, the int8 kernel's
+// __mul24(S, sc).  The scaling that follows (dx per sub-block, d per block,
+// the min term on the fp32 matrix cores) is the int8 kernel's, operation for
+// operation; the 8 sub-blocks of a block are summed in order (the int8 kernel
+// splits them over waves when a workgroup has fewer tiles than waves, which
+// changes fp32 rounding only).  What changes is the work
+// per tile: one FMA per result instead of a multiply, a conversion and an FMA,
+// and the weight operand is built once per row tile for the wave's token tiles
+// (v_perm_b32 makes fp16 1024+q, one v_pk_fma_f16 gives (1024+q)*sc - 1024*sc).
+// With weights as A and tokens as B, a result lane holds rows 4g..4g+3 of one
+// token: dx is one value per lane and sub-block.
+//
+// Workgroup: RT waves, wave w owns weight rows 16w..16w+15 and all 16*TTW
+// tokens (TTW token tiles) of the workgroup; one Q4_K block per ring stage.
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Activation re-layout for the fp16 kernel (TW = 16*TTW tokens per workgroup,
+// Tp % TW == 0; slots past T zero):
+//   xh [kb][g][t][8]                   fp16 copies of values 8g..8g+7 of record kb
+//   dxt[kb][t/TW][t%16][(t/16)%TTW]    d     (one read: a lane's TTW token tiles)
+//   gxt                                d * (sum of the 32 int8), same layout
+template <int TTW>
+__global__ __launch_bounds__(256) void k_gemm_prep16(const uint8_t* __restrict__ XQ8, int T,
+                                                     int Tp, int nkb, uint8_t* __restrict__ xh,
+                                                     float* __restrict__ dxt,
+                                                     float* __restrict__ gxt) {
+    constexpr int TW = 16 * TTW;
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;  // kb * Tp + t
+    if (i >= (long)nkb * Tp) return;
+    const int t = (int)(i % Tp), kb = (int)(i / Tp);
+    uint32_t w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    float d = 0.f;
+    int sum = 0;
+    if (t < T) {
+        const uint8_t* p = XQ8 + ((size_t)t * nkb + kb) * Q8_0_BYTES;
+        d = __uint_as_float(ld4(p));
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            w[k] = ld4(p + 4 + 4 * k);
+            sum = dot4((int)w[k], 0x01010101, sum);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        v8h_t v;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            v[e] = (_Float16)(float)(int8_t)(w[2 * g + e / 4] >> (8 * (e % 4)));
+        *reinterpret_cast<v8h_t*>(xh + (((size_t)kb * 4 + g) * Tp + t) * 16) = v;
+    }
+    const size_t q = (((size_t)kb * (Tp / TW) + t / TW) * 16 + (t & 15)) * TTW + ((t >> 4) % TTW);
+    dxt[q] = d;
+    gxt[q] = d * (float)sum;
+}
+
+// One stage: [RW rows][144 B] weights | xh [8][4][TW][16 B] | dxt [8][16][TTW] | gxt [8][16][TTW]
+template <int RT, int TTW, int S>
+struct Stage16 {
+    static constexpr int NW = RT, RW = kTile * RT, TW = kTile * TTW;
+    static constexpr int WB = RW * Q4K_BYTES;
+    static constexpr int XB = 8 * 4 * TW * 16;
+    static constexpr int DB = 8 * TW * 4;
+    static constexpr int BYTES = WB + XB + 2 * DB;
+    static constexpr int PIECES = (BYTES + 1023) / 1024;
+    static constexpr int ALLOC = PIECES * 1024;
+    static constexpr int PMAX = (PIECES + NW - 1) / NW;
+    static constexpr int PMIN = PIECES / NW;
+    static_assert(WB % 16 == 0 && XB % 1024 == 0 && DB % 128 == 0, "piece alignment");
+    static_assert(S * ALLOC <= 160 * 1024, "LDS");
+};
+
+// N consecutive floats from LDS (N = 2 or 4: one 8- or 16-byte read)
+template <int N>
+__device__ __forceinline__ void lds_floats(const float* p, float (&out)[N]) {
+    if constexpr (N == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+    } else {
+        static_assert(N == 2, "2 or 4 token tiles");
+        const float2 v = *reinterpret_cast<const float2*>(p);
+        out[0] = v.x; out[1] = v.y;
+    }
+}
+
+// fp16 pair (1024 + n0, 1024 + n1) from two nibbles in bytes of u (v_perm_b32),
+// then (1024 + n)*sc - 1024*sc = n*sc, exact (one rounding of an exact value)
+__device__ __forceinline__ uint32_t nib_times_sc(uint32_t u, uint32_t sel, h2_t sc2, h2_t off2) {
+    const uint32_t bits = __builtin_amdgcn_perm(0x64646464u, u, sel);
+    const h2_t r = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, bits), sc2, off2);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+template <int RT, int TTW, int S>
+__device__ __forceinline__ void gemm16_step(
+    const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt, bool do_copy, int bnext, int i,
+    int nb, const uint8_t* const (&src)[Stage16<RT, TTW, S>::PMAX],
+    const uint32_t (&step)[Stage16<RT, TTW, S>::PMAX], int wave, int lane, int col, int g,
+    v4f_t (&acc)[TTW], v4f_t (&macc)[TTW]) {
+    using G = Stage16<RT, TTW, S>;
+    constexpr int NW = G::NW, TW = G::TW;
+    if (do_copy) {
+#pragma unroll
+        for (int j = 0; j < G::PMAX; j++) {
+            if (wave + NW * j < G::PIECES)
+                __builtin_amdgcn_global_load_lds((gmem_t*)(src[j] + (size_t)bnext * step[j]),
+                                                 (lmem_t*)(nxt + (wave + NW * j) * 1024), 16, 0,
+                                                 0);
+        }
+    }
+    if (i < 0) return;
+    wait_later<G::PMIN, S - 1>(min(S - 1, nb - 1 - i));
+    __builtin_amdgcn_s_barrier();
+
+    const uint8_t* wl = cur + (kTile * wave + col) * Q4K_BYTES;  // this lane's A row
+    const uint8_t* xl = cur + G::WB;
+    const float* dl = reinterpret_cast<const float*>(cur + G::WB + G::XB);
+    const float* gl = dl + 8 * TW;
+    const uint4 h = *reinterpret_cast<const uint4*>(wl);
+    const float dmin = h2f(h.x >> 16);
+    const uint32_t sc03 = h.y & 0x3f3f3f3fu;
+    const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    long qv[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) qv[p] = *reinterpret_cast<const long*>(wl + 16 + 32 * p + 8 * g);
+
+    const v4f_t zero = {0.f, 0.f, 0.f, 0.f};
+    v4f_t accb[TTW];
+#pragma unroll
+    for (int j = 0; j < TTW; j++) accb[j] = zero;
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const uint32_t scv = ((s < 4 ? sc03 : sc47) >> (8 * (s & 3))) & 0xffu;
+        const _Float16 scf = (_Float16)(float)scv;               // exact
+        const _Float16 offf = (_Float16)(-1024.f * (float)scv);  // exact (<= 64512)
+        const h2_t sc2 = {scf, scf}, off2 = {offf, offf};
+        const int sh = 4 * (s & 1);
+        const uint32_t u0 = ((uint32_t)qv[s >> 1] >> sh) & 0x0f0f0f0fu;
+        const uint32_t u1 = ((uint32_t)((uint64_t)qv[s >> 1] >> 32) >> sh) & 0x0f0f0f0fu;
+        const u32x4_t aw = {nib_times_sc(u0, 0x04010400u, sc2, off2),
+                            nib_times_sc(u0, 0x04030402u, sc2, off2),
+                            nib_times_sc(u1, 0x04010400u, sc2, off2),
+                            nib_times_sc(u1, 0x04030402u, sc2, off2)};
+        const v8h_t a = __builtin_bit_cast(v8h_t, aw);
+        float dxs[TTW];
+        lds_floats<TTW>(dl + (s * 16 + col) * TTW, dxs);
+        v4f_t c[TTW];
+#pragma unroll
+        for (int j = 0; j < TTW; j++) {
+            const v8h_t b =
+                *reinterpret_cast<const v8h_t*>(xl + ((s * 4 + g) * TW + 16 * j + col) * 16);
+            c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, zero, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < TTW; j++) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) accb[j][ii] = fmaf(c[j][ii], dxs[j], accb[j][ii]);
+        }
+    }
+    // d of the result rows 4g..4g+3
+    float dout[4];
+#pragma unroll
+    for (int ii = 0; ii < 4; ii++)
+        dout[ii] = h2f(*reinterpret_cast<const uint16_t*>(cur + (kTile * wave + 4 * g + ii) *
+                                                          Q4K_BYTES));
+#pragma unroll
+    for (int j = 0; j < TTW; j++) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++) acc[j][ii] = fmaf(dout[ii], accb[j][ii], acc[j][ii]);
+    }
+    // min term: A = dmin*m (row col, sub-blocks g and 4+g), B = d*sum (tokens)
+    const uint32_t m03 = h.z & 0x3f3f3f3fu;
+    const uint32_t m47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+    const float am0 = dmin * (float)((m03 >> (8 * g)) & 0xffu);
+    const float am1 = dmin * (float)((m47 >> (8 * g)) & 0xffu);
+    float g0[TTW], g1[TTW];
+    lds_floats<TTW>(gl + (g * 16 + col) * TTW, g0);
+    lds_floats<TTW>(gl + ((4 + g) * 16 + col) * TTW, g1);
+#pragma unroll
+    for (int j = 0; j < TTW; j++) {
+        macc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(am0, g0[j], macc[j], 0, 0, 0);
+        macc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(am1, g1[j], macc[j], 0, 0, 0);
+    }
+    // stage free for chunk i + S
+    __builtin_amdgcn_s_barrier();
+}
+
+// grid = 8 * ceil(nrt / 8) * (Tp / TW) workgroups, XCD-aware: workgroup L runs
+// on XCD L % 8 (round-robin dispatch), and every token group of a row tile
+// runs on one XCD, so the tile's weights are fetched into that XCD's L2 once.
+template <int RT, int TTW, int S>
+__global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
+    float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ xh,
+    const float* __restrict__ dxt, const float* __restrict__ gxt, int rows, int nb,
+    long row_bytes, int T, int Tp, int nrt) {
+    using G = Stage16<RT, TTW, S>;
+    constexpr int NW = G::NW, RW = G::RW, TW = G::TW;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[S * G::ALLOC];
+    const int ntg = Tp / TW;
+    const int L = blockIdx.x, xcd = L & 7, k = L >> 3;
+    const int rt = (k / ntg) * 8 + xcd, ty = k % ntg;
+    if (rt >= nrt) return;  // the whole workgroup, before any barrier
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int col = lane & 15, g = lane >> 4;
+    const int row_base = rt * RW, tok_base = ty * TW;
+
+    const uint8_t* src[G::PMAX];
+    uint32_t step[G::PMAX];
+#pragma unroll
+    for (int j = 0; j < G::PMAX; j++) {
+        int o = (wave + NW * j) * 1024 + lane * 16;
+        if (o >= G::BYTES) o = 0;  // tail of the last piece: a harmless duplicate
+        if (o < G::WB) {
+            const int r = o / Q4K_BYTES;
+            src[j] = W + (long)min(row_base + r, rows - 1) * row_bytes + (o - r * Q4K_BYTES);
+            step[j] = Q4K_BYTES;
+        } else if (o < G::WB + G::XB) {
+            const int x = o - G::WB, s = x / (4 * TW * 16), gg = (x / (TW * 16)) & 3,
+                      t = (x % (TW * 16)) / 16;
+            src[j] = xh + (((size_t)s * 4 + gg) * Tp + tok_base + t) * 16;
+            step[j] = 8u * 4u * (uint32_t)Tp * 16u;
+        } else {
+            const int y = o - G::WB - G::XB, which = y / G::DB, z = y - which * G::DB;
+            const float* base = which == 0 ? dxt : gxt;
+            src[j] = reinterpret_cast<const uint8_t*>(base) +
+                     ((size_t)(z / (TW * 4)) * (Tp / TW) + tok_base / TW) * (TW * 4) +
+                     (z % (TW * 4));
+            step[j] = 8u * (uint32_t)Tp * 4u;
+        }
+    }
+    v4f_t acc[TTW], macc[TTW];
+#pragma unroll
+    for (int j = 0; j < TTW; j++) {
+        acc[j] = v4f_t{0.f, 0.f, 0.f, 0.f};
+        macc[j] = v4f_t{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int i = 1 - S; i < nb; i++) {
+        const int inext = i + S - 1;
+        gemm16_step<RT, TTW, S>(smem + ((i + S) % S) * G::ALLOC, smem + (inext % S) * G::ALLOC,
+                                inext < nb, inext, i, nb, src, step, wave, lane, col, g, acc,
+                                macc);
+    }
+#pragma unroll
+    for (int j = 0; j < TTW; j++) {
+        const v4f_t v = acc[j] - macc[j];
+        const int tok = tok_base + 16 * j + col;
+        if (tok < T) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) {
+                const int o = row_base + kTile * wave + 4 * g + ii;
+                if (o < rows) Y[(size_t)tok * rows + o] = v[ii];
+            }
+        }
+    }
+}
+
+template <int RT, int TTW, int S>
+void launch16_cfg(float* Y, const uint8_t* W, const uint8_t* XQ8, uint8_t* scratch, int rows,
+                  int nb, long row_bytes, int T, hipStream_t st) {
+    constexpr int TW = kTile * TTW;
+    const int Tp = (T + TW - 1) / TW * TW, nkb = nb * 8;
+    auto* xh = scratch;
+    auto* dxt = reinterpret_cast<float*>(xh + (size_t)nkb * Tp * 64);
+    auto* gxt = dxt + (size_t)nkb * Tp;
+    const long n = (long)nkb * Tp;
+    hipLaunchKernelGGL(k_gemm_prep16<TTW>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       XQ8, T, Tp, nkb, xh, dxt, gxt);
+    const int nrt = (rows + kTile * RT - 1) / (kTile * RT);
+    const unsigned grid = (unsigned)((nrt + 7) / 8 * 8 * (Tp / TW));
+    hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S>), dim3(grid), dim3(RT * 64), 0, st, Y, W, xh,
+                       dxt, gxt, rows, nb, row_bytes, T, Tp, nrt);
 }
 
 // ---------------------------------------------------------------------------
@@ -736,8 +1018,17 @@ hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int
     return hipGetLastError();
 }
 
+// 65+ tokens: the fp16 kernel, 128-row x 32-token workgroups (8 waves, two
+// 36 KiB stages: two workgroups per CU), measured on the 512-token prefill
+// against 64-token workgroups and 3-deep rings
+constexpr int kF16MinTokens = 65;
+
 size_t gemm_mfma_scratch_bytes(int T, int nb) {
     if (T <= 0 || nb <= 0) return 0;
+    if (T >= kF16MinTokens) {
+        const size_t tp = (size_t)((T + 31) / 32 * 32);  // 32-token groups
+        return (size_t)nb * 8 * tp * (64 + 4 + 4);
+    }
     const size_t tp = (size_t)padded_tokens(T, pick_mfma(T, nb));
     return (size_t)nb * 8 * tp * (32 + 4 + 4);
 }
@@ -745,6 +1036,13 @@ size_t gemm_mfma_scratch_bytes(int T, int nb) {
 hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
                                    int nb, long row_bytes, void* scratch, hipStream_t st) {
     if (rows <= 0 || T <= 0 || nb <= 0 || scratch == nullptr) return hipErrorInvalidValue;
+    if (T >= kF16MinTokens) {
+        const auto* w = static_cast<const uint8_t*>(W);
+        const auto* xq = static_cast<const uint8_t*>(XQ8);
+        auto* sc = static_cast<uint8_t*>(scratch);
+        launch16_cfg<8, 2, 2>(Y, w, xq, sc, rows, nb, row_bytes, T, st);
+        return hipGetLastError();
+    }
     const MfmaCfg c = pick_mfma(T, nb);
     const int Tp = padded_tokens(T, c);
     const int nkb = nb * 8;

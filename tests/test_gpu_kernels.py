@@ -176,7 +176,9 @@ def test_gemv_rejects_bad_arguments(ctx):
 # ---------------------------------------------------------------------------
 
 GEMM_CASES = [(11008, 4096, 1), (11008, 4096, 4), (1024, 4096, 16), (512, 4096, 64),
-              (75, 11008, 5), (33, 256, 9), (40, 512, 17), (300, 1024, 33), (64, 768, 130)]
+              (75, 11008, 5), (33, 256, 9), (40, 512, 17), (300, 1024, 33), (64, 768, 130),
+              # the fp16 matrix-core kernel (65+ tokens): ragged 128-row and 64-token tiles
+              (300, 1024, 200), (520, 2048, 65), (1100, 4096, 96)]
 
 
 @pytest.mark.parametrize("path", [None, 1, 2], ids=["auto", "dot4", "mfma"])
@@ -201,6 +203,26 @@ def test_gemm_q4k_q8(ctx, rows, cols, T, path):
         dict(rtol=1e-4, atol=1e-5)
     ok, err = close(got[t], ctx.download(dy, np.float32, rows), **tol)
     assert ok, err
+
+
+def test_gemm_q4k_q8_wide_kernel_matches_int8_kernel(ctx):
+    """The fp16 matrix-core kernel (65+ tokens) computes the int8 kernel's
+    sums (sc * S exact in both): token t's row depends on token t alone, so
+    the first 64 rows of a 130-token product match the 64-token product (int8
+    kernel) up to the order of the sub-block sums (the int8 kernel splits a
+    tile's sub-blocks over two waves at 64 tokens): fp32 rounding only."""
+    rows, cols = 300, 2048
+    W = weights(Q4K, rows, cols, 9)
+    X = np.random.default_rng(130).standard_normal(130 * cols).astype(np.float32)
+    XQ = O.quantize_q8_0(X)
+    dW, dX = ctx.upload(W), ctx.upload(XQ)
+    rb = O.row_bytes(Q4K, cols)
+    out = {}
+    for T in (130, 64):
+        dY = ctx.alloc(T * rows * 4)
+        ctx.gemm_q4k_q8(dY, dW, dX, rows, T, cols, rb, path=2)
+        out[T] = ctx.download(dY, np.float32, T * rows).reshape(T, rows)
+    np.testing.assert_allclose(out[130][:64], out[64], rtol=1e-5, atol=1e-5)
 
 
 GEMM6_CASES = [(4096, 4096, 1), (4096, 11008, 4), (512, 11008, 9), (2048, 2048, 17),
