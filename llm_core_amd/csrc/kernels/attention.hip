@@ -139,12 +139,19 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     // 2. the whole K/V tile into registers.  Rows past n re-read row t0 (a
     //    written, finite row); their score is -inf and their weight 0 below.
     //    The new row p (still stale in the cache) is replaced after the RoPE.
+    //    K rows first: the scores and the softmax need only them, and run
+    //    while the V rows are still arriving.
     float4 kr[NI], vr[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         const int r = wave * RPW + i * RPI + rsub;
         const size_t off = (size_t)(r < n ? t0 + r : t0) * kve + (size_t)kvh * HD + col;
         kr[i] = *reinterpret_cast<const float4*>(a.kcache + off);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int r = wave * RPW + i * RPI + rsub;
+        const size_t off = (size_t)(r < n ? t0 + r : t0) * kve + (size_t)kvh * HD + col;
         vr[i] = *reinterpret_cast<const float4*>(a.vcache + off);
     }
 
@@ -195,8 +202,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
 #pragma unroll
         for (int g = 0; g < GM; g++) {
             if (g < G) {
-                const float s = group_sum<LPR>(dot4f(qv[g], kr[i], 0.f));
-                if (lane % LPR == 0) sc[g][r] = r < n ? s * scale : -INFINITY;
+                // DPP reduction: the row's sum lands in its last lane
+                const float s = group_sum_last<LPR>(dot4f(qv[g], kr[i], 0.f));
+                if (lane % LPR == LPR - 1) sc[g][r] = r < n ? s * scale : -INFINITY;
             }
         }
     }
@@ -205,11 +213,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     // 5. per-head max, exp, sum: wave w takes heads w, w+4, ...; lane = row
     for (int g = wave; g < G; g += kAttnWaves) {
         const float s = sc[g][lane];
-        const float m = wave_max(s);
+        const float m = wave_max_bcast(s);
         const float e = lane < n ? expf(s - m) : 0.f;
         sc[g][lane] = e;
-        const float l = wave_sum(e);
-        if (lane == 0) {
+        const float l = group_sum_last<64>(e);
+        if (lane == 63) {
             stat[g][0] = m;
             stat[g][1] = l;
         }

@@ -70,6 +70,19 @@ __device__ __forceinline__ float group_sum_last(float v) {
     return v;
 }
 
+// Maximum over the wave, returned in every lane: the DPP steps of
+// group_sum_last<64> with max (masked rows keep -inf), then lane 63 read into
+// a scalar register.
+__device__ __forceinline__ float wave_max_bcast(float v) {
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0xb1, 0xf, 0xf, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x4e, 0xf, 0xf, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x141, 0xf, 0xf, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x140, 0xf, 0xf, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x142, 0xa, 0xf, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x143, 0xc, 0xf, false));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
