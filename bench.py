@@ -116,6 +116,13 @@ def q6k_sweep(ctx, Ms=(1, 8, 16, 64)):
     return res
 
 
+# --eager: the --only gemm sweep launches each GEMM directly instead of
+# replaying a captured graph (kernel traces: the profiler's instrumentation has
+# crashed the host process inside graph capture here; timings then include the
+# host's launch gaps, the kernel durations in the trace do not)
+EAGER_GEMM = False
+
+
 def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL_BYTES + (96 << 20),
               qtype=None):
     """The T-token Q4_K (or Q6_K) x Q8_0 GEMM (config 4: Q4_K 11008x4096, M
@@ -135,9 +142,19 @@ def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL
     dY = ctx.alloc(M * rows * 4)
     alg = W.nbytes + M * (cols // 32 * 36) + 4 * M * rows
     res = {"M": M}
+    gemm = ctx.gemm_q4k_q8 if qtype == hip.AXF_TYPE_Q4_K else ctx.gemm_q6k_q8
     for name, path in (("dot4", 1), ("mfma", 2), ("auto", 0)):
-        ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2, path, qtype)
-        ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps, path, qtype)
+        if EAGER_GEMM:  # direct launches (no graph capture); host gaps included
+            for b in bufs[:2]:
+                gemm(dY, b, xq, rows, M, cols, rb, path=path or None)
+            ctx.timer_start()
+            for _ in range(reps):
+                for b in bufs:
+                    gemm(dY, b, xq, rows, M, cols, rb, path=path or None)
+            ms = ctx.timer_stop()
+        else:
+            ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2, path, qtype)
+            ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps, path, qtype)
         res[f"{name}_us"] = round(ms * 1000.0 / (reps * n_copies), 3)
     us = res["auto_us"]
     for b in bufs:
@@ -254,6 +271,8 @@ def main() -> int:
                     help="approximate CPU seconds spent on the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill"], default="all")
+    ap.add_argument("--eager", action="store_true",
+                    help="--only gemm: direct launches, no graph capture (for kernel traces)")
     ap.add_argument("--skip-c4", action="store_true",
                     help="leave out the config-4 GEMM sweep (shorter profiling runs)")
     ap.add_argument("--no-e2e", action="store_true",
@@ -290,6 +309,8 @@ def main() -> int:
     out: dict = {}
 
     if args.only == "gemm":  # config 4 sweep alone (not a bench line)
+        global EAGER_GEMM
+        EAGER_GEMM = args.eager
         print(json.dumps({"c4_q4k_q8_gemm_11008x4096": c4_sweep(ctx),
                           "q6k_q8_gemm_4096x11008": q6k_sweep(ctx)}))
         return 0

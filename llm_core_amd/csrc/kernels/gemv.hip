@@ -110,29 +110,68 @@ __device__ __forceinline__ int hi_dot_fix(int dot16, int xsum) {
 }
 
 // ---------------------------------------------------------------------------
-// Q6_K byte fetch: 2-byte aligned sources read as 16-byte vectors.
+// Q6_K byte fetch from 2-byte aligned blocks, two ways:
+//   A = false: aligned dwords + v_alignbyte (more load instructions and VALU);
+//   A = true:  16-byte vectors at the unaligned address (global loads take
+//              them; fewer instructions, but on the 255 MB config-2 head the
+//              2-byte-misaligned vectors stream ~14% slower).
+// The 64-lane-row GEMVs (K >= 4096, VALU-heavy in the fused decode kernels)
+// take A = true; the 16/32-lane rows (K <= 2048, bandwidth-bound) A = false.
 // ---------------------------------------------------------------------------
-template <int N>
+template <int N, bool A>
 __device__ __forceinline__ void load_u2(const uint8_t* p, uint32_t (&out)[N]) {
-    static_assert(N % 4 == 0, "whole 16-byte vectors");
+    if constexpr (A) {
+        static_assert(N % 4 == 0, "whole 16-byte vectors");
 #pragma unroll
-    for (int k = 0; k < N / 4; k++) {
-        const uint4 v = ld16_a2(p + 16 * k);
-        out[4 * k] = v.x;
-        out[4 * k + 1] = v.y;
-        out[4 * k + 2] = v.z;
-        out[4 * k + 3] = v.w;
+        for (int k = 0; k < N / 4; k++) {
+            const uint4 v = ld16_a2(p + 16 * k);
+            out[4 * k] = v.x;
+            out[4 * k + 1] = v.y;
+            out[4 * k + 2] = v.z;
+            out[4 * k + 3] = v.w;
+        }
+    } else {
+        // reads [p & ~3, (p & ~3) + 4*(N+1)), inside the 210-byte block for the
+        // ql/qh fields (N = 8)
+        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+        const uint32_t sh = (uint32_t)(a & 3);
+        uint32_t w[N + 1];
+#pragma unroll
+        for (int k = 0; k <= N; k++) w[k] = ld4(base + 4 * k);
+#pragma unroll
+        for (int k = 0; k < N; k++) out[k] = alignbyte(w[k + 1], w[k], sh);
     }
 }
 
-// Scales (16 bytes at blk+192) and d (2 bytes at blk+208).
+// Scales (16 bytes at blk+192) and d (2 bytes at blk+208), never past blk+210.
+template <bool A>
 __device__ __forceinline__ void load_q6_tail(const uint8_t* blk, uint32_t (&sc)[4], uint32_t& dbits) {
-    const uint4 v = ld16_a2(blk + 192);
-    sc[0] = v.x;
-    sc[1] = v.y;
-    sc[2] = v.z;
-    sc[3] = v.w;
-    dbits = ld2(blk + 208);
+    if constexpr (A) {
+        const uint4 v = ld16_a2(blk + 192);
+        sc[0] = v.x;
+        sc[1] = v.y;
+        sc[2] = v.z;
+        sc[3] = v.w;
+        dbits = ld2(blk + 208);
+    } else {
+        const uint8_t* p = blk + 192;
+        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+        const uint32_t sh = (uint32_t)(a & 3);
+        uint32_t w[5];
+#pragma unroll
+        for (int k = 0; k < 4; k++) w[k] = ld4(base + 4 * k);
+        if (sh) {
+            w[4] = ld4(base + 16);  // bytes p+14..p+17: inside the block
+            dbits = w[4] >> 16;
+        } else {
+            w[4] = 0;
+            dbits = ld2(p + 16);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) sc[k] = alignbyte(w[k + 1], w[k], sh);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -234,11 +273,12 @@ struct Q6Chunk {
     uint32_t ql[8], qh[8], sc[4], dbits;
 };
 
+template <bool A>
 __device__ __forceinline__ void load_q6_chunk(const uint8_t* blk, int c, Q6Chunk& k) {
     const int h = (c >> 1) & 1, t = c & 1;
-    load_u2<8>(blk + 64 * h + 32 * t, k.ql);
-    load_u2<8>(blk + 128 + 32 * h, k.qh);
-    load_q6_tail(blk, k.sc, k.dbits);
+    load_u2<8, A>(blk + 64 * h + 32 * t, k.ql);
+    load_u2<8, A>(blk + 128 + 32 * h, k.qh);
+    load_q6_tail<A>(blk, k.sc, k.dbits);
 }
 
 // ---------------------------------------------------------------------------
@@ -506,7 +546,7 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
 #pragma unroll
             for (int i = 0; i < CPL; i++) {
                 const int c = min(rl + i * LPR, nchunks - 1);
-                load_q6_chunk(W + row * rb + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
+                load_q6_chunk<LPR == 64>(W + row * rb + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -636,7 +676,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q6k_f32(float* __restrict__ y
         for (int i = 0; i < CPL; i++) {
             const int c = rl + i * LPR;
             if (row < rows && c < nchunks) {
-                load_q6_chunk(W + row * row_bytes + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
+                load_q6_chunk<LPR == 64>(W + row * row_bytes + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
             } else {
 #pragma unroll
                 for (int k = 0; k < 8; k++) wk[n][i].ql[k] = wk[n][i].qh[k] = 0;
@@ -836,7 +876,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q6k_q8(float* __restrict__ Y,
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
             const int c = min(rl + i * LPR, nchunks - 1);
-            load_q6_chunk(W + row * row_bytes + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
+            load_q6_chunk<LPR == 64>(W + row * row_bytes + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
         }
     }
     // token records: the clamped token t0 + min(t, nt - 1), so every record is valid
