@@ -248,6 +248,23 @@ def summarize_traffic(fetch_dir: str, write_dir: str) -> tuple[str, float | None
     return "\n".join(lines), total
 
 
+def summarize_counters(dirs: list[str]) -> str:
+    """Per (kernel, grid) mean of every counter over the dispatches of one or
+    more rocprofv3 --pmc passes (-f csv), for counters other than the traffic
+    pair (SQ instruction and cycle counts)."""
+    import collections
+    agg: dict = collections.defaultdict(lambda: collections.defaultdict(list))
+    for d in dirs:
+        for r in _csv(d, "_counter_collection.csv"):
+            key = (r["Kernel_Name"][:90], int(r["Grid_Size"]))
+            agg[key][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    lines = []
+    for (name, grid), cs in sorted(agg.items(), key=lambda kv: -kv[0][1]):
+        vals = "  ".join(f"{c}={sum(v) / len(v):.4g}" for c, v in sorted(cs.items()))
+        lines.append(f"{name}  grid {grid}  (n={len(next(iter(cs.values())))})\n    {vals}")
+    return "\n".join(lines)
+
+
 def committed_traffic() -> float | None:
     """traffic_bytes_per_launch from the committed rocprofv3 --pmc summary."""
     try:
@@ -283,10 +300,15 @@ def main() -> int:
                     help="also time the roofline GEMV on one weight copy (Infinity-Cache warm)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
                     help="print a summary of rocprofv3 csv output directories and exit")
+    ap.add_argument("--counters", nargs="+", metavar="DIR",
+                    help="summarize rocprofv3 --pmc passes: mean counter values per kernel")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="HBM traffic of the roofline kernel from two rocprofv3 --pmc csv "
                          "directories (FETCH_SIZE, WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.counters:
+        print(summarize_counters(args.counters))
+        return 0
     if args.summarize or args.traffic:
         for d in args.summarize or []:
             print(f"== {d}")
