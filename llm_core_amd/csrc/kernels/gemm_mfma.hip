@@ -159,7 +159,8 @@ __device__ __forceinline__ void mfma_sub_blocks(const uint8_t* wl, const uint8_t
         for (int sj = 0; sj < NS; sj++) {
             const int s = KPH + G::KS * sj;
             const int tok = kTile * (tt0 + w);
-            xv[w][sj] = *reinterpret_cast<const uint2*>(xl + (s * TW + tok + col) * 32 + 8 * g);
+            xv[w][sj] = *reinterpret_cast<const uint2*>(
+                xl + (s * TW + tok + col) * 32 + 8 * (g ^ (2 * ((col >> 3) & 1))));
             dx[w][sj] = *reinterpret_cast<const float4*>(dl + s * TW + tok + 4 * g);
         }
     v4i_t c[G::WT][NS];
@@ -296,8 +297,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_mfma_q4k(
             src[j] = W + (long)min(row_base + r, rows - 1) * row_bytes + (o - r * Q4K_BYTES);
             step[j] = Q4K_BYTES;
         } else if (o < G::WB + G::XB) {
-            const int x = o - G::WB, k = x / (TW * 32);
-            src[j] = xs + ((size_t)k * Tp + tok_base) * 32 + (x - k * TW * 32);
+            // halves of token t swapped when bit 3 of t is set (bank-conflict-free
+            // 8-byte reads, as in the Q6_K kernel)
+            const int x = o - G::WB, k = x / (TW * 32), r = x - k * TW * 32, t = r >> 5;
+            const int hb = ((r >> 4) & 1) ^ ((t >> 3) & 1);
+            src[j] = xs + ((size_t)k * Tp + tok_base) * 32 + t * 32 + hb * 16;
             step[j] = 8u * (uint32_t)Tp * 32u;
         } else {
             const int y = o - G::WB - G::XB;
@@ -670,7 +674,9 @@ template <int RT, int TT, int KS, int TS, int S>
 struct Stage6 {
     static constexpr int RW = kTile * RT, TW = kTile * TT;
     static constexpr int NW = KS * RT * TS;
-    static constexpr int SLOT = 224;
+    // a row's span is 224 bytes (14 pieces of 16); the slot is 240 bytes so
+    // that the 16 rows a wave reads sit 60 banks apart
+    static constexpr int SPAN = 224, SLOT = 240;
     static constexpr int WSB = RW * SLOT;     // weights of one super-block
     static constexpr int XSB = 8 * TW * 32;   // int8 activations of one super-block
     static constexpr int DSB = 8 * TW * 4;    // dx of one super-block
@@ -788,8 +794,8 @@ __device__ __forceinline__ void gemm6_step(
                 const int tok = kTile * (tt0 + w);
                 // (a scalar 64-bit read: its LDS access keeps the noalias scope
                 // that lets the copies into the other stage buffers stay in flight)
-                const long a =
-                    *reinterpret_cast<const long*>(xl + (kb * TW + tok + col) * 32 + 8 * g);
+                const long a = *reinterpret_cast<const long*>(
+                    xl + (kb * TW + tok + col) * 32 + 8 * (g ^ (2 * ((col >> 3) & 1))));
                 const float4 dx = *reinterpret_cast<const float4*>(dl + kb * TW + tok + 4 * g);
                 const v4i_t c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zi, 0, 0, 0);
                 const v4i_t c2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b2, zi, 0, 0, 0);
@@ -839,12 +845,17 @@ __global__ __launch_bounds__(KS * RT * TS * 64) void k_gemm_mfma_q6k(
             const int ks = o / G::WSB, y = o - ks * G::WSB, r = y / G::SLOT;
             pl.ks[j] = (uint32_t)ks;
             pl.base[j] = w0 + (uint32_t)min(row_base + r, rows - 1) * (uint32_t)row_bytes;
-            pl.aux[j] = (uint32_t)(y - r * G::SLOT);
+            const int a = y - r * G::SLOT;
+            pl.aux[j] = (uint32_t)(a < G::SPAN ? a : 0);  // slot padding: a duplicate
         } else if (o < G::WB + G::XB) {
             const int x = o - G::WB, ks = x / G::XSB, y = x - ks * G::XSB, k = y / (TW * 32);
+            // token t's two 16-byte halves are swapped in LDS when bit 3 of t is
+            // set, so the 8-byte reads of 32 lanes (16 tokens x 2 k-groups) hit
+            // distinct banks
+            const int r = y - k * TW * 32, t = r >> 5, hb = ((r >> 4) & 1) ^ ((t >> 3) & 1);
             pl.ks[j] = (uint32_t)ks;
             pl.base[j] = reinterpret_cast<uint64_t>(xs + ((size_t)k * Tp + tok_base) * 32 +
-                                                    (y - k * TW * 32));
+                                                    t * 32 + hb * 16);
             pl.aux[j] = 8u * (uint32_t)Tp * 32u;
         } else {
             const int x = o - G::WB - G::XB, ks = x / G::DSB, y = x - ks * G::DSB,
