@@ -96,6 +96,34 @@ def c5_run(gpu, hp, e2e_too=True):
             "generated_head": [int(t) for t in gen[:8]]}
 
 
+def c3_run(ctx, warmup=10, steps=100):
+    """Config 3: one Qwen2.5-3B-like decoder layer (hidden 2048, 16/2 heads,
+    head_dim 128, FFN 11008, q/k/v biases, eps 1e-6, theta 1e6; Q4_K_M mix)
+    decoding at position 1024 over 1024 prior KV rows of N(0,1).  Timed as the
+    graph-replayed decode step of a 1-layer model whose vocabulary is 512, so
+    that the step is the layer plus a small embedding, head and argmax."""
+    import numpy as np
+    from llm_core_amd import hip
+    from llm_core_amd.model import QWEN25_3B_LAYER, Hparams, LlamaHip, SynthLlama
+
+    hp = Hparams(n_ctx=1025, **{**QWEN25_3B_LAYER, "n_vocab": 512})
+    model = SynthLlama(hp, seed=7, with_bias=True)
+    kve = hp.n_kv_heads * hp.head_dim
+    pos = 1024
+    k = hip.synth_normal(hp.n_ctx * kve, 701).reshape(hp.n_ctx, kve)
+    v = hip.synth_normal(hp.n_ctx * kve, 702).reshape(hp.n_ctx, kve)
+    with LlamaHip(ctx, model) as gpu:
+        gpu.set_kv(0, k, v, pos)
+        ms = gpu.bench_decode(pos, warmup, steps) / steps
+    nbytes = model.weight_bytes_per_token() + 2 * pos * kve * 4
+    log(f"config 3 layer (1-layer model, vocab 512) decode step @pos {pos}: {ms * 1e3:.1f} us, "
+        f"{nbytes / (ms * 1e-3) / 1e9:.0f} GB/s over {nbytes / 1e6:.1f} MB")
+    return {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": int(nbytes),
+            "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "what": "decode step of a 1-layer Qwen2.5-3B-like model (vocab 512) at position "
+                    "1024: the layer plus embedding, a 512-row head and argmax"}
+
+
 def c4_sweep(ctx, Ms=(1, 2, 4, 8, 16, 32, 64)):
     res = [gemm_case(ctx, M) for M in Ms]
     for g4 in res:
@@ -287,11 +315,12 @@ def main() -> int:
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="approximate CPU seconds spent on the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill"], default="all")
+    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill", "c3"],
+                    default="all")
     ap.add_argument("--eager", action="store_true",
                     help="--only gemm: direct launches, no graph capture (for kernel traces)")
     ap.add_argument("--skip-c4", action="store_true",
-                    help="leave out the config-4 GEMM sweep (shorter profiling runs)")
+                    help="leave out the config-3 layer and config-4 GEMM timings (shorter profiling runs)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="--only prefill: time the prefill alone (no graph-replayed generation)")
     ap.add_argument("--skip-c5", action="store_true",
@@ -330,6 +359,9 @@ def main() -> int:
     log(f"device: {ctx.device_name()}")
     out: dict = {}
 
+    if args.only == "c3":  # config 3 layer alone (not a bench line)
+        print(json.dumps({"c3_qwen25_3b_layer_decode": c3_run(ctx, args.warmup, args.steps)}))
+        return 0
     if args.only == "gemm":  # config 4 sweep alone (not a bench line)
         global EAGER_GEMM
         EAGER_GEMM = args.eager
@@ -383,6 +415,7 @@ def main() -> int:
             "q6k_q8_gemm_4096x11008": g6,
             "c1_q4k_f32_4096x4096": {"us": round(c1["us_per_launch"], 3), "GBs": round(c1["gbs"], 1)},
             "c2_q6k_q8_151936x2048": {"us": round(c2["us_per_launch"], 3), "GBs": round(c2["gbs"], 1)},
+            "c3_qwen25_3b_layer_decode": None if args.skip_c4 else c3_run(ctx),
         }
         if args.only == "gemv" and not args.no_cpu:
             from oracle import oracle as O

@@ -97,9 +97,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     __shared__ float ov[kAttnWaves][GM * HD];
     __shared__ float stat[GM][2];
 
-    // kv head fastest: workgroups dispatched together read adjacent bytes of each KV row
-    const int kvh = blockIdx.x, j = blockIdx.y, tok = blockIdx.z;
+    // kv head fastest: workgroups dispatched together read adjacent bytes of each
+    // KV row.  blockIdx.x = kv head * groups + group: a workgroup serves query
+    // heads g0 .. g0+Gl-1 of its kv head (GM per group; several groups re-read
+    // the same K/V rows, from L2, when there are few kv heads and splits).
     const int G = a.n_heads / a.n_kv_heads;
+    const int ngrp = (G + GM - 1) / GM;
+    const int kvh = blockIdx.x / ngrp, g0 = (blockIdx.x % ngrp) * GM;
+    const int Gl = min(GM, G - g0);
+    const int j = blockIdx.y, tok = blockIdx.z;
     const int p = (a.pos_dev ? *a.pos_dev : a.pos) + tok;
     // query row tok and its partials (tok > 0 only in batched prefill)
     const float* qp = a.q + (size_t)tok * a.q_ld;
@@ -110,7 +116,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     const size_t kve = (size_t)a.n_kv_heads * HD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = (lane % LPR) * 4, rsub = lane / LPR;
+    // the split holding the new row uses it; the first head group stores it
     const bool owns_new = a.store_kv && p - t0 < kAttnSplit;
+    const bool stores_new = owns_new && g0 == 0;
     const int tid = threadIdx.x;
 
     // 1. small operands first, so their latency hides under the tile loads:
@@ -121,8 +129,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     float qraw[QPT], qb[QPT];
 #pragma unroll
     for (int k = 0; k < QPT; k++) {
-        const int t = min(tid + k * kAttnThreads, G * HD - 1);
-        const size_t e = ((size_t)kvh * G + t / HD) * HD + t % HD;
+        const int t = min(tid + k * kAttnThreads, Gl * HD - 1);
+        const size_t e = ((size_t)kvh * G + g0 + t / HD) * HD + t % HD;
         qraw[k] = qp[e];
         qb[k] = (a.bq ? a.bq : qp)[e];
     }
@@ -159,7 +167,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
 #pragma unroll
     for (int k = 0; k < QPT; k++) {
         const int t = tid + k * kAttnThreads;
-        if (t < G * HD) qs[t] = a.bq ? qraw[k] + qb[k] : qraw[k];
+        if (t < Gl * HD) qs[t] = a.bq ? qraw[k] + qb[k] : qraw[k];
     }
     if (owns_new && tid < HD) {
         knew[tid] = a.bk ? kk + kb : kk;
@@ -171,12 +179,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     }
     __syncthreads();
     if (a.cos_t) {
-        rope_in_lds<HD>(qs, G, crs, srs);
+        rope_in_lds<HD>(qs, Gl, crs, srs);
         if (owns_new) rope_in_lds<HD>(knew, 1, crs, srs);
     }
     __syncthreads();
     if (owns_new) {
-        if (tid < HD) {
+        if (stores_new && tid < HD) {
             a.kcache[(size_t)p * kve + (size_t)kvh * HD + tid] = knew[tid];
             a.vcache[(size_t)p * kve + (size_t)kvh * HD + tid] = vnew[tid];
         }
@@ -194,14 +202,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     float4 qv[GM];
 #pragma unroll
     for (int g = 0; g < GM; g++)
-        qv[g] = g < G ? *reinterpret_cast<const float4*>(qs + g * HD + col)
+        qv[g] = g < Gl ? *reinterpret_cast<const float4*>(qs + g * HD + col)
                       : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         const int r = wave * RPW + i * RPI + rsub;
 #pragma unroll
         for (int g = 0; g < GM; g++) {
-            if (g < G) {
+            if (g < Gl) {
                 // DPP reduction: the row's sum lands in its last lane
                 const float s = group_sum_last<LPR>(dot4f(qv[g], kr[i], 0.f));
                 if (lane % LPR == LPR - 1) sc[g][r] = r < n ? s * scale : -INFINITY;
@@ -211,7 +219,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
     __syncthreads();
 
     // 5. per-head max, exp, sum: wave w takes heads w, w+4, ...; lane = row
-    for (int g = wave; g < G; g += kAttnWaves) {
+    for (int g = wave; g < Gl; g += kAttnWaves) {
         const float s = sc[g][lane];
         const float m = wave_max_bcast(s);
         const float e = lane < n ? expf(s - m) : 0.f;
@@ -233,11 +241,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
         const int r = wave * RPW + i * RPI + rsub;
 #pragma unroll
         for (int g = 0; g < GM; g++)
-            if (g < G) o[g] = fma4(sc[g][r], vr[i], o[g]);
+            if (g < Gl) o[g] = fma4(sc[g][r], vr[i], o[g]);
     }
 #pragma unroll
     for (int g = 0; g < GM; g++) {
-        if (g < G) {
+        if (g < Gl) {
 #pragma unroll
             for (int off = LPR; off < 64; off <<= 1) {
                 o[g].x += __shfl_xor(o[g].x, off);
@@ -249,15 +257,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
         }
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < G * HD; t += kAttnThreads) {
+    for (int t = threadIdx.x; t < Gl * HD; t += kAttnThreads) {
         const int g = t / HD, d = t % HD;
         float acc = ov[0][t];
 #pragma unroll
         for (int w = 1; w < kAttnWaves; w++) acc += ov[w][t];
-        part[((size_t)(kvh * G + g) * a.nsplit + j) * (HD + 2) + 2 + d] = acc;
+        part[((size_t)(kvh * G + g0 + g) * a.nsplit + j) * (HD + 2) + 2 + d] = acc;
     }
-    if (threadIdx.x < G) {
-        float* dst = part + ((size_t)(kvh * G + threadIdx.x) * a.nsplit + j) * (HD + 2);
+    if ((int)threadIdx.x < Gl) {
+        float* dst = part + ((size_t)(kvh * G + g0 + threadIdx.x) * a.nsplit + j) * (HD + 2);
         dst[0] = stat[threadIdx.x][0];
         dst[1] = stat[threadIdx.x][1];
     }
@@ -582,17 +590,29 @@ hipError_t launch_attention_prefill(const AttnArgs& a, int head_dim, hipStream_t
     }
 }
 
+// Query heads per workgroup: all G of a kv head when kv heads x splits fill
+// the GPU; fewer (down to 1) when they do not, so that a model with 2 kv heads
+// at context 1024 runs 272 workgroups instead of 34.  Groups of one kv head
+// each read its K/V rows (from L2 after the first).
+static int attn_heads_per_group(int G, long kv_work) {
+    int gm = 1;
+    while (gm < G && gm < 8) gm *= 2;  // G rounded up to a power of two
+    while (gm > 1 && kv_work * ((G + gm - 1) / gm) < 256) gm /= 2;
+    return gm;
+}
+
 template <int HD>
 static hipError_t launch_attn_hd(const AttnArgs& a, int G, hipStream_t st) {
     const unsigned nt = a.n_tok > 1 ? (unsigned)a.n_tok : 1u;
-    const dim3 grid((unsigned)a.n_kv_heads, (unsigned)a.nsplit, nt);
-    if (G == 1)
+    const int gm = attn_heads_per_group(G, (long)a.n_kv_heads * a.nsplit * nt);
+    const dim3 grid((unsigned)(a.n_kv_heads * ((G + gm - 1) / gm)), (unsigned)a.nsplit, nt);
+    if (gm == 1)
         hipLaunchKernelGGL((k_attn_split<HD, 1>), grid, dim3(kAttnThreads), 0, st, a);
-    else if (G == 2)
+    else if (gm == 2)
         hipLaunchKernelGGL((k_attn_split<HD, 2>), grid, dim3(kAttnThreads), 0, st, a);
-    else if (G <= 4)
+    else if (gm == 4)
         hipLaunchKernelGGL((k_attn_split<HD, 4>), grid, dim3(kAttnThreads), 0, st, a);
-    else if (G <= 8)
+    else if (gm == 8)
         hipLaunchKernelGGL((k_attn_split<HD, 8>), grid, dim3(kAttnThreads), 0, st, a);
     else
         return hipErrorInvalidValue;
