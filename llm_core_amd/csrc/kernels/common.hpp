@@ -42,6 +42,7 @@ __device__ __forceinline__ uint4 ld16_a2(const uint8_t* p) {
     const u32x4_a2_t v = *reinterpret_cast<const u32x4_a2_t*>(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+typedef uint32_t u32x2_a2_t __attribute__((ext_vector_type(2), aligned(2)));  // 8 bytes, 2-aligned
 
 // Sum over groups of `width` consecutive lanes (width a power of two <= 64);
 // every lane of the group receives the group sum.

@@ -54,6 +54,14 @@ static inline KernCfg pick_cfg_nt(int nchunks, int nt) {
     if (nt == 1024) k.nr = (k.lpr == 64 && k.cpl == 1) ? 2 : 1;
     return k;
 }
+// Rows of 9..16 super-blocks (K 2304..4096) at 512/1024 threads run half-block
+// units (PAIR): 32 lanes per row, one unit (two chunks sharing the block
+// header or the Q6_K half's qh/scales) per lane, one row per 32 lanes, so a
+// workgroup holds (threads / 32) rows, as many as the one-chunk layout's two
+// rows per lane at 64 lanes.  Measured at 11008 x 4096 (Q4_K) and 4096 x 4096
+// (Q6_K): ~9% faster than one chunk per lane; at K = 11008 it is not.
+static inline bool pair_cfg(int nb) { return nb > 8 && nb <= 16; }
+
 // K <= 8192 (fused normalisation); fp32 activations up to K = 16384 at 512
 // threads and K = 12288 at 1024 (the 128-VGPR budget holds 3 Q6_K chunks per lane)
 #define AXF_GEMV_CFGS_512_NORM(X) X(16, 1, 2) X(32, 1, 2) X(64, 1, 2) X(64, 2, 1)
@@ -133,9 +141,8 @@ __device__ __forceinline__ void load_u2(const uint8_t* p, uint32_t (&out)[N]) {
     } else {
         // reads [p & ~3, (p & ~3) + 4*(N+1)), inside the 210-byte block for the
         // ql/qh fields (N = 8)
-        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-        const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-        const uint32_t sh = (uint32_t)(a & 3);
+        const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);
+        const uint8_t* base = p - sh;  // (pointer arithmetic keeps the global address space)
         uint32_t w[N + 1];
 #pragma unroll
         for (int k = 0; k <= N; k++) w[k] = ld4(base + 4 * k);
@@ -156,19 +163,16 @@ __device__ __forceinline__ void load_q6_tail(const uint8_t* blk, uint32_t (&sc)[
         dbits = ld2(blk + 208);
     } else {
         const uint8_t* p = blk + 192;
-        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-        const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-        const uint32_t sh = (uint32_t)(a & 3);
+        const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);
+        const uint8_t* base = p - sh;
         uint32_t w[5];
 #pragma unroll
         for (int k = 0; k < 4; k++) w[k] = ld4(base + 4 * k);
-        if (sh) {
-            w[4] = ld4(base + 16);  // bytes p+14..p+17: inside the block
-            dbits = w[4] >> 16;
-        } else {
-            w[4] = 0;
-            dbits = ld2(p + 16);
-        }
+        // sh = 2: bytes p+14..p+17 (inside the block).  sh = 0: the dword is
+        // not used (alignbyte by 0 takes w[3]); it is read from p+12 so the
+        // load stays inside the block, with no branch between the loads.
+        w[4] = ld4(base + (sh ? 16 : 12));
+        dbits = ld2(p + 16);
 #pragma unroll
         for (int k = 0; k < 4; k++) sc[k] = alignbyte(w[k + 1], w[k], sh);
     }
@@ -423,19 +427,101 @@ __device__ __forceinline__ void direct_sums(uint4 (&dx)[5]) {
     }
 }
 
-template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI>
+// One Q4_K chunk (64 weights: sub-blocks 2*part, 2*part+1, qs bytes qa|qb)
+// of one row against its activation record (xa, xb, meta = {d_A, d_B, sum_A,
+// sum_B}); returns acc plus the chunk's contribution.
+__device__ __forceinline__ float q4k_chunk_dot(float acc, const uint4& h, const uint4& qa,
+                                               const uint4& qb, int part,
+                                               const uint32_t (&xa)[8], const uint32_t (&xb)[8],
+                                               const uint4& meta) {
+    const float dx0 = __uint_as_float(meta.x), dx1 = __uint_as_float(meta.y);
+    const float sx0 = (float)(int)meta.z, sx1 = (float)(int)meta.w;
+    const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+    uint32_t sc0, m0, sc1, m1;
+    q4k_scales(h.y, h.z, h.w, part, sc0, m0, sc1, m1);
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    int dlo = 0, dhi = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        dlo = dot4((int)(q[k] & 0x0f0f0f0fu), (int)xa[k], dlo);
+        dhi = dot4(hi_nibbles_x16(q[k]), (int)xb[k], dhi);
+    }
+    dhi = hi_dot_fix(dhi, (int)meta.w);
+    const float s0 = ((float)sc0 * d) * dx0, mm0 = ((float)m0 * dmin) * dx0;
+    const float s1 = ((float)sc1 * d) * dx1, mm1 = ((float)m1 * dmin) * dx1;
+    float v = acc;
+    v = fmaf(s0, (float)dlo, v);
+    v = fmaf(-mm0, sx0, v);
+    v = fmaf(s1, (float)dhi, v);
+    v = fmaf(-mm1, sx1, v);
+    return v;
+}
+
+// One Q6_K chunk t of a half block: ql = its 8 ql dwords (low nibbles: part
+// t, high nibbles: part t+2), qh = the half's 8 qh dwords, sa / sb = the
+// half's scale bytes 0-3 / 4-7, d the block scale.  The -32 offset comes from
+// the record's per-16 activation sums.
+__device__ __forceinline__ float q6k_chunk_dot(float acc, const uint32_t* ql, const uint32_t* qh,
+                                               int t, uint32_t sa, uint32_t sb, float d,
+                                               const uint32_t (&xa)[8], const uint32_t (&xb)[8],
+                                               const uint4& meta) {
+    const float dxa = __uint_as_float(meta.x), dxb = __uint_as_float(meta.y);
+    const int sA0 = (int8_t)(sa >> (16 * t)), sA1 = (int8_t)(sa >> (16 * t + 8));
+    const int sB0 = (int8_t)(sb >> (16 * t)), sB1 = (int8_t)(sb >> (16 * t + 8));
+    int iA0 = -32 * (int)(int16_t)(meta.z & 0xffffu), iA1 = -32 * ((int)meta.z >> 16);
+    int iB0 = -32 * (int)(int16_t)(meta.w & 0xffffu), iB1 = -32 * ((int)meta.w >> 16);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t l = ql[k], hs = qh[k] >> (2 * t);
+        // 6-bit values: low nibble from ql, bits 4-5 from qh
+        const uint32_t qA = (l & 0x0f0f0f0fu) | ((hs << 4) & 0x30303030u);
+        const uint32_t qB = ((l >> 4) & 0x0f0f0f0fu) | (hs & 0x30303030u);
+        if (k < 4) {
+            iA0 = dot4((int)qA, (int)xa[k], iA0);
+            iB0 = dot4((int)qB, (int)xb[k], iB0);
+        } else {
+            iA1 = dot4((int)qA, (int)xa[k], iA1);
+            iB1 = dot4((int)qB, (int)xb[k], iB1);
+        }
+    }
+    float v = acc;
+    v = fmaf((d * (float)sA0) * dxa, (float)iA0, v);
+    v = fmaf((d * (float)sA1) * dxa, (float)iA1, v);
+    v = fmaf((d * (float)sB0) * dxb, (float)iB0, v);
+    v = fmaf((d * (float)sB1) * dxb, (float)iB1, v);
+    return v;
+}
+
+__device__ __forceinline__ void rec_load(const uint32_t* rec, int c, uint32_t (&xa)[8],
+                                         uint32_t (&xb)[8], uint4& meta) {
+    const uint4* r4 = reinterpret_cast<const uint4*>(rec + 20 * c);
+    const uint4 a0 = r4[0], a1 = r4[1], b0 = r4[2], b1 = r4[3];
+    meta = r4[4];
+    xa[0] = a0.x; xa[1] = a0.y; xa[2] = a0.z; xa[3] = a0.w;
+    xa[4] = a1.x; xa[5] = a1.y; xa[6] = a1.z; xa[7] = a1.w;
+    xb[0] = b0.x; xb[1] = b0.y; xb[2] = b0.z; xb[3] = b0.w;
+    xb[4] = b1.x; xb[5] = b1.y; xb[6] = b1.z; xb[7] = b1.w;
+}
+
+// Work units: PAIR = false: a unit is one chunk, lane (rl, i) owns chunk
+// rl + i*LPR.  PAIR = true: a unit is half a super-block (chunks 2u, 2u+1,
+// 128 weights), lane (rl, i) owns unit u = rl + i*LPR; the two chunks share
+// the block header (Q4_K d, dmin, scales) or the half's qh bytes, scales and d
+// (Q6_K), which are loaded and decoded once.  CPL counts units per lane.
+template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI, bool PAIR>
 __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __restrict__ W,
                                            long rb, int rows, float* __restrict__ y, int wg,
                                            uint32_t* rec, float* red) {
     constexpr int RPP = 64 / LPR;
     constexpr int RW = (NT / 64) * RPP * NR;  // rows per workgroup
-    constexpr bool REG = NT >= kWide;          // activation built from registers
-    // float4s of x per thread: K / 4 <= 16 * LPR * CPL
-    constexpr int KPT = (16 * LPR * CPL + NT - 1) / NT;
-    static_assert(REG ? ACT != (int)QAct::Q8 : ACT != (int)QAct::Norm, "prologue / workgroup");
+    constexpr int UC = PAIR ? 2 : 1;          // chunks per unit
+    constexpr bool REG = NT >= kWide && ACT != (int)QAct::Q8;  // activation built from registers
+    // float4s of x per thread: K / 4 <= 16 * LPR * CPL * UC
+    constexpr int KPT = (16 * LPR * CPL * UC + NT - 1) / NT;
+    static_assert(ACT != (int)QAct::Norm || REG, "the fused normalisation needs 512+ threads");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rl = lane % LPR, rg = lane / LPR;
-    const int nchunks = 4 * a.nb;
+    const int nunits = 4 * a.nb / UC;
     const int rloc0 = wave * (RPP * NR) + rg;
     const long row0 = (long)wg * RW + rloc0;
     float acc[NR];
@@ -444,10 +530,10 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
 
     // One chunk per lane with Q8_0 input: each lane reads its chunk's two Q8_0
     // blocks itself (L2-resident), before its weight loads; no LDS staging.
-    constexpr bool DIRECT = ACT == (int)QAct::Q8 && CPL == 1 && NT == kThreads;
+    constexpr bool DIRECT = ACT == (int)QAct::Q8 && CPL == 1 && NT == kThreads && !PAIR;
     uint4 dx[5];  // the chunk's activation record (DIRECT)
     if constexpr (DIRECT) {
-        const int c = min(rl, nchunks - 1);
+        const int c = min(rl, nunits - 1);
         const int A = QT == kQ4K ? 2 * c : 2 * c - (c & 1);
         const int B = QT == kQ4K ? A + 1 : A + 2;
         const uint8_t* pa = a.xq8 + (size_t)A * Q8_0_BYTES;
@@ -473,22 +559,8 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    if constexpr (QT == kQ4K) {
-        uint4 hdr[NR][CPL], qa[NR][CPL], qb[NR][CPL];
-#pragma unroll
-        for (int n = 0; n < NR; n++) {
-            const long row = min(row0 + (long)n * RPP, (long)rows - 1);
-#pragma unroll
-            for (int i = 0; i < CPL; i++) {
-                const int c = min(rl + i * LPR, nchunks - 1);
-                const uint8_t* blk = W + row * rb + (long)(c >> 2) * Q4K_BYTES;
-                const int part = c & 3;
-                hdr[n][i] = ld16(blk);
-                qa[n][i] = ld16(blk + 16 + 32 * part);
-                qb[n][i] = ld16(blk + 32 + 32 * part);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
+    // the activation, once this lane's weight loads are in flight
+    auto stage = [&]() {
         if constexpr (DIRECT)
             direct_sums<QT>(dx);
         else if constexpr (REG)
@@ -496,110 +568,117 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
         else
             stage_act<QT, NT, ACT>(rec, a);
         if constexpr (!DIRECT) __syncthreads();
-        // every chunk is computed on clamped (valid) data and its contribution
+    };
+
+    if constexpr (QT == kQ4K) {
+        // unit (n, i): header, then 16-byte qs vectors (2 per chunk)
+        uint4 hdr[NR][CPL], qv[NR][CPL][2 * UC];
+#pragma unroll
+        for (int n = 0; n < NR; n++) {
+            const long row = min(row0 + (long)n * RPP, (long)rows - 1);
+#pragma unroll
+            for (int i = 0; i < CPL; i++) {
+                const int u = min(rl + i * LPR, nunits - 1);
+                const uint8_t* blk = W + row * rb + (long)(u * UC >> 2) * Q4K_BYTES;
+                // first qs byte of the unit: 32 * part (chunk) or 64 * half (pair)
+                const int q0 = 16 + (PAIR ? 64 * (u & 1) : 32 * (u & 3));
+                hdr[n][i] = ld16(blk);
+#pragma unroll
+                for (int k = 0; k < 2 * UC; k++) qv[n][i][k] = ld16(blk + q0 + 16 * k);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        stage();
+        // every unit is computed on clamped (valid) data and its contribution
         // selected, so no load is sunk into a branch
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
-            const bool live = rl + i * LPR < nchunks;
-            const int c = min(rl + i * LPR, nchunks - 1);
-            {
-                const uint4* r4 = reinterpret_cast<const uint4*>(rec + 20 * c);
-                const uint4 xa0 = DIRECT ? dx[0] : r4[0], xa1 = DIRECT ? dx[1] : r4[1];
-                const uint4 xb0 = DIRECT ? dx[2] : r4[2], xb1 = DIRECT ? dx[3] : r4[3];
-                const uint4 meta = DIRECT ? dx[4] : r4[4];
-                const float dx0 = __uint_as_float(meta.x), dx1 = __uint_as_float(meta.y);
-                const float sx0 = (float)(int)meta.z, sx1 = (float)(int)meta.w;
-                const uint32_t xa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
-                const uint32_t xb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
+            const bool live = rl + i * LPR < nunits;
+            const int u = min(rl + i * LPR, nunits - 1);
+#pragma unroll
+            for (int j = 0; j < UC; j++) {
+                const int c = u * UC + j;
+                uint32_t xa[8], xb[8];
+                uint4 meta;
+                if constexpr (DIRECT) {
+                    const uint4 r[4] = {dx[0], dx[1], dx[2], dx[3]};
+                    xa[0] = r[0].x; xa[1] = r[0].y; xa[2] = r[0].z; xa[3] = r[0].w;
+                    xa[4] = r[1].x; xa[5] = r[1].y; xa[6] = r[1].z; xa[7] = r[1].w;
+                    xb[0] = r[2].x; xb[1] = r[2].y; xb[2] = r[2].z; xb[3] = r[2].w;
+                    xb[4] = r[3].x; xb[5] = r[3].y; xb[6] = r[3].z; xb[7] = r[3].w;
+                    meta = dx[4];
+                } else {
+                    rec_load(rec, c, xa, xb, meta);
+                }
                 const int part = c & 3;
 #pragma unroll
                 for (int n = 0; n < NR; n++) {
-                    const uint4 h = hdr[n][i];
-                    const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
-                    uint32_t sc0, m0, sc1, m1;
-                    q4k_scales(h.y, h.z, h.w, part, sc0, m0, sc1, m1);
-                    const uint32_t q[8] = {qa[n][i].x, qa[n][i].y, qa[n][i].z, qa[n][i].w,
-                                           qb[n][i].x, qb[n][i].y, qb[n][i].z, qb[n][i].w};
-                    int dlo = 0, dhi = 0;
-#pragma unroll
-                    for (int k = 0; k < 8; k++) {
-                        dlo = dot4((int)(q[k] & 0x0f0f0f0fu), (int)xa[k], dlo);
-                        dhi = dot4(hi_nibbles_x16(q[k]), (int)xb[k], dhi);
-                    }
-                    dhi = hi_dot_fix(dhi, (int)meta.w);
-                    const float s0 = ((float)sc0 * d) * dx0, mm0 = ((float)m0 * dmin) * dx0;
-                    const float s1 = ((float)sc1 * d) * dx1, mm1 = ((float)m1 * dmin) * dx1;
-                    float v = acc[n];
-                    v = fmaf(s0, (float)dlo, v);
-                    v = fmaf(-mm0, sx0, v);
-                    v = fmaf(s1, (float)dhi, v);
-                    v = fmaf(-mm1, sx1, v);
+                    const float v = q4k_chunk_dot(acc[n], hdr[n][i], qv[n][i][2 * j],
+                                                  qv[n][i][2 * j + 1], part, xa, xb, meta);
                     acc[n] = live ? v : acc[n];
                 }
             }
         }
     } else {
-        Q6Chunk wk[NR][CPL];
+        // unit (n, i): ql (8 dwords per chunk), the half's qh (8 dwords), scales, d
+        uint32_t ql[NR][CPL][8 * UC], qh[NR][CPL][8], sc[NR][CPL][4], db[NR][CPL];
 #pragma unroll
         for (int n = 0; n < NR; n++) {
             const long row = min(row0 + (long)n * RPP, (long)rows - 1);
 #pragma unroll
             for (int i = 0; i < CPL; i++) {
-                const int c = min(rl + i * LPR, nchunks - 1);
-                load_q6_chunk<LPR == 64>(W + row * rb + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
+                const int u = min(rl + i * LPR, nunits - 1);
+                const int c0 = u * UC;  // first chunk of the unit
+                const int h = (c0 >> 1) & 1, t = c0 & 1;
+                const uint8_t* blk = W + row * rb + (long)(c0 >> 2) * Q6K_BYTES;
+                if constexpr (PAIR) {
+                    // 64 ql bytes, 32 qh bytes, 8 scale bytes of half h, and d;
+                    // 16-byte vectors at 2-byte aligned addresses
+                    load_u2<16, true>(blk + 64 * h, ql[n][i]);
+                    load_u2<8, true>(blk + 128 + 32 * h, qh[n][i]);
+                    const u32x2_a2_t s = *reinterpret_cast<const u32x2_a2_t*>(blk + 192 + 8 * h);
+                    sc[n][i][0] = s.x;
+                    sc[n][i][1] = s.y;
+                    sc[n][i][2] = sc[n][i][3] = 0u;
+                    db[n][i] = ld2(blk + 208);
+                } else {
+                    load_u2<8, LPR == 64>(blk + 64 * h + 32 * t, ql[n][i]);
+                    load_u2<8, LPR == 64>(blk + 128 + 32 * h, qh[n][i]);
+                    load_q6_tail<LPR == 64>(blk, sc[n][i], db[n][i]);
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (DIRECT)
-            direct_sums<QT>(dx);
-        else if constexpr (REG)
-            stage_regs<QT, NT, KPT, ACT>(rec, xv, wv, n4, a.eps, red);
-        else
-            stage_act<QT, NT, ACT>(rec, a);
-        if constexpr (!DIRECT) __syncthreads();
+        stage();
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
-            const bool live = rl + i * LPR < nchunks;
-            const int c = min(rl + i * LPR, nchunks - 1);
-            {
-                const uint4* r4 = reinterpret_cast<const uint4*>(rec + 20 * c);
-                const uint4 xa0 = DIRECT ? dx[0] : r4[0], xa1 = DIRECT ? dx[1] : r4[1];
-                const uint4 xb0 = DIRECT ? dx[2] : r4[2], xb1 = DIRECT ? dx[3] : r4[3];
-                const uint4 meta = DIRECT ? dx[4] : r4[4];
-                const float dxa = __uint_as_float(meta.x), dxb = __uint_as_float(meta.y);
-                // -32 * (sum of the 16 activation values under each scale)
-                const int oA0 = -32 * (int)(int16_t)(meta.z & 0xffffu), oA1 = -32 * ((int)meta.z >> 16);
-                const int oB0 = -32 * (int)(int16_t)(meta.w & 0xffffu), oB1 = -32 * ((int)meta.w >> 16);
-                const uint32_t xa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
-                const uint32_t xb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
+            const bool live = rl + i * LPR < nunits;
+            const int u = min(rl + i * LPR, nunits - 1);
+#pragma unroll
+            for (int j = 0; j < UC; j++) {
+                const int c = u * UC + j;
+                uint32_t xa[8], xb[8];
+                uint4 meta;
+                if constexpr (DIRECT) {
+                    const uint4 r[4] = {dx[0], dx[1], dx[2], dx[3]};
+                    xa[0] = r[0].x; xa[1] = r[0].y; xa[2] = r[0].z; xa[3] = r[0].w;
+                    xa[4] = r[1].x; xa[5] = r[1].y; xa[6] = r[1].z; xa[7] = r[1].w;
+                    xb[0] = r[2].x; xb[1] = r[2].y; xb[2] = r[2].z; xb[3] = r[2].w;
+                    xb[4] = r[3].x; xb[5] = r[3].y; xb[6] = r[3].z; xb[7] = r[3].w;
+                    meta = dx[4];
+                } else {
+                    rec_load(rec, c, xa, xb, meta);
+                }
                 const int h = (c >> 1) & 1, t = c & 1;
 #pragma unroll
                 for (int n = 0; n < NR; n++) {
-                    const Q6Chunk& k6 = wk[n][i];
-                    const float d = h2f(k6.dbits);
-                    const uint32_t sa = h ? k6.sc[2] : k6.sc[0], sb = h ? k6.sc[3] : k6.sc[1];
-                    const int sA0 = (int8_t)(sa >> (16 * t)), sA1 = (int8_t)(sa >> (16 * t + 8));
-                    const int sB0 = (int8_t)(sb >> (16 * t)), sB1 = (int8_t)(sb >> (16 * t + 8));
-                    int iA0 = oA0, iA1 = oA1, iB0 = oB0, iB1 = oB1;
-#pragma unroll
-                    for (int k = 0; k < 8; k++) {
-                        const uint32_t l = k6.ql[k], hs = k6.qh[k] >> (2 * t);
-                        // 6-bit values: low nibble from ql, bits 4-5 from qh
-                        const uint32_t qA = (l & 0x0f0f0f0fu) | ((hs << 4) & 0x30303030u);
-                        const uint32_t qB = ((l >> 4) & 0x0f0f0f0fu) | (hs & 0x30303030u);
-                        if (k < 4) {
-                            iA0 = dot4((int)qA, (int)xa[k], iA0);
-                            iB0 = dot4((int)qB, (int)xb[k], iB0);
-                        } else {
-                            iA1 = dot4((int)qA, (int)xa[k], iA1);
-                            iB1 = dot4((int)qB, (int)xb[k], iB1);
-                        }
-                    }
-                    float v = acc[n];
-                    v = fmaf((d * (float)sA0) * dxa, (float)iA0, v);
-                    v = fmaf((d * (float)sA1) * dxa, (float)iA1, v);
-                    v = fmaf((d * (float)sB0) * dxb, (float)iB0, v);
-                    v = fmaf((d * (float)sB1) * dxb, (float)iB1, v);
+                    // PAIR: the scale dwords are the half's; otherwise all 16 scales
+                    // (selected by mask, not by a runtime array index)
+                    const uint32_t hm = PAIR ? 0u : 0u - (uint32_t)h;
+                    const uint32_t sa = sc[n][i][0] ^ ((sc[n][i][0] ^ sc[n][i][2]) & hm);
+                    const uint32_t sb = sc[n][i][1] ^ ((sc[n][i][1] ^ sc[n][i][3]) & hm);
+                    const float v = q6k_chunk_dot(acc[n], &ql[n][i][8 * j], qh[n][i], t, sa, sb,
+                                                  h2f(db[n][i]), xa, xb, meta);
                     acc[n] = live ? v : acc[n];
                 }
             }
@@ -628,26 +707,27 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
     }
 }
 
-template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI>
+template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI, bool PAIR>
 __global__ __launch_bounds__(NT) void k_qgemv(QGemvArgs a) {
     extern __shared__ uint4 smem[];
     uint32_t* rec = reinterpret_cast<uint32_t*>(smem);
     float* red = reinterpret_cast<float*>(rec + 80 * a.nb);
-    qgemv_body<QT, NT, LPR, CPL, NR, ACT, EPI>(a, a.W0, a.rb0, a.rows0, a.y0, blockIdx.x, rec, red);
+    qgemv_body<QT, NT, LPR, CPL, NR, ACT, EPI, PAIR>(a, a.W0, a.rb0, a.rows0, a.y0, blockIdx.x,
+                                                      rec, red);
 }
 
 // Workgroups [0, nwg0) run the Q4_K segment, the rest the Q6_K segment.
-template <int NT, int LPR, int CPL, int NR, int ACT>
+template <int NT, int LPR, int CPL, int NR, int ACT, bool PAIR>
 __global__ __launch_bounds__(NT) void k_qgemv2(QGemvArgs a) {
     extern __shared__ uint4 smem[];
     uint32_t* rec = reinterpret_cast<uint32_t*>(smem);
     float* red = reinterpret_cast<float*>(rec + 80 * a.nb);
     if ((int)blockIdx.x < a.nwg0)
-        qgemv_body<kQ4K, NT, LPR, CPL, NR, ACT, EPI_Y>(a, a.W0, a.rb0, a.rows0, a.y0, blockIdx.x,
-                                                        rec, red);
+        qgemv_body<kQ4K, NT, LPR, CPL, NR, ACT, EPI_Y, PAIR>(a, a.W0, a.rb0, a.rows0, a.y0,
+                                                              blockIdx.x, rec, red);
     else
-        qgemv_body<kQ6K, NT, LPR, CPL, NR, ACT, EPI_Y>(a, a.W1, a.rb1, a.rows1, a.y1,
-                                                        blockIdx.x - a.nwg0, rec, red);
+        qgemv_body<kQ6K, NT, LPR, CPL, NR, ACT, EPI_Y, PAIR>(a, a.W1, a.rb1, a.rows1, a.y1,
+                                                              blockIdx.x - a.nwg0, rec, red);
 }
 
 
@@ -960,21 +1040,28 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q6k_q8(float* __restrict__ Y,
 
 static inline size_t qgemv_lds(int nb) { return (size_t)320 * nb + 4 * (16 + 256); }
 
-template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI>
+template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI, bool PAIR>
 static hipError_t qgemv_cfg(const QGemvArgs& a, hipStream_t st) {
     constexpr int RW = (NT / 64) * (64 / LPR) * NR;
     const dim3 grid((unsigned)((a.rows0 + RW - 1) / RW));
-    hipLaunchKernelGGL((k_qgemv<QT, NT, LPR, CPL, NR, ACT, EPI>), grid, dim3(NT), qgemv_lds(a.nb),
-                       st, a);
+    hipLaunchKernelGGL((k_qgemv<QT, NT, LPR, CPL, NR, ACT, EPI, PAIR>), grid, dim3(NT),
+                       qgemv_lds(a.nb), st, a);
     return hipGetLastError();
 }
 
 template <int QT, int NT, int ACT, int EPI>
 static hipError_t qgemv_pick(const QGemvArgs& a, hipStream_t st) {
+    if constexpr (NT >= kWide) {
+        if (pair_cfg(a.nb)) return qgemv_cfg<QT, NT, 32, 1, 1, ACT, EPI, true>(a, st);
+        if constexpr (ACT == (int)QAct::Q8) return hipErrorInvalidValue;  // Q8 at 512: pairs only
+    }
     const KernCfg k = pick_cfg_nt(4 * a.nb, NT);
 #define AXF_Q(L, C, N) \
-    if (k.lpr == L && k.cpl == C && k.nr == N) return qgemv_cfg<QT, NT, L, C, N, ACT, EPI>(a, st);
-    if constexpr (NT == kWider && ACT == (int)QAct::Norm) {
+    if (k.lpr == L && k.cpl == C && k.nr == N)   \
+        return qgemv_cfg<QT, NT, L, C, N, ACT, EPI, false>(a, st);
+    if constexpr (ACT == (int)QAct::Q8 && NT == kWide) {
+        // (pairs only, above)
+    } else if constexpr (NT == kWider && ACT == (int)QAct::Norm) {
         AXF_GEMV_CFGS_1024_NORM(AXF_Q)
     } else if constexpr (NT == kWider) {
         AXF_GEMV_CFGS_1024(AXF_Q)
@@ -994,7 +1081,7 @@ static hipError_t qgemv_pick(const QGemvArgs& a, hipStream_t st) {
 bool qgemv_threads_ok(QAct act, int nb, int threads) {
     const int cpl = pick_cfg(4 * nb).cpl;
     switch (act) {
-        case QAct::Q8: return threads == kThreads;
+        case QAct::Q8: return threads == kThreads || (threads == kWide && pair_cfg(nb));
         case QAct::Norm: return nb <= 32 && (threads == kWide || threads == kWider);
         case QAct::F32:
             return threads == kWider ? cpl <= 3 : (threads == kWide ? cpl <= 4 : threads == kThreads && cpl > 4);
@@ -1003,13 +1090,14 @@ bool qgemv_threads_ok(QAct act, int nb, int threads) {
 }
 
 int qgemv_threads(QAct act, int nb) {
-    if (act == QAct::Q8) return kThreads;
+    if (act == QAct::Q8) return pair_cfg(nb) ? kWide : kThreads;
     if (act == QAct::Norm) return kWide;
     const int cpl = pick_cfg(4 * nb).cpl;
     return cpl <= 3 ? kWider : (cpl == 4 ? kWide : kThreads);
 }
 
 int qgemv_rows_per_wg(int nb, int threads) {
+    if (threads >= kWide && pair_cfg(nb)) return (threads / 64) * 2;  // 32 lanes per row
     const KernCfg k = pick_cfg_nt(4 * nb, threads);
     return (threads / 64) * (64 / k.lpr) * k.nr;
 }
@@ -1032,7 +1120,8 @@ hipError_t launch_qgemv(int qtype, QAct act, bool swiglu, QGemvArgs a, int threa
             return hipErrorInvalidValue;
         return threads == kWider ? AXF_QT(kWider, NORM, EPI_SWIGLU) : AXF_QT(kWide, NORM, EPI_SWIGLU);
     }
-    if (act == QAct::Q8) return AXF_QT(kThreads, Q8, EPI_Y);
+    if (act == QAct::Q8)
+        return threads == kWide ? AXF_QT(kWide, Q8, EPI_Y) : AXF_QT(kThreads, Q8, EPI_Y);
     if (act == QAct::Norm)
         return threads == kWider ? AXF_QT(kWider, NORM, EPI_Y) : AXF_QT(kWide, NORM, EPI_Y);
     if (threads == kWider) return AXF_QT(kWider, F32, EPI_Y);
@@ -1049,11 +1138,16 @@ hipError_t launch_qgemv2(QAct act, QGemvArgs a, int threads, hipStream_t st) {
     const int rw = qgemv_rows_per_wg(a.nb, threads);
     a.nwg0 = (a.rows0 + rw - 1) / rw;
     const dim3 grid((unsigned)(a.nwg0 + (a.rows1 + rw - 1) / rw));
-#define AXF_Q2(L, C, N)                                                                      \
-    if (k.lpr == L && k.cpl == C && k.nr == N) {                                             \
-        hipLaunchKernelGGL((k_qgemv2<kWide, L, C, N, (int)QAct::Norm>), grid, dim3(kWide),   \
-                           qgemv_lds(a.nb), st, a);                                         \
-        return hipGetLastError();                                                            \
+    if (pair_cfg(a.nb)) {
+        hipLaunchKernelGGL((k_qgemv2<kWide, 32, 1, 1, (int)QAct::Norm, true>), grid, dim3(kWide),
+                           qgemv_lds(a.nb), st, a);
+        return hipGetLastError();
+    }
+#define AXF_Q2(L, C, N)                                                                         \
+    if (k.lpr == L && k.cpl == C && k.nr == N) {                                                \
+        hipLaunchKernelGGL((k_qgemv2<kWide, L, C, N, (int)QAct::Norm, false>), grid, dim3(kWide), \
+                           qgemv_lds(a.nb), st, a);                                            \
+        return hipGetLastError();                                                               \
     }
     AXF_GEMV_CFGS_512_NORM(AXF_Q2)
 #undef AXF_Q2
@@ -1076,9 +1170,13 @@ static hipError_t launch_cfg(GemvKind kind, float* y, const void* W, const void*
         a.nb = nb;
         a.accumulate = accumulate;
         a.xq8 = static_cast<const uint8_t*>(x);
+        if (pair_cfg(nb))  // half-block units, 512 threads
+            return kind == GemvKind::Q4K_Q8
+                       ? qgemv_cfg<kQ4K, kWide, 32, 1, 1, (int)QAct::Q8, EPI_Y, true>(a, st)
+                       : qgemv_cfg<kQ6K, kWide, 32, 1, 1, (int)QAct::Q8, EPI_Y, true>(a, st);
         return kind == GemvKind::Q4K_Q8
-                   ? qgemv_cfg<kQ4K, kThreads, LPR, CPL, NR, (int)QAct::Q8, EPI_Y>(a, st)
-                   : qgemv_cfg<kQ6K, kThreads, LPR, CPL, NR, (int)QAct::Q8, EPI_Y>(a, st);
+                   ? qgemv_cfg<kQ4K, kThreads, LPR, CPL, NR, (int)QAct::Q8, EPI_Y, false>(a, st)
+                   : qgemv_cfg<kQ6K, kThreads, LPR, CPL, NR, (int)QAct::Q8, EPI_Y, false>(a, st);
     }
     if (kind == GemvKind::Q4K_F32)
         hipLaunchKernelGGL((k_gemv_q4k_f32<LPR, CPL, NR>), grid, block,

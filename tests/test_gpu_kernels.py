@@ -98,9 +98,13 @@ GEMV_SHAPES = [
     (Q4K, 100, 2048),
     (Q4K, 75, 11008),    # 43 blocks per row
     (Q4K, 33, 16384),
+    (Q4K, 21, 2304),     # half-block units: 18 per row, 14 idle lanes of 32
+    (Q4K, 1001, 4096),   # half-block units, last workgroup partly past the rows
     (Q6K, 1, 256),
     (Q6K, 37, 2048),
     (Q6K, 64, 4096),
+    (Q6K, 23, 2304),     # half-block units on 1890-byte rows (odd rows 2-byte aligned)
+    (Q6K, 77, 3072),
     (Q6K, 101, 11008),   # 9030-byte rows: odd rows start 2 bytes past a dword
     (Q6K, 17, 14336),
 ]

@@ -24,7 +24,7 @@ def within(gpu, ref, rtol=1e-3, atol=1e-4):
     return (not bad.any()), float(np.max(np.abs(gpu - ref)))
 
 
-def _layer_parity(ctx, cfg, prior, with_bias, seed):
+def _layer_parity(ctx, cfg, prior, with_bias, seed, max_abs=2e-3):
     from llm_core_amd import hip
     from llm_core_amd.model import Hparams, LlamaHip, SynthLlama
 
@@ -62,7 +62,7 @@ def _layer_parity(ctx, cfg, prior, with_bias, seed):
     d_gpu, d_orc = got_x.astype(np.float64) - x0, want_x.astype(np.float64) - x0
     rel = np.linalg.norm(d_gpu - d_orc) / np.linalg.norm(d_orc)
     assert rel < 1e-3, f"layer update relative error {rel}"
-    assert np.max(np.abs(got_x - want_x)) < 2e-3
+    assert np.max(np.abs(got_x - want_x)) < max_abs
     # the layer added a non-trivial update to the residual
     assert np.max(np.abs(want_x - x0)) > 1e-2
     del want_k, want_v
@@ -81,6 +81,16 @@ def test_layer_parity_llama7b_shape(ctx):
     from llm_core_amd.model import LLAMA2_7B
 
     _layer_parity(ctx, LLAMA2_7B, 2047, False, 4)
+
+
+def test_layer_parity_hidden3072(ctx):
+    """Hidden 3072 (12 super-blocks: half-block units on 24 of the 32 lanes of
+    a row), GQA 24/8, FFN 8192, biases, context 300.  One element of this
+    layer's update differs by 2.5e-3 after a one-step Q8_0 rounding flip (the
+    norm-wise error stays below 1e-3), hence the wider elementwise bound."""
+    cfg = dict(n_embd=3072, n_heads=24, n_kv_heads=8, ffn_dim=8192, rms_eps=1e-6,
+               rope_theta=1e6)
+    _layer_parity(ctx, cfg, 300, True, 5, max_abs=4e-3)
 
 
 def test_layer_stepwise_qwen25_3b(ctx):
