@@ -41,10 +41,15 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+GEMV_ROUNDS = 8  # passes over the rotating copies inside one captured graph (--gemv-rounds)
+
+
 def gemv_case(ctx, kind, qtype, rows, cols, reps, seed, min_bytes=2 * MALL_BYTES + (96 << 20),
               warm=False):
     """Time one GEMV shape with weights rotated over enough copies to exceed
-    min_bytes (warm=True: the same single copy for every launch of the graph)."""
+    min_bytes (warm=True: the same single copy for every launch of the graph).
+    One graph holds GEMV_ROUNDS passes over the copies, so the gap between
+    graph replays is spread over that many launches."""
     from llm_core_amd import hip
 
     W = hip.synth_weight(qtype, rows, cols, seed)
@@ -61,9 +66,10 @@ def gemv_case(ctx, kind, qtype, rows, cols, reps, seed, min_bytes=2 * MALL_BYTES
         ctx.quantize_q8_0(act, dx, cols)
         act_bytes = cols // 32 * 36
     dy = ctx.alloc(rows * 4)
-    ctx.bench_gemv(kind, dy, bufs, act, rows, cols, rb, 2)  # warm-up replays
-    ms = ctx.bench_gemv(kind, dy, bufs, act, rows, cols, rb, reps)
-    launches = reps * n_copies
+    seq = bufs * GEMV_ROUNDS
+    ctx.bench_gemv(kind, dy, seq, act, rows, cols, rb, 2)  # warm-up replays
+    ms = ctx.bench_gemv(kind, dy, seq, act, rows, cols, rb, reps)
+    launches = reps * len(seq)
     us = ms * 1000.0 / launches
     alg = W.nbytes + act_bytes + rows * 4
     res = dict(rows=rows, cols=cols, weight_bytes=W.nbytes, algorithmic_bytes=alg,
@@ -210,8 +216,10 @@ def copy_probe(ctx, nbytes=256 << 20, reps=10):
             "GBs_read_plus_write": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}
 
 
-ROOF_KERNEL = "k_qgemv<12, 256, 64, 1, 1, 0, 0>"  # Q4_K, Q8_0 activations, 4 rows per workgroup
-ROOF_GRID = 704512  # threads of one 11008-row launch (2752 workgroups x 256)
+# Q4_K, Q8_0 activations, half-block units (32 lanes per row), 16 rows per workgroup
+ROOF_KERNEL = "k_qgemv<12, 512, 32, 1, 1, 0, 0, true>"
+ROOF_KERNEL_ID = "axf::k_qgemv<12,512,32,1,1,0,0,true> (Q4_K x Q8_0 GEMV, 11008x4096, M=1)"
+ROOF_GRID = 352256  # threads of one 11008-row launch (688 workgroups x 512)
 COPY_GRID = 131072  # threads of the runtime's 256 MiB copy kernel
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "gemv_q4k_q8_11008x4096_traffic.txt")
@@ -306,12 +314,17 @@ def committed_traffic() -> float | None:
 
 
 def main() -> int:
+    global GEMV_ROUNDS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--ctx", type=int, default=2048, help="decode context length")
     ap.add_argument("--gemv-reps", type=int, default=40)
+    ap.add_argument("--gemv-rounds", type=int, default=GEMV_ROUNDS,
+                    help="passes over the rotating weight copies per captured GEMV graph "
+                         "(rocprofv3's kernel trace has crashed capturing graphs of several "
+                         "hundred nodes: profile with 1)")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="approximate CPU seconds spent on the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
@@ -335,6 +348,7 @@ def main() -> int:
                     help="HBM traffic of the roofline kernel from two rocprofv3 --pmc csv "
                          "directories (FETCH_SIZE, WRITE_SIZE) and exit")
     args = ap.parse_args()
+    GEMV_ROUNDS = max(1, args.gemv_rounds)
     if args.counters:
         print(summarize_counters(args.counters))
         return 0
@@ -394,7 +408,7 @@ def main() -> int:
         log(f"gemv q6k 151936x2048 (config 2 head): {c2['us_per_launch']:.2f} us, {c2['gbs']:.0f} GB/s")
         roof = {
             "bound": "hbm",
-            "kernel": "axf::k_qgemv<12,256,64,1,1,0,0> (Q4_K x Q8_0 GEMV, 11008x4096, M=1)",
+            "kernel": ROOF_KERNEL_ID,
             "achieved": round(g["gbs"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
