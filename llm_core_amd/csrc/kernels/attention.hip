@@ -50,10 +50,7 @@ __device__ __forceinline__ void rope_in_lds(float* v, int n_vec, const float* cr
 
 // Q8_0 of 32 values held as float4 by 8 consecutive lanes (sub = lane & 7).
 __device__ __forceinline__ void q8_store4(uint8_t* blk, int sub, float4 v) {
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     const float d = amax / 127.f;
     const float id = amax > 0.f ? 127.f / amax : 0.f;
     auto q = [&](float f) -> uint32_t {

@@ -71,6 +71,26 @@ __device__ __forceinline__ float group_sum_last(float v) {
     return v;
 }
 
+// Reductions over groups of 8 consecutive lanes with DPP (quad_perm swaps,
+// then row_half_mirror pairs each lane with one of the other quad); every
+// lane of the group receives the result.  No LDS round trip (ds_bpermute).
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false));  // row_half_mirror
+    return v;
+}
+// sum over the lane's quad (every lane of the quad receives it)
+__device__ __forceinline__ int sum_quad(int v) {
+    v += __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false);
+    return v;
+}
+// the value of lane 7 - (lane & 7) of the lane's group of 8 (row_half_mirror)
+__device__ __forceinline__ int half_mirror(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false);
+}
+
 // Maximum over the wave, returned in every lane: the DPP steps of
 // group_sum_last<64> with max (masked rows keep -inf), then lane 63 read into
 // a scalar register.
@@ -180,10 +200,7 @@ __device__ __forceinline__ float rms_scale(const float4 (&xv)[KPT], int n, float
 // Q8_0 of one 32-value block held as float4 by 8 consecutive lanes
 // (sub = lane & 7): returns this lane's 4 packed int8 and, in d, the block scale.
 __device__ __forceinline__ uint32_t q8_quant4(float4 v, float& d) {
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     d = amax / 127.f;
     const float id = amax > 0.f ? 127.f / amax : 0.f;
     auto q = [&](float f) -> uint32_t {

@@ -386,10 +386,8 @@ __device__ __forceinline__ void stage_regs(uint32_t* rec, float4 (&xv)[KPT],
         float d;
         const uint32_t q = q8_quant4(v, d);
         // integer sums over the block (Q4_K) or its two halves (Q6_K)
-        int s = dot4((int)q, 0x01010101, 0);
-        s += __shfl_xor(s, 1, 8);
-        s += __shfl_xor(s, 2, 8);
-        const int s_hi = __shfl_xor(s, 4, 8);  // lane sub 0 receives the sum of lanes 4-7
+        const int s = sum_quad(dot4((int)q, 0x01010101, 0));
+        const int s_hi = half_mirror(s);  // lane sub 0 receives the sum of lanes 4-7
         const int sub = i4 & 7;
         if (i4 < n4) {
             int slot;

@@ -83,10 +83,7 @@ __global__ void k_dequant_q6k(float* __restrict__ out, const uint8_t* __restrict
 // d = amax/127, id = 127/amax (0 when amax == 0), q = rne(x*id) saturated.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void q8_block_store(uint8_t* blk, int sub, float4 v) {
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     const float d = amax / 127.f;
     const float id = amax > 0.f ? 127.f / amax : 0.f;
     auto q = [&](float f) -> uint32_t {
