@@ -165,10 +165,11 @@ __device__ __forceinline__ void q8_quant32(const float (&v)[32], uint32_t (&q)[8
 // with one fixed summation order, so every kernel that normalises the same x
 // gets the same bits whatever its workgroup size: 1024 slots, slot s
 // accumulating the squares of float4 s, s+1024, ... in ascending order (fmaf
-// chain x, y, z, w); slots 64w..64w+63 reduced by the xor tree into partial
-// w; the 16 partials added in order.  Called by all NT threads of a workgroup
-// (NT = 256, 512 or 1024) with the thread's float4s of x: xv[k] = float4
-// t + NT*k, zero past the end (thread t holds slots t + NT*j, j < 1024/NT).
+// chain x, y, z, w); slots 64w..64w+63 reduced by the DPP row tree of
+// group_sum_last into partial w; the 16 partials added in order.  Called by
+// all NT threads of a workgroup (NT = 256, 512 or 1024) with the thread's
+// float4s of x: xv[k] = float4 t + NT*k, zero past the end (thread t holds
+// slots t + NT*j, j < 1024/NT).
 // red: 16 floats of LDS.  Ends with a barrier.
 template <int NT, int KPT>
 __device__ __forceinline__ float rms_scale(const float4 (&xv)[KPT], int n, float eps, float* red) {
@@ -187,8 +188,8 @@ __device__ __forceinline__ float rms_scale(const float4 (&xv)[KPT], int n, float
     }
 #pragma unroll
     for (int j = 0; j < NS; j++) {
-        const float v = wave_sum(s[j]);
-        if ((threadIdx.x & 63) == 0) red[(threadIdx.x >> 6) + (NT / 64) * j] = v;
+        const float v = group_sum_last<64>(s[j]);  // valid in lane 63
+        if ((threadIdx.x & 63) == 63) red[(threadIdx.x >> 6) + (NT / 64) * j] = v;
     }
     __syncthreads();
     float ss = red[0];
