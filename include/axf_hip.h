@@ -367,6 +367,36 @@ int axf_llama_fill_kv_random(axf_llama* m, int n_pos, uint64_t seed);
 int axf_llama_get_logits(axf_llama* m, float* logits);
 /* One decoder layer at `pos` on the residual stream (eager). */
 int axf_llama_forward_layer(axf_llama* m, int layer, int pos);
+/* Stages first..last (1 <= first <= last <= 5) of one decoder layer at `pos`,
+ * eager, with the kernels the decode step runs: 1 the q|k|v projections of
+ * RMSNorm(x) * attn_norm (before bias), 2 attention (bias and RoPE of q and k,
+ * K/V row `pos` stored, output and its Q8_0), 3 o projection and x +=, 4
+ * gate|up of RMSNorm(x) * ffn_norm and SwiGLU, 5 down projection of Q8_0(h)
+ * and x +=.  The stages of llama_forward_token's layer body
+ * (llama_model.cpp:1222-1325); no reference counterpart as an entry point:
+ * it exists so parity tests can check each fused kernel on its own. */
+int axf_llama_forward_layer_stages(axf_llama* m, int layer, int pos, int first, int last);
+/* Read back a decoder buffer (the device counterparts of LlamaState's s.x,
+ * s.q|s.k|s.v, s.attn_out, xq8 and s.gate, llama_model.cpp:1096-1166).
+ * `bytes` must equal the buffer's size:
+ *   X        n_embd floats (residual stream)
+ *   QKV      (n_heads + 2 n_kv_heads) * head_dim floats: q|k|v projections
+ *            before bias and RoPE, as written by stage 1
+ *   ATTN     n_heads * head_dim floats: attention output (stage 2)
+ *   ATTN_Q8  its Q8_0 blocks, n_heads * head_dim / 32 * 36 bytes
+ *   H        ffn_dim floats: SwiGLU output (stage 4)
+ *   LOGITS   n_vocab floats */
+enum {
+    AXF_LLAMA_BUF_X = 0,
+    AXF_LLAMA_BUF_QKV = 1,
+    AXF_LLAMA_BUF_ATTN = 2,
+    AXF_LLAMA_BUF_ATTN_Q8 = 3,
+    AXF_LLAMA_BUF_H = 4,
+    AXF_LLAMA_BUF_LOGITS = 5
+};
+int axf_llama_get_buffer(axf_llama* m, int which, void* out, size_t bytes);
+/* KV cache rows pos0..pos0+n_pos-1 of a layer (K after RoPE, as stored). */
+int axf_llama_get_kv(axf_llama* m, int layer, float* k, float* v, int pos0, int n_pos);
 /* Full single-token forward (embedding .. logits), eager. */
 int axf_llama_forward_token(axf_llama* m, int token, int pos);
 /* Batched prefill: replaces llama_forward_batch (llama_model.cpp:1339-1462).
@@ -379,7 +409,9 @@ int axf_llama_forward_batch(axf_llama* m, const int32_t* tokens, int T, int pos_
 /* Greedy generation (greedy loop of llama_generate_cpu_impl,
  * llama_model.cpp:1568-1624, without EOS): the prompt is prefilled as one batch
  * when n_prompt > 1 (as the reference does), then n_gen tokens are decoded.
- * use_graph != 0 replays one captured HIP graph per decode step. */
+ * use_graph != 0 replays one captured HIP graph per decode step.  The
+ * reference stops at n_past >= n_ctx, i.e. after n_ctx - n_prompt tokens;
+ * n_gen above that is AXF_ERR_INVALID_ARG. */
 int axf_llama_generate(axf_llama* m, const int32_t* prompt, int n_prompt, int n_gen,
                        int32_t* out_tokens, int use_graph);
 /* As axf_llama_generate; batched_prefill == 0 prefills token by token (the

@@ -24,6 +24,14 @@ AXF_TYPE_Q8_0 = 8
 AXF_TYPE_Q4_K = 12
 AXF_TYPE_Q6_K = 14
 
+# axf_llama_get_buffer
+AXF_LLAMA_BUF_X = 0
+AXF_LLAMA_BUF_QKV = 1
+AXF_LLAMA_BUF_ATTN = 2
+AXF_LLAMA_BUF_ATTN_Q8 = 3
+AXF_LLAMA_BUF_H = 4
+AXF_LLAMA_BUF_LOGITS = 5
+
 
 class AxfError(RuntimeError):
     def __init__(self, code: int, msg: str):
@@ -186,6 +194,9 @@ SIGNATURES: dict[str, list] = {
     "axf_llama_fill_kv_random": [vp, i32, u64],
     "axf_llama_get_logits": [vp, vp],
     "axf_llama_forward_layer": [vp, i32, i32],
+    "axf_llama_forward_layer_stages": [vp, i32, i32, i32, i32],
+    "axf_llama_get_buffer": [vp, i32, vp, sz],
+    "axf_llama_get_kv": [vp, i32, vp, vp, i32, i32],
     "axf_llama_forward_token": [vp, i32, i32],
     "axf_llama_generate": [vp, vp, i32, i32, vp, i32],
     "axf_llama_generate_ex": [vp, vp, i32, i32, vp, i32, i32],

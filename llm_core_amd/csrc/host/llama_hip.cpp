@@ -334,7 +334,10 @@ hipError_t embed(axf_llama* m, float* out, const int* tok_dev, int tok, int T, h
 }
 
 // Enqueue one decoder layer; pos from device memory when pos_dev != nullptr.
-hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
+// Stages first..last of the five (1: q|k|v projections, 2: attention, 3: o
+// and x +=, 4: gate|up and SwiGLU, 5: down and x +=); the step runs 1..5.
+hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int first = 1,
+                         int last = 5) {
     const auto& hp = m->hp;
     const int E = hp.n_embd, H = hp.n_heads, KVH = hp.n_kv_heads, HD = m->hd, FD = hp.ffn_dim;
     const int qo = H * HD, kvo = KVH * HD;
@@ -347,8 +350,10 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
     hipError_t e;
 #define ST(call)               \
     if ((e = (call)) != hipSuccess) return e;
+    auto stage = [&](int k) { return first <= k && k <= last; };
     // 1. q|k and v from RMSNorm(x) * attn_norm
-    if (L.qk_fused && L.wv.qtype == AXF_TYPE_Q6_K) {
+    if (!stage(1)) {
+    } else if (L.qk_fused && L.wv.qtype == AXF_TYPE_Q6_K) {
         QGemvArgs a = weights(L.wq, qo + kvo, q, E);
         a.W1 = L.wv.d;
         a.rb1 = (long)L.wv.row_bytes;
@@ -368,7 +373,7 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
         ST(gemv_norm(L.wv, v, m->x, L.attn_norm, hp.rms_eps, kvo, E, false, st));
     }
     // 2./3. attention -> Q8_0 of its output
-    {
+    if (stage(2)) {
         AttnArgs a{};
         a.q = q;
         a.k = k;
@@ -392,9 +397,10 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
         ST(launch_attention_fused(a, HD, st));
     }
     // 4. x += o
-    ST(gemv_q8(L.wo, m->x, m->xq8, E, qo, true, st));
+    if (stage(3)) ST(gemv_q8(L.wo, m->x, m->xq8, E, qo, true, st));
     // 5. h = SwiGLU(gate, up) from RMSNorm(x) * ffn_norm
-    if (L.gu_interleaved) {
+    if (!stage(4)) {
+    } else if (L.gu_interleaved) {
         ST(gemv_norm(L.wgate, m->h, m->x, L.ffn_norm, hp.rms_eps, 2 * FD, E, true, st));
     } else {
         ST(gemv_norm(L.wgate, m->gateup, m->x, L.ffn_norm, hp.rms_eps, FD, E, false, st));
@@ -402,7 +408,7 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos) {
         ST(launch_swiglu(m->h, nullptr, m->gateup, m->gateup + FD, FD, st));
     }
     // 6. x += down(Q8_0(h))
-    {
+    if (stage(5)) {
         QGemvArgs a = weights(L.wdown, E, m->x, FD);
         a.x = m->h;
         a.accumulate = 1;
@@ -879,6 +885,52 @@ int axf_llama_forward_layer(axf_llama* m, int layer, int pos) {
     return AXF_OK;
 }
 
+int axf_llama_forward_layer_stages(axf_llama* m, int layer, int pos, int first, int last) {
+    LL_LOADED(m);
+    if (layer < 0 || layer >= m->hp.n_layer || pos < 0 || pos >= m->hp.n_ctx || first < 1 ||
+        last > 5 || first > last)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_forward_layer_stages: bad layer/pos/stages");
+    LL_HIP(enqueue_layer(m, layer, nullptr, pos, first, last));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    return AXF_OK;
+}
+
+int axf_llama_get_buffer(axf_llama* m, int which, void* out, size_t bytes) {
+    LL_LOADED(m);
+    const auto& hp = m->hp;
+    const size_t qo = (size_t)hp.n_heads * m->hd, kvo = (size_t)m->kv_embd;
+    const void* src = nullptr;
+    size_t n = 0;
+    switch (which) {
+        case AXF_LLAMA_BUF_X: src = m->x; n = (size_t)hp.n_embd * 4; break;
+        case AXF_LLAMA_BUF_QKV: src = m->qkv; n = (qo + 2 * kvo) * 4; break;
+        case AXF_LLAMA_BUF_ATTN: src = m->attn_out; n = qo * 4; break;
+        case AXF_LLAMA_BUF_ATTN_Q8: src = m->xq8; n = qo / 32 * Q8_0_BYTES; break;
+        case AXF_LLAMA_BUF_H: src = m->h; n = (size_t)hp.ffn_dim * 4; break;
+        case AXF_LLAMA_BUF_LOGITS: src = m->logits; n = (size_t)hp.n_vocab * 4; break;
+        default: return fail(AXF_ERR_INVALID_ARG, "axf_llama_get_buffer: unknown buffer");
+    }
+    if (!out || bytes != n)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_get_buffer: wrong size (want " +
+                                             std::to_string(n) + " bytes)");
+    LL_HIP(hipMemcpyAsync(out, src, n, hipMemcpyDeviceToHost, m->ctx->stream));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    return AXF_OK;
+}
+
+int axf_llama_get_kv(axf_llama* m, int layer, float* k, float* v, int pos0, int n_pos) {
+    LL_LOADED(m);
+    if (layer < 0 || layer >= m->hp.n_layer || pos0 < 0 || n_pos < 0 ||
+        pos0 + n_pos > m->hp.n_ctx || (n_pos && (!k || !v)))
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_get_kv: bad arguments");
+    const size_t off = ((size_t)layer * m->hp.n_ctx + pos0) * m->kv_embd;
+    const size_t bytes = (size_t)n_pos * m->kv_embd * 4;
+    LL_HIP(hipMemcpyAsync(k, m->kv_k + off, bytes, hipMemcpyDeviceToHost, m->ctx->stream));
+    LL_HIP(hipMemcpyAsync(v, m->kv_v + off, bytes, hipMemcpyDeviceToHost, m->ctx->stream));
+    LL_HIP(hipStreamSynchronize(m->ctx->stream));
+    return AXF_OK;
+}
+
 int axf_llama_forward_token(axf_llama* m, int token, int pos) {
     LL_LOADED(m);
     if (token < 0 || token >= m->hp.n_vocab || pos < 0 || pos >= m->hp.n_ctx)
@@ -934,8 +986,10 @@ int axf_llama_generate_ex(axf_llama* m, const int32_t* prompt, int n_prompt, int
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || prompt[i] >= m->hp.n_vocab)
             return fail(AXF_ERR_INVALID_ARG, "axf_llama_generate: prompt token out of range");
-    // the last generated token is produced at position n_prompt + n_gen - 2
-    if (n_prompt + (n_gen > 0 ? n_gen - 1 : 0) > m->hp.n_ctx)
+    // the reference emits a token only while n_past < n_ctx (:1613), n_past
+    // starting at n_prompt: at most n_ctx - n_prompt tokens.  Asking for more
+    // is an error here rather than a shorter result.
+    if (n_prompt > m->hp.n_ctx || n_gen > m->hp.n_ctx - n_prompt)
         return fail(AXF_ERR_INVALID_ARG, "axf_llama_generate: context too long");
     hipStream_t st = m->ctx->stream;
     LL_HIP(launch_set_int(m->d_step, 0, st));

@@ -13,7 +13,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from . import hip
+from . import _ffi, hip
 from ._ffi import (AXF_TYPE_F16, AXF_TYPE_F32, AXF_TYPE_Q4_K, AXF_TYPE_Q5_0, AXF_TYPE_Q6_K,
                    AXF_TYPE_Q8_0, LlamaHparams, call, lib)
 
@@ -224,6 +224,34 @@ class LlamaHip:
 
     def forward_layer(self, layer: int, pos: int) -> None:
         call("axf_llama_forward_layer", self.handle, layer, pos)
+
+    def forward_layer_stages(self, layer: int, pos: int, first: int, last: int) -> None:
+        """Stages first..last (1 q|k|v, 2 attention, 3 o, 4 gate|up+SwiGLU,
+        5 down) of one layer, with the decode step's fused kernels."""
+        call("axf_llama_forward_layer_stages", self.handle, layer, pos, first, last)
+
+    def buffer(self, which: int) -> np.ndarray:
+        """A decoder buffer (AXF_LLAMA_BUF_*): fp32, or uint8 for ATTN_Q8."""
+        hp = self.hp
+        qo, kvo = hp.n_heads * hp.head_dim, hp.n_kv_heads * hp.head_dim
+        shape = {_ffi.AXF_LLAMA_BUF_X: (np.float32, hp.n_embd),
+                 _ffi.AXF_LLAMA_BUF_QKV: (np.float32, qo + 2 * kvo),
+                 _ffi.AXF_LLAMA_BUF_ATTN: (np.float32, qo),
+                 _ffi.AXF_LLAMA_BUF_ATTN_Q8: (np.uint8, qo // 32 * 36),
+                 _ffi.AXF_LLAMA_BUF_H: (np.float32, hp.ffn_dim),
+                 _ffi.AXF_LLAMA_BUF_LOGITS: (np.float32, hp.n_vocab)}[which]
+        out = np.empty(shape[1], shape[0])
+        call("axf_llama_get_buffer", self.handle, which, out.ctypes.data_as(C.c_void_p),
+             C.c_size_t(out.nbytes))
+        return out
+
+    def get_kv(self, layer: int, pos0: int, n_pos: int) -> tuple[np.ndarray, np.ndarray]:
+        kve = self.hp.n_kv_heads * self.hp.head_dim
+        k = np.empty((n_pos, kve), np.float32)
+        v = np.empty((n_pos, kve), np.float32)
+        call("axf_llama_get_kv", self.handle, layer, k.ctypes.data_as(C.c_void_p),
+             v.ctypes.data_as(C.c_void_p), pos0, n_pos)
+        return k, v
 
     def forward_token(self, token: int, pos: int) -> None:
         call("axf_llama_forward_token", self.handle, token, pos)

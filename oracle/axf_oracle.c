@@ -895,6 +895,11 @@ float* orc_state_logits(orc_state* s) { return s->logits; }
 float* orc_state_x(orc_state* s) { return s->x; }
 float* orc_state_kv_k(orc_state* s) { return s->kv_k; }
 float* orc_state_kv_v(orc_state* s) { return s->kv_v; }
+/* Intermediates of the last orc_forward_layer: q after bias and RoPE, the
+ * attention output, and the SwiGLU output h (the down projection's input). */
+float* orc_state_q(orc_state* s) { return s->q; }
+float* orc_state_attn_out(orc_state* s) { return s->attn_out; }
+float* orc_state_h(orc_state* s) { return s->gate; }
 
 static size_t wt_row_bytes(const orc_wt* w, int in) {
     if (w->type == 8) return (size_t)((in + 31) / 32) * 34;  /* Q8_0 */

@@ -122,6 +122,9 @@ float* orc_state_logits(orc_state* s);
 float* orc_state_x(orc_state* s);
 float* orc_state_kv_k(orc_state* s);
 float* orc_state_kv_v(orc_state* s);
+float* orc_state_q(orc_state* s);
+float* orc_state_attn_out(orc_state* s);
+float* orc_state_h(orc_state* s);
 void orc_forward_token(const orc_model* m, orc_state* s, int token, int pos);
 void orc_forward_layer(const orc_model* m, orc_state* s, int layer, int pos);
 void orc_forward_batch(const orc_model* m, orc_state* s, const int32_t* tokens, int T,

@@ -67,6 +67,9 @@ def _load_orc() -> C.CDLL:
         "orc_state_x": ([vp], C.POINTER(C.c_float)),
         "orc_state_kv_k": ([vp], C.POINTER(C.c_float)),
         "orc_state_kv_v": ([vp], C.POINTER(C.c_float)),
+        "orc_state_q": ([vp], C.POINTER(C.c_float)),
+        "orc_state_attn_out": ([vp], C.POINTER(C.c_float)),
+        "orc_state_h": ([vp], C.POINTER(C.c_float)),
         "orc_forward_token": ([vp, vp, i32, i32], None),
         "orc_forward_layer": ([vp, vp, i32, i32], None),
         "orc_forward_batch": ([vp, vp, vp, i32, i32], None),
@@ -376,6 +379,20 @@ class OracleModel:
 
     def x_view(self):
         return np.ctypeslib.as_array(orc.orc_state_x(self.state), (self.hp.n_embd,))
+
+    def q_view(self):
+        """q of the last forward_layer, after bias and RoPE."""
+        hp = self.hp
+        return np.ctypeslib.as_array(orc.orc_state_q(self.state), (hp.n_heads * hp.head_dim,))
+
+    def attn_out_view(self):
+        hp = self.hp
+        return np.ctypeslib.as_array(orc.orc_state_attn_out(self.state),
+                                     (hp.n_heads * hp.head_dim,))
+
+    def h_view(self):
+        """SwiGLU output of the last forward_layer (the down projection's input)."""
+        return np.ctypeslib.as_array(orc.orc_state_h(self.state), (self.hp.ffn_dim,))
 
     def logits(self):
         return np.ctypeslib.as_array(orc.orc_state_logits(self.state), (self.hp.n_vocab,)).copy()

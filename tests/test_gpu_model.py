@@ -53,7 +53,12 @@ def _layer_parity(ctx, cfg, prior, with_bias, seed, max_abs=2e-3):
     g.set_x(x0)
     g.forward_layer(0, prior)
     got_x = g.get_x()
+    got_k, got_v = g.get_kv(0, prior, 1)
     g.close()
+    # the K row (bias, RoPE) and V row (bias) the fused attention kernel stored
+    for tag, got, want in (("K row", got_k[0], want_k), ("V row", got_v[0], want_v)):
+        ok, err = within(got, want)
+        assert ok, f"{tag} at position {prior}: max |err| {err:.3e}"
     # The layer re-quantizes four activations to Q8_0; fp32 reduction order
     # (GPU vs x86) can flip an element sitting within an ulp of a rounding
     # boundary by one q8 step, which moves the layer update by up to ~1e-3
@@ -65,7 +70,6 @@ def _layer_parity(ctx, cfg, prior, with_bias, seed, max_abs=2e-3):
     assert np.max(np.abs(got_x - want_x)) < max_abs
     # the layer added a non-trivial update to the residual
     assert np.max(np.abs(want_x - x0)) > 1e-2
-    del want_k, want_v
 
 
 def test_layer_parity_qwen25_3b(ctx):
@@ -306,11 +310,25 @@ def test_generate_rejects_bad_input(ctx):
     from llm_core_amd.model import Hparams, LlamaHip, SynthLlama
 
     hp = Hparams(**SMALL)
-    g = LlamaHip(ctx, SynthLlama(hp, seed=9))
+    synth = SynthLlama(hp, seed=9)
+    g = LlamaHip(ctx, synth)
     with pytest.raises(AxfError):
         g.generate(np.array([1, 5000], np.int32), 4)  # token id beyond the vocabulary
     with pytest.raises(AxfError):
         g.generate(np.arange(60, dtype=np.int32), 10)  # exceeds n_ctx
+    # the context stop of llama_generate_cpu_impl (:1613): with 60 prompt
+    # tokens and n_ctx 64 the reference emits 4 tokens; the oracle's loop
+    # (pinned on the CPU) agrees, and the device takes 4 but refuses 5
+    prompt = np.arange(1, 61, dtype=np.int32)
+    om = O.OracleModel(hp, synth.tensors)
+    try:
+        want, _ = om.generate(prompt, 5)
+    finally:
+        om.close()
+    assert len(want) == hp.n_ctx - len(prompt)
+    assert len(g.generate(prompt, len(want))) == len(want)
+    with pytest.raises(AxfError):
+        g.generate(prompt, len(want) + 1)
     g.close()
 
 

@@ -9,40 +9,7 @@ import pytest
 
 from oracle import oracle as O
 
-F16_ONE, F16_HALF, F16_QUARTER = 0x3C00, 0x3800, 0x3400
-
-
-# ---------------------------------------------------------------------------
-# Q4_K / Q6_K layouts (block_q4_K: dtype.hpp:149; block_q6_K: dtype.hpp:152)
-# ---------------------------------------------------------------------------
-
-def pack_q4k(d16, dmin16, sc, mn, q):
-    """One Q4_K block from 8 6-bit scales, 8 6-bit mins and 256 4-bit values."""
-    s = np.zeros(12, np.uint8)
-    for j in range(4):
-        s[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
-        s[j + 4] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
-        s[j + 8] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
-    qs = np.zeros(128, np.uint8)
-    for c in range(4):                      # 64-weight chunk c: low nibbles, then high
-        for l in range(32):
-            qs[32 * c + l] = q[64 * c + l] | (q[64 * c + 32 + l] << 4)
-    hdr = np.array([d16, dmin16], np.uint16).view(np.uint8)
-    return np.concatenate([hdr, s, qs]).astype(np.uint8)
-
-
-def pack_q6k(d16, sc, q):
-    """One Q6_K block from 16 int8 scales and 256 6-bit values (0..63)."""
-    ql = np.zeros(128, np.uint8)
-    qh = np.zeros(64, np.uint8)
-    for n in range(2):                      # 128-weight halves
-        for l in range(32):
-            q1, q2, q3, q4 = (q[128 * n + l + 32 * k] for k in range(4))
-            ql[64 * n + l] = (q1 & 15) | ((q3 & 15) << 4)
-            ql[64 * n + l + 32] = (q2 & 15) | ((q4 & 15) << 4)
-            qh[32 * n + l] = (q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6)
-    return np.concatenate([ql, qh, np.asarray(sc, np.int8).view(np.uint8),
-                           np.array([d16], np.uint16).view(np.uint8)]).astype(np.uint8)
+from qblocks import F16_HALF, F16_ONE, F16_QUARTER, pack_q4k, pack_q6k, unpack_q8  # noqa: F401
 
 
 def test_q4k_known_answer_including_high_scale_bits():
@@ -83,13 +50,6 @@ def test_fp16_conversion_special_values():
 # ---------------------------------------------------------------------------
 # Q8_0 (block_q8_0: q8_block.hpp:8-15; quantize: quant_q8_avx2.cpp:33-84)
 # ---------------------------------------------------------------------------
-
-def unpack_q8(b):
-    b = b.reshape(-1, 36)
-    d = b[:, :4].copy().view(np.float32).reshape(-1)
-    q = b[:, 4:].view(np.int8).astype(np.int32)
-    return d, q
-
 
 def test_q8_0_invariants():
     rng = np.random.default_rng(3)
@@ -241,6 +201,44 @@ def test_rope_identity_pairs_and_norm():
     nz = set(np.nonzero(r)[0])
     assert nz <= {5, 5 + hd // 2}
     assert r[5] == c[37 * hd // 2 + 5] and r[5 + hd // 2] == s[37 * hd // 2 + 5]
+
+
+def test_rope_exact_rotations_and_rounding_bound():
+    """apply_rope (llama_model.cpp:1046-1080) on tables whose products are exact:
+    a quarter turn maps (x0, x1) to (-x1, x0), a half turn negates, and the
+    bilinear form (x0 c - x1 s, x0 s + x1 c) with c = 0.5, s = 0.75 on small
+    integers is exact whether or not the compiler contracts it into FMAs.  On
+    the real table the result is within one rounding of each product of the
+    float64 rotation.  Which FMA contraction GCC applies to the reference's
+    expression cannot be observed here (llama_model.cpp does not build); the
+    two candidates differ by at most one ulp of the larger product, and the GPU
+    kernels follow the oracle's choice bit for bit."""
+    hd, H = 16, 2
+    half = hd // 2
+    rng = np.random.default_rng(21)
+    x = rng.integers(-1000, 1000, H * hd).astype(np.float32)
+    xh = x.reshape(H, 2, half)
+    for cv, sv, want0, want1 in ((0.0, 1.0, -xh[:, 1], xh[:, 0]),
+                                 (-1.0, 0.0, -xh[:, 0], -xh[:, 1]),
+                                 (0.5, 0.75, 0.5 * xh[:, 0] - 0.75 * xh[:, 1],
+                                  0.75 * xh[:, 0] + 0.5 * xh[:, 1])):
+        c = np.ones(2 * half, np.float32)
+        s = np.zeros(2 * half, np.float32)
+        c[half:] = cv
+        s[half:] = sv
+        y = O.rope(x, 1, H, hd, c, s).reshape(H, 2, half)
+        assert np.array_equal(y[:, 0], want0.astype(np.float32))
+        assert np.array_equal(y[:, 1], want1.astype(np.float32))
+    c, s = O.rope_table(64, 10000.0, 300)
+    xr = rng.standard_normal(4 * 64).astype(np.float32)
+    for pos in (1, 77, 299):
+        y = O.rope(xr, pos, 4, 64, c, s).astype(np.float64).reshape(4, 2, 32)
+        cr = c[pos * 32:(pos + 1) * 32].astype(np.float64)
+        sr = s[pos * 32:(pos + 1) * 32].astype(np.float64)
+        a, b = xr.astype(np.float64).reshape(4, 2, 32)[:, 0], xr.astype(np.float64).reshape(4, 2, 32)[:, 1]
+        bound = 2.0 ** -23 * (np.abs(a * cr) + np.abs(b * sr) + np.abs(a * sr) + np.abs(b * cr))
+        assert np.all(np.abs(y[:, 0] - (a * cr - b * sr)) <= bound)
+        assert np.all(np.abs(y[:, 1] - (a * sr + b * cr)) <= bound)
 
 
 def attn64(q, K, V, H, KVH, hd):
