@@ -127,6 +127,17 @@ int axf_hip_gemm_q4k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* 
                              int T, int cols, size_t row_bytes, int path);
 int axf_hip_gemm_q6k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
                              int T, int cols, size_t row_bytes, int path);
+/* As axf_hip_gemm_q4k_q8, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The matrix-core path's
+ * activation re-layout goes to a fixed 8 MiB device array inside the library
+ * (one per GPU, held until the process ends) instead of the context's
+ * hipMalloc'd scratch; this call allocates nothing.  Token counts whose
+ * re-layout exceeds 8 MiB (T > 320 at cols 11008, T > 896 at cols 4096) are
+ * AXF_ERR_INVALID_ARG.  Every call on one GPU shares the array: calls whose
+ * kernels overlap on one GPU (other streams or contexts) race. */
+int axf_hip_gemm_q4k_q8_noalloc(axf_ctx* ctx, float* Y, const void* W, const void* XQ8,
+                                int rows, int T, int cols, size_t row_bytes);
 
 /* Other GGUF weight types of the decode path (LM heads of Qwen / DeepSeek files,
  * F16 models).  cols is a multiple of 32 for the block types, rows of

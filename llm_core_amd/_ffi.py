@@ -128,6 +128,7 @@ SIGNATURES: dict[str, list] = {
     "axf_hip_gemv_q6k_q8": [vp, vp, vp, vp, i32, i32, sz, i32],
     "axf_hip_gemm_q4k_q8": [vp, vp, vp, vp, i32, i32, i32, sz],
     "axf_hip_gemm_q4k_q8_path": [vp, vp, vp, vp, i32, i32, i32, sz, i32],
+    "axf_hip_gemm_q4k_q8_noalloc": [vp, vp, vp, vp, i32, i32, i32, sz],
     "axf_hip_gemm_q6k_q8": [vp, vp, vp, vp, i32, i32, i32, sz],
     "axf_hip_gemm_q6k_q8_path": [vp, vp, vp, vp, i32, i32, i32, sz, i32],
     "axf_hip_argmax_f32": [vp, vp, vp, i32],

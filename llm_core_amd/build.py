@@ -37,6 +37,7 @@ SOURCES = [
     "kernels/sample.hip",
     "kernels/gemv_misc.hip",
     "capi.cpp",
+    "gemm_noalloc.cpp",
     "host/synth.cpp",
     "host/llama_hip.cpp",
     "host/gguf.cpp",

@@ -190,8 +190,10 @@ int axf_hip_quantize_q8_0(axf_ctx* ctx, void* xq8, const float* x, int n) {
     return AXF_OK;
 }
 
-static int check_gemv(const char* fn, int qtype, const void* W, const void* x, const float* y,
-                      int rows, int cols, size_t row_bytes, bool f32x) {
+}  // extern "C"
+
+int axf::check_gemv(const char* fn, int qtype, const void* W, const void* x, const float* y,
+                    int rows, int cols, size_t row_bytes, bool f32x) {
     if (rows < 0 || cols < 0) return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": negative size");
     if (cols % QK_K != 0)
         return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": cols must be a multiple of 256");
@@ -222,6 +224,8 @@ static int check_gemv(const char* fn, int qtype, const void* W, const void* x, c
     }
     return AXF_OK;
 }
+
+extern "C" {
 
 static int do_gemv(axf_ctx* ctx, const char* fn, GemvKind kind, int qtype, float* y,
                    const void* W, const void* x, int rows, int cols, size_t row_bytes,

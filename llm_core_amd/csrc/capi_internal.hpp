@@ -27,6 +27,10 @@ constexpr int kMaxBlocksPerRow = 128;
 int fail(int code, const std::string& msg);
 int hip_fail(hipError_t e, const char* where);
 int ctx_scratch(axf_ctx* ctx, size_t bytes, void** p);
+// Argument checks shared by the GEMV/GEMM entry points (sizes, alignment of W,
+// x and y; f32x: fp32 activation instead of Q8_0 blocks).
+int check_gemv(const char* fn, int qtype, const void* W, const void* x, const float* y, int rows,
+               int cols, size_t row_bytes, bool f32x);
 
 enum class GemvKind { Q4K_Q8, Q4K_F32, Q6K_Q8, Q6K_F32 };
 
