@@ -1,0 +1,103 @@
+"""Helpers shared by the GPU parity tests (not a test module)."""
+import numpy as np
+
+from oracle import oracle as O
+
+
+def within(gpu, ref, rtol=1e-3, atol=1e-4):
+    """The north-star bound |gpu - ref| <= atol + rtol |ref| elementwise:
+    (ok, max |err|, number of elements outside)."""
+    gpu = np.asarray(gpu, np.float64)
+    ref = np.asarray(ref, np.float64)
+    bad = np.abs(gpu - ref) > atol + rtol * np.abs(ref)
+    return (not bad.any()), float(np.max(np.abs(gpu - ref))), int(bad.sum())
+
+
+def check(tag, got, want, rtol=1e-3, atol=1e-4):
+    ok, err, nbad = within(got, want, rtol, atol)
+    print(f"  {tag}: max |err| {err:.3e}", flush=True)
+    assert ok, f"{tag}: {nbad} elements outside tolerance, max |err| {err:.3e}"
+
+
+def device_norm_q8(ctx, x, w, eps):
+    """Q8_0 of RMSNorm(x) * w from the device's RMSNorm kernel (the fused GEMV
+    prologues share its summation order).  Checked two ways: the device's
+    fp32 RMSNorm is within fp32 summation noise of the oracle's (1e-5
+    relative, norm-wise), and the device's blocks are bit for bit the Q8_0
+    quantisation of that fp32 output.  So where the two differ from the
+    oracle's own blocks, the device's RMSNorm value lies across a rounding
+    boundary from the oracle's."""
+    n = x.size
+    dx, dw = ctx.upload(np.ascontiguousarray(x, np.float32)), ctx.upload(w)
+    y, yq = ctx.alloc(n * 4), ctx.alloc(n // 32 * 36)
+    ctx.rmsnorm(y, yq, dx, dw, n, eps)
+    got = ctx.download(yq, np.uint8, n // 32 * 36)
+    yd = ctx.download(y, np.float32, n)
+    for b in (dx, dw, y, yq):
+        b.free()
+    yo = O.rmsnorm(x, w, eps).astype(np.float64)
+    rel = np.linalg.norm(yd - yo) / np.linalg.norm(yo)
+    assert rel < 1e-5, f"device RMSNorm differs from the oracle's by {rel:.2e} (norm-wise)"
+    assert np.array_equal(got, O.quantize_q8_0(yd)), "device Q8_0 differs from Q8_0(device RMSNorm)"
+    return got
+
+
+def layer_stage_errors(ctx, g, T, hp, layer, pos):
+    """Run the five fused stages of `layer` at `pos` on the device (from the
+    device's current x and cache rows 0..pos-1) and compare each with the
+    oracle on that stage's device inputs.  Returns a list of
+    (stage, max |err|, elements outside the north-star bound, norm-wise
+    relative error); the K/V rows and the attention Q8_0 blocks must be
+    bit-exact (asserted).  T maps tensor names to host arrays."""
+    from llm_core_amd import _ffi
+
+    E, H, KVH, HD, FD = hp.n_embd, hp.n_heads, hp.n_kv_heads, hp.head_dim, hp.ffn_dim
+    qo, kvo = H * HD, KVH * HD
+    b = f"blk.{layer}."
+    cos_t, sin_t = O.rope_table(HD, hp.rope_theta, hp.n_ctx)
+    res = []
+
+    def rec(tag, got, want, rtol=1e-3, atol=1e-4):
+        ok, err, nbad = within(got, want, rtol, atol)
+        w = np.asarray(want, np.float64)
+        rel = float(np.linalg.norm(np.asarray(got, np.float64) - w) / max(np.linalg.norm(w), 1e-30))
+        res.append((tag, err, nbad, rel))
+
+    x0 = g.buffer(_ffi.AXF_LLAMA_BUF_X)
+    g.forward_layer_stages(layer, pos, 1, 1)
+    qkv = g.buffer(_ffi.AXF_LLAMA_BUF_QKV)
+    xq = device_norm_q8(ctx, x0, T[b + "attn_norm.weight"], hp.rms_eps)
+    qt = {n: (O.Q4K if n != "attn_v" else O.Q6K) for n in ("attn_q", "attn_k", "attn_v")}
+    rec("q", qkv[:qo], O.gemv_q8(qt["attn_q"], T[b + "attn_q.weight"], xq, qo, E))
+    rec("k", qkv[qo:qo + kvo], O.gemv_q8(qt["attn_k"], T[b + "attn_k.weight"], xq, kvo, E))
+    rec("v", qkv[qo + kvo:], O.gemv_q8(qt["attn_v"], T[b + "attn_v.weight"], xq, kvo, E))
+
+    g.forward_layer_stages(layer, pos, 2, 2)
+    zero = np.zeros(kvo, np.float32)
+    q = qkv[:qo] + T.get(b + "attn_q.bias", np.zeros(qo, np.float32))
+    k = qkv[qo:qo + kvo] + T.get(b + "attn_k.bias", zero)
+    v = qkv[qo + kvo:] + T.get(b + "attn_v.bias", zero)
+    k_dev, v_dev = g.get_kv(layer, 0, pos + 1)
+    assert np.array_equal(k_dev[pos], O.rope(k, pos, KVH, HD, cos_t, sin_t)), "stored K row"
+    assert np.array_equal(v_dev[pos], v), "stored V row"
+    att = g.buffer(_ffi.AXF_LLAMA_BUF_ATTN)
+    rec("attention", att, O.attention(O.rope(q, pos, H, HD, cos_t, sin_t), k_dev, v_dev, pos + 1,
+                                      H, KVH, HD), 1e-5, 1e-6)
+    aq = g.buffer(_ffi.AXF_LLAMA_BUF_ATTN_Q8)
+    assert np.array_equal(aq, O.quantize_q8_0(att)), "attention Q8_0 blocks"
+
+    g.forward_layer_stages(layer, pos, 3, 3)
+    x1 = g.buffer(_ffi.AXF_LLAMA_BUF_X)
+    rec("x + o", x1, x0 + O.gemv_q8(O.Q4K, T[b + "attn_output.weight"], aq, E, qo))
+
+    g.forward_layer_stages(layer, pos, 4, 4)
+    h = g.buffer(_ffi.AXF_LLAMA_BUF_H)
+    xq2 = device_norm_q8(ctx, x1, T[b + "ffn_norm.weight"], hp.rms_eps)
+    gate = O.gemv_q8(O.Q4K, T[b + "ffn_gate.weight"], xq2, FD, E)
+    up = O.gemv_q8(O.Q4K, T[b + "ffn_up.weight"], xq2, FD, E)
+    rec("swiglu(gate, up)", h, O.swiglu(gate, up))
+
+    g.forward_layer_stages(layer, pos, 5, 5)
+    x2 = g.buffer(_ffi.AXF_LLAMA_BUF_X)
+    rec("x + down", x2, x1 + O.gemv_q8(O.Q6K, T[b + "ffn_down.weight"], O.quantize_q8_0(h), E, FD))
+    return res

@@ -7,19 +7,26 @@ and the head), a 512-token uniform-random prompt, greedy decode, context 2048
     HIP-graph replay and eager launches, and repeatable; the token-by-token
     prefill gives the same ids wherever the device's own teacher-forced top-2
     margin exceeds the logit difference between the two prefill paths;
-  * the oracle, with its KV cache rows 0..510 copied from the device's
-    batched prefill, recomputes the last prompt row and three teacher-forced
-    decode steps (positions 511..514).  Its K/V rows at 511 and its logits
-    are compared with the device's, and the device's greedy choice must equal
-    the oracle's wherever the oracle's top-2 margin exceeds twice the logit
-    difference.  The bound on the logits is norm-wise (a Q8_0 requantisation
-    of an activation that sits within fp32 noise of a rounding boundary moves
-    single logits by up to ~1e-3 after 32 layers; see DESIGN.md's parity
-    section for the measurement).
+  * with the cache rows 0..510 of the device's batched prefill, the last
+    prompt row (position 511) and three teacher-forced decode steps run stage
+    by stage through all 32 layers: each fused stage (q|k|v, attention with
+    the K/V store, o, gate|up with SwiGLU, down) is compared with the oracle on
+    that stage's device inputs at the north-star tolerance (K/V rows and the
+    attention's Q8_0 bit-exact); then the whole step in one call must give the
+    same bits, and its logits must match the oracle's head on the device's
+    final row.  Whole-model comparisons would test the random model's
+    sensitivity instead: a Q8_0 requantisation that lands on the other side of
+    a rounding boundary (device and oracle sum RMSNorm in different orders)
+    moves that layer's update by up to a few 1e-3, and such differences grow
+    through the later layers.  The test prints that growth (the batched
+    prefill's row 511 against the decode path's row over the same cache, per
+    layer) and requires layer 0, where nothing has grown yet, to agree to fp32
+    rounding.
 """
 import numpy as np
 import pytest
 
+from gpu_helpers import device_norm_q8, layer_stage_errors, within
 from oracle import oracle as O
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
@@ -69,6 +76,9 @@ def test_config5_full_size(ctx):
         _, d0 = rel_err(tbt0, dev_logits[0])
         print(f"  prefill paths: last-row logits max |diff| {d0:.2e}; "
               f"margins min {margins.min():.3e}", flush=True)
+        same = int(np.argmax(graph != tbt)) if np.any(graph != tbt) else N_GEN
+        print(f"  token-by-token prefill: first {same} of {N_GEN} ids equal the batched run's",
+              flush=True)
         for i in range(N_GEN):
             if graph[i] != tbt[i]:
                 # the first divergence must sit at a step the paths' difference can flip
@@ -79,32 +89,50 @@ def test_config5_full_size(ctx):
     finally:
         g.close()
 
-    # oracle: KV rows 0..510 from the device's batched prefill, then the last
-    # prompt row (position 511) and three teacher-forced decode steps
-    om = O.OracleModel(hp, model.tensors)
+    # oracle, stage by stage at every layer: the cache rows 0..510 of the
+    # device's batched prefill, then the last prompt row (position 511) and
+    # three teacher-forced decode steps.  Each fused stage of each layer is
+    # compared with the oracle on that stage's device inputs.
+    g = LlamaHip(ctx, model)
     try:
-        ok_, ov_ = om.kv_view()
         for layer, (kk, vv) in enumerate(kv_dev):
-            ok_[layer, :N_PROMPT - 1] = kk
-            ov_[layer, :N_PROMPT - 1] = vv
-        om.forward_token(int(prompt[-1]), N_PROMPT - 1)
-        for layer in range(hp.n_layer):
-            for tag, got, want in (("K", k511[layer][0], ok_[layer, N_PROMPT - 1]),
-                                   ("V", v511[layer][0], ov_[layer, N_PROMPT - 1])):
-                r, _ = rel_err(got, want)
-                assert r < 1e-3, f"layer {layer} {tag} row {N_PROMPT - 1}: relative error {r:.2e}"
-        steps = [(N_PROMPT - 1, om.logits(), dev_logits[0])]
-        for i in range(3):
-            om.forward_token(int(graph[i]), N_PROMPT + i)
-            steps.append((N_PROMPT + i, om.logits(), dev_logits[i + 1]))
-        for pos, want, got in steps:
+            g.set_kv(layer, kk, vv, N_PROMPT - 1)
+        T = {k: v[1] for k, v in model.tensors.items()}
+        qt, emb = model.tensors["token_embd.weight"]
+        rb = O.row_bytes(qt, hp.n_embd)
+        out_qt, out_w = model.tensors["output.weight"]
+        growth = []
+        for tok, pos in ([(int(prompt[-1]), N_PROMPT - 1)] +
+                         [(int(graph[i]), N_PROMPT + i) for i in range(3)]):
+            g.set_x(O.dequant(qt, emb[tok * rb:(tok + 1) * rb]))
+            worst = {}
+            for layer in range(hp.n_layer):
+                for tag, err, nbad, rel in layer_stage_errors(ctx, g, T, hp, layer, pos):
+                    assert nbad == 0, (f"pos {pos} layer {layer} {tag}: {nbad} elements outside "
+                                       f"tolerance, max |err| {err:.3e}")
+                    worst[tag] = max(worst.get(tag, 0.0), rel)
+                if pos == N_PROMPT - 1:
+                    # the batched prefill's row 511 vs the decode path's, same rows 0..510
+                    growth.append(rel_err(k511[layer][0], g.get_kv(layer, pos, 1)[0][0])[0])
+            xf = g.get_x()
+            g.forward_token(tok, pos)                  # the same kernels in one call + head
+            assert np.array_equal(g.get_x(), xf)
+            got = g.logits()
+            # the head on the device's Q8_0 of the final norm (oracle-checked inside)
+            xq = device_norm_q8(ctx, xf, model.tensors["output_norm.weight"][1], hp.rms_eps)
+            want = O.gemv_q8(out_qt, out_w, xq, hp.n_vocab, hp.n_embd)
             r, mx = rel_err(got, want)
             m = O.top2_margin(want)
-            print(f"  pos {pos}: logits relative error {r:.2e}, max |diff| {mx:.2e}, "
-                  f"oracle margin {m:.3e}, argmax gpu {int(np.argmax(got))} "
-                  f"oracle {O.argmax(want)}", flush=True)
-            assert r < 1e-3, f"position {pos}: logits relative error {r:.2e}"
+            print(f"  pos {pos}: worst stage errors (norm-wise) "
+                  + ", ".join(f"{k} {v:.1e}" for k, v in worst.items())
+                  + f"; logits max |diff| {mx:.2e}, margin {m:.3e}, argmax gpu "
+                  f"{int(np.argmax(got))} oracle {O.argmax(want)}", flush=True)
+            ok, err, _ = within(got, want)
+            assert ok, f"pos {pos}: logits max |err| {err:.3e}"
             if m > 2 * mx:
                 assert int(np.argmax(got)) == O.argmax(want), f"position {pos}: argmax differs"
+        print("  batched-prefill K row 511 vs the decode path on the same cache, per layer: "
+              + " ".join(f"{v:.1e}" for v in growth), flush=True)
+        assert growth[0] < 1e-5, "layer 0 K rows of the two paths differ beyond fp32 rounding"
     finally:
-        om.close()
+        g.close()

@@ -22,50 +22,13 @@ Reference: llama_forward_token's layer body, llama_model.cpp:1222-1325.
 import numpy as np
 import pytest
 
-from oracle import oracle as O
+from gpu_helpers import layer_stage_errors
 
 pytestmark = pytest.mark.gpu
 
 
-def within(gpu, ref, rtol=1e-3, atol=1e-4):
-    gpu = np.asarray(gpu, np.float64)
-    ref = np.asarray(ref, np.float64)
-    bad = np.abs(gpu - ref) > atol + rtol * np.abs(ref)
-    return (not bad.any()), float(np.max(np.abs(gpu - ref))), int(bad.sum())
-
-
-def check(tag, got, want, rtol=1e-3, atol=1e-4):
-    ok, err, nbad = within(got, want, rtol, atol)
-    print(f"  {tag}: max |err| {err:.3e}", flush=True)
-    assert ok, f"{tag}: {nbad} elements outside tolerance, max |err| {err:.3e}"
-
-
-def device_norm_q8(ctx, x, w, eps):
-    """Q8_0 of RMSNorm(x) * w from the device's RMSNorm kernel, checked
-    against the oracle's blocks: a block may differ only by a one-step
-    rounding of an element whose oracle value x*id sits within 1e-3 of .5."""
-    n = x.size
-    dx, dw = ctx.upload(np.ascontiguousarray(x, np.float32)), ctx.upload(w)
-    y, yq = ctx.alloc(n * 4), ctx.alloc(n // 32 * 36)
-    ctx.rmsnorm(y, yq, dx, dw, n, eps)
-    got = ctx.download(yq, np.uint8, n // 32 * 36)
-    want = O.quantize_q8_0(O.rmsnorm(x, w, eps))
-    if not np.array_equal(got, want):
-        from qblocks import unpack_q8
-
-        dg, qg = unpack_q8(got)
-        dw_, qw = unpack_q8(want)
-        xn = O.rmsnorm(x, w, eps).reshape(-1, 32).astype(np.float64)
-        frac = np.abs(xn / np.where(dw_ > 0, dw_, 1)[:, None])
-        frac = np.abs(frac - np.floor(frac) - 0.5)
-        diff = qg != qw
-        assert np.all(np.abs(qg - qw) <= 1) and np.all(frac[diff] < 1e-3)
-        assert np.allclose(dg, dw_, rtol=1e-6, atol=0)
-    return got
-
-
 def fused_stage_parity(ctx, cfg, prior, with_bias, seed):
-    from llm_core_amd import _ffi, hip
+    from llm_core_amd import hip
     from llm_core_amd.model import Hparams, LlamaHip, SynthLlama
 
     cfg = dict(cfg)
@@ -74,62 +37,19 @@ def fused_stage_parity(ctx, cfg, prior, with_bias, seed):
     hp = Hparams(n_ctx=prior + 1, **cfg)
     m = SynthLlama(hp, seed=seed, norm_std=0.1, with_bias=with_bias)
     T = {k: v[1] for k, v in m.tensors.items()}
-    E, H, KVH, HD, FD = hp.n_embd, hp.n_heads, hp.n_kv_heads, hp.head_dim, hp.ffn_dim
-    qo, kvo, pos = H * HD, KVH * HD, prior
+    E, kvo, pos = hp.n_embd, hp.n_kv_heads * hp.head_dim, prior
     kc = hip.synth_normal(prior * kvo, 41).reshape(prior, kvo)
     vc = hip.synth_normal(prior * kvo, 42).reshape(prior, kvo)
     x0 = hip.synth_normal(E, 43)
-    cos_t, sin_t = O.rope_table(HD, hp.rope_theta, hp.n_ctx)
-    zero = np.zeros(kvo, np.float32)
 
     g = LlamaHip(ctx, m)
     try:
         g.set_kv(0, kc, vc, prior)
         g.set_x(x0)
-
-        # 1. q|k|v GEMVs with the attention RMSNorm in the prologue (before bias)
-        g.forward_layer_stages(0, pos, 1, 1)
-        qkv = g.buffer(_ffi.AXF_LLAMA_BUF_QKV)
-        xq = device_norm_q8(ctx, x0, T["blk.0.attn_norm.weight"], hp.rms_eps)
-        check("q", qkv[:qo], O.gemv_q8(O.Q4K, T["blk.0.attn_q.weight"], xq, qo, E))
-        check("k", qkv[qo:qo + kvo], O.gemv_q8(O.Q4K, T["blk.0.attn_k.weight"], xq, kvo, E))
-        check("v", qkv[qo + kvo:], O.gemv_q8(O.Q6K, T["blk.0.attn_v.weight"], xq, kvo, E))
-
-        # 2. attention: bias + RoPE of q and k, K/V row `pos` stored, output and Q8_0
-        g.forward_layer_stages(0, pos, 2, 2)
-        q = qkv[:qo] + T.get("blk.0.attn_q.bias", np.zeros(qo, np.float32))
-        k = qkv[qo:qo + kvo] + T.get("blk.0.attn_k.bias", zero)
-        v = qkv[qo + kvo:] + T.get("blk.0.attn_v.bias", zero)
-        kr = O.rope(k, pos, KVH, HD, cos_t, sin_t)
-        k_dev, v_dev = g.get_kv(0, 0, pos + 1)
-        assert np.array_equal(k_dev[pos], kr), "stored K row differs from RoPE(k + bk)"
-        assert np.array_equal(v_dev[pos], v), "stored V row differs from v + bv"
-        assert np.array_equal(k_dev[:pos], kc) and np.array_equal(v_dev[:pos], vc)
-        att_want = O.attention(O.rope(q, pos, H, HD, cos_t, sin_t), k_dev, v_dev, pos + 1, H,
-                               KVH, HD)
-        att = g.buffer(_ffi.AXF_LLAMA_BUF_ATTN)
-        check("attention", att, att_want, 1e-5, 1e-6)
-        aq = g.buffer(_ffi.AXF_LLAMA_BUF_ATTN_Q8)
-        assert np.array_equal(aq, O.quantize_q8_0(att)), "attention Q8_0 blocks differ"
-
-        # 3. o projection, x += o
-        g.forward_layer_stages(0, pos, 3, 3)
-        x1 = g.buffer(_ffi.AXF_LLAMA_BUF_X)
-        check("x + o", x1, x0 + O.gemv_q8(O.Q4K, T["blk.0.attn_output.weight"], aq, E, qo))
-
-        # 4. gate|up with the FFN RMSNorm prologue and the SwiGLU epilogue
-        g.forward_layer_stages(0, pos, 4, 4)
-        h = g.buffer(_ffi.AXF_LLAMA_BUF_H)
-        xq2 = device_norm_q8(ctx, x1, T["blk.0.ffn_norm.weight"], hp.rms_eps)
-        gate = O.gemv_q8(O.Q4K, T["blk.0.ffn_gate.weight"], xq2, FD, E)
-        up = O.gemv_q8(O.Q4K, T["blk.0.ffn_up.weight"], xq2, FD, E)
-        check("swiglu(gate, up)", h, O.swiglu(gate, up))
-
-        # 5. down projection of Q8_0(h) (quantised in the prologue), x += down
-        g.forward_layer_stages(0, pos, 5, 5)
-        x2 = g.buffer(_ffi.AXF_LLAMA_BUF_X)
-        check("x + down", x2,
-              x1 + O.gemv_q8(O.Q6K, T["blk.0.ffn_down.weight"], O.quantize_q8_0(h), E, FD))
+        for tag, err, nbad, rel in layer_stage_errors(ctx, g, T, hp, 0, pos):
+            print(f"  {tag}: max |err| {err:.3e}, norm-wise {rel:.2e}", flush=True)
+            assert nbad == 0, f"{tag}: {nbad} elements outside tolerance, max |err| {err:.3e}"
+        x2 = g.get_x()
 
         # the whole layer in one call runs the same kernels: the same bits
         g.set_kv(0, kc, vc, prior)
