@@ -150,11 +150,12 @@ def q6k_sweep(ctx, Ms=(1, 8, 16, 64)):
     return res
 
 
-# --eager: the --only gemm sweep launches each GEMM directly instead of
-# replaying a captured graph (kernel traces: the profiler's instrumentation has
-# crashed the host process inside graph capture here; timings then include the
-# host's launch gaps, the kernel durations in the trace do not)
-EAGER_GEMM = False
+def under_profiler() -> bool:
+    """rocprofv3 runs the program with its ROCPROF_* / ROCPROFILER_* settings in
+    the environment.  Its kernel-trace instrumentation has crashed the host
+    process while graphs of a few hundred kernel nodes were being captured, so
+    under it every benchmark helper launches directly (no graph capture)."""
+    return any(k.startswith(("ROCPROF_", "ROCPROFILER_")) for k in os.environ)
 
 
 def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL_BYTES + (96 << 20),
@@ -176,19 +177,9 @@ def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL
     dY = ctx.alloc(M * rows * 4)
     alg = W.nbytes + M * (cols // 32 * 36) + 4 * M * rows
     res = {"M": M}
-    gemm = ctx.gemm_q4k_q8 if qtype == hip.AXF_TYPE_Q4_K else ctx.gemm_q6k_q8
     for name, path in (("dot4", 1), ("mfma", 2), ("auto", 0)):
-        if EAGER_GEMM:  # direct launches (no graph capture); host gaps included
-            for b in bufs[:2]:
-                gemm(dY, b, xq, rows, M, cols, rb, path=path or None)
-            ctx.timer_start()
-            for _ in range(reps):
-                for b in bufs:
-                    gemm(dY, b, xq, rows, M, cols, rb, path=path or None)
-            ms = ctx.timer_stop()
-        else:
-            ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2, path, qtype)
-            ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps, path, qtype)
+        ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2, path, qtype)
+        ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps, path, qtype)
         res[f"{name}_us"] = round(ms * 1000.0 / (reps * n_copies), 3)
     us = res["auto_us"]
     for b in bufs:
@@ -196,6 +187,105 @@ def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL
     res.update({"GBs": round(alg / (us * 1e-6) / 1e9, 1),
                 "TOPs": round(2.0 * M * rows * cols / (us * 1e-6) / 1e12, 2)})
     return res
+
+
+def read_probe(ctx, nbytes, n_copies, reps=40):
+    """The plain streaming read (axf_hip_bench_read) of nbytes per launch over
+    n_copies rotating buffers, swept over launch shapes (16-byte loads in
+    flight per thread x workgroups of 256); the fastest shape is the read
+    ceiling of one launch of that size.  One graph holds GEMV_ROUNDS passes
+    over the copies, as for the GEMVs."""
+    bufs = [ctx.alloc(nbytes) for _ in range(n_copies)]
+    for b in bufs:  # contents do not matter; make them defined
+        ctx.write(b, np.zeros(16, np.uint8))
+    seq = bufs * GEMV_ROUNDS
+    best, sweep = None, []
+    one_each = -(-nbytes // (16 * 256))  # workgroups giving one vector per thread
+    for unroll in (1, 2, 4, 8):
+        for wgs in (512, 1024, 2048, 4096, one_each):
+            if wgs * 256 * unroll * 16 > 2 * nbytes and wgs != one_each:
+                continue
+            if wgs == one_each and unroll > 1:
+                continue
+            ctx.bench_read(seq, nbytes, unroll, wgs, 2)
+            us = ctx.bench_read(seq, nbytes, unroll, wgs, reps) * 1000.0 / (reps * len(seq))
+            sweep.append((unroll, wgs, round(us, 3)))
+            if best is None or us < best[2]:
+                best = (unroll, wgs, us)
+    for b in bufs:
+        b.free()
+    unroll, wgs, us = best
+    return {"bytes": nbytes, "n_copies": n_copies, "us": round(us, 3),
+            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1), "best_launch": f"{wgs}x256 threads, "
+            f"{unroll} x 16 B per thread in flight", "sweep_unroll_wgs_us": sweep}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_legs(ctx_gpu_results: dict) -> dict:
+    """The reference's own x86 kernels (oracle/_ref, compiled from its sources)
+    on this host for configs 1-4, each a bounded sample (median of the timed
+    calls after 3 warm-ups, weights rotated past the host's last-level cache),
+    beside the GPU figures of the same run."""
+    from llm_core_amd import hip
+    from llm_core_amd.model import QWEN25_3B_LAYER, Hparams, SynthLlama
+    from oracle import oracle as O
+
+    out: dict = {"cpu_model": cpu_model(),
+                 "isa": "AVX-VNNI" if O.ref.ref_has_avxvnni() else "AVX2"}
+    # config 1: Q4_K x F32 4096 x 4096 (gemv_q4k_avx2_range) and the decode
+    # variant (Q8_0 quantise + r8 GEMV)
+    W = hip.synth_weight(hip.AXF_TYPE_Q4_K, 4096, 4096, 1)
+    x = hip.synth_normal(4096, 2)
+    t, n = O.ref_time_gemv_f32(hip.AXF_TYPE_Q4_K, W, 4096, 4096, x, 30)
+    t8, _ = O.ref_time_decode_gemv(hip.AXF_TYPE_Q4_K, W, 4096, 4096, x, n_copies=64, iters=30)
+    out["threads"] = n
+    out["c1_q4k_f32_4096x4096"] = {"us": round(t * 1e6, 1), "GBs": round(9469952 / t / 1e9, 2),
+                                   "decode_variant_q8_r8_us": round(t8 * 1e6, 1)}
+    # config 2: Q6_K 151936 x 2048 head + greedy pick
+    W = hip.synth_weight(hip.AXF_TYPE_Q6_K, 151936, 2048, 2)
+    x = hip.synth_normal(2048, 3)
+    t, _, _ = O.ref_time_head_argmax(W, 151936, 2048, x, 10)
+    out["c2_q6k_q8_151936x2048_argmax"] = {"us": round(t * 1e6, 1),
+                                           "GBs": round(255868416 / t / 1e9, 2)}
+    del W
+    # config 4: Q4_K 11008 x 4096, M = 1 (r8 GEMV) and M = 4, 16, 64 (GEMM)
+    W = hip.synth_weight(hip.AXF_TYPE_Q4_K, 11008, 4096, 4)
+    c4 = []
+    for M in (1, 4, 16, 64):
+        X = hip.synth_normal(M * 4096, 11 + M)
+        if M == 1:
+            t, _ = O.ref_time_decode_gemv(hip.AXF_TYPE_Q4_K, W, 11008, 4096, X, n_copies=26,
+                                          iters=20)
+        else:
+            XQ = np.concatenate([O.quantize_q8_0(X[i * 4096:(i + 1) * 4096]) for i in range(M)])
+            t, _ = O.ref_time_gemm_q4k(W, 11008, 4096, XQ, M, 10)
+        alg = W.nbytes + M * 4096 // 32 * 36 + 4 * M * 11008
+        c4.append({"M": M, "us": round(t * 1e6, 1), "GBs": round(alg / t / 1e9, 2),
+                   "GOPs": round(2 * M * 11008 * 4096 / t / 1e9, 1)})
+    out["c4_q4k_q8_gemm_11008x4096"] = c4
+    del W
+    # config 3: the Qwen2.5-3B-like layer decoding at position 1024 (as the
+    # GPU leg: a 1-layer model with a 512-row head)
+    hp = Hparams(n_ctx=1025, **{**QWEN25_3B_LAYER, "n_vocab": 512})
+    model = SynthLlama(hp, seed=7, with_bias=True)
+    kve = hp.n_kv_heads * hp.head_dim
+    k = hip.synth_normal(hp.n_ctx * kve, 701)
+    v = hip.synth_normal(hp.n_ctx * kve, 702)
+    om = O.OracleModel(hp, model.tensors)
+    t, _, _ = O.ref_time_decode_step(om, k, v, 1024, 3, 20)
+    om.close()
+    out["c3_qwen25_3b_layer_decode"] = {"us_per_step": round(t * 1e6, 1)}
+    return out
 
 
 def copy_probe(ctx, nbytes=256 << 20, reps=10):
@@ -331,7 +421,8 @@ def main() -> int:
     ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill", "c3"],
                     default="all")
     ap.add_argument("--eager", action="store_true",
-                    help="--only gemm: direct launches, no graph capture (for kernel traces)")
+                    help="direct launches instead of captured-graph replay in every timing "
+                         "(implied under rocprofv3); timings then include host launch gaps")
     ap.add_argument("--skip-c4", action="store_true",
                     help="leave out the config-3 layer and config-4 GEMM timings (shorter profiling runs)")
     ap.add_argument("--no-e2e", action="store_true",
@@ -371,14 +462,17 @@ def main() -> int:
 
     ctx = hip.Context(0)
     log(f"device: {ctx.device_name()}")
-    out: dict = {}
+    eager = args.eager or under_profiler()
+    if eager:
+        ctx.bench_set_eager(True)
+        log("direct kernel launches (no graph capture): "
+            + ("running under rocprofv3" if under_profiler() else "--eager"))
+    out: dict = {"launch": "eager" if eager else "hip-graph replay"}
 
     if args.only == "c3":  # config 3 layer alone (not a bench line)
         print(json.dumps({"c3_qwen25_3b_layer_decode": c3_run(ctx, args.warmup, args.steps)}))
         return 0
     if args.only == "gemm":  # config 4 sweep alone (not a bench line)
-        global EAGER_GEMM
-        EAGER_GEMM = args.eager
         print(json.dumps({"c4_q4k_q8_gemm_11008x4096": c4_sweep(ctx),
                           "q6k_q8_gemm_4096x11008": q6k_sweep(ctx)}))
         return 0
@@ -395,6 +489,9 @@ def main() -> int:
     if args.only in ("all", "gemv"):
         g, W_up, x_up = gemv_case(ctx, 0, hip.AXF_TYPE_Q4_K, 11008, 4096, args.gemv_reps, 4)
         log(f"gemv q4k 11008x4096: {g['us_per_launch']:.2f} us/launch, {g['gbs']:.0f} GB/s")
+        rd = read_probe(ctx, g["algorithmic_bytes"] // 16 * 16, g["n_copies"])
+        log(f"plain read of {rd['bytes'] / 1e6:.1f} MB per launch ({rd['best_launch']}): "
+            f"{rd['us']:.2f} us, {rd['GBs']:.0f} GB/s")
         warm = None
         if args.mall_warm:
             warm, _, _ = gemv_case(ctx, 0, hip.AXF_TYPE_Q4_K, 11008, 4096, args.gemv_reps, 4,
@@ -420,10 +517,15 @@ def main() -> int:
             "algorithmic_bytes_per_launch": g["algorithmic_bytes"],
             "weight_copies": g["n_copies"],
             "mall_warm_us_per_launch": round(warm["us_per_launch"], 3) if warm else None,
+            "plain_read_us": rd["us"],
+            "plain_read_GBs": rd["GBs"],
+            "plain_read_frac_of_peak": round(rd["GBs"] / HBM_PEAK_GBS, 4),
+            "gemv_vs_plain_read": round(rd["us"] / g["us_per_launch"], 4),
         }
         c4 = None if args.skip_c4 else c4_sweep(ctx)
         g6 = None if args.skip_c4 else q6k_sweep(ctx)
         out["kernels"] = {
+            "plain_read_25MB": rd,
             "copy_256MiB_d2d": cp,
             "c4_q4k_q8_gemm_11008x4096": c4,
             "q6k_q8_gemm_4096x11008": g6,
@@ -431,6 +533,19 @@ def main() -> int:
             "c2_q6k_q8_151936x2048": {"us": round(c2["us_per_launch"], 3), "GBs": round(c2["gbs"], 1)},
             "c3_qwen25_3b_layer_decode": None if args.skip_c4 else c3_run(ctx),
         }
+        if not args.no_cpu and not args.skip_c4:
+            from oracle import oracle as O
+            if O.ref is None:
+                log("oracle/_ref not built: CPU legs of configs 1-4 skipped")
+            else:
+                t0 = time.time()
+                out["cpu_configs"] = cpu_legs(out["kernels"])
+                cc = out["cpu_configs"]
+                log(f"cpu ({cc['cpu_model']}, {cc['threads']} threads, {cc['isa']}) configs 1-4 "
+                    f"in {time.time() - t0:.1f}s: c1 {cc['c1_q4k_f32_4096x4096']['us']} us, "
+                    f"c2 {cc['c2_q6k_q8_151936x2048_argmax']['us']} us, "
+                    f"c3 {cc['c3_qwen25_3b_layer_decode']['us_per_step']} us, c4 "
+                    + ", ".join(f"M={e['M']} {e['us']} us" for e in cc["c4_q4k_q8_gemm_11008x4096"]))
         if args.only == "gemv" and not args.no_cpu:
             from oracle import oracle as O
             if O.ref is not None:
@@ -486,6 +601,9 @@ def main() -> int:
                     "value": round(1.0 / t, 3),
                     "unit": "tokens/s",
                     "cores": used,
+                    "cpu_model": cpu_model(),
+                    "isa": ("r8 Q4_K GEMV with AVX-VNNI" if O.ref.ref_has_avxvnni()
+                            else "r8 Q4_K GEMV with AVX2"),
                     "kind": "reference",
                     "sample": (f"median of {n} decode steps (+1 warm-up) of the same 7B Q4_K_M "
                                f"synthetic model at context {n_ctx}: reference x86 kernels "

@@ -250,6 +250,20 @@ int axf_hip_timer_stop(axf_ctx* ctx, float* ms); /* waits for the stop event */
 int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_list, int n_w,
                        const void* x, int rows, int cols, size_t row_bytes, int reps, float* ms);
 
+/* Benchmark helper (no reference counterpart): a plain streaming read of
+ * `bytes` (a multiple of 16) from each of the n device buffers in turn,
+ * reps times over the list, as axf_hip_bench_gemv times its GEMVs; unroll
+ * (1, 2, 4, 8) 16-byte loads in flight per thread, wgs workgroups of 256
+ * threads.  *ms = elapsed milliseconds of the timed passes.  It measures what
+ * one launch of a given size can read, the ceiling the GEMVs are compared to. */
+int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t bytes, int unroll,
+                       int wgs, int reps, float* ms);
+/* Benchmark helpers (no reference counterpart): eager != 0 makes
+ * axf_hip_bench_gemv, axf_hip_bench_gemm and axf_llama_bench_decode on this
+ * context launch every kernel directly instead of capturing and replaying a
+ * HIP graph (for runs under a profiler; the timings then include the host's
+ * launch gaps). */
+int axf_hip_bench_set_eager(axf_ctx* ctx, int eager);
 /* Benchmark helper (no reference counterpart): as axf_hip_bench_gemv for the
  * T-token GEMM of axf_hip_gemm_q4k_q8 / axf_hip_gemm_q6k_q8 (qtype AXF_TYPE_Q4_K or
  * AXF_TYPE_Q6_K weights, Q8_0 activations); path as for axf_hip_gemm_q4k_q8_path. */

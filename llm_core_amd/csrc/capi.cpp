@@ -576,6 +576,18 @@ int axf_hip_timer_stop(axf_ctx* ctx, float* ms) {
 template <class F>
 static int bench_graph(axf_ctx* ctx, const char* fn, int n, int reps, float* ms, F launch) {
     hipStream_t st = ctx->stream;
+    if (ctx->bench_eager) {  // direct launches: one warm-up pass, then reps passes
+        hipError_t e = hipSuccess;
+        for (int i = 0; i < n && e == hipSuccess; i++) e = launch(i, st);
+        if (e == hipSuccess) e = hipEventRecord(ctx->ev0, st);
+        for (int r = 0; r < reps && e == hipSuccess; r++)
+            for (int i = 0; i < n && e == hipSuccess; i++) e = launch(i, st);
+        if (e == hipSuccess) e = hipEventRecord(ctx->ev1, st);
+        if (e == hipSuccess) e = hipEventSynchronize(ctx->ev1);
+        if (e == hipSuccess) e = hipEventElapsedTime(ms, ctx->ev0, ctx->ev1);
+        if (e != hipSuccess) return hip_fail(e, fn);
+        return AXF_OK;
+    }
     AXF_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
     hipError_t e = hipSuccess;
     for (int i = 0; i < n && e == hipSuccess; i++) e = launch(i, st);
@@ -601,6 +613,27 @@ static int bench_graph(axf_ctx* ctx, const char* fn, int n, int reps, float* ms,
 }
 
 extern "C" {
+
+int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t bytes, int unroll,
+                       int wgs, int reps, float* ms) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(bufs && n > 0 && reps > 0 && ms && bytes >= 16 && bytes % 16 == 0 && wgs > 0,
+                "bad arguments");
+    AXF_REQUIRE(unroll == 1 || unroll == 2 || unroll == 4 || unroll == 8, "unroll must be 1/2/4/8");
+    for (int i = 0; i < n; i++) AXF_REQUIRE(bufs[i] && aligned(bufs[i], 16), "buffer misaligned");
+    void* sink = nullptr;
+    int rc = ctx_scratch(ctx, 16, &sink);  // before any capture
+    if (rc) return rc;
+    return bench_graph(ctx, __func__, n, reps, ms, [&](int i, hipStream_t st) {
+        return launch_stream_read(bufs[i], bytes, unroll, wgs, static_cast<uint32_t*>(sink), st);
+    });
+}
+
+int axf_hip_bench_set_eager(axf_ctx* ctx, int eager) {
+    AXF_CHECK_CTX(ctx);
+    ctx->bench_eager = eager ? 1 : 0;
+    return AXF_OK;
+}
 
 int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_list, int n_w,
                        const void* x, int rows, int cols, size_t row_bytes, int reps, float* ms) {

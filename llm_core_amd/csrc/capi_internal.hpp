@@ -14,6 +14,9 @@ struct axf_ctx {
     void* scratch = nullptr;  // grown on demand by eager entry points (never during capture)
     size_t scratch_bytes = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    // benchmark helpers launch kernels directly instead of replaying a
+    // captured graph (axf_hip_bench_set_eager; for runs under a profiler)
+    int bench_eager = 0;
 };
 
 namespace axf {
@@ -159,6 +162,10 @@ hipError_t launch_add(float* y, const float* a, const float* b, int n, hipStream
 hipError_t launch_silu(float* y, const float* x, int n, hipStream_t st);
 hipError_t launch_mul(float* y, const float* a, const float* b, int n, hipStream_t st);
 hipError_t launch_set_int(int* p, int v, hipStream_t st);
+// measurement kernel: read every 16-byte vector of [p, p + bytes) once
+// (unroll 1/2/4/8 vectors in flight per thread, wgs workgroups of 256)
+hipError_t launch_stream_read(const void* p, size_t bytes, int unroll, int wgs, uint32_t* sink,
+                              hipStream_t st);
 hipError_t launch_push_token(int* tokens, int* step, const int* tok, hipStream_t st);
 // Device sampler (kernels/sample.hip).  sample_candidates returns the number of
 // candidate keys (uint64) launch_sample needs in `cand`, 0 when k is beyond

@@ -1091,12 +1091,16 @@ int axf_llama_bench_decode(axf_llama* m, int pos, int warmup, int steps, float* 
     if (!ms || pos < 0 || pos >= m->hp.n_ctx || warmup < 0 || steps <= 0)
         return fail(AXF_ERR_INVALID_ARG, "axf_llama_bench_decode: bad arguments");
     hipStream_t st = m->ctx->stream;
-    LL_TRY(ensure_graph(m, 1));
+    const bool eager = m->ctx->bench_eager != 0;  // direct launches (profilers)
+    if (!eager) LL_TRY(ensure_graph(m, 1));
     LL_HIP(launch_set_int(m->d_pos, pos, st));
     LL_HIP(launch_set_int(m->d_token, 1, st));
-    for (int i = 0; i < warmup; i++) LL_HIP(hipGraphLaunch(m->exec[1], st));
+    auto step = [&]() -> hipError_t {
+        return eager ? enqueue_step(m, true, 0, 0, false) : hipGraphLaunch(m->exec[1], st);
+    };
+    for (int i = 0; i < warmup; i++) LL_HIP(step());
     LL_HIP(hipEventRecord(m->ctx->ev0, st));
-    for (int i = 0; i < steps; i++) LL_HIP(hipGraphLaunch(m->exec[1], st));
+    for (int i = 0; i < steps; i++) LL_HIP(step());
     LL_HIP(hipEventRecord(m->ctx->ev1, st));
     LL_HIP(hipEventSynchronize(m->ctx->ev1));
     LL_HIP(hipEventElapsedTime(ms, m->ctx->ev0, m->ctx->ev1));

@@ -577,4 +577,42 @@ hipError_t launch_push_token(int* tokens, int* step, const int* tok, hipStream_t
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Plain streaming read (a measurement kernel): every 16-byte vector of
+// [p, p + n16*16) is loaded once; thread i of a grid of G threads loads
+// vectors i, i + G, ... (U of them in flight per loop trip: one wave
+// instruction covers 1 KiB of contiguous bytes) and XORs them.  Nothing is
+// written unless the XOR equals a magic value, so the kernel's bytes are the
+// reads alone: the practical read ceiling of a launch of this size.
+// ---------------------------------------------------------------------------
+template <int U>
+__global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ p, long n16,
+                                                     uint32_t* __restrict__ sink) {
+    const long G = (long)gridDim.x * 256;
+    uint32_t acc = 0;
+    for (long i0 = (long)blockIdx.x * 256 + threadIdx.x; i0 < n16; i0 += G * U) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = p[min(i0 + u * G, n16 - 1)];
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+hipError_t launch_stream_read(const void* p, size_t bytes, int unroll, int wgs, uint32_t* sink,
+                              hipStream_t st) {
+    const long n16 = (long)(bytes / 16);
+    if (n16 <= 0 || wgs <= 0) return hipErrorInvalidValue;
+    const auto* q = static_cast<const uint4*>(p);
+    switch (unroll) {
+        case 1: hipLaunchKernelGGL(k_stream_read<1>, dim3(wgs), dim3(256), 0, st, q, n16, sink); break;
+        case 2: hipLaunchKernelGGL(k_stream_read<2>, dim3(wgs), dim3(256), 0, st, q, n16, sink); break;
+        case 4: hipLaunchKernelGGL(k_stream_read<4>, dim3(wgs), dim3(256), 0, st, q, n16, sink); break;
+        case 8: hipLaunchKernelGGL(k_stream_read<8>, dim3(wgs), dim3(256), 0, st, q, n16, sink); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace axf

@@ -188,6 +188,18 @@ class Context:
         call("axf_hip_embed", self.handle, C.c_void_p(int(out)), qtype, C.c_void_p(int(W)), token,
              rows, cols)
 
+    def bench_read(self, bufs, nbytes: int, unroll: int, wgs: int, reps: int) -> float:
+        """Milliseconds for reps passes of a plain streaming read over bufs."""
+        arr = (C.c_void_p * len(bufs))(*[int(b) for b in bufs])
+        ms = C.c_float(0)
+        call("axf_hip_bench_read", self.handle, arr, len(bufs), C.c_size_t(nbytes), unroll, wgs,
+             reps, C.byref(ms))
+        return ms.value
+
+    def bench_set_eager(self, eager: bool) -> None:
+        """Benchmark helpers launch directly instead of replaying captured graphs."""
+        call("axf_hip_bench_set_eager", self.handle, 1 if eager else 0)
+
     def timer_start(self) -> None:
         call("axf_hip_timer_start", self.handle)
 

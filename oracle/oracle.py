@@ -102,6 +102,12 @@ def _load_ref() -> C.CDLL | None:
                                   C.POINTER(i32)], C.c_double),
         "ref_time_decode_step": ([vp, vp, vp, i32, i32, i32, i32, C.POINTER(i32),
                                   C.POINTER(i32)], C.c_double),
+        "ref_time_gemv_f32": ([i32, C.POINTER(vp), i32, i32, i32, vp, vp, i32, i32,
+                               C.POINTER(i32)], C.c_double),
+        "ref_time_gemm_q4k": ([C.POINTER(vp), i32, i32, i32, vp, i32, vp, i32, i32,
+                               C.POINTER(i32)], C.c_double),
+        "ref_time_head_argmax": ([C.POINTER(vp), i32, i32, i32, vp, vp, i32, i32, C.POINTER(i32),
+                                  C.POINTER(i32)], C.c_double),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -224,6 +230,55 @@ def ref_time_decode_gemv(qtype: int, W: np.ndarray, rows: int, cols: int, x: np.
     t = ref.ref_time_decode_gemv(qtype, arr, n_copies, rows, cols, _ptr(x), _ptr(y), iters,
                                  n_threads, C.byref(used))
     return t, used.value
+
+
+def _copies(W: np.ndarray, min_bytes: int):
+    n = max(2, -(-min_bytes // max(W.nbytes, 1)))
+    copies = [W] + [W.copy() for _ in range(n - 1)]
+    return copies, (C.c_void_p * n)(*[c.ctypes.data for c in copies]), n
+
+
+def ref_time_gemv_f32(qtype: int, W: np.ndarray, rows: int, cols: int, x: np.ndarray,
+                      iters: int, min_bytes: int = 640 << 20, n_threads: int = 0):
+    """Median seconds of the reference's fp32-activation GEMV (gemv_wt) over
+    weight copies rotated past min_bytes; (seconds, threads)."""
+    assert ref is not None, "oracle/_ref not built"
+    keep, arr, n = _copies(np.ascontiguousarray(W), min_bytes)
+    y = np.empty(rows, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    used = C.c_int(0)
+    t = ref.ref_time_gemv_f32(qtype, arr, n, rows, cols, _ptr(x), _ptr(y), iters, n_threads,
+                              C.byref(used))
+    del keep
+    return t, used.value
+
+
+def ref_time_gemm_q4k(W: np.ndarray, rows: int, cols: int, XQ8: np.ndarray, T: int, iters: int,
+                      min_bytes: int = 640 << 20, n_threads: int = 0):
+    """Median seconds of the reference's T-token Q4_K GEMM (gemm_wt_q8)."""
+    assert ref is not None, "oracle/_ref not built"
+    keep, arr, n = _copies(np.ascontiguousarray(W), min_bytes)
+    Y = np.empty(T * rows, np.float32)
+    XQ8 = np.ascontiguousarray(XQ8)
+    used = C.c_int(0)
+    t = ref.ref_time_gemm_q4k(arr, n, rows, cols, _ptr(XQ8), T, _ptr(Y), iters, n_threads,
+                              C.byref(used))
+    del keep
+    return t, used.value
+
+
+def ref_time_head_argmax(W: np.ndarray, rows: int, cols: int, x: np.ndarray, iters: int,
+                         min_bytes: int = 640 << 20, n_threads: int = 0):
+    """Median seconds of Q8_0 quantise + Q6_K head GEMV + greedy pick; (s, threads, argmax)."""
+    assert ref is not None, "oracle/_ref not built"
+    keep, arr, n = _copies(np.ascontiguousarray(W), min_bytes)
+    y = np.empty(rows, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    used, am = C.c_int(0), C.c_int(0)
+    t = ref.ref_time_head_argmax(arr, n, rows, cols, _ptr(x), _ptr(y), iters, n_threads,
+                                 C.byref(used), C.byref(am))
+    del keep
+    return t, used.value, am.value
 
 
 def ref_time_decode_step(model: "OracleModel", kv_k: np.ndarray, kv_v: np.ndarray, pos: int,

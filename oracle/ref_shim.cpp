@@ -167,6 +167,117 @@ double ref_time_decode_gemv(int qtype, const uint8_t* const* W_copies, int n_cop
 }
 
 // ---------------------------------------------------------------------------
+// CPU baselines of the other configurations, each with the reference's
+// dispatch on its ThreadPool (n_threads = min(16, nproc), pinned as above),
+// weights rotated over n_copies buffers; median seconds per call over `iters`
+// timed calls after 3 warm-ups.
+//   ref_time_gemv_f32: gemv_wt (llama_model.cpp:670-700) for Q4_K / Q6_K with
+//     fp32 activations: parallel_for over rows (>= 32) of gemv_q4k_avx2_range /
+//     gemv_q6k_avx2_range (config 1).
+//   ref_time_gemm_q4k: gemm_wt_q8's Q4_K branch (llama_model.cpp:837-858):
+//     parallel_for over rows (>= 32) of gemm_q4k_q8_{avxvnni,avx2}_range on T
+//     Q8_0 token rows already quantised (config 4).
+//   ref_time_head_argmax: the decode GEMV of ref_time_decode_gemv for a Q6_K
+//     head, then the greedy pick std::max_element (sample, :1466-1471)
+//     (config 2).
+// ---------------------------------------------------------------------------
+}  // extern "C"
+
+namespace {
+
+template <class F>
+double time_median(const uint8_t* const* W_copies, int n_copies, int iters, F&& one) {
+    for (int i = 0; i < 3; i++) one(W_copies[i % n_copies]);
+    std::vector<double> t((size_t)std::max(iters, 1));
+    for (int i = 0; i < iters; i++) {
+        const uint8_t* W = W_copies[(i + 3) % n_copies];
+        auto t0 = std::chrono::steady_clock::now();
+        one(W);
+        auto t1 = std::chrono::steady_clock::now();
+        t[i] = std::chrono::duration<double>(t1 - t0).count();
+    }
+    std::sort(t.begin(), t.begin() + iters);
+    return iters > 0 ? t[iters / 2] : 0.0;
+}
+
+struct PinnedPool {
+    cpu_set_t orig;
+    std::unique_ptr<axonforge::ThreadPool> pool;
+    explicit PinnedPool(int& n_threads) {
+        if (n_threads <= 0) n_threads = std::min(16, (int)std::thread::hardware_concurrency());
+        sched_getaffinity(0, sizeof(orig), &orig);
+        if (n_threads > 1) {
+            pool = std::make_unique<axonforge::ThreadPool>(n_threads - 1);
+            axonforge::ThreadPool::pin_caller(n_threads - 1);
+        }
+    }
+    ~PinnedPool() {
+        pool.reset();
+        sched_setaffinity(0, sizeof(orig), &orig);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+double ref_time_gemv_f32(int qtype, const uint8_t* const* W_copies, int n_copies, int rows,
+                         int cols, const float* x, float* y, int iters, int n_threads,
+                         int* threads_used) {
+    PinnedPool pp(n_threads);
+    if (threads_used) *threads_used = n_threads;
+    const bool q6 = (qtype == 14);
+    const size_t rb = (size_t)(cols / 256) * (q6 ? 210 : 144);
+    return time_median(W_copies, n_copies, iters, [&](const uint8_t* W) {
+        auto fn = [&](int s, int e) {
+            if (q6)
+                cx::gemv_q6k_avx2_range(y, W, x, s, e, cols, rb);
+            else
+                cx::gemv_q4k_avx2_range(y, W, x, s, e, cols, rb);
+        };
+        if (pp.pool && rows >= 32) pp.pool->parallel_for(rows, fn); else fn(0, rows);
+    });
+}
+
+double ref_time_gemm_q4k(const uint8_t* const* W_copies, int n_copies, int rows, int cols,
+                         const void* XQ8, int T, float* Y, int iters, int n_threads,
+                         int* threads_used) {
+    PinnedPool pp(n_threads);
+    if (threads_used) *threads_used = n_threads;
+    const size_t rb = (size_t)(cols / 256) * 144;
+    const bool vnni = cx::cpu_features().avxvnni;
+    auto* xq = static_cast<const block_q8_0*>(XQ8);
+    return time_median(W_copies, n_copies, iters, [&](const uint8_t* W) {
+        auto fn = [&](int s, int e) {
+            if (vnni)
+                cx::gemm_q4k_q8_avxvnni_range(Y, W, xq, rows, T, cols, rb, s, e);
+            else
+                cx::gemm_q4k_q8_avx2_range(Y, W, xq, rows, T, cols, rb, s, e);
+        };
+        if (pp.pool && rows >= 32) pp.pool->parallel_for(rows, fn); else fn(0, rows);
+    });
+}
+
+double ref_time_head_argmax(const uint8_t* const* W_copies, int n_copies, int rows, int cols,
+                            const float* x, float* y, int iters, int n_threads, int* threads_used,
+                            int* argmax) {
+    PinnedPool pp(n_threads);
+    if (threads_used) *threads_used = n_threads;
+    const size_t rb = (size_t)(cols / 256) * 210;
+    std::vector<block_q8_0> xq8((size_t)cols / 32);
+    int best = 0;
+    const double t = time_median(W_copies, n_copies, iters, [&](const uint8_t* W) {
+        cx::quantize_q8_avx2(xq8.data(), x, cols);
+        const block_q8_0* xq = xq8.data();
+        auto fn = [&](int s, int e) { cx::gemv_q6k_q8_avx2_range(y, W, xq, s, e, cols, rb); };
+        if (pp.pool && rows >= 32) pp.pool->parallel_for(rows, fn); else fn(0, rows);
+        best = (int)(std::max_element(y, y + rows) - y);
+    });
+    if (argmax) *argmax = best;
+    return t;
+}
+
+// ---------------------------------------------------------------------------
 // CPU baseline for the whole decode step: llama_forward_token
 // (llama_model.cpp:1207-1333) with the reference's dispatch — Q8_0 quantize,
 // r8 Q4_K GEMV (VNNI or AVX2 by CPUID) over 8-row groups, Q6_K 4-row GEMV,
@@ -280,6 +391,9 @@ extern "C" double ref_time_decode_step(const orc_model* m, float* kv_k, float* k
             gemv_wt_q8(q.data(), wq[l], xq, H * HD, E, pool.get(), vnni);
             gemv_wt_q8(k.data(), wk[l], xq, kve, E, pool.get(), vnni);
             gemv_wt_q8(v.data(), wv[l], xq, kve, E, pool.get(), vnni);
+            for (int i = 0; lw.bq && i < H * HD; i++) q[i] += lw.bq[i];
+            for (int i = 0; lw.bk && i < kve; i++) k[i] += lw.bk[i];
+            for (int i = 0; lw.bv && i < kve; i++) v[i] += lw.bv[i];
             orc_rope(q.data(), q.data(), pos, H, HD, rc.data(), rs.data());
             orc_rope(kc + (size_t)pos * kve, k.data(), pos, KVH, HD, rc.data(), rs.data());
             std::memcpy(vc + (size_t)pos * kve, v.data(), sizeof(float) * kve);
