@@ -134,7 +134,8 @@ def c4_sweep(ctx, Ms=(1, 2, 4, 8, 16, 32, 64)):
     res = [gemm_case(ctx, M) for M in Ms]
     for g4 in res:
         log(f"gemm q4k 11008x4096 M={g4['M']} (config 4): dot4 {g4['dot4_us']:.2f} us, "
-            f"mfma {g4['mfma_us']:.2f} us, auto {g4['auto_us']:.2f} us = {g4['GBs']:.0f} GB/s, "
+            f"mfma {g4['mfma_us']:.2f} us, stream {g4['stream_us']:.2f} us, "
+            f"auto {g4['auto_us']:.2f} us = {g4['GBs']:.0f} GB/s, "
             f"{g4['TOPs']:.2f} TOP/s")
     return res
 
@@ -177,7 +178,10 @@ def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL
     dY = ctx.alloc(M * rows * 4)
     alg = W.nbytes + M * (cols // 32 * 36) + 4 * M * rows
     res = {"M": M}
-    for name, path in (("dot4", 1), ("mfma", 2), ("auto", 0)):
+    paths = (("dot4", 1), ("mfma", 2), ("stream", 3), ("auto", 0))
+    if qtype != hip.AXF_TYPE_Q4_K:
+        paths = tuple(pp for pp in paths if pp[0] != "stream")
+    for name, path in paths:
         ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, 2, path, qtype)
         ms = ctx.bench_gemm(dY, bufs, xq, rows, M, cols, rb, reps, path, qtype)
         res[f"{name}_us"] = round(ms * 1000.0 / (reps * n_copies), 3)
@@ -423,6 +427,9 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true",
                     help="direct launches instead of captured-graph replay in every timing "
                          "(implied under rocprofv3); timings then include host launch gaps")
+    ap.add_argument("--gemm-ms", default="",
+                    help="--only gemm: comma-separated token counts (default 1,2,4,8,16,32,64; "
+                         "given: the Q4_K sweep alone)")
     ap.add_argument("--skip-c4", action="store_true",
                     help="leave out the config-3 layer and config-4 GEMM timings (shorter profiling runs)")
     ap.add_argument("--no-e2e", action="store_true",
@@ -473,8 +480,9 @@ def main() -> int:
         print(json.dumps({"c3_qwen25_3b_layer_decode": c3_run(ctx, args.warmup, args.steps)}))
         return 0
     if args.only == "gemm":  # config 4 sweep alone (not a bench line)
-        print(json.dumps({"c4_q4k_q8_gemm_11008x4096": c4_sweep(ctx),
-                          "q6k_q8_gemm_4096x11008": q6k_sweep(ctx)}))
+        ms = tuple(int(m) for m in args.gemm_ms.split(",")) if args.gemm_ms else None
+        print(json.dumps({"c4_q4k_q8_gemm_11008x4096": c4_sweep(ctx, *(ms and (ms,) or ())),
+                          "q6k_q8_gemm_4096x11008": None if ms else q6k_sweep(ctx)}))
         return 0
     if args.only == "prefill":  # config 5 prefill + end to end alone (not a bench line)
         hp = Hparams(n_ctx=args.ctx, **LLAMA2_7B)

@@ -116,9 +116,12 @@ int axf_hip_gemm_q4k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, 
 int axf_hip_gemm_q6k_q8(axf_ctx* ctx, float* Y, const void* W, const void* XQ8, int rows,
                         int T, int cols, size_t row_bytes);
 /* The same GEMMs with the kernel chosen explicitly (no reference counterpart;
- * for tests and measurement): path 0 automatic (matrix cores from 8 tokens up),
- * 1 the dot4 kernel, 2 the matrix-core (int8 MFMA) kernel.  Results of the two
- * kernels differ only in float summation order.  Q6_K takes the matrix cores
+ * for tests and measurement): path 0 automatic (1 below 8 tokens, 3 up to 64,
+ * 2 above), 1 the dot4 kernel, 2 the matrix-core (int8 MFMA) kernel with an
+ * LDS ring, 3 the int8 MFMA kernel with the weights loaded straight into
+ * registers and split-K partial sums (Q4_K, T <= 64, 16-byte aligned W, XQ8
+ * and row_bytes; otherwise as 2).  Results of the kernels differ only in float
+ * summation order.  Q6_K takes the matrix cores
  * only where the last row's last block ends on a 16-byte boundary, under 2 GiB
  * from W (true of a 16-byte aligned W with row_bytes = cols / 256 * 210 and
  * rows * cols / 256 a multiple of 8); other Q6_K matrices take the dot4 kernel
@@ -129,12 +132,13 @@ int axf_hip_gemm_q6k_q8_path(axf_ctx* ctx, float* Y, const void* W, const void* 
                              int T, int cols, size_t row_bytes, int path);
 /* As axf_hip_gemm_q4k_q8, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  No counterpart in the reference.  The matrix-core path's
- * activation re-layout goes to a fixed 8 MiB device array inside the library
- * (one per GPU, held until the process ends) instead of the context's
- * hipMalloc'd scratch; this call allocates nothing.  Token counts whose
- * re-layout exceeds 8 MiB (T > 320 at cols 11008, T > 896 at cols 4096) are
- * AXF_ERR_INVALID_ARG.  Every call on one GPU shares the array: calls whose
+ * hipMalloc).  No counterpart in the reference.  The matrix-core paths'
+ * scratch (activation re-layout, or split-K partials) goes to a fixed 8 MiB
+ * device array inside the library (one per GPU, held until the process ends)
+ * instead of the context's hipMalloc'd scratch; this call allocates nothing.
+ * Where path 0's kernel needs more than 8 MiB the LDS-ring kernel (path 2)
+ * runs; token counts whose re-layout exceeds 8 MiB even there (T > 320 at
+ * cols 11008, T > 896 at cols 4096) are AXF_ERR_INVALID_ARG.  Every call on one GPU shares the array: calls whose
  * kernels overlap on one GPU (other streams or contexts) race. */
 int axf_hip_gemm_q4k_q8_noalloc(axf_ctx* ctx, float* Y, const void* W, const void* XQ8,
                                 int rows, int T, int cols, size_t row_bytes);

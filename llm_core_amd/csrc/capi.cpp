@@ -266,11 +266,12 @@ static int do_gemm(axf_ctx* ctx, const char* fn, int qtype, float* Y, const void
                    const void* XQ8, int rows, int T, int cols, size_t row_bytes, int path) {
     AXF_CHECK_CTX(ctx);
     AXF_REQUIRE(T >= 0, "negative T");
-    AXF_REQUIRE(path >= 0 && path <= 2, "path must be 0 (auto), 1 (dot4) or 2 (matrix cores)");
+    AXF_REQUIRE(path >= 0 && path <= 3,
+                "path must be 0 (auto), 1 (dot4), 2 (matrix cores) or 3 (matrix cores, streamed)");
     int rc = check_gemv(fn, qtype, W, XQ8, Y, rows, cols, row_bytes, false);
     if (rc) return rc;
     if (rows == 0 || cols == 0 || T == 0) return AXF_OK;
-    const size_t sb = gemm_scratch_bytes(qtype, (GemmPath)path, T, cols / QK_K);
+    const size_t sb = gemm_scratch_bytes(qtype, (GemmPath)path, T, cols / QK_K, rows);
     void* scratch = nullptr;
     if (sb) {
         rc = ctx_scratch(ctx, sb, &scratch);
@@ -658,12 +659,13 @@ int axf_hip_bench_gemm(axf_ctx* ctx, int qtype, float* Y, const void* const* W_l
     AXF_REQUIRE(W_list && n_w > 0 && reps > 0 && ms && T > 0 && rows > 0 && cols > 0,
                 "bad arguments");
     AXF_REQUIRE(qtype == AXF_TYPE_Q4_K || qtype == AXF_TYPE_Q6_K, "qtype must be Q4_K or Q6_K");
-    AXF_REQUIRE(path >= 0 && path <= 2, "path must be 0 (auto), 1 (dot4) or 2 (matrix cores)");
+    AXF_REQUIRE(path >= 0 && path <= 3,
+                "path must be 0 (auto), 1 (dot4), 2 (matrix cores) or 3 (matrix cores, streamed)");
     for (int i = 0; i < n_w; i++) {
         int rc = check_gemv(__func__, qtype, W_list[i], XQ8, Y, rows, cols, row_bytes, false);
         if (rc) return rc;
     }
-    const size_t sb = gemm_scratch_bytes(qtype, (GemmPath)path, T, cols / QK_K);
+    const size_t sb = gemm_scratch_bytes(qtype, (GemmPath)path, T, cols / QK_K, rows);
     void* scratch = nullptr;
     if (sb) {  // allocated before capture
         int rc = ctx_scratch(ctx, sb, &scratch);

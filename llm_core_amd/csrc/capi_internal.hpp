@@ -68,13 +68,18 @@ hipError_t launch_qgemv2(QAct act, QGemvArgs a, int threads, hipStream_t st);
 int qgemv_threads(QAct act, int nb);  // default workgroup size for launch_qgemv
 bool qgemv_threads_ok(QAct act, int nb, int threads);
 int qgemv_rows_per_wg(int nb, int threads);
-// Q4_K / Q6_K x Q8_0 GEMM, Y token-major.  Auto picks the matrix-core kernel
-// from kGemmMfmaMinT tokens up, the dot4 kernel below.  The matrix-core path
-// needs gemm_scratch_bytes() of device scratch (activation re-layout).
-enum class GemmPath { Auto = 0, Dot4 = 1, Mfma = 2 };
+// Q4_K / Q6_K x Q8_0 GEMM, Y token-major.  Auto: the dot4 kernel below
+// kGemmMfmaMinT tokens, Stream up to kGemmStreamMaxT, Mfma above.  The
+// matrix-core paths need gemm_scratch_bytes() of device scratch (activation
+// re-layout, or Stream's split-K partials).  Stream: the Q4_K matrix-core
+// kernel with the weights loaded straight into registers (T <= 64; it needs
+// 16-byte-aligned W, XQ8 and row_bytes and otherwise runs as Mfma; Q6_K
+// weights take Mfma).
+enum class GemmPath { Auto = 0, Dot4 = 1, Mfma = 2, Stream = 3 };
 constexpr int kGemmMfmaMinT = 8;
+constexpr int kGemmStreamMaxT = 64;
 GemmPath gemm_resolve(GemmPath path, int T);
-size_t gemm_scratch_bytes(int qtype, GemmPath path, int T, int nb);
+size_t gemm_scratch_bytes(int qtype, GemmPath path, int T, int nb, int rows);
 hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
                               long row_bytes, GemmPath path, void* scratch, hipStream_t st);
 // Q6_K: the matrix-core kernel runs only when gemm_mfma_q6k_ok (the last
@@ -84,6 +89,10 @@ hipError_t launch_gemm_q6k_q8(float* Y, const void* W, const void* XQ8, int rows
                               long row_bytes, GemmPath path, void* scratch, hipStream_t st);
 // the matrix-core kernels (kernels/gemm_mfma.hip)
 size_t gemm_mfma_scratch_bytes(int T, int nb);
+bool gemm_stream_q4k_ok(int T, int nb, int rows);
+size_t gemm_stream_scratch_bytes(int T, int nb, int rows);
+hipError_t launch_gemm_stream_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
+                                     int nb, long row_bytes, void* scratch, hipStream_t st);
 hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
                                    int nb, long row_bytes, void* scratch, hipStream_t st);
 size_t gemm_mfma_q6k_scratch_bytes(int T, int nb);

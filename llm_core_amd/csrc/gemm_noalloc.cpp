@@ -1,9 +1,10 @@
 // gemm_noalloc.cpp — axf_hip_gemm_q4k_q8_noalloc: the Q4_K x Q8_0 small-M GEMM
 // of axf_hip_gemm_q4k_q8 for callers that cannot allocate device memory.
 //
-// The matrix-core path re-lays the Q8_0 activations into a scratch buffer
-// before the GEMM (k_gemm_prep / k_gemm_prep16 write every byte of it,
-// token padding included, so nothing needs clearing).  axf_hip_gemm_q4k_q8
+// The matrix-core paths need a scratch buffer: the LDS-ring kernel's re-laid
+// Q8_0 activations (k_gemm_prep / k_gemm_prep16 write every byte of it, token
+// padding included), or the register-weights kernel's split-K partial sums
+// (every element written before it is summed); nothing needs clearing.  axf_hip_gemm_q4k_q8
 // takes that buffer from the context, growing it with hipMalloc.  Here it
 // is `scratch`, a file-scope device array of kNoAllocScratchBytes: each GPU
 // the library runs on holds its own copy until the process ends.  Its device
@@ -61,7 +62,13 @@ extern "C" int axf_hip_gemm_q4k_q8_noalloc(axf_ctx* ctx, float* Y, const void* W
     int rc = check_gemv(fn, AXF_TYPE_Q4_K, W, XQ8, Y, rows, cols, row_bytes, false);
     if (rc) return rc;
     if (rows == 0 || cols == 0 || T == 0) return AXF_OK;
-    const size_t need = gemm_scratch_bytes(AXF_TYPE_Q4_K, GemmPath::Auto, T, cols / QK_K);
+    // the automatic choice, or the LDS-ring kernel where that needs less scratch
+    GemmPath path = GemmPath::Auto;
+    size_t need = gemm_scratch_bytes(AXF_TYPE_Q4_K, path, T, cols / QK_K, rows);
+    if (need > kNoAllocScratchBytes) {
+        path = GemmPath::Mfma;
+        need = gemm_scratch_bytes(AXF_TYPE_Q4_K, path, T, cols / QK_K, rows);
+    }
     if (need > kNoAllocScratchBytes)
         return fail(AXF_ERR_INVALID_ARG,
                     std::string(fn) + ": T = " + std::to_string(T) + " tokens at cols = " +
@@ -73,8 +80,8 @@ extern "C" int axf_hip_gemm_q4k_q8_noalloc(axf_ctx* ctx, float* Y, const void* W
         rc = scratch_address(ctx->device, &sp);
         if (rc) return rc;
     }
-    hipError_t e = launch_gemm_q4k_q8(Y, W, XQ8, rows, T, cols / QK_K, (long)row_bytes,
-                                      GemmPath::Auto, sp, ctx->stream);
+    hipError_t e = launch_gemm_q4k_q8(Y, W, XQ8, rows, T, cols / QK_K, (long)row_bytes, path,
+                                      sp, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, fn);
     return AXF_OK;
 }

@@ -501,10 +501,17 @@ int prefill_alloc(axf_llama* m) {
     }
     LL_TRY(dalloc(m, C * (kmax > qo ? kmax : qo) / 32 * Q8_0_BYTES, &p));
     m->pf_q8 = static_cast<uint8_t*>(p);
-    const size_t g4 = gemm_scratch_bytes(AXF_TYPE_Q4_K, GemmPath::Auto, cap, kmax / QK_K);
-    const size_t g6 = gemm_scratch_bytes(AXF_TYPE_Q6_K, GemmPath::Auto, cap, kmax / QK_K);
-    const size_t gs = g4 > g6 ? g4 : g6;
-    LL_TRY(dalloc(m, gs > 16 ? gs : 16, &p));
+    // GEMM scratch for every chunk size up to cap (the Auto path differs by T)
+    int rmax = qo + kvo > 2 * FD ? qo + kvo : 2 * FD;
+    if (E > rmax) rmax = E;
+    size_t gs = 16;
+    for (int t : {cap, 64, 16, 8})
+        if (t <= cap)
+            for (int qt : {AXF_TYPE_Q4_K, AXF_TYPE_Q6_K}) {
+                const size_t b = gemm_scratch_bytes(qt, GemmPath::Auto, t, kmax / QK_K, rmax);
+                if (b > gs) gs = b;
+            }
+    LL_TRY(dalloc(m, gs, &p));
     m->pf_gemm = static_cast<uint8_t*>(p);
     m->pf_cap = cap;
     return AXF_OK;

@@ -367,6 +367,200 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_mfma_q4k(
 }
 
 // ---------------------------------------------------------------------------
+// Q4_K x Q8_0 for a few tokens (T <= 64), weights loaded straight into
+// registers and no activation re-layout kernel.
+//
+// Measured on the 25.4 MB 11008x4096 matrix: 16-byte loads that cover 64
+// contiguous bytes of each of 16 rows run at the plain-read rate (5.7-5.9 us),
+// loads of 8 bytes per lane in the MFMA operand layout do not (8.5 us), and
+// every extra vector-memory instruction per wave and block (activation
+// fragments, dx) costs about 0.35 us.  So:
+//   * a workgroup owns RT row tiles (wave w: 16 rows) and a K range of KB
+//     blocks (split-K over gridDim.y = ceil(nb / KB) workgroups);
+//   * lane (col, g) loads its row's block header and qs bytes 32g..32g+31
+//     (chunk g: sub-blocks 2g and 2g+1) as 16-byte loads, all up front;
+//     two rounds of v_permlane32_swap / v_permlane16_swap turn "lane g holds
+//     chunk g" into "lane g holds bytes 8g..8g+7 of every chunk", the B
+//     operand layout of v_mfma_i32_16x16x32_i8;
+//   * the workgroup stages its K range of the activations once, 16 tokens at
+//     a time, into LDS (per token a contiguous run of Q8_0 records, copied by
+//     16-byte loads; one pad chunk per token spreads the tokens over the
+//     banks), then derives dx and dx*bsum per (record, token) from it;
+//   * per sub-block: one int8 MFMA (A = token x from LDS, B = the nibbles),
+//     S*sc by a 24-bit multiply, dx by an fp32 FMA, d per block, the min term
+//     by two v_mfma_f32_16x16x4f32 per block, as in the ring kernel above;
+//   * with gridDim.y > 1 each workgroup writes its partial tiles to scratch,
+//     and the last of a row group's workgroups to finish (a counter per row
+//     group, reset by that workgroup) sums the partials in K order: results
+//     are deterministic whatever the finishing order.
+// ---------------------------------------------------------------------------
+template <int RT, int KB, int TT>
+struct Rx {
+    static constexpr int CPT = KB * 18;           // 16-B chunks of one token's K range
+    static constexpr int TSTR = CPT + 1;          // LDS token stride in chunks (one pad)
+    static constexpr int XCH = kTile * TT * TSTR; // chunks staged (all token tiles)
+    static constexpr int XP = (XCH + 63) / 64;    // 1 KiB pieces (64 lanes x 16 B)
+    static constexpr int XPW = (XP + RT - 1) / RT;
+    static constexpr int NS = 8 * KB;             // Q8_0 records per token
+};
+
+template <int RT, int KB, int TT>
+__global__ __launch_bounds__(RT * 64) void k_gemm_q4k_rx(
+    float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ8,
+    float* __restrict__ part, int rows, int nb, long row_bytes, int T) {
+    using G = Rx<RT, KB, TT>;
+    __shared__ __align__(16) uint8_t xl[G::XP * 1024];
+    __shared__ __align__(16) float dxl[TT * G::NS * kTile];  // [tile][record][token]
+    __shared__ float gxl[TT * G::NS * kTile];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, g = lane >> 4;
+    const int S = (int)gridDim.y, ks = (int)blockIdx.y, kb0 = ks * KB;
+    const size_t tok_bytes = (size_t)nb * 8 * Q8_0_BYTES;
+    // chunks of a token row from record 8*kb0 on (the last K range may be short)
+    const int cend = min(G::CPT, (nb - kb0) * 18) - 1;
+    const int row0 = ((int)blockIdx.x * RT + wave) * kTile;
+    const int o = row0 + col;
+
+    // activations: slot (u, j) with u = 16*tile + t, j < CPT: chunk j of
+    // token u's K range (tokens past T repeat token T-1).  Issued before the
+    // weights, so that they are waited for first.
+    uint4 xr[G::XPW];
+#pragma unroll
+    for (int k = 0; k < G::XPW; k++) {
+        const int piece = wave + RT * k;
+        if (piece < G::XP) {
+            const int slot = piece * 64 + lane;
+            const int u = min(slot / G::TSTR, kTile * TT - 1);
+            const int j = min(slot - (slot / G::TSTR) * G::TSTR, cend);
+            const int tok = min(u, T - 1);
+            xr[k] = ld16(XQ8 + (size_t)tok * tok_bytes + (size_t)kb0 * 8 * Q8_0_BYTES + 16 * j);
+        }
+    }
+    // weights: row o (clamped), blocks kb0.. (clamped; blocks past nb are
+    // computed on block nb-1 and their contribution dropped)
+    const uint8_t* wr = W + (size_t)min(o, rows - 1) * row_bytes;
+    uint4 hdr[KB];
+    uint32_t P[KB][4][2];
+#pragma unroll
+    for (int b = 0; b < KB; b++) {
+        const uint8_t* blk = wr + (size_t)min(kb0 + b, nb - 1) * Q4K_BYTES;
+        hdr[b] = ld16(blk);
+        const uint4 qa = ld16(blk + 16 + 32 * g), qb = ld16(blk + 32 + 32 * g);
+        P[b][0][0] = qa.x; P[b][0][1] = qa.y; P[b][1][0] = qa.z; P[b][1][1] = qa.w;
+        P[b][2][0] = qb.x; P[b][2][1] = qb.y; P[b][3][0] = qb.z; P[b][3][1] = qb.w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < G::XPW; k++) {
+        const int piece = wave + RT * k;
+        if (piece < G::XP) *reinterpret_cast<uint4*>(xl + piece * 1024 + lane * 16) = xr[k];
+    }
+    __syncthreads();
+    // dx and dx*bsum per (tile, record, token)
+    for (int i = threadIdx.x; i < TT * G::NS * kTile; i += RT * 64) {
+        const int t = i & (kTile - 1), sr = (i >> 4) % G::NS, w = (i >> 4) / G::NS;
+        const uint32_t* rec = reinterpret_cast<const uint32_t*>(
+            xl + (kTile * w + t) * G::TSTR * 16 + sr * Q8_0_BYTES);
+        const float d = __uint_as_float(rec[0]);
+        int sum = 0;
+#pragma unroll
+        for (int k = 1; k <= 8; k++) sum = dot4((int)rec[k], 0x01010101, sum);
+        dxl[i] = d;
+        gxl[i] = d * (float)sum;
+    }
+    __syncthreads();
+
+    const v4i_t zi = {0, 0, 0, 0};
+    v4f_t acc[TT], macc[TT];
+#pragma unroll
+    for (int w = 0; w < TT; w++) acc[w] = macc[w] = v4f_t{0.f, 0.f, 0.f, 0.f};
+    // One block per iteration (a runtime loop keeps the compiler from
+    // scheduling all blocks' operands at once); block b's weights are in
+    // P[0] / hdr[0], the later blocks' move down one slot per iteration.
+#pragma unroll 1
+    for (int b = 0; b < KB; b++) {
+        // lane g holds chunk g (pieces 0..3 = bytes 8j..8j+7 of qs 32g..32g+31);
+        // afterwards Q[c] = bytes 8g..8g+7 of chunk c
+        uint32_t Q[4][2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const auto r02 = __builtin_amdgcn_permlane32_swap(P[0][0][e], P[0][2][e], false, false);
+            const auto r13 = __builtin_amdgcn_permlane32_swap(P[0][1][e], P[0][3][e], false, false);
+            const auto r01 = __builtin_amdgcn_permlane16_swap(r02[0], r13[0], false, false);
+            const auto r23 = __builtin_amdgcn_permlane16_swap(r02[1], r13[1], false, false);
+            Q[0][e] = r01[0]; Q[1][e] = r01[1];
+            Q[2][e] = r23[0]; Q[3][e] = r23[1];
+        }
+        const uint4 h = hdr[0];
+        const bool lv = kb0 + b < nb;
+#pragma unroll
+        for (int k = 0; k + 1 < KB; k++) {
+            hdr[k] = hdr[k + 1];
+#pragma unroll
+            for (int c = 0; c < 4; c++) { P[k][c][0] = P[k + 1][c][0]; P[k][c][1] = P[k + 1][c][1]; }
+        }
+        const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+        const uint32_t sc03 = h.y & 0x3f3f3f3fu;
+        const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+        const uint32_t m03 = h.z & 0x3f3f3f3fu;
+        const uint32_t m47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+        const float am0 = dmin * (float)((m03 >> (8 * g)) & 0xffu);
+        const float am1 = dmin * (float)((m47 >> (8 * g)) & 0xffu);
+#pragma unroll
+        for (int w = 0; w < TT; w++) {
+            const uint8_t* xt = xl + (kTile * w + col) * G::TSTR * 16 + 4 + 8 * g + 8 * b * Q8_0_BYTES;
+            const float* dw = dxl + (w * G::NS + 8 * b) * kTile;
+            const float* gw = gxl + (w * G::NS + 8 * b) * kTile;
+            v4f_t accb = v4f_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sb = 0; sb < 8; sb++) {
+                const int c = sb >> 1, sh = (sb & 1) * 4;
+                const long bw = pack2((Q[c][0] >> sh) & 0x0f0f0f0fu, (Q[c][1] >> sh) & 0x0f0f0f0fu);
+                const uint32_t* xa = reinterpret_cast<const uint32_t*>(xt + sb * Q8_0_BYTES);
+                const v4i_t cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(pack2(xa[0], xa[1]), bw, zi, 0, 0, 0);
+                const v4f_t dx = *reinterpret_cast<const v4f_t*>(dw + sb * kTile + 4 * g);
+                const int scv = (int)(((sb < 4 ? sc03 : sc47) >> (8 * (sb & 3))) & 0xffu);
+                // |S| < 2^17 and sc < 64: the 24-bit multiply is exact
+                accb[0] = fmaf((float)__mul24(cc[0], scv), dx[0], accb[0]);
+                accb[1] = fmaf((float)__mul24(cc[1], scv), dx[1], accb[1]);
+                accb[2] = fmaf((float)__mul24(cc[2], scv), dx[2], accb[2]);
+                accb[3] = fmaf((float)__mul24(cc[3], scv), dx[3], accb[3]);
+            }
+            v4f_t a2 = acc[w];
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) a2[ii] = fmaf(d, accb[ii], a2[ii]);
+            v4f_t m2 = __builtin_amdgcn_mfma_f32_16x16x4f32(gw[g * kTile + col], am0, macc[w], 0, 0, 0);
+            m2 = __builtin_amdgcn_mfma_f32_16x16x4f32(gw[(4 + g) * kTile + col], am1, m2, 0, 0, 0);
+            acc[w] = lv ? a2 : acc[w];
+            macc[w] = lv ? m2 : macc[w];
+        }
+    }
+    if (o < rows) {
+        float* dst = S == 1 ? Y : part + (size_t)ks * T * rows;
+#pragma unroll
+        for (int w = 0; w < TT; w++) {
+            const v4f_t v = acc[w] - macc[w];
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) {
+                const int tok = kTile * w + 4 * g + ii;
+                if (tok < T) dst[(size_t)tok * rows + o] = v[ii];
+            }
+        }
+    }
+}
+
+// Y[t][o] = sum over k = 0..S-1, in that order, of part[k][t][o]
+__global__ __launch_bounds__(256) void k_gemm_splitk_sum(float* __restrict__ Y,
+                                                         const float* __restrict__ part,
+                                                         int n, int S) {
+    const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (i >= n) return;
+    float sum = part[i];
+    for (int k = 1; k < S; k++) sum += part[(size_t)k * n + i];
+    Y[i] = sum;
+}
+
+// ---------------------------------------------------------------------------
 // Q4_K x Q8_0 for wide token tiles on the fp16 matrix cores, the same sums
 // with the 6-bit sub-block scale folded into the weight operand:
 //   A (weight rows) = q*sc as fp16, B (tokens) = the int8 values as fp16.
@@ -1042,6 +1236,52 @@ size_t gemm_mfma_scratch_bytes(int T, int nb) {
     }
     const size_t tp = (size_t)padded_tokens(T, pick_mfma(T, nb));
     return (size_t)nb * 8 * tp * (32 + 4 + 4);
+}
+
+// Register-weights kernel (k_gemm_q4k_rx): 4 row tiles per workgroup; K
+// ranges of 4 blocks for up to 16 tokens, 2 blocks for up to 64 (the LDS holds
+// all token tiles of a K range).
+constexpr int kRxRT = 4;
+
+static int rx_kb(int T) { return T <= 16 ? 4 : 2; }
+static int rx_row_groups(int rows) { return (rows + kTile * kRxRT - 1) / (kTile * kRxRT); }
+static int rx_splits(int T, int nb) { return (nb + rx_kb(T) - 1) / rx_kb(T); }
+
+bool gemm_stream_q4k_ok(int T, int nb, int rows) {
+    return T >= 1 && T <= kGemmStreamMaxT && nb >= 1 && rows >= 1 &&
+           (size_t)T * rows < ((size_t)1 << 31);
+}
+
+size_t gemm_stream_scratch_bytes(int T, int nb, int rows) {
+    if (!gemm_stream_q4k_ok(T, nb, rows) || rx_splits(T, nb) == 1) return 0;
+    return (size_t)rx_splits(T, nb) * T * rows * sizeof(float);
+}
+
+hipError_t launch_gemm_stream_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
+                                     int nb, long row_bytes, void* scratch, hipStream_t st) {
+    if (!gemm_stream_q4k_ok(T, nb, rows)) return hipErrorInvalidValue;
+    // 16-byte loads of weights and activations
+    if (((uintptr_t)W | (uintptr_t)XQ8 | (uintptr_t)row_bytes) & 15) return hipErrorInvalidValue;
+    const int S = rx_splits(T, nb);
+    if (S > 1 && scratch == nullptr) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)rx_row_groups(rows), (unsigned)rx_splits(T, nb));
+    const auto* w = static_cast<const uint8_t*>(W);
+    const auto* x = static_cast<const uint8_t*>(XQ8);
+    auto* pt = static_cast<float*>(scratch);
+    const int TT = (T + kTile - 1) / kTile;
+    if (TT == 1)
+        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, 4, 1>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
+    else if (TT == 2)
+        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, 2, 2>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
+    else if (TT == 3)
+        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, 2, 3>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
+    else
+        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, 2, 4>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
+    if (S > 1) {
+        const int n = T * rows;
+        hipLaunchKernelGGL(k_gemm_splitk_sum, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, Y, pt, n, S);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,

@@ -1285,18 +1285,30 @@ static hipError_t launch_gemm6_dot4(float* Y, const void* W, const void* XQ8, in
 
 GemmPath gemm_resolve(GemmPath path, int T) {
     if (path != GemmPath::Auto) return path;
-    return T >= kGemmMfmaMinT ? GemmPath::Mfma : GemmPath::Dot4;
+    if (T < kGemmMfmaMinT) return GemmPath::Dot4;
+    return T <= kGemmStreamMaxT ? GemmPath::Stream : GemmPath::Mfma;
 }
 
-size_t gemm_scratch_bytes(int qtype, GemmPath path, int T, int nb) {
-    if (gemm_resolve(path, T) != GemmPath::Mfma) return 0;
-    return qtype == AXF_TYPE_Q6_K ? gemm_mfma_q6k_scratch_bytes(T, nb)
-                                  : gemm_mfma_scratch_bytes(T, nb);
+size_t gemm_scratch_bytes(int qtype, GemmPath path, int T, int nb, int rows) {
+    const GemmPath p = gemm_resolve(path, T);
+    if (p == GemmPath::Dot4) return 0;
+    if (qtype == AXF_TYPE_Q6_K) return gemm_mfma_q6k_scratch_bytes(T, nb);
+    const size_t mf = gemm_mfma_scratch_bytes(T, nb);
+    if (p == GemmPath::Stream && gemm_stream_q4k_ok(T, nb, rows)) {
+        // room for the Mfma fallback (unaligned operands) as well
+        const size_t sb = gemm_stream_scratch_bytes(T, nb, rows);
+        return sb > mf ? sb : mf;
+    }
+    return mf;
 }
 
 hipError_t launch_gemm_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T, int nb,
                               long row_bytes, GemmPath path, void* scratch, hipStream_t st) {
-    if (gemm_resolve(path, T) == GemmPath::Mfma)
+    const GemmPath p = gemm_resolve(path, T);
+    if (p == GemmPath::Stream && gemm_stream_q4k_ok(T, nb, rows) &&
+        (((uintptr_t)W | (uintptr_t)XQ8 | (uintptr_t)row_bytes) & 15) == 0)
+        return launch_gemm_stream_q4k_q8(Y, W, XQ8, rows, T, nb, row_bytes, scratch, st);
+    if (p != GemmPath::Dot4)
         return launch_gemm_mfma_q4k_q8(Y, W, XQ8, rows, T, nb, row_bytes, scratch, st);
     return launch_gemm_dot4(Y, W, XQ8, rows, T, nb, row_bytes, st);
 }
@@ -1305,7 +1317,7 @@ hipError_t launch_gemm_q6k_q8(float* Y, const void* W, const void* XQ8, int rows
                               long row_bytes, GemmPath path, void* scratch, hipStream_t st) {
     // the matrix-core kernel copies 16-byte-aligned spans of the 2-byte-aligned
     // blocks: it needs a last block that ends on a 16-byte boundary (and < 2 GiB)
-    if (gemm_resolve(path, T) == GemmPath::Mfma && gemm_mfma_q6k_ok(W, rows, nb, row_bytes))
+    if (gemm_resolve(path, T) != GemmPath::Dot4 && gemm_mfma_q6k_ok(W, rows, nb, row_bytes))
         return launch_gemm_mfma_q6k_q8(Y, W, XQ8, rows, T, nb, row_bytes, scratch, st);
     return launch_gemm6_dot4(Y, W, XQ8, rows, T, nb, row_bytes, st);
 }

@@ -127,7 +127,8 @@ class Context:
 
     def gemm_q4k_q8(self, Y: int, W: int, XQ8: int, rows: int, T: int, cols: int, rb: int,
                     path: int | None = None) -> None:
-        """Token-major Q4_K x Q8_0 GEMM; path None = automatic, 1 dot4, 2 matrix cores."""
+        """Token-major Q4_K x Q8_0 GEMM; path None = automatic, 1 dot4, 2 matrix cores
+        (LDS ring), 3 matrix cores with the weights streamed into registers."""
         if path is None:
             call("axf_hip_gemm_q4k_q8", self.handle, C.c_void_p(int(Y)), C.c_void_p(int(W)),
                  C.c_void_p(int(XQ8)), rows, T, cols, C.c_size_t(rb))
