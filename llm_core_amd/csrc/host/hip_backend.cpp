@@ -13,10 +13,26 @@
 #include <utility>
 
 #include "../capi_internal.hpp"
+
+// Interface switch.  In this tree the plugin interface comes from
+// axf_backend.hpp (namespace axf).  Built inside the reference tree, define
+// AXF_AXONFORGE_HEADERS: the interface then comes from its own
+// include/axonforge/backend.hpp (namespace axonforge, DeviceType::HIP added
+// to its common.hpp), and the core types below (Tensor, storage,
+// BackendRegistry) are the reference's own definitions.
+#if defined(AXF_AXONFORGE_HEADERS)
+#include "axonforge/backend.hpp"
+namespace axf_api = axonforge;
+#else
 #include "axf_backend.hpp"
+namespace axf_api = axf;
+#endif
 
 namespace axf {
 
+using namespace axf_api;
+
+#if !defined(AXF_AXONFORGE_HEADERS)
 // ---- core types ----------------------------------------------------------
 
 size_t tensor_nbytes(DType dtype, int64_t numel) {
@@ -107,6 +123,7 @@ std::vector<std::string> BackendRegistry::available_backends() const {
     for (const auto& kv : factories_) ids.push_back(kv.first);
     return ids;
 }
+#endif  // !AXF_AXONFORGE_HEADERS
 
 // ---- HIP backend ---------------------------------------------------------
 
@@ -130,7 +147,7 @@ public:
     void* data() noexcept override { return ptr_; }
     const void* data() const noexcept override { return ptr_; }
     size_t byte_size() const noexcept override { return bytes_; }
-    DeviceId device() const noexcept override { return DeviceId::hip(ctx_->device); }
+    DeviceId device() const noexcept override { return DeviceId{DeviceType::HIP, ctx_->device}; }
 
 private:
     axf_ctx* ctx_;
@@ -311,7 +328,7 @@ public:
     ~HipBackend() override { finalize(); }
 
     std::string_view name() const noexcept override { return "hip"; }
-    DeviceId device_id() const noexcept override { return DeviceId::hip(0); }
+    DeviceId device_id() const noexcept override { return DeviceId{DeviceType::HIP, 0}; }
 
     bool initialize() override {
         if (ctx_) return true;
@@ -404,6 +421,6 @@ private:
 }  // namespace axf
 
 [[gnu::constructor]] static void axf_register_hip_backend() {
-    axf::BackendRegistry::instance().register_backend(
-        "hip", []() -> std::unique_ptr<axf::IBackend> { return std::make_unique<axf::HipBackend>(); });
+    axf_api::BackendRegistry::instance().register_backend(
+        "hip", []() -> std::unique_ptr<axf_api::IBackend> { return std::make_unique<axf::HipBackend>(); });
 }
