@@ -203,6 +203,8 @@ def read_probe(ctx, nbytes, n_copies, reps=40):
     for b in bufs:  # contents do not matter; make them defined
         ctx.write(b, np.zeros(16, np.uint8))
     seq = bufs * GEMV_ROUNDS
+    if under_profiler():  # counters and traces need a few dispatches per shape, not timings
+        reps = 1
     best, sweep = None, []
     one_each = -(-nbytes // (16 * 256))  # workgroups giving one vector per thread
     for unroll in (1, 2, 4, 8):
@@ -589,7 +591,11 @@ def main() -> int:
         result = dict(ms_step=ms_step, tok_s=tok_s, w_bytes=w_bytes, kv_bytes=kv_bytes)
         # config 5 end to end: batched prefill of a 512-token prompt, then 128
         # greedy tokens (decode from position 512; rows of the cache re-written)
-        if not args.skip_c5:
+        if not args.skip_c5 and under_profiler():
+            # generation captures HIP graphs (the decode step, the sampler);
+            # rocprofv3's kernel tracing has crashed the host in that capture
+            log("config 5 end-to-end run skipped under rocprofv3 (it captures HIP graphs)")
+        elif not args.skip_c5:
             result["c5"] = c5_run(gpu, hp)
         gpu.close()
 
