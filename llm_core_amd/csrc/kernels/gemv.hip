@@ -94,9 +94,9 @@ __device__ __forceinline__ void stage_q8_q4k(uint32_t* rec, const uint8_t* xq8, 
 }
 
 // F32 activation, padded: element i at float index i + 4*(i >> shift).
-template <int shift>
+template <int shift, int NT = kThreads>
 __device__ __forceinline__ void stage_f32(float* xs, const float* x, int K) {
-    for (int i4 = threadIdx.x; i4 < K / 4; i4 += kThreads) {
+    for (int i4 = threadIdx.x; i4 < K / 4; i4 += NT) {
         const float4 v = reinterpret_cast<const float4*>(x)[i4];
         const int i = 4 * i4;
         *reinterpret_cast<float4*>(xs + i + 4 * (i >> shift)) = v;
@@ -181,19 +181,20 @@ __device__ __forceinline__ void load_q6_tail(const uint8_t* blk, uint32_t (&sc)[
 // ---------------------------------------------------------------------------
 // Q4_K x F32
 // ---------------------------------------------------------------------------
-template <int LPR, int CPL, int NR>
-__global__ __launch_bounds__(kThreads) void k_gemv_q4k_f32(float* __restrict__ y,
-                                                           const uint8_t* __restrict__ W,
-                                                           const float* __restrict__ x, int rows,
-                                                           int nb, long row_bytes,
-                                                           int accumulate) {
+// NT threads per workgroup: every workgroup stages the whole activation (4 KB
+// per 1024 weights of a row), so larger workgroups stage it fewer times.
+template <int LPR, int CPL, int NR, int NT = kThreads>
+__global__ __launch_bounds__(NT) void k_gemv_q4k_f32(float* __restrict__ y,
+                                                     const uint8_t* __restrict__ W,
+                                                     const float* __restrict__ x, int rows,
+                                                     int nb, long row_bytes, int accumulate) {
     extern __shared__ uint4 smem[];
     float* xs = reinterpret_cast<float*>(smem);
     constexpr int RPP = 64 / LPR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rl = lane % LPR, rg = lane / LPR;
     const int nchunks = 4 * nb;
-    const long row0 = ((long)blockIdx.x * kWaves + wave) * (RPP * NR) + rg;
+    const long row0 = ((long)blockIdx.x * (NT / 64) + wave) * (RPP * NR) + rg;
 
     uint4 hdr[NR][CPL], qa[NR][CPL], qb[NR][CPL];
 #pragma unroll
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q4k_f32(float* __restrict__ y
         }
     }
 
-    stage_f32<6>(xs, x, nb * QK_K);  // 64-float chunk c at float offset 68*c
+    stage_f32<6, NT>(xs, x, nb * QK_K);  // 64-float chunk c at float offset 68*c
     __syncthreads();
 
     float acc[NR];
@@ -1152,6 +1153,10 @@ hipError_t launch_qgemv2(QAct act, QGemvArgs a, int threads, hipStream_t st) {
     return hipErrorInvalidValue;
 }
 
+// Q4_K x F32 GEMV workgroup: 512 threads (config 1, 4096x4096: 5.37 us at 256
+// threads, 5.20 at 512, 5.21 at 1024)
+constexpr int kF32Threads = 512;
+
 template <int LPR, int CPL, int NR>
 static hipError_t launch_cfg(GemvKind kind, float* y, const void* W, const void* x, int rows,
                              int nb, long row_bytes, int accumulate, hipStream_t st) {
@@ -1176,11 +1181,14 @@ static hipError_t launch_cfg(GemvKind kind, float* y, const void* W, const void*
                    ? qgemv_cfg<kQ4K, kThreads, LPR, CPL, NR, (int)QAct::Q8, EPI_Y, false>(a, st)
                    : qgemv_cfg<kQ6K, kThreads, LPR, CPL, NR, (int)QAct::Q8, EPI_Y, false>(a, st);
     }
-    if (kind == GemvKind::Q4K_F32)
-        hipLaunchKernelGGL((k_gemv_q4k_f32<LPR, CPL, NR>), grid, block,
+    if (kind == GemvKind::Q4K_F32) {
+        constexpr int NT = kF32Threads;
+        constexpr int RW = (NT / 64) * (64 / LPR) * NR;
+        const dim3 g2((unsigned)((rows + RW - 1) / RW));
+        hipLaunchKernelGGL((k_gemv_q4k_f32<LPR, CPL, NR, NT>), g2, dim3(NT),
                            (size_t)nb * QK_K * 4 * 17 / 16, st, y, Wb,
                            static_cast<const float*>(x), rows, nb, row_bytes, accumulate);
-    else
+    } else
         hipLaunchKernelGGL((k_gemv_q6k_f32<LPR, CPL, NR>), grid, block,
                            (size_t)nb * QK_K * 4 * 9 / 8, st, y, Wb,
                            static_cast<const float*>(x), rows, nb, row_bytes, accumulate);
