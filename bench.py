@@ -226,6 +226,36 @@ def read_probe(ctx, nbytes, n_copies, reps=40):
             f"{unroll} x 16 B per thread in flight", "sweep_unroll_wgs_us": sweep}
 
 
+PROBES = [(0, "plain_read"), (1, "mfma_operand_layout"), (2, "rows16_x_64B"), (3, "gemv_halfblock_units"),
+          (4, "contiguous_same_lanes"), (5, "contiguous_lds_exchange"), (6, "lds_tile_natural_stride"),
+          (7, "lds_tile_rotated"), (8, "sync_none"), (9, "sync_atomic"), (10, "sync_release_fence_atomic"),
+          (11, "sync_threadfence_atomic")]
+
+
+def probe_run(ctx, reps=20):
+    """The design probes of axf_hip_bench_probe: load patterns over the 25.4 MB
+    of an 11008x4096 Q4_K matrix (rotating copies, as the GEMV), and the cost of
+    grid-wide synchronisation (1024 workgroups writing 520-byte partials)."""
+    rows = 11008
+    nbytes = rows * 2304
+    n_copies = math.ceil((2 * MALL_BYTES + (96 << 20)) / nbytes)
+    bufs = [ctx.alloc(nbytes) for _ in range(n_copies)]
+    for b in bufs:
+        ctx.write(b, np.zeros(16, np.uint8))
+    if under_profiler():
+        reps = 1
+    out = {}
+    for probe, name in PROBES:
+        seq = bufs * GEMV_ROUNDS if probe <= 7 else [bufs[0]] * 64
+        ctx.bench_probe(probe, seq, rows, 1)
+        us = ctx.bench_probe(probe, seq, rows, reps) * 1000.0 / (reps * len(seq))
+        out[name] = round(us, 3)
+        log(f"probe {name}: {us:.3f} us per launch")
+    for b in bufs:
+        b.free()
+    return {"bytes": nbytes, "n_copies": n_copies, "us_per_launch": out}
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -424,7 +454,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="approximate CPU seconds spent on the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill", "c3"],
+    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill", "c3", "probes"],
                     default="all")
     ap.add_argument("--eager", action="store_true",
                     help="direct launches instead of captured-graph replay in every timing "
@@ -438,8 +468,8 @@ def main() -> int:
                     help="--only prefill: time the prefill alone (no graph-replayed generation)")
     ap.add_argument("--skip-c5", action="store_true",
                     help="leave out the config-5 prefill and end-to-end timing")
-    ap.add_argument("--mall-warm", action="store_true",
-                    help="also time the roofline GEMV on one weight copy (Infinity-Cache warm)")
+    ap.add_argument("--no-mall-warm", dest="mall_warm", action="store_false",
+                    help="skip timing the roofline GEMV on one weight copy (Infinity-Cache warm)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
                     help="print a summary of rocprofv3 csv output directories and exit")
     ap.add_argument("--counters", nargs="+", metavar="DIR",
@@ -478,6 +508,9 @@ def main() -> int:
             + ("running under rocprofv3" if under_profiler() else "--eager"))
     out: dict = {"launch": "eager" if eager else "hip-graph replay"}
 
+    if args.only == "probes":  # design probes alone (not a bench line)
+        print(json.dumps({"probes": probe_run(ctx)}))
+        return 0
     if args.only == "c3":  # config 3 layer alone (not a bench line)
         print(json.dumps({"c3_qwen25_3b_layer_decode": c3_run(ctx, args.warmup, args.steps)}))
         return 0

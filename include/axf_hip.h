@@ -262,6 +262,21 @@ int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_li
  * one launch of a given size can read, the ceiling the GEMVs are compared to. */
 int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t bytes, int unroll,
                        int wgs, int reps, float* ms);
+/* Benchmark helper (no reference counterpart): design probes over Q4_K rows of
+ * 2304 bytes (K = 4096; each buffer rows * 2304 bytes, 16-byte aligned,
+ * rows >= 16), timed as axf_hip_bench_read times its reads.  probe: 0 plain
+ * contiguous read; 1 the int8 MFMA operand layout loaded directly (16 rows x
+ * 32 bytes per instruction); 2 16 rows x 64 contiguous bytes per instruction;
+ * 3 the GEMV's half-block units (32 lanes per row, 16 bytes in every 72); 4 the
+ * same bytes loaded contiguously by the same lanes; 5 as 4, then exchanged
+ * into the unit layout through LDS; 6 a 16-row tile staged in LDS at its
+ * natural stride, read in the MFMA operand layout; 7 as 6 with the rows
+ * rotated by chunks; 8-11 1024 workgroups writing 520-byte partials with no
+ * synchronisation, a device-scope atomic per workgroup, a release fence and
+ * the atomic, __threadfence and the atomic (bufs unused).  *ms = elapsed
+ * milliseconds of reps passes over the n buffers. */
+int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
+                        int reps, float* ms);
 /* Benchmark helpers (no reference counterpart): eager != 0 makes
  * axf_hip_bench_gemv, axf_hip_bench_gemm and axf_llama_bench_decode on this
  * context launch every kernel directly instead of capturing and replaying a

@@ -36,6 +36,7 @@ SOURCES = [
     "kernels/attention.hip",
     "kernels/sample.hip",
     "kernels/gemv_misc.hip",
+    "kernels/probes.hip",
     "capi.cpp",
     "gemm_noalloc.cpp",
     "host/synth.cpp",

@@ -630,6 +630,22 @@ int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t byte
     });
 }
 
+int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
+                        int reps, float* ms) {
+    AXF_CHECK_CTX(ctx);
+    AXF_REQUIRE(probe >= 0 && probe <= 11 && n > 0 && reps > 0 && ms, "bad arguments");
+    if (probe <= 7) {
+        AXF_REQUIRE(bufs && rows >= 16, "probes 0-7 need buffers of rows >= 16 rows");
+        for (int i = 0; i < n; i++) AXF_REQUIRE(bufs[i] && aligned(bufs[i], 16), "buffer misaligned");
+    }
+    void* scratch = nullptr;
+    int rc = ctx_scratch(ctx, probe_scratch_bytes(), &scratch);  // before any capture
+    if (rc) return rc;
+    return bench_graph(ctx, __func__, n, reps, ms, [&](int i, hipStream_t st) {
+        return launch_probe(probe, probe <= 7 ? bufs[i] : nullptr, rows, scratch, st);
+    });
+}
+
 int axf_hip_bench_set_eager(axf_ctx* ctx, int eager) {
     AXF_CHECK_CTX(ctx);
     ctx->bench_eager = eager ? 1 : 0;

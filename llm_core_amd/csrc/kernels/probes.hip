@@ -1,0 +1,247 @@
+// probes.hip — measurement kernels behind axf_hip_bench_probe (no reference
+// counterpart).  They isolate what the GEMV and GEMM designs depend on:
+//
+//   * how fast 25.4 MB of Q4_K rows (11008 x 2304 bytes) streams under the
+//     load patterns the kernels could use (every probe reads every byte once
+//     and XORs it into a value stored only if it equals an impossible magic,
+//     so no load is dead);
+//   * what grid-wide synchronisation costs: 1024 workgroups each writing a
+//     520-byte partial, with no synchronisation, with one device-scope atomic
+//     per workgroup, with a release fence before it, or with __threadfence.
+#include "common.hpp"
+
+namespace axf {
+
+namespace {
+
+constexpr int kPrRow = 2304;  // bytes per row: 16 Q4_K blocks (K = 4096)
+constexpr int kPrNb = kPrRow / Q4K_BYTES;
+constexpr uint32_t kMagic = 0x9e3779b9u;
+
+typedef __attribute__((address_space(1))) const void prb_gmem_t;
+typedef __attribute__((address_space(3))) void prb_lmem_t;
+typedef int prb_v4i_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ long prb_pack2(uint32_t lo, uint32_t hi) {
+    return (long)(((uint64_t)hi << 32) | lo);
+}
+
+// plain contiguous read: grid-stride 16-byte loads
+__global__ __launch_bounds__(256) void k_probe_plain(const uint8_t* W, long n16, uint32_t* sink) {
+    uint32_t a = 0;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n16; i += (long)gridDim.x * 256) {
+        const uint4 v = reinterpret_cast<const uint4*>(W)[i];
+        a ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (a == kMagic) sink[0] = a;
+}
+
+// the int8 MFMA B-operand layout loaded directly: a workgroup of 8 waves owns
+// 16 rows, wave w blocks w and w+8; lane (col, g) loads row col's header and
+// 4 x 8 bytes (qs 32c + 8g): each instruction touches 16 rows x 32 bytes
+__global__ __launch_bounds__(512) void k_probe_operand(const uint8_t* W, int rows, uint32_t* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, g = lane >> 4;
+    const uint8_t* wr = W + (size_t)min((int)blockIdx.x * 16 + col, rows - 1) * kPrRow;
+    uint4 h[2];
+    uint2 q[2][4];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const uint8_t* blk = wr + (wave + 8 * p) * Q4K_BYTES;
+        h[p] = ld16(blk);
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[p][c] = *reinterpret_cast<const uint2*>(blk + 16 + 32 * c + 8 * g);
+    }
+    uint32_t a = 0;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        a ^= h[p].x ^ h[p].y ^ h[p].z ^ h[p].w;
+#pragma unroll
+        for (int c = 0; c < 4; c++) a ^= q[p][c].x ^ q[p][c].y;
+    }
+    if (a == kMagic) sink[0] = a;
+}
+
+// 16 rows x 64 contiguous bytes per instruction: a workgroup of 4 waves owns
+// 16 rows, wave w 4 adjacent blocks; lane (col, g) loads 16-byte chunks g,
+// g+4, ... of row col's 576-byte span (the register-weights GEMM's pattern)
+__global__ __launch_bounds__(256) void k_probe_wide(const uint8_t* W, int rows, uint32_t* sink) {
+    constexpr int CH = 4 * 9, PER = CH / 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, g = lane >> 4;
+    const uint8_t* wr = W + (size_t)min((int)blockIdx.x * 16 + col, rows - 1) * kPrRow +
+                        (size_t)wave * 4 * Q4K_BYTES;
+    uint4 v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) v[k] = ld16(wr + 16 * (g + 4 * k));
+    uint32_t a = 0;
+#pragma unroll
+    for (int k = 0; k < PER; k++) a ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    if (a == kMagic) sink[0] = a;
+}
+
+// the GEMV's half-block units: 512 threads, 32 lanes per row, lane rl loads
+// the header and 4 x 16 bytes of half-block rl (16 bytes in every 72 per
+// instruction)
+__global__ __launch_bounds__(512) void k_probe_units(const uint8_t* W, int rows, uint32_t* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 31, rg = lane >> 5;
+    const long row = min((long)blockIdx.x * 16 + wave * 2 + rg, (long)rows - 1);
+    const uint8_t* blk = W + row * kPrRow + (rl >> 1) * Q4K_BYTES;
+    const int q0 = 16 + 64 * (rl & 1);
+    const uint4 h = ld16(blk);
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = ld16(blk + q0 + 16 * k);
+    uint32_t a = h.x ^ h.y ^ h.z ^ h.w;
+#pragma unroll
+    for (int k = 0; k < 4; k++) a ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    if (a == kMagic) sink[0] = a;
+}
+
+// the same lanes and bytes as k_probe_units, loaded contiguously: lane rl of
+// a row group loads 16-byte chunks rl, rl+32, ... of its row (512 contiguous
+// bytes per row and instruction); X: then exchanged through a per-wave LDS
+// region into the half-block unit layout
+template <bool X>
+__global__ __launch_bounds__(512) void k_probe_contig(const uint8_t* W, int rows, uint32_t* sink) {
+    extern __shared__ uint4 prb_lds[];
+    constexpr int RBP = kPrRow + 16;  // LDS row stride (one pad chunk)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 31, rg = lane >> 5;
+    const long row = min((long)blockIdx.x * 16 + wave * 2 + rg, (long)rows - 1);
+    const uint8_t* r = W + row * kPrRow;
+    uint4 v[5];
+#pragma unroll
+    for (int k = 0; k < 5; k++) v[k] = ld16(r + 16 * min(rl + 32 * k, 9 * kPrNb - 1));
+    uint32_t a = 0;
+    if constexpr (X) {
+        uint8_t* wl = reinterpret_cast<uint8_t*>(prb_lds) + (wave * 2 + rg) * RBP;
+#pragma unroll
+        for (int k = 0; k < 5; k++)
+            if (rl + 32 * k < 9 * kPrNb) *reinterpret_cast<uint4*>(wl + 16 * (rl + 32 * k)) = v[k];
+        const uint8_t* blk = wl + (rl >> 1) * Q4K_BYTES;
+        const int q0 = 16 + 64 * (rl & 1);
+        const uint4 h = *reinterpret_cast<const uint4*>(blk);
+        a = h.x ^ h.y ^ h.z ^ h.w;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint4 u = *reinterpret_cast<const uint4*>(blk + q0 + 16 * k);
+            a ^= u.x ^ u.y ^ u.z ^ u.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 5; k++) a ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    if (a == kMagic) sink[0] = a;
+}
+
+// a 16-row tile (36 KiB, contiguous in HBM) copied into LDS by
+// global_load_lds_dwordx4, then read by 8 waves in the MFMA operand layout
+// with int8 MFMAs on it.  ROT = false: rows at their natural 2304-byte stride
+// (every row on the same bank); true: row r's chunk j at slot r*144 + (j+r)%144.
+template <bool ROT>
+__global__ __launch_bounds__(512) void k_probe_lds(const uint8_t* W, int rows, uint32_t* sink) {
+    extern __shared__ uint4 prb_lds[];
+    uint8_t* lds = reinterpret_cast<uint8_t*>(prb_lds);
+    constexpr int PIECES = 16 * kPrRow / 1024;  // 36
+    constexpr int CPR = kPrRow / 16;            // 144 chunks per row
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, g = lane >> 4;
+    const int row0 = min((int)blockIdx.x * 16, rows - 16);
+    const uint8_t* w0 = W + (size_t)row0 * kPrRow;
+    for (int p = wave; p < PIECES; p += 8) {
+        const int slot = p * 64 + lane, r = slot / CPR, q = slot - r * CPR;
+        int j = q;
+        if (ROT) {
+            j = q - r;
+            if (j < 0) j += CPR;
+        }
+        __builtin_amdgcn_global_load_lds((prb_gmem_t*)(w0 + r * kPrRow + j * 16),
+                                         (prb_lmem_t*)(lds + p * 1024), 16, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t a = 0;
+    prb_v4i_t acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int b = wave + 8 * p;
+        const uint8_t* wl = lds + col * kPrRow;
+        auto chunk = [&](int j) {
+            int q = j;
+            if (ROT) {
+                q = j + col;
+                if (q >= CPR) q -= CPR;
+            }
+            return wl + 16 * q;
+        };
+        const uint4 h = *reinterpret_cast<const uint4*>(chunk(9 * b));
+        a ^= h.x ^ h.y ^ h.z ^ h.w;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint2 q = *reinterpret_cast<const uint2*>(chunk(9 * b + 1 + 2 * c + (g >> 1)) + 8 * (g & 1));
+            const long b0 = prb_pack2(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu);
+            const long b1 = prb_pack2((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu);
+            acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)lane, b0, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)lane, b1, acc, 0, 0, 0);
+        }
+    }
+    a ^= (uint32_t)(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]);
+    if (a == kMagic) sink[0] = a;
+}
+
+// 1024 workgroups each write a 520-byte partial (130 floats); MODE 0: nothing
+// more; 1: one device-scope atomic add per workgroup; 2: an agent-scope
+// release fence, then the atomic; 3: __threadfence, then the atomic.
+template <int MODE>
+__global__ __launch_bounds__(256) void k_probe_sync(float* part, uint32_t* cnt) {
+    if (threadIdx.x < 130) part[(size_t)blockIdx.x * 130 + threadIdx.x] = (float)threadIdx.x;
+    if constexpr (MODE == 0) return;
+    if constexpr (MODE == 2) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if constexpr (MODE == 3) __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(cnt, 1u);
+}
+
+}  // namespace
+
+size_t probe_scratch_bytes() { return (size_t)1024 * 130 * 4 + 256; }
+
+hipError_t launch_probe(int probe, const void* buf, int rows, void* scratch, hipStream_t st) {
+    const auto* W = static_cast<const uint8_t*>(buf);
+    auto* sink = static_cast<uint32_t*>(scratch);
+    if (probe <= 7 && (rows < 16 || !W)) return hipErrorInvalidValue;
+    const unsigned tiles = (unsigned)((rows + 15) / 16);
+    switch (probe) {
+        case 0:
+            hipLaunchKernelGGL(k_probe_plain, dim3(2048), dim3(256), 0, st, W,
+                               (long)rows * kPrRow / 16, sink);
+            break;
+        case 1: hipLaunchKernelGGL(k_probe_operand, dim3(tiles), dim3(512), 0, st, W, rows, sink); break;
+        case 2: hipLaunchKernelGGL(k_probe_wide, dim3(tiles), dim3(256), 0, st, W, rows, sink); break;
+        case 3: hipLaunchKernelGGL(k_probe_units, dim3(tiles), dim3(512), 0, st, W, rows, sink); break;
+        case 4: hipLaunchKernelGGL(k_probe_contig<false>, dim3(tiles), dim3(512), 0, st, W, rows, sink); break;
+        case 5:
+            hipLaunchKernelGGL(k_probe_contig<true>, dim3(tiles), dim3(512), 16 * (kPrRow + 16), st, W,
+                               rows, sink);
+            break;
+        case 6:
+            hipLaunchKernelGGL(k_probe_lds<false>, dim3(tiles), dim3(512), 16 * kPrRow, st, W, rows, sink);
+            break;
+        case 7:
+            hipLaunchKernelGGL(k_probe_lds<true>, dim3(tiles), dim3(512), 16 * kPrRow, st, W, rows, sink);
+            break;
+        case 8:
+        case 9:
+        case 10:
+        case 11: {
+            auto* part = reinterpret_cast<float*>(static_cast<uint8_t*>(scratch) + 256);
+            auto* cnt = sink + 16;
+            if (probe == 8) hipLaunchKernelGGL(k_probe_sync<0>, dim3(1024), dim3(256), 0, st, part, cnt);
+            if (probe == 9) hipLaunchKernelGGL(k_probe_sync<1>, dim3(1024), dim3(256), 0, st, part, cnt);
+            if (probe == 10) hipLaunchKernelGGL(k_probe_sync<2>, dim3(1024), dim3(256), 0, st, part, cnt);
+            if (probe == 11) hipLaunchKernelGGL(k_probe_sync<3>, dim3(1024), dim3(256), 0, st, part, cnt);
+            break;
+        }
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace axf
