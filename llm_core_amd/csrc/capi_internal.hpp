@@ -57,17 +57,28 @@ struct QGemvArgs {
     const float* x;     // activation fp32 (QAct::Norm, QAct::F32)
     const float* nw;    // RMSNorm weight (QAct::Norm)
     float eps;
+    int shape;          // launcher hint: kShapeNR1 or 0
+    float* pv;          // launch_qgemv_argmax: per-workgroup maximum ...
+    int* pi;            // ... and the first row index holding it
 };
+// kShapeNR1: one row per lane group (NR = 1) where the default places two,
+// i.e. twice as many, smaller workgroups; the results are the same bits.
+constexpr int kShapeNR1 = 1;
 enum class QAct { Q8, Norm, F32 };
 // One weight type (qtype 12 or 14).  swiglu: rows are blocks of R/2 gate rows
 // then R/2 up rows (R = qgemv_rows_per_wg(nb, threads)); y0[i] = swiglu(gate_i, up_i).
 hipError_t launch_qgemv(int qtype, QAct act, bool swiglu, QGemvArgs a, int threads,
                         hipStream_t st);
+// QAct::Norm GEMV whose epilogue also writes each workgroup's (maximum, first
+// row index) of y to a.pv / a.pi (the first stage of argmax); workgroups:
+// qgemv_wgs(rows0, nb, threads, a.shape).  256 or 512 threads.
+hipError_t launch_qgemv_argmax(int qtype, QGemvArgs a, int threads, hipStream_t st);
+int qgemv_wgs(int rows, int nb, int threads, int shape);
 // Q4_K segment (W0) and Q6_K segment (W1) over the same activation, one launch.
 hipError_t launch_qgemv2(QAct act, QGemvArgs a, int threads, hipStream_t st);
 int qgemv_threads(QAct act, int nb);  // default workgroup size for launch_qgemv
 bool qgemv_threads_ok(QAct act, int nb, int threads);
-int qgemv_rows_per_wg(int nb, int threads);
+int qgemv_rows_per_wg(int nb, int threads, int shape = 0);
 // Q4_K / Q6_K x Q8_0 GEMM, Y token-major.  Auto: the dot4 kernel below
 // kGemmMfmaMinT tokens, Stream up to kGemmStreamMaxT, Mfma above.  The
 // matrix-core paths need gemm_scratch_bytes() of device scratch (activation
@@ -167,6 +178,9 @@ hipError_t launch_embed(int qtype, float* out, const void* W, const int* tok_dev
 int argmax_parts();
 hipError_t launch_argmax(int* out, float* pv, int* pi, const float* x, int n, int* tokens,
                          int* step, int* pos, hipStream_t st);
+// second stage alone: the nparts (value, index) pairs of a first stage
+hipError_t launch_argmax_final(int* out, const float* pv, const int* pi, int nparts, int* tokens,
+                               int* step, int* pos, hipStream_t st);
 hipError_t launch_add(float* y, const float* a, const float* b, int n, hipStream_t st);
 hipError_t launch_silu(float* y, const float* x, int n, hipStream_t st);
 hipError_t launch_mul(float* y, const float* a, const float* b, int n, hipStream_t st);

@@ -80,8 +80,9 @@ struct axf_llama {
     uint8_t* xq8 = nullptr;
     float* attn_part = nullptr;
     int nsplit = 0;
-    float* arg_v = nullptr;
+    float* arg_v = nullptr;  // argmax first-stage pairs: arg_n of each
     int* arg_i = nullptr;
+    int arg_n = 0;
     int *d_token = nullptr, *d_pos = nullptr, *d_step = nullptr, *d_tokens = nullptr;
     int max_tokens = 0;
 
@@ -265,6 +266,19 @@ int upload_gate_up(axf_llama* m, int l, Layer& L) {
     return AXF_OK;
 }
 
+// Workgroup size of a decode GEMV (Q8_0 or normalised activation): the
+// default, or, where the default leaves fewer than 256 workgroups (the
+// 2048-wide layers of config 3, small heads), 256 threads with one row per
+// lane group, 4-16x the workgroups (config-3 step 51.7 -> 49.2 us).
+int decode_gemv_threads(QAct act, int rows, int nb, int* shape) {
+    const int t = qgemv_threads(act, nb);
+    const int rw = qgemv_rows_per_wg(nb, t);
+    *shape = 0;
+    if ((rows + rw - 1) / rw >= 256 || !qgemv_threads_ok(act, nb, 256)) return t;
+    *shape = kShapeNR1;
+    return 256;
+}
+
 QGemvArgs weights(const DevW& w, int rows, float* y, int cols) {
     QGemvArgs a{};
     a.W0 = w.d;
@@ -281,7 +295,8 @@ hipError_t gemv_q8(const DevW& w, float* y, const void* xq8, int rows, int cols,
     QGemvArgs a = weights(w, rows, y, cols);
     a.xq8 = static_cast<const uint8_t*>(xq8);
     a.accumulate = acc ? 1 : 0;
-    return launch_qgemv(w.qtype, QAct::Q8, false, a, qgemv_threads(QAct::Q8, a.nb), st);
+    const int threads = decode_gemv_threads(QAct::Q8, rows, a.nb, &a.shape);
+    return launch_qgemv(w.qtype, QAct::Q8, false, a, threads, st);
 }
 
 // y = W * Q8_0(RMSNorm(x) * nw), the normalisation in the GEMV prologue;
@@ -292,7 +307,8 @@ hipError_t gemv_norm(const DevW& w, float* y, const float* x, const float* nw, f
     a.x = x;
     a.nw = nw;
     a.eps = eps;
-    const int threads = swiglu ? gateup_threads(cols) : qgemv_threads(QAct::Norm, a.nb);
+    const int threads =
+        swiglu ? gateup_threads(cols) : decode_gemv_threads(QAct::Norm, rows, a.nb, &a.shape);
     return launch_qgemv(w.qtype, QAct::Norm, swiglu, a, threads, st);
 }
 
@@ -318,6 +334,36 @@ hipError_t head_logits(axf_llama* m, const float* x, float* scratch, hipStream_t
         return launch_gemv_q5_0_f32(m->logits, w.d, scratch, hp.n_vocab, hp.n_embd / 32,
                                     (long)w.row_bytes, st);
     return launch_gemv_f16_f32(m->logits, w.d, scratch, nullptr, hp.n_vocab, hp.n_embd, st);
+}
+
+// The greedy head of a Q4_K / Q6_K output matrix (K <= 8192): logits and the
+// first argmax stage in one launch (each workgroup's maximum and first index),
+// then the final stage; *parts = the first stage's pairs.  False where the
+// head takes head_logits + launch_argmax instead.
+bool head_argmax_shape(const axf_llama* m, int* threads, int* shape, int* parts) {
+    const auto& hp = m->hp;
+    const int nb = hp.n_embd / QK_K;
+    if (misc_type(m->output.qtype) || !qgemv_threads_ok(QAct::Norm, nb, 512)) return false;
+    *threads = decode_gemv_threads(QAct::Norm, hp.n_vocab, nb, shape);
+    *parts = qgemv_wgs(hp.n_vocab, nb, *threads, *shape);
+    return true;
+}
+
+hipError_t head_argmax(axf_llama* m, bool record, bool advance_pos, hipStream_t st) {
+    const auto& hp = m->hp;
+    int threads, parts;
+    QGemvArgs a = weights(m->output, hp.n_vocab, m->logits, hp.n_embd);
+    if (!head_argmax_shape(m, &threads, &a.shape, &parts) || parts > m->arg_n)
+        return hipErrorInvalidValue;
+    a.x = m->x;
+    a.nw = m->output_norm;
+    a.eps = hp.rms_eps;
+    a.pv = m->arg_v;
+    a.pi = m->arg_i;
+    hipError_t e = launch_qgemv_argmax(m->output.qtype, a, threads, st);
+    if (e != hipSuccess) return e;
+    return launch_argmax_final(m->d_token, m->arg_v, m->arg_i, parts, record ? m->d_tokens : nullptr,
+                               record ? m->d_step : nullptr, advance_pos ? m->d_pos : nullptr, st);
 }
 
 // Embedding rows of T tokens (token ids on the device) or one token.
@@ -364,7 +410,8 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int f
         a.x = m->x;
         a.nw = L.attn_norm;
         a.eps = hp.rms_eps;
-        ST(launch_qgemv2(QAct::Norm, a, qgemv_threads(QAct::Norm, a.nb), st));
+        const int threads = decode_gemv_threads(QAct::Norm, a.rows0 + a.rows1, a.nb, &a.shape);
+        ST(launch_qgemv2(QAct::Norm, a, threads, st));
     } else {
         if (L.qk_fused) {
             ST(gemv_norm(L.wq, q, m->x, L.attn_norm, hp.rms_eps, qo + kvo, E, false, st));
@@ -457,6 +504,9 @@ hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, boo
     if (e != hipSuccess) return e;
     for (int l = 0; l < hp.n_layer; l++)
         if ((e = enqueue_layer(m, l, pd, pos)) != hipSuccess) return e;
+    int t, sh, parts;
+    if (!smp && head_argmax_shape(m, &t, &sh, &parts))
+        return head_argmax(m, record, device_state && record, st);
     if ((e = head_logits(m, m->x, m->attn_out, st)) != hipSuccess) return e;
     return enqueue_pick(m, record, device_state && record, smp);
 }
@@ -815,9 +865,14 @@ int axf_llama_load(axf_llama* m) {
     m->nsplit = attn_nsplit(hp.n_ctx);
     LL_TRY(dalloc(m, (size_t)hp.n_heads * m->nsplit * (m->hd + 2) * 4, &p));
     m->attn_part = static_cast<float*>(p);
-    LL_TRY(dalloc(m, (size_t)argmax_parts() * 8, &p));
+    {
+        int t, sh, parts = 0;
+        m->arg_n = argmax_parts();
+        if (head_argmax_shape(m, &t, &sh, &parts) && parts > m->arg_n) m->arg_n = parts;
+    }
+    LL_TRY(dalloc(m, (size_t)m->arg_n * 8, &p));
     m->arg_v = static_cast<float*>(p);
-    m->arg_i = reinterpret_cast<int*>(m->arg_v + argmax_parts());
+    m->arg_i = reinterpret_cast<int*>(m->arg_v + m->arg_n);
     m->max_tokens = hp.n_ctx + 1;
     LL_TRY(dalloc(m, (size_t)(3 + m->max_tokens) * 4, &p));
     m->d_token = static_cast<int*>(p);

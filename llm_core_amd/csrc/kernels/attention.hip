@@ -50,16 +50,8 @@ __device__ __forceinline__ void rope_in_lds(float* v, int n_vec, const float* cr
 
 // Q8_0 of 32 values held as float4 by 8 consecutive lanes (sub = lane & 7).
 __device__ __forceinline__ void q8_store4(uint8_t* blk, int sub, float4 v) {
-    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    const float d = amax / 127.f;
-    const float id = amax > 0.f ? 127.f / amax : 0.f;
-    auto q = [&](float f) -> uint32_t {
-        float r = rintf(f * id);
-        r = fminf(fmaxf(r, -128.f), 127.f);
-        return (uint32_t)((int)r & 0xff);
-    };
-    *reinterpret_cast<uint32_t*>(blk + 4 + 4 * sub) =
-        q(v.x) | (q(v.y) << 8) | (q(v.z) << 16) | (q(v.w) << 24);
+    float d;
+    *reinterpret_cast<uint32_t*>(blk + 4 + 4 * sub) = q8_quant4(v, d);
     if (sub == 0) *reinterpret_cast<float*>(blk) = d;
 }
 

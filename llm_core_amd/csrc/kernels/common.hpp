@@ -80,10 +80,21 @@ __device__ __forceinline__ float max8(float v) {
     v = fmaxf(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false));  // row_half_mirror
     return v;
 }
+// Maximum over the 8-lane group of non-negative floats (absolute values),
+// taken on their bit patterns: non-negative floats order as unsigned
+// integers, so each DPP step is one integer max (fmaxf would add a
+// canonicalisation per step).  Equals max8 for inputs that are not NaN.
+__device__ __forceinline__ float max8_nonneg(float v) {
+    uint32_t u = __float_as_uint(v);
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0xb1, 0xf, 0xf, false));
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x4e, 0xf, 0xf, false));
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x141, 0xf, 0xf, false));
+    return __uint_as_float(u);
+}
 // sum over the lane's quad (every lane of the quad receives it)
 __device__ __forceinline__ int sum_quad(int v) {
-    v += __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false);
-    v += __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false);
     return v;
 }
 // the value of lane 7 - (lane & 7) of the lane's group of 8 (row_half_mirror)
@@ -192,24 +203,61 @@ __device__ __forceinline__ float rms_scale(const float4 (&xv)[KPT], int n, float
         if ((threadIdx.x & 63) == 63) red[(threadIdx.x >> 6) + (NT / 64) * j] = v;
     }
     __syncthreads();
-    float ss = red[0];
+    // one wave adds the partials and takes the square root; the others read
+    // the scale after a second barrier (the same bits in every workgroup)
+    if (threadIdx.x < 64) {
+        float ss = red[0];
 #pragma unroll
-    for (int w = 1; w < 16; w++) ss += red[w];
-    return 1.f / sqrtf(ss / (float)n + eps);
+        for (int w = 1; w < 16; w++) ss += red[w];
+        const float r = 1.f / sqrtf(ss / (float)n + eps);
+        if (threadIdx.x == 0) red[0] = r;
+    }
+    __syncthreads();
+    return red[0];
+}
+
+// amax / 127, correctly rounded, for every non-negative finite amax:
+// q0 = amax * RN(1/127), r = amax - q0 * 127 (exact by fma), q0 + r * RN(1/127).
+// Checked against the IEEE division on all 2^31 - 2^23 non-negative finite
+// floats (the fma correction of a product by the rounded reciprocal,
+// P. Markstein, "Computation of elementary functions on the IBM RISC
+// System/6000 processor", IBM J. Res. Dev. 34(1), 1990).
+__device__ __forceinline__ float div127(float a) {
+    constexpr float y = 1.f / 127.f;
+    const float q0 = a * y;
+    const float r = __builtin_fmaf(-q0, 127.f, a);
+    return __builtin_fmaf(r, y, q0);
+}
+
+// rint(a * b) of |a * b| < 2^22 as the low byte of a float's bits: the
+// product is rounded to fp32 first (the empty asm keeps the compiler from
+// fusing it into the add: one rounding of the exact product could land on
+// the other side of a half), then adding 1.5 * 2^23 rounds it to an integer
+// (to nearest, ties to even, as rintf) that occupies the low mantissa bits,
+// two's complement around 0x4B400000.
+__device__ __forceinline__ uint32_t rint_mul_bits(float a, float b) {
+    float p = a * b;
+    asm volatile("" : "+v"(p));
+    return __float_as_uint(p + 12582912.f);
 }
 
 // Q8_0 of one 32-value block held as float4 by 8 consecutive lanes
 // (sub = lane & 7): returns this lane's 4 packed int8 and, in d, the block scale.
+// Same bits as q8_quant32 on the block (for inputs that are not NaN): |v * id|
+// rounds to at most 127 (|v| <= amax), so the int8 saturation never applies
+// and rint_mul_bits' low byte is the int8 value.
 __device__ __forceinline__ uint32_t q8_quant4(float4 v, float& d) {
-    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    d = amax / 127.f;
+    const float amax =
+        max8_nonneg(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    d = div127(amax);
     const float id = amax > 0.f ? 127.f / amax : 0.f;
-    auto q = [&](float f) -> uint32_t {
-        float r = rintf(f * id);
-        r = fminf(fmaxf(r, -128.f), 127.f);
-        return (uint32_t)((int)r & 0xff);
-    };
-    return q(v.x) | (q(v.y) << 8) | (q(v.z) << 16) | (q(v.w) << 24);
+    const uint32_t b0 = rint_mul_bits(v.x, id), b1 = rint_mul_bits(v.y, id);
+    const uint32_t b2 = rint_mul_bits(v.z, id), b3 = rint_mul_bits(v.w, id);
+    // low bytes of b0..b3 -> bytes 0..3 (v_perm_b32 selectors: 0-3 the second
+    // operand's bytes, 4-7 the first's, 0x0c zero)
+    const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);
+    return lo | hi;
 }
 
 // Q4_K scale/min pair for sub-blocks j0 = 2*part and j1 = 2*part + 1 from the

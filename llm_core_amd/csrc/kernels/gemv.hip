@@ -64,10 +64,16 @@ static inline bool pair_cfg(int nb) { return nb > 8 && nb <= 16; }
 
 // K <= 8192 (fused normalisation); fp32 activations up to K = 16384 at 512
 // threads and K = 12288 at 1024 (the 128-VGPR budget holds 3 Q6_K chunks per lane)
-#define AXF_GEMV_CFGS_512_NORM(X) X(16, 1, 2) X(32, 1, 2) X(64, 1, 2) X(64, 2, 1)
+#define AXF_GEMV_CFGS_512_NORM(X) X(16, 1, 2) X(32, 1, 2) X(64, 1, 2) X(64, 2, 1) \
+    X(16, 1, 1) X(32, 1, 1) X(64, 1, 1)
 #define AXF_GEMV_CFGS_512(X) AXF_GEMV_CFGS_512_NORM(X) X(64, 3, 1) X(64, 4, 1)
-#define AXF_GEMV_CFGS_1024_NORM(X) X(16, 1, 1) X(32, 1, 1) X(64, 1, 2) X(64, 2, 1)
+#define AXF_GEMV_CFGS_1024_NORM(X) X(16, 1, 1) X(32, 1, 1) X(64, 1, 2) X(64, 2, 1) X(64, 1, 1)
 #define AXF_GEMV_CFGS_1024(X) AXF_GEMV_CFGS_1024_NORM(X) X(64, 3, 1)
+// 256 threads: one row per lane group (kShapeNR1) for Q8_0 activations; the
+// fused normalisation (K <= 8192)
+#define AXF_GEMV_CFGS_256_NR1(X) X(16, 1, 1) X(32, 1, 1)
+#define AXF_GEMV_CFGS_256_NORM(X) X(16, 1, 2) X(32, 1, 2) X(64, 1, 1) X(64, 2, 1) \
+    AXF_GEMV_CFGS_256_NR1(X)
 
 // ---------------------------------------------------------------------------
 // Activation staging
@@ -297,6 +303,8 @@ __device__ __forceinline__ void load_q6_chunk(const uint8_t* blk, int c, Q6Chunk
 //   EPI_Y       y[row] = v, or y[row] += v (accumulate: residual adds)
 //   EPI_SWIGLU  the rows of a workgroup are R/2 gate rows then R/2 up rows;
 //               y[i] = swiglu(gate_i, up_i) (no SwiGLU kernel runs)
+//   EPI_ARGMAX  y[row] = v, and the workgroup's largest v with its first row
+//               index to pv[wg], pi[wg] (no argmax-partial kernel runs)
 // Norm and F32 (K <= 16384) run 512- or 1024-thread workgroups whose threads load
 // their float4s of x (and w) before issuing the weight loads, and build the
 // records from registers while the weights stream in.
@@ -309,7 +317,7 @@ __device__ __forceinline__ void load_q6_chunk(const uint8_t* blk, int c, Q6Chunk
 // Weight loads use clamped (in-range) addresses; rows and chunks past the end
 // are computed on those bytes and never stored.
 // ---------------------------------------------------------------------------
-enum { EPI_Y = 0, EPI_SWIGLU = 1 };
+enum { EPI_Y = 0, EPI_SWIGLU = 1, EPI_ARGMAX = 2 };
 constexpr int kQ4K = AXF_TYPE_Q4_K, kQ6K = AXF_TYPE_Q6_K;
 constexpr int kWide = 512, kWider = 1024;  // workgroups of the register prologue
 
@@ -514,10 +522,10 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
     constexpr int RPP = 64 / LPR;
     constexpr int RW = (NT / 64) * RPP * NR;  // rows per workgroup
     constexpr int UC = PAIR ? 2 : 1;          // chunks per unit
-    constexpr bool REG = NT >= kWide && ACT != (int)QAct::Q8;  // activation built from registers
+    // activation built from registers: the fused normalisation, and fp32 at 512+ threads
+    constexpr bool REG = ACT == (int)QAct::Norm || (NT >= kWide && ACT == (int)QAct::F32);
     // float4s of x per thread: K / 4 <= 16 * LPR * CPL * UC
     constexpr int KPT = (16 * LPR * CPL * UC + NT - 1) / NT;
-    static_assert(ACT != (int)QAct::Norm || REG, "the fused normalisation needs 512+ threads");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rl = lane % LPR, rg = lane / LPR;
     const int nunits = 4 * a.nb / UC;
@@ -690,6 +698,47 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
             const float v = group_sum_last<LPR>(acc[n]);
             const long row = row0 + (long)n * RPP;
             if (rl == LPR - 1 && row < rows) y[row] = a.accumulate ? y[row] + v : v;
+        }
+    } else if constexpr (EPI == EPI_ARGMAX) {
+        static_assert(RW <= 64, "one wave merges the workgroup's rows");
+        float* hv = red + 16;  // the RW row results of this workgroup
+#pragma unroll
+        for (int n = 0; n < NR; n++) {
+            const float v = group_sum_last<LPR>(acc[n]);
+            const long row = row0 + (long)n * RPP;
+            if (rl == LPR - 1) {
+                if (row < rows) y[row] = v;
+                hv[rloc0 + n * RPP] = v;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            // the argmax merge: a larger value wins, an equal value with a
+            // smaller index wins, NaN never wins; from (-inf, INT_MAX), so a
+            // workgroup of NaN rows reports (-inf, INT_MAX)
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+            const int row = wg * RW + (int)threadIdx.x;
+            if ((int)threadIdx.x < RW && row < rows) {
+                const float v = hv[threadIdx.x];
+                if (v > bv || v == bv) {
+                    bv = v;
+                    bi = row;
+                }
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float v2 = __shfl_xor(bv, off, 64);
+                const int i2 = __shfl_xor(bi, off, 64);
+                if (v2 > bv || (v2 == bv && i2 < bi)) {
+                    bv = v2;
+                    bi = i2;
+                }
+            }
+            if (threadIdx.x == 0) {
+                a.pv[wg] = bv;
+                a.pi[wg] = bi;
+            }
         }
     } else {
         float* hv = red + 16;  // RW row results of this workgroup
@@ -1054,7 +1103,8 @@ static hipError_t qgemv_pick(const QGemvArgs& a, hipStream_t st) {
         if (pair_cfg(a.nb)) return qgemv_cfg<QT, NT, 32, 1, 1, ACT, EPI, true>(a, st);
         if constexpr (ACT == (int)QAct::Q8) return hipErrorInvalidValue;  // Q8 at 512: pairs only
     }
-    const KernCfg k = pick_cfg_nt(4 * a.nb, NT);
+    KernCfg k = pick_cfg_nt(4 * a.nb, NT);
+    if (a.shape & kShapeNR1) k.nr = 1;
 #define AXF_Q(L, C, N) \
     if (k.lpr == L && k.cpl == C && k.nr == N)   \
         return qgemv_cfg<QT, NT, L, C, N, ACT, EPI, false>(a, st);
@@ -1070,8 +1120,11 @@ static hipError_t qgemv_pick(const QGemvArgs& a, hipStream_t st) {
         AXF_GEMV_CFGS_512(AXF_Q)
     } else if constexpr (ACT == (int)QAct::F32) {
         AXF_GEMV_CFGS_GT4(AXF_Q)
+    } else if constexpr (ACT == (int)QAct::Norm) {
+        AXF_GEMV_CFGS_256_NORM(AXF_Q)
     } else {
         AXF_GEMV_CFGS(AXF_Q)
+        AXF_GEMV_CFGS_256_NR1(AXF_Q)
     }
 #undef AXF_Q
     return hipErrorInvalidValue;
@@ -1081,7 +1134,7 @@ bool qgemv_threads_ok(QAct act, int nb, int threads) {
     const int cpl = pick_cfg(4 * nb).cpl;
     switch (act) {
         case QAct::Q8: return threads == kThreads || (threads == kWide && pair_cfg(nb));
-        case QAct::Norm: return nb <= 32 && (threads == kWide || threads == kWider);
+        case QAct::Norm: return nb <= 32 && (threads == kThreads || threads == kWide || threads == kWider);
         case QAct::F32:
             return threads == kWider ? cpl <= 3 : (threads == kWide ? cpl <= 4 : threads == kThreads && cpl > 4);
     }
@@ -1095,9 +1148,10 @@ int qgemv_threads(QAct act, int nb) {
     return cpl <= 3 ? kWider : (cpl == 4 ? kWide : kThreads);
 }
 
-int qgemv_rows_per_wg(int nb, int threads) {
+int qgemv_rows_per_wg(int nb, int threads, int shape) {
     if (threads >= kWide && pair_cfg(nb)) return (threads / 64) * 2;  // 32 lanes per row
-    const KernCfg k = pick_cfg_nt(4 * nb, threads);
+    KernCfg k = pick_cfg_nt(4 * nb, threads);
+    if (shape & kShapeNR1) k.nr = 1;
     return (threads / 64) * (64 / k.lpr) * k.nr;
 }
 
@@ -1115,42 +1169,72 @@ hipError_t launch_qgemv(int qtype, QAct act, bool swiglu, QGemvArgs a, int threa
 #define AXF_QT(NT, ACT, EPI) \
     (q4 ? qgemv_pick<kQ4K, NT, ACT, EPI>(a, st) : qgemv_pick<kQ6K, NT, ACT, EPI>(a, st))
     if (swiglu) {
-        if (act != QAct::Norm || a.rows0 % qgemv_rows_per_wg(a.nb, threads) != 0)
+        if (act != QAct::Norm || threads < kWide ||
+            a.rows0 % qgemv_rows_per_wg(a.nb, threads, a.shape) != 0)
             return hipErrorInvalidValue;
         return threads == kWider ? AXF_QT(kWider, NORM, EPI_SWIGLU) : AXF_QT(kWide, NORM, EPI_SWIGLU);
     }
     if (act == QAct::Q8)
         return threads == kWide ? AXF_QT(kWide, Q8, EPI_Y) : AXF_QT(kThreads, Q8, EPI_Y);
     if (act == QAct::Norm)
-        return threads == kWider ? AXF_QT(kWider, NORM, EPI_Y) : AXF_QT(kWide, NORM, EPI_Y);
+        return threads == kWider ? AXF_QT(kWider, NORM, EPI_Y)
+                                 : (threads == kWide ? AXF_QT(kWide, NORM, EPI_Y) : AXF_QT(kThreads, NORM, EPI_Y));
     if (threads == kWider) return AXF_QT(kWider, F32, EPI_Y);
     if (threads == kWide) return AXF_QT(kWide, F32, EPI_Y);
     return AXF_QT(kThreads, F32, EPI_Y);
 #undef AXF_QT
 }
 
-hipError_t launch_qgemv2(QAct act, QGemvArgs a, int threads, hipStream_t st) {
-    if (act != QAct::Norm || threads != kWide || a.nb <= 0 || a.nb > 32 || a.rows0 <= 0 ||
-        a.rows1 <= 0)
+int qgemv_wgs(int rows, int nb, int threads, int shape) {
+    const int rw = qgemv_rows_per_wg(nb, threads, shape);
+    return (rows + rw - 1) / rw;
+}
+
+hipError_t launch_qgemv_argmax(int qtype, QGemvArgs a, int threads, hipStream_t st) {
+    if (a.nb <= 0 || a.nb > 32 || a.rows0 <= 0 || !a.pv || !a.pi || a.accumulate ||
+        (threads != kThreads && threads != kWide) || (qtype != kQ4K && qtype != kQ6K))
         return hipErrorInvalidValue;
-    const KernCfg k = pick_cfg_nt(4 * a.nb, threads);
-    const int rw = qgemv_rows_per_wg(a.nb, threads);
+    constexpr int NORM = (int)QAct::Norm;
+    if (qtype == kQ4K)
+        return threads == kWide ? qgemv_pick<kQ4K, kWide, NORM, EPI_ARGMAX>(a, st)
+                                : qgemv_pick<kQ4K, kThreads, NORM, EPI_ARGMAX>(a, st);
+    return threads == kWide ? qgemv_pick<kQ6K, kWide, NORM, EPI_ARGMAX>(a, st)
+                            : qgemv_pick<kQ6K, kThreads, NORM, EPI_ARGMAX>(a, st);
+}
+
+template <int NT>
+static hipError_t qgemv2_pick(QGemvArgs a, hipStream_t st) {
+    const int rw = qgemv_rows_per_wg(a.nb, NT, a.shape);
     a.nwg0 = (a.rows0 + rw - 1) / rw;
     const dim3 grid((unsigned)(a.nwg0 + (a.rows1 + rw - 1) / rw));
-    if (pair_cfg(a.nb)) {
-        hipLaunchKernelGGL((k_qgemv2<kWide, 32, 1, 1, (int)QAct::Norm, true>), grid, dim3(kWide),
-                           qgemv_lds(a.nb), st, a);
+    constexpr int NORM = (int)QAct::Norm;
+    if (NT >= kWide && pair_cfg(a.nb)) {
+        hipLaunchKernelGGL((k_qgemv2<NT, 32, 1, 1, NORM, true>), grid, dim3(NT), qgemv_lds(a.nb),
+                           st, a);
         return hipGetLastError();
     }
-#define AXF_Q2(L, C, N)                                                                         \
-    if (k.lpr == L && k.cpl == C && k.nr == N) {                                                \
-        hipLaunchKernelGGL((k_qgemv2<kWide, L, C, N, (int)QAct::Norm, false>), grid, dim3(kWide), \
-                           qgemv_lds(a.nb), st, a);                                            \
-        return hipGetLastError();                                                               \
+    KernCfg k = pick_cfg_nt(4 * a.nb, NT);
+    if (a.shape & kShapeNR1) k.nr = 1;
+#define AXF_Q2(L, C, N)                                                                          \
+    if (k.lpr == L && k.cpl == C && k.nr == N) {                                                 \
+        hipLaunchKernelGGL((k_qgemv2<NT, L, C, N, NORM, false>), grid, dim3(NT), qgemv_lds(a.nb), \
+                           st, a);                                                               \
+        return hipGetLastError();                                                                \
     }
-    AXF_GEMV_CFGS_512_NORM(AXF_Q2)
+    if constexpr (NT == kWide) {
+        AXF_GEMV_CFGS_512_NORM(AXF_Q2)
+    } else {
+        AXF_GEMV_CFGS_256_NORM(AXF_Q2)
+    }
 #undef AXF_Q2
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_qgemv2(QAct act, QGemvArgs a, int threads, hipStream_t st) {
+    if (act != QAct::Norm || (threads != kWide && threads != kThreads) || a.nb <= 0 || a.nb > 32 ||
+        a.rows0 <= 0 || a.rows1 <= 0)
+        return hipErrorInvalidValue;
+    return threads == kWide ? qgemv2_pick<kWide>(a, st) : qgemv2_pick<kThreads>(a, st);
 }
 
 // Q4_K x F32 GEMV workgroup: 512 threads (config 1, 4096x4096: 5.37 us at 256

@@ -83,15 +83,8 @@ __global__ void k_dequant_q6k(float* __restrict__ out, const uint8_t* __restrict
 // d = amax/127, id = 127/amax (0 when amax == 0), q = rne(x*id) saturated.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void q8_block_store(uint8_t* blk, int sub, float4 v) {
-    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    const float d = amax / 127.f;
-    const float id = amax > 0.f ? 127.f / amax : 0.f;
-    auto q = [&](float f) -> uint32_t {
-        float r = rintf(f * id);
-        r = fminf(fmaxf(r, -128.f), 127.f);
-        return (uint32_t)((int)r & 0xff);
-    };
-    const uint32_t packed = q(v.x) | (q(v.y) << 8) | (q(v.z) << 16) | (q(v.w) << 24);
+    float d;
+    const uint32_t packed = q8_quant4(v, d);
     *reinterpret_cast<uint32_t*>(blk + 4 + 4 * sub) = packed;
     if (sub == 0) *reinterpret_cast<float*>(blk) = d;
 }
@@ -542,6 +535,14 @@ hipError_t launch_embed(int qtype, float* out, const void* W, const int* tok_dev
 
 constexpr int kArgParts = 256;
 int argmax_parts() { return kArgParts; }
+
+hipError_t launch_argmax_final(int* out, const float* pv, const int* pi, int nparts, int* tokens,
+                               int* step, int* pos, hipStream_t st) {
+    if (nparts <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(kArgThreads), 0, st, out, pv, pi, nparts,
+                       tokens, step, pos);
+    return hipGetLastError();
+}
 
 hipError_t launch_argmax(int* out, float* pv, int* pi, const float* x, int n, int* tokens,
                          int* step, int* pos, hipStream_t st) {
