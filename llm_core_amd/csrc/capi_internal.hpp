@@ -60,6 +60,14 @@ struct QGemvArgs {
     int shape;          // launcher hint: kShapeNR1 or 0
     float* pv;          // launch_qgemv_argmax: per-workgroup maximum ...
     int* pi;            // ... and the first row index holding it
+    // QAct::Norm with emb != nullptr: x is row `*tok_dev` (or `tok`) of the
+    // Q4_K embedding matrix emb (emb_rb bytes per row), dequantised in the
+    // prologue; workgroup 0 also writes it to x_out (no embedding kernel runs)
+    const uint8_t* emb;
+    long emb_rb;
+    const int* tok_dev;
+    int tok;
+    float* x_out;
 };
 // kShapeNR1: one row per lane group (NR = 1) where the default places two,
 // i.e. twice as many, smaller workgroups; the results are the same bits.

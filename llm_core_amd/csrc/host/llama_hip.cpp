@@ -384,8 +384,16 @@ hipError_t embed(axf_llama* m, float* out, const int* tok_dev, int tok, int T, h
 // and x +=, 4: gate|up and SwiGLU, 5: down and x +=); the step runs 1..5.
 constexpr int kDownThreads = 512;  // F32-prologue down projection workgroup
 
+// Layer 0 of a step may take x from the embedding in its q|k|v prologue
+// (Q4_K embeddings, fused q|k + v launch): embed_fusable, and the step then
+// runs no embedding kernel.
+bool embed_fusable(const axf_llama* m) {
+    const Layer& L = m->layers[0];
+    return m->tok_embd.qtype == AXF_TYPE_Q4_K && L.qk_fused && L.wv.qtype == AXF_TYPE_Q6_K;
+}
+
 hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int first = 1,
-                         int last = 5) {
+                         int last = 5, const int* emb_tok_dev = nullptr, int emb_tok = -1) {
     const auto& hp = m->hp;
     const int E = hp.n_embd, H = hp.n_heads, KVH = hp.n_kv_heads, HD = m->hd, FD = hp.ffn_dim;
     const int qo = H * HD, kvo = KVH * HD;
@@ -410,6 +418,13 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int f
         a.x = m->x;
         a.nw = L.attn_norm;
         a.eps = hp.rms_eps;
+        if (emb_tok_dev || emb_tok >= 0) {  // x = the token's embedding row, written by the prologue
+            a.emb = m->tok_embd.d;
+            a.emb_rb = (long)m->tok_embd.row_bytes;
+            a.tok_dev = emb_tok_dev;
+            a.tok = emb_tok;
+            a.x_out = m->x;
+        }
         const int threads = decode_gemv_threads(QAct::Norm, a.rows0 + a.rows1, a.nb, &a.shape);
         ST(launch_qgemv2(QAct::Norm, a, threads, st));
     } else {
@@ -500,10 +515,14 @@ hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, boo
     hipStream_t st = m->ctx->stream;
     const int* pd = device_state ? m->d_pos : nullptr;
     const int* td = device_state ? m->d_token : nullptr;
-    hipError_t e = embed(m, m->x, td, token, 1, st);
-    if (e != hipSuccess) return e;
-    for (int l = 0; l < hp.n_layer; l++)
-        if ((e = enqueue_layer(m, l, pd, pos)) != hipSuccess) return e;
+    hipError_t e = hipSuccess;
+    const bool fuse = embed_fusable(m);
+    if (!fuse && (e = embed(m, m->x, td, token, 1, st)) != hipSuccess) return e;
+    for (int l = 0; l < hp.n_layer; l++) {
+        const bool e0 = fuse && l == 0;
+        e = enqueue_layer(m, l, pd, pos, 1, 5, e0 ? td : nullptr, e0 && !td ? token : -1);
+        if (e != hipSuccess) return e;
+    }
     int t, sh, parts;
     if (!smp && head_argmax_shape(m, &t, &sh, &parts))
         return head_argmax(m, record, device_state && record, st);

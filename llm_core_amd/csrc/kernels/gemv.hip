@@ -555,19 +555,58 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
 
     float4 xv[KPT], wv[KPT];
     const int n4 = a.nb * (QK_K / 4);
+    // embedding row (QAct::Norm with a.emb): per float4, the Q4_K block header
+    // and the dword of 4 nibbles, decoded once the weight loads are in flight
+    const bool emb = ACT == (int)QAct::Norm && a.emb != nullptr;
+    uint4 eh[ACT == (int)QAct::Norm ? KPT : 1];
+    uint32_t eq[ACT == (int)QAct::Norm ? KPT : 1];
     if constexpr (REG) {
+        if (ACT == (int)QAct::Norm && emb) {
+            const int id = a.tok_dev ? *a.tok_dev : a.tok;
+            const uint8_t* er = a.emb + (long)id * a.emb_rb;
 #pragma unroll
-        for (int k = 0; k < KPT; k++) {
-            const int i4 = min((int)threadIdx.x + NT * k, n4 - 1);
-            xv[k] = reinterpret_cast<const float4*>(a.x)[i4];
-            wv[k] = ACT == (int)QAct::Norm ? reinterpret_cast<const float4*>(a.nw)[i4]
-                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int k = 0; k < KPT; k++) {
+                const int i4 = min((int)threadIdx.x + NT * k, n4 - 1);
+                const uint8_t* blk = er + (long)(i4 >> 6) * Q4K_BYTES;
+                // elements 4*i4 .. +3: chunk (i4 >> 4) & 3, nibble run (i4 >> 3) & 1
+                eh[k] = ld16(blk);
+                eq[k] = ld4(blk + 16 + 32 * ((i4 >> 4) & 3) + 4 * (i4 & 7));
+                wv[k] = reinterpret_cast<const float4*>(a.nw)[i4];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < KPT; k++) {
+                const int i4 = min((int)threadIdx.x + NT * k, n4 - 1);
+                xv[k] = reinterpret_cast<const float4*>(a.x)[i4];
+                wv[k] = ACT == (int)QAct::Norm ? reinterpret_cast<const float4*>(a.nw)[i4]
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
 
     // the activation, once this lane's weight loads are in flight
     auto stage = [&]() {
+        if constexpr (REG && ACT == (int)QAct::Norm) {
+            if (emb) {
+                // k_embed_q4k's arithmetic: fmaf(d*sc, q, -(dmin*m)) per element
+#pragma unroll
+                for (int k = 0; k < KPT; k++) {
+                    const int i4 = (int)threadIdx.x + NT * k;
+                    const int c = (i4 >> 4) & 3, hi = (i4 >> 3) & 1;
+                    const float d = h2f(eh[k].x & 0xffffu), dmin = h2f(eh[k].x >> 16);
+                    uint32_t sc0, m0, sc1, m1;
+                    q4k_scales(eh[k].y, eh[k].z, eh[k].w, c, sc0, m0, sc1, m1);
+                    const float ds = d * (float)(hi ? sc1 : sc0), dm = dmin * (float)(hi ? m1 : m0);
+                    const uint32_t q = hi ? eq[k] >> 4 : eq[k];
+                    xv[k] = make_float4(fmaf(ds, (float)(q & 0xfu), -dm),
+                                        fmaf(ds, (float)((q >> 8) & 0xfu), -dm),
+                                        fmaf(ds, (float)((q >> 16) & 0xfu), -dm),
+                                        fmaf(ds, (float)((q >> 24) & 0xfu), -dm));
+                    if (blockIdx.x == 0 && i4 < n4) reinterpret_cast<float4*>(a.x_out)[i4] = xv[k];
+                }
+            }
+        }
         if constexpr (DIRECT)
             direct_sums<QT>(dx);
         else if constexpr (REG)
