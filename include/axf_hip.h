@@ -273,7 +273,10 @@ int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t byte
  * natural stride, read in the MFMA operand layout; 7 as 6 with the rows
  * rotated by chunks; 8-11 1024 workgroups writing 520-byte partials with no
  * synchronisation, a device-scope atomic per workgroup, a release fence and
- * the atomic, __threadfence and the atomic (bufs unused).  *ms = elapsed
+ * the atomic, __threadfence and the atomic; 12-13 the last-arriver reduction
+ * (write-through partials, an agent-scope atomic per workgroup on one of 32
+ * group counters (12) or on one counter (13), the last arriver of a group
+ * summing 32 partials) (8-13: bufs unused).  *ms = elapsed
  * milliseconds of reps passes over the n buffers. */
 int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
                         int reps, float* ms);

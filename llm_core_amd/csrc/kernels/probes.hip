@@ -199,9 +199,45 @@ __global__ __launch_bounds__(256) void k_probe_sync(float* part, uint32_t* cnt) 
     if (threadIdx.x == 0) atomicAdd(cnt, 1u);
 }
 
+// Last-arriver reduction without a cache writeback: each of 1024 workgroups
+// writes its 130-float partial with agent-scope (write-through) stores, waits
+// for them, and adds 1 to its group's counter (agent-scope atomic; GROUPS
+// counters 128 bytes apart, each launch adds 1024/GROUPS to each, so the
+// arrival index is old % (1024/GROUPS)); the last arriver of a group reads the
+// group's 32 partials (of its first 32 members) with agent-scope loads and
+// writes their sum.  GROUPS = 32: 32 workgroups per counter; 1: all on one.
+template <int GROUPS>
+__global__ __launch_bounds__(256) void k_probe_lastarrive(float* part, uint32_t* cnt, float* out) {
+    constexpr int PER = 1024 / GROUPS;
+    if (threadIdx.x < 130)
+        __hip_atomic_store(&part[(size_t)blockIdx.x * 130 + threadIdx.x], (float)threadIdx.x,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ uint32_t last;
+    const int g = (int)blockIdx.x / PER;
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&cnt[32 * g], 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        last = old % PER == PER - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x < 130) {
+        float acc = 0.f;
+        const int m0 = g * PER;
+        for (int j = 0; j < 32; j++)
+            acc += __hip_atomic_load(&part[(size_t)(m0 + j) * 130 + threadIdx.x], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        out[g * 130 + threadIdx.x] = acc;
+    }
+}
+
 }  // namespace
 
-size_t probe_scratch_bytes() { return (size_t)1024 * 130 * 4 + 256; }
+// sink (256 B), then 32 group counters 128 B apart (4 KiB), the partials
+// (1024 x 130 floats) and the group sums (32 x 130 floats)
+size_t probe_scratch_bytes() { return 256 + 4096 + (size_t)1024 * 130 * 4 + 32 * 130 * 4; }
 
 hipError_t launch_probe(int probe, const void* buf, int rows, void* scratch, hipStream_t st) {
     const auto* W = static_cast<const uint8_t*>(buf);
@@ -227,11 +263,23 @@ hipError_t launch_probe(int probe, const void* buf, int rows, void* scratch, hip
         case 7:
             hipLaunchKernelGGL(k_probe_lds<true>, dim3(tiles), dim3(512), 16 * kPrRow, st, W, rows, sink);
             break;
+        case 12:
+        case 13: {
+            auto* base = static_cast<uint8_t*>(scratch);
+            auto* cnt = reinterpret_cast<uint32_t*>(base + 256);
+            auto* part = reinterpret_cast<float*>(base + 256 + 4096);
+            float* out = part + 1024 * 130;
+            if (probe == 12)
+                hipLaunchKernelGGL(k_probe_lastarrive<32>, dim3(1024), dim3(256), 0, st, part, cnt, out);
+            else
+                hipLaunchKernelGGL(k_probe_lastarrive<1>, dim3(1024), dim3(256), 0, st, part, cnt, out);
+            break;
+        }
         case 8:
         case 9:
         case 10:
         case 11: {
-            auto* part = reinterpret_cast<float*>(static_cast<uint8_t*>(scratch) + 256);
+            auto* part = reinterpret_cast<float*>(static_cast<uint8_t*>(scratch) + 256 + 4096);
             auto* cnt = sink + 16;
             if (probe == 8) hipLaunchKernelGGL(k_probe_sync<0>, dim3(1024), dim3(256), 0, st, part, cnt);
             if (probe == 9) hipLaunchKernelGGL(k_probe_sync<1>, dim3(1024), dim3(256), 0, st, part, cnt);
