@@ -181,10 +181,10 @@ typedef struct {
 /* One token choice: the reference's apply_rep_penalty over the last
  * rep_penalty_last_n of hist[0..n_hist) (llama_model.cpp:1595-1605; applied to
  * logits_dev in place, as the reference does to state.logits), then sample()
- * (:1466-1498) with the uniform draw r.  *token (host) receives the id.  The
- * device path sorts at most 16384 candidates: ceil(n_vocab / 4096) *
- * min(k, 4096) must not exceed it (AXF_ERR_UNSUPPORTED otherwise; e.g. top_k
- * up to 431 at n_vocab 151936, 2048 at 32000, any k at n_vocab <= 16384).
+ * (:1466-1498) with the uniform draw r.  *token (host) receives the id.  Any
+ * top_k: up to 16384 candidates (ceil(n_vocab / 4096) * min(k, 4096)) are
+ * sorted in LDS, more (e.g. top_k above 431 at n_vocab 151936, or the whole
+ * vocabulary) in place in device memory by one workgroup, a few ms per call.
  * Among exactly equal scores the lower index ranks first. */
 int axf_hip_sample(axf_ctx* ctx, float* logits_dev, int n_vocab, const axf_sampling* s,
                    const int32_t* hist, int n_hist, float r, int32_t* token);

@@ -12,9 +12,10 @@
 //      complemented index, so equal values keep the lower index first) and
 //      writes its best kc keys.
 //   3. k_sample_pick: one workgroup sorts the candidates of all chunks the same
-//      way and keeps the first k — the reference's partial_sort prefix (its
-//      order among exactly equal scores is unspecified; here lower index
-//      first) — then one thread runs the reference's sequential float
+//      way (in LDS up to 16384 candidates; beyond, k_sample_pick_large sorts
+//      them in place in global memory) and keeps the first k — the
+//      reference's partial_sort prefix (its order among exactly equal scores is
+//      unspecified; here lower index first) — then one thread runs the reference's sequential float
 //      arithmetic: probs = exp(s - max), their sum in order, division, the
 //      top-p cut and renormalisation, and the pick of the first i with
 //      r < cumulative probability.  r is the step's uniform draw, precomputed on
@@ -108,22 +109,13 @@ __device__ void pick_sorted(uint64_t* keys, const uint64_t* __restrict__ cand, i
     bitonic_desc<N>(keys);
 }
 
-// Final choice.  Outputs as the greedy argmax kernel: *out, and when given
-// tokens[*step] = token, *step += 1, *pos += 1; the token is always appended to
-// the penalty history (hist[*hist_n], *hist_n += 1) when hist is given.
-__global__ __launch_bounds__(kSortThreads) void k_sample_pick(
-    int* __restrict__ out, const uint64_t* __restrict__ cand, int n_cand, int pow2, int k,
-    float top_p, const float* __restrict__ r_table, float r_fixed, int* tokens, int* step,
-    int* pos, int* hist, int* hist_n) {
-    __shared__ uint64_t keys[kPickMax];
-    switch (pow2) {
-    case 1024: pick_sorted<1024>(keys, cand, n_cand); break;
-    case 2048: pick_sorted<2048>(keys, cand, n_cand); break;
-    case 4096: pick_sorted<4096>(keys, cand, n_cand); break;
-    case 8192: pick_sorted<8192>(keys, cand, n_cand); break;
-    default: pick_sorted<16384>(keys, cand, n_cand); break;
-    }
-    if (threadIdx.x != 0) return;
+// Final choice over keys sorted in descending order (one thread).  Outputs as
+// the greedy argmax kernel: *out, and when given tokens[*step] = token,
+// *step += 1, *pos += 1; the token is always appended to the penalty history
+// (hist[*hist_n], *hist_n += 1) when hist is given.
+__device__ void finish_pick(const uint64_t* keys, int k, float top_p,
+                            const float* __restrict__ r_table, float r_fixed, int* out,
+                            int* tokens, int* step, int* pos, int* hist, int* hist_n) {
     int chosen;
     if (k == 1) {
         chosen = (int)~(uint32_t)keys[0];
@@ -177,15 +169,70 @@ __global__ __launch_bounds__(kSortThreads) void k_sample_pick(
     }
 }
 
+__global__ __launch_bounds__(kSortThreads) void k_sample_pick(
+    int* __restrict__ out, const uint64_t* __restrict__ cand, int n_cand, int pow2, int k,
+    float top_p, const float* __restrict__ r_table, float r_fixed, int* tokens, int* step,
+    int* pos, int* hist, int* hist_n) {
+    __shared__ uint64_t keys[kPickMax];
+    switch (pow2) {
+    case 1024: pick_sorted<1024>(keys, cand, n_cand); break;
+    case 2048: pick_sorted<2048>(keys, cand, n_cand); break;
+    case 4096: pick_sorted<4096>(keys, cand, n_cand); break;
+    case 8192: pick_sorted<8192>(keys, cand, n_cand); break;
+    default: pick_sorted<16384>(keys, cand, n_cand); break;
+    }
+    if (threadIdx.x == 0)
+        finish_pick(keys, k, top_p, r_table, r_fixed, out, tokens, step, pos, hist, hist_n);
+}
+
+// More than kPickMax candidates (large top_k, or the whole of a large
+// vocabulary): the workgroup pads them with zero keys to pow2 and sorts them in
+// place in `cand` (bitonic, the same comparisons as bitonic_desc, global
+// memory ordered between the workgroup's steps by the barriers), then the same
+// final pass.  One workgroup: slow (a few ms at 2^18 keys) but any k works.
+__global__ __launch_bounds__(kSortThreads) void k_sample_pick_large(
+    int* __restrict__ out, uint64_t* __restrict__ cand, int n_cand, int pow2, int k, float top_p,
+    const float* __restrict__ r_table, float r_fixed, int* tokens, int* step, int* pos, int* hist,
+    int* hist_n) {
+    for (int t = n_cand + (int)threadIdx.x; t < pow2; t += kSortThreads) cand[t] = 0;
+    __syncthreads();
+    for (int size = 2; size <= pow2; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < pow2 / 2; t += kSortThreads) {
+                const int i = 2 * stride * (t / stride) + (t % stride);
+                const int j = i + stride;
+                const uint64_t a = cand[i], b = cand[j];
+                const bool desc = (i & size) == 0;
+                if (desc ? (a < b) : (a > b)) {
+                    cand[i] = b;
+                    cand[j] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (threadIdx.x == 0)
+        finish_pick(cand, k, top_p, r_table, r_fixed, out, tokens, step, pos, hist, hist_n);
+}
+
 }  // namespace
 
 int sample_chunks(int n_vocab) { return (n_vocab + kChunk - 1) / kChunk; }
 
-// candidates per chunk and in total; 0 if k exceeds what the device path sorts
-int sample_candidates(int n_vocab, int k) {
+// candidate keys the chunk pass writes
+static long sample_n_cand(int n_vocab, int k) {
     const int kc = k < kChunk ? k : kChunk;
-    const long n = (long)sample_chunks(n_vocab) * kc;
-    return n <= kPickMax ? (int)n : 0;
+    return (long)sample_chunks(n_vocab) * kc;
+}
+
+// keys of `cand` launch_sample needs: the candidates, or beyond kPickMax the
+// power of two the in-place sort pads them to
+int sample_candidates(int n_vocab, int k) {
+    const long n = sample_n_cand(n_vocab, k);
+    if (n <= kPickMax) return (int)n;
+    long p = kPickMax;
+    while (p < n) p <<= 1;
+    return p <= (1L << 30) ? (int)p : 0;
 }
 
 hipError_t launch_rep_penalty(float* logits, const int* hist, const int* hist_n, int last_n,
@@ -203,14 +250,20 @@ hipError_t launch_sample(int* out, uint64_t* cand, const float* logits, int n_vo
     int k = greedy ? 1 : ((top_k > 0 && top_k < n_vocab) ? top_k : n_vocab);
     const int kc = k < kChunk ? k : kChunk;
     const int chunks = sample_chunks(n_vocab);
-    const int n_cand = chunks * kc;
-    if (n_cand > kPickMax) return hipErrorInvalidValue;
+    const int n_cand = (int)sample_n_cand(n_vocab, k);
+    if (sample_candidates(n_vocab, k) == 0) return hipErrorInvalidValue;
     int pow2 = 1024;
     while (pow2 < n_cand) pow2 <<= 1;
     hipLaunchKernelGGL(k_topk_chunks, dim3(chunks), dim3(kSortThreads), 0, st, cand, logits,
                        n_vocab, temperature, greedy ? 0 : 1, kc);
-    hipLaunchKernelGGL(k_sample_pick, dim3(1), dim3(kSortThreads), 0, st, out, cand, n_cand, pow2,
-                       k, greedy ? 1.0f : top_p, r_table, r_fixed, tokens, step, pos, hist, hist_n);
+    if (n_cand <= kPickMax)
+        hipLaunchKernelGGL(k_sample_pick, dim3(1), dim3(kSortThreads), 0, st, out, cand, n_cand,
+                           pow2, k, greedy ? 1.0f : top_p, r_table, r_fixed, tokens, step, pos,
+                           hist, hist_n);
+    else
+        hipLaunchKernelGGL(k_sample_pick_large, dim3(1), dim3(kSortThreads), 0, st, out, cand,
+                           n_cand, pow2, k, greedy ? 1.0f : top_p, r_table, r_fixed, tokens, step,
+                           pos, hist, hist_n);
     return hipGetLastError();
 }
 
