@@ -379,13 +379,19 @@ typedef struct axf_llama axf_llama;
 typedef struct {
     int n_layer, n_embd, n_heads, n_kv_heads, ffn_dim, n_vocab, n_ctx;
     float rms_eps, rope_theta;
+    /* QkNormOrder (llama_model.cpp:955-959, chosen from the architecture at
+     * :1520-1522): 0 none, 1 per-head q/k RMSNorm before RoPE (qwen3), 2 after
+     * RoPE (hunyuan-dense); the weights are blk.N.attn_{q,k}_norm.weight
+     * (head_dim floats, optional as in the reference) */
+    int qk_norm_order;
 } axf_llama_hparams;
 
 int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out);
 int axf_llama_destroy(axf_llama* m);
 /* Register a host tensor by its GGUF name (token_embd.weight, output_norm.weight,
  * output.weight, blk.N.{attn_norm,ffn_norm,attn_q,attn_k,attn_v,attn_output,
- * ffn_gate,ffn_up,ffn_down}.weight, optional blk.N.attn_{q,k,v}.bias).  The host
+ * ffn_gate,ffn_up,ffn_down}.weight, optional blk.N.attn_{q,k,v}.bias and, with
+ * qk_norm_order != 0, blk.N.attn_{q,k}_norm.weight).  The host
  * buffer must stay valid until axf_llama_load returns. */
 int axf_llama_set_tensor(axf_llama* m, const char* name, int qtype, const void* host,
                          size_t bytes);
@@ -393,12 +399,11 @@ int axf_llama_set_tensor(axf_llama* m, const char* name, int qtype, const void* 
 int axf_llama_load(axf_llama* m);
 /* Register every model tensor of an open GGUF file (the names build_weights
  * reads, llama_model.cpp:975-1006) straight from the mapping and load.  F32,
- * Q4_K and Q6_K tensors; per-head q/k norms (attn_q_norm / attn_k_norm) are
- * AXF_ERR_UNSUPPORTED. */
+ * Q4_K and Q6_K tensors (and Q8_0 / Q5_0 / F16 for the embedding and head). */
 int axf_llama_load_gguf(axf_llama* m, const axf_gguf* g);
 /* Engine::from_gguf + the model construction of llama_generate_cpu_impl
- * (llama_model.cpp:1508-1518): hyperparameters from the file's metadata with
- * the reference's defaults, context = min(context_length, max_context_len)
+ * (llama_model.cpp:1508-1522): hyperparameters from the file's metadata with
+ * the reference's defaults, the q/k norm order from the architecture, context = min(context_length, max_context_len)
  * (max_context_len <= 0: 4096, LlamaConfig's default), weights uploaded from
  * the mapping.  The file is closed before returning. */
 int axf_llama_from_gguf(axf_ctx* ctx, const char* path, int max_context_len, axf_llama** out);

@@ -50,6 +50,7 @@ class LlamaHparams(C.Structure):
         ("n_ctx", C.c_int),
         ("rms_eps", C.c_float),
         ("rope_theta", C.c_float),
+        ("qk_norm_order", C.c_int),
     ]
 
 

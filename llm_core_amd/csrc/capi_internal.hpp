@@ -179,6 +179,26 @@ hipError_t launch_attention_fused(const AttnArgs& a, int head_dim, hipStream_t s
 // already in the cache; q, bq, cos_t/sin_t, kcache, vcache, pos, n_heads,
 // n_kv_heads, out, outq8, n_tok, q_ld, out_ld are used).
 hipError_t launch_attention_prefill(const AttnArgs& a, int head_dim, hipStream_t st);
+// Per-head q/k RMSNorm models (order 1: before RoPE, 2: after): bias, norm and
+// RoPE of the query rows in place and of the K rows into the cache, V rows
+// (+ bias) into the cache, for n_tok rows at positions (pos_dev ? *pos_dev :
+// pos) + t; the attention then runs with no bias, RoPE or store.
+struct QkPrepArgs {
+    float* q;
+    int q_ld;
+    const float *k, *v;
+    int k_ld, v_ld;
+    const float *bq, *bk, *bv;  // optional
+    const float *qn, *kn;       // per-head norm weights (hd floats); nullptr: none
+    int order;
+    float eps;
+    float *kcache, *vcache;
+    const int* pos_dev;
+    int pos;
+    int n_heads, n_kv_heads, hd;
+    const float *cos_t, *sin_t;
+};
+hipError_t launch_qk_prep(const QkPrepArgs& a, int n_tok, hipStream_t st);
 hipError_t launch_swiglu(float* out, void* outq8, const float* gate, const float* up, int n,
                          hipStream_t st);
 hipError_t launch_embed(int qtype, float* out, const void* W, const int* tok_dev, int tok,

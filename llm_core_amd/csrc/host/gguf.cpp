@@ -479,10 +479,6 @@ int axf_llama_load_gguf(axf_llama* m, const axf_gguf* g) {
                                   t.name == "output_norm.weight" ||
                                   t.name.compare(0, 4, "blk.") == 0;
         if (!model_tensor) continue;
-        if (t.name.find("attn_q_norm") != std::string::npos ||
-            t.name.find("attn_k_norm") != std::string::npos)
-            return fail(AXF_ERR_UNSUPPORTED,
-                        "axf_llama_load_gguf: per-head q/k norms (" + t.name + ") are not supported");
         // Q8_0 / Q5_0 / F16 only for the embedding and the head (the layer
         // matrices run the fused Q4_K / Q6_K kernels)
         const bool head = t.name == "token_embd.weight" || t.name == "output.weight";
@@ -538,11 +534,10 @@ int axf_llama_from_gguf(axf_ctx* ctx, const char* path, int max_context_len, axf
                                              std::to_string(c.n_vocab) + " entries, token_embd " +
                                              std::to_string(embd_rows) + " rows");
     }
-    if (std::strcmp(c.arch, "qwen3") == 0 || std::strcmp(c.arch, "hunyuan-dense") == 0) {
-        axf_gguf_close(g);
-        return fail(AXF_ERR_UNSUPPORTED, std::string("axf_llama_from_gguf: architecture ") +
-                                             c.arch + " needs per-head q/k norms");
-    }
+    // QkNormOrder from the architecture (llama_model.cpp:1520-1522)
+    hp.qk_norm_order = std::strcmp(c.arch, "hunyuan-dense") == 0 ? 2
+                       : std::strcmp(c.arch, "qwen3") == 0     ? 1
+                                                                : 0;
     axf_llama* m = nullptr;
     rc = axf_llama_create(ctx, &hp, &m);
     if (!rc) rc = axf_llama_load_gguf(m, g);

@@ -56,6 +56,7 @@ struct Layer {
     bool qk_fused = false;
     bool gu_interleaved = false;  // wgate holds gate and up rows interleaved by row blocks
     float *bq = nullptr, *bk = nullptr, *bv = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr;  // per-head norms (qk_norm_order != 0)
 };
 
 }  // namespace
@@ -438,15 +439,41 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int f
     }
     // 2./3. attention -> Q8_0 of its output
     if (stage(2)) {
+        const bool qkn = hp.qk_norm_order != 0;
+        if (qkn) {  // per-head q/k norms: q, K, V finished and stored first
+            QkPrepArgs pa{};
+            pa.q = q;
+            pa.q_ld = qo + 2 * kvo;
+            pa.k = k;
+            pa.v = v;
+            pa.k_ld = pa.v_ld = qo + 2 * kvo;
+            pa.bq = L.bq;
+            pa.bk = L.bk;
+            pa.bv = L.bv;
+            pa.qn = L.q_norm;
+            pa.kn = L.k_norm;
+            pa.order = hp.qk_norm_order;
+            pa.eps = hp.rms_eps;
+            pa.kcache = m->kv_k + loff;
+            pa.vcache = m->kv_v + loff;
+            pa.pos_dev = pos_dev;
+            pa.pos = pos;
+            pa.n_heads = H;
+            pa.n_kv_heads = KVH;
+            pa.hd = HD;
+            pa.cos_t = m->rope_cos;
+            pa.sin_t = m->rope_sin;
+            ST(launch_qk_prep(pa, 1, st));
+        }
         AttnArgs a{};
         a.q = q;
         a.k = k;
         a.v = v;
-        a.bq = L.bq;
+        a.bq = qkn ? nullptr : L.bq;
         a.bk = L.bk;
         a.bv = L.bv;
-        a.cos_t = m->rope_cos;
-        a.sin_t = m->rope_sin;
+        a.cos_t = qkn ? nullptr : m->rope_cos;
+        a.sin_t = qkn ? nullptr : m->rope_sin;
         a.kcache = m->kv_k + loff;
         a.vcache = m->kv_v + loff;
         a.pos_dev = pos_dev;
@@ -454,7 +481,7 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int f
         a.n_heads = H;
         a.n_kv_heads = KVH;
         a.nsplit = m->nsplit;
-        a.store_kv = 1;
+        a.store_kv = qkn ? 0 : 1;
         a.part = m->attn_part;
         a.out = m->attn_out;
         a.outq8 = m->xq8;
@@ -631,14 +658,41 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     }
     ST(gemm_rows(m, L.wv, m->pf_v, m->pf_q8, kvo, T, E, st));
     // K, V rows into the cache, then attention of every row -> Q8_0
-    ST(launch_rope_kv_rows(k, k_ld, m->pf_v, kvo, L.bk, L.bv, m->kv_k + loff, m->kv_v + loff,
-                           pos0, T, KVH, HD, m->rope_cos, m->rope_sin, st));
+    const bool qkn = hp.qk_norm_order != 0;
+    if (qkn) {  // per-head q/k norms: q rows finished in place, K/V rows stored
+        QkPrepArgs pa{};
+        pa.q = q;
+        pa.q_ld = q_ld;
+        pa.k = k;
+        pa.k_ld = k_ld;
+        pa.v = m->pf_v;
+        pa.v_ld = kvo;
+        pa.bq = L.bq;
+        pa.bk = L.bk;
+        pa.bv = L.bv;
+        pa.qn = L.q_norm;
+        pa.kn = L.k_norm;
+        pa.order = hp.qk_norm_order;
+        pa.eps = hp.rms_eps;
+        pa.kcache = m->kv_k + loff;
+        pa.vcache = m->kv_v + loff;
+        pa.pos = pos0;
+        pa.n_heads = H;
+        pa.n_kv_heads = KVH;
+        pa.hd = HD;
+        pa.cos_t = m->rope_cos;
+        pa.sin_t = m->rope_sin;
+        ST(launch_qk_prep(pa, T, st));
+    } else {
+        ST(launch_rope_kv_rows(k, k_ld, m->pf_v, kvo, L.bk, L.bv, m->kv_k + loff,
+                               m->kv_v + loff, pos0, T, KVH, HD, m->rope_cos, m->rope_sin, st));
+    }
     {
         AttnArgs a{};
         a.q = q;
-        a.bq = L.bq;
-        a.cos_t = m->rope_cos;
-        a.sin_t = m->rope_sin;
+        a.bq = qkn ? nullptr : L.bq;
+        a.cos_t = qkn ? nullptr : m->rope_cos;
+        a.sin_t = qkn ? nullptr : m->rope_sin;
         a.kcache = m->kv_k + loff;
         a.vcache = m->kv_v + loff;
         a.pos = pos0;
@@ -784,6 +838,8 @@ int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out)
         return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: dimension above 32768");
     if (h.n_embd > 8192)  // the GEMVs that fuse RMSNorm take K <= 8192
         return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: n_embd above 8192");
+    if (h.qk_norm_order < 0 || h.qk_norm_order > 2)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_create: qk_norm_order must be 0, 1 or 2");
     auto* m = new axf_llama();
     m->ctx = ctx;
     m->hp = h;
@@ -847,6 +903,10 @@ int axf_llama_load(axf_llama* m) {
         LL_TRY(upload_f32(m, n("attn_q.bias"), qo, &L.bq, false));
         LL_TRY(upload_f32(m, n("attn_k.bias"), kvo, &L.bk, false));
         LL_TRY(upload_f32(m, n("attn_v.bias"), kvo, &L.bv, false));
+        if (hp.qk_norm_order) {  // the reference ignores them without an order
+            LL_TRY(upload_f32(m, n("attn_q_norm.weight"), m->hd, &L.q_norm, false));
+            LL_TRY(upload_f32(m, n("attn_k_norm.weight"), m->hd, &L.k_norm, false));
+        }
     }
     // KV cache and buffers
     const size_t kv_floats = (size_t)hp.n_layer * hp.n_ctx * m->kv_embd;

@@ -48,6 +48,70 @@ __device__ __forceinline__ void rope_in_lds(float* v, int n_vec, const float* cr
     }
 }
 
+// Per-head q/k RMSNorm (qwen3: before RoPE, hunyuan-dense: after it) with
+// the bias, RoPE and the K/V store: workgroup (head hh, row t) of 64 threads
+// finishes query head hh (hh < H, in place) or kv head hh - H (K and V rows
+// into the caches at position pos + t).  The attention kernels then run
+// with no bias, no RoPE and no store.  The norm is rms_norm_avx2's
+// (llama_model.cpp:371-393): 8 partial sums, partial j the fma chain over
+// elements j, j+8, ... in order, added 0 + p0 + ... + p7, then
+// 1/sqrt(ss/n + eps), x = w * (x * scale); RoPE as rope_in_lds.
+__global__ __launch_bounds__(64) void k_qk_prep(QkPrepArgs a) {
+    __shared__ float buf[256];
+    __shared__ float part[9];
+    const int hh = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, HD = a.hd, half = HD / 2;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + t;
+    const bool isq = hh < a.n_heads;
+    const int kh = hh - a.n_heads;
+    const size_t kve = (size_t)a.n_kv_heads * HD;
+    const float* src = isq ? a.q + (size_t)t * a.q_ld + (size_t)hh * HD
+                           : a.k + (size_t)t * a.k_ld + (size_t)kh * HD;
+    const float* bias = isq ? (a.bq ? a.bq + (size_t)hh * HD : nullptr)
+                            : (a.bk ? a.bk + (size_t)kh * HD : nullptr);
+    const float* w = isq ? a.qn : a.kn;
+    float* dst = isq ? a.q + (size_t)t * a.q_ld + (size_t)hh * HD
+                     : a.kcache + (size_t)pos * kve + (size_t)kh * HD;
+    for (int i = tid; i < HD; i += 64) buf[i] = bias ? src[i] + bias[i] : src[i];
+    if (!isq) {  // V row (+ bias), unrotated and not normalised
+        const float* vs = a.v + (size_t)t * a.v_ld + (size_t)kh * HD;
+        float* vd = a.vcache + (size_t)pos * kve + (size_t)kh * HD;
+        for (int i = tid; i < HD; i += 64) vd[i] = a.bv ? vs[i] + a.bv[(size_t)kh * HD + i] : vs[i];
+    }
+    __syncthreads();
+    auto norm = [&]() {
+        if (!w) return;
+        if (tid < 8) {
+            float acc = 0.f;
+            for (int i = tid; i < HD; i += 8) acc = fmaf(buf[i], buf[i], acc);
+            part[tid] = acc;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float ss = 0.f;
+            for (int j = 0; j < 8; j++) ss += part[j];
+            part[8] = 1.f / sqrtf(ss / (float)HD + a.eps);
+        }
+        __syncthreads();
+        const float r = part[8];
+        for (int i = tid; i < HD; i += 64) buf[i] = w[i] * (buf[i] * r);
+        __syncthreads();
+    };
+    auto rope = [&]() {
+        const float* cr = a.cos_t + (size_t)pos * half;
+        const float* sr = a.sin_t + (size_t)pos * half;
+        for (int i = tid; i < half; i += 64) {
+            const float x0 = buf[i], x1 = buf[i + half], c = cr[i], sn = sr[i];
+            buf[i] = fmaf(x0, c, -(x1 * sn));
+            buf[i + half] = fmaf(x0, sn, x1 * c);
+        }
+        __syncthreads();
+    };
+    if (a.order == 1) norm();
+    rope();
+    if (a.order == 2) norm();
+    for (int i = tid; i < HD; i += 64) dst[i] = buf[i];
+}
+
 // Q8_0 of 32 values held as float4 by 8 consecutive lanes (sub = lane & 7).
 __device__ __forceinline__ void q8_store4(uint8_t* blk, int sub, float4 v) {
     float d;
@@ -609,6 +673,15 @@ static hipError_t launch_attn_hd(const AttnArgs& a, int G, hipStream_t st) {
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((k_attn_combine<HD>), dim3((unsigned)a.n_heads, nt), dim3(kAttnThreads), 0,
                        st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_prep(const QkPrepArgs& a, int n_tok, hipStream_t st) {
+    if (a.hd < 2 || a.hd > 256 || a.hd % 8 || n_tok < 1 || !a.cos_t || !a.sin_t ||
+        (a.order != 1 && a.order != 2))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_qk_prep, dim3((unsigned)(a.n_heads + a.n_kv_heads), (unsigned)n_tok),
+                       dim3(64), 0, st, a);
     return hipGetLastError();
 }
 

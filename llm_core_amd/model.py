@@ -3,7 +3,8 @@
 SynthLlama draws every weight N(0, std) from a seed and quantizes it with the
 Q4_K_M mix of the reference's benchmarks (Q4_K: token_embd, attn_q, attn_k,
 attn_output, ffn_gate, ffn_up; Q6_K: attn_v, ffn_down, output); norm weights
-are 1.0 unless norm_std > 0.  LlamaHip uploads such a model once and drives the
+are 1.0 unless norm_std > 0 (also the per-head q/k norm weights of a model
+with qk_norm_order != 0).  LlamaHip uploads such a model once and drives the
 decode step on the GPU through the C-ABI.
 """
 from __future__ import annotations
@@ -29,6 +30,7 @@ class Hparams:
     n_ctx: int
     rms_eps: float = 1e-5
     rope_theta: float = 10000.0
+    qk_norm_order: int = 0  # per-head q/k RMSNorm: 0 none, 1 before RoPE (qwen3), 2 after
 
     @property
     def head_dim(self) -> int:
@@ -36,7 +38,8 @@ class Hparams:
 
     def to_c(self) -> LlamaHparams:
         return LlamaHparams(self.n_layer, self.n_embd, self.n_heads, self.n_kv_heads,
-                            self.ffn_dim, self.n_vocab, self.n_ctx, self.rms_eps, self.rope_theta)
+                            self.ffn_dim, self.n_vocab, self.n_ctx, self.rms_eps, self.rope_theta,
+                            self.qk_norm_order)
 
 
 # LLaMA-2-7B architecture (the decode benchmark) and a Qwen2.5-3B-like layer
@@ -138,6 +141,9 @@ class SynthLlama:
                 for base, n in (("attn_q", qo), ("attn_k", kvo), ("attn_v", kvo)):
                     self.tensors[f"blk.{layer}.{base}.bias"] = (
                         AXF_TYPE_F32, hip.synth_normal(n, seed(), 0.0, 0.02))
+            if hp.qk_norm_order:
+                norm(f"blk.{layer}.attn_q_norm.weight", hd)
+                norm(f"blk.{layer}.attn_k_norm.weight", hd)
 
     def weight_bytes_per_token(self) -> int:
         """Bytes of quantized and norm weights one decode step reads (one embedding row)."""
@@ -182,7 +188,7 @@ class LlamaHip:
         c = LlamaHparams()
         call("axf_llama_get_hparams", self.handle, C.byref(c))
         self.hp = Hparams(c.n_layer, c.n_embd, c.n_heads, c.n_kv_heads, c.ffn_dim, c.n_vocab,
-                          c.n_ctx, c.rms_eps, c.rope_theta)
+                          c.n_ctx, c.rms_eps, c.rope_theta, c.qk_norm_order)
         return self
 
     def close(self) -> None:

@@ -484,6 +484,12 @@ void orc_rmsnorm(float* dst, const float* src, const float* w, int n, float eps)
     for (; i < n; i++) dst[i] = w[i] * src[i] * ss;
 }
 
+void orc_rmsnorm_heads(float* x, const float* w, int n_heads, int head_dim, float eps) {
+    if (!w) return;
+    for (int h = 0; h < n_heads; h++)
+        orc_rmsnorm(x + (size_t)h * head_dim, x + (size_t)h * head_dim, w, head_dim, eps);
+}
+
 /* RopeCache::build, llama_model.cpp:1031-1043 (glibc powf/cosf/sinf). */
 void orc_rope_table(float* cos_t, float* sin_t, int hd, float theta, int max_pos) {
     const int half = hd / 2;
@@ -979,8 +985,19 @@ void orc_forward_layer(const orc_model* m, orc_state* s, int l, int pos) {
     add_bias(s->q, lw->bq, H * HD);
     add_bias(s->k, lw->bk, KVH * HD);
     add_bias(s->v, lw->bv, KVH * HD);
+    /* per-head q/k norms (:1236-1248): before RoPE, or after it (K normed in
+     * the cache row, the same values the reference copies there) */
+    float* krow = kc + (size_t)pos * s->kv_embd;
+    if (m->qk_norm_order == ORC_QK_BEFORE_ROPE) {
+        orc_rmsnorm_heads(s->q, lw->q_norm, H, HD, m->rms_eps);
+        orc_rmsnorm_heads(s->k, lw->k_norm, KVH, HD, m->rms_eps);
+    }
     orc_rope(s->q, s->q, pos, H, HD, s->rope_cos, s->rope_sin);
-    orc_rope(kc + (size_t)pos * s->kv_embd, s->k, pos, KVH, HD, s->rope_cos, s->rope_sin);
+    orc_rope(krow, s->k, pos, KVH, HD, s->rope_cos, s->rope_sin);
+    if (m->qk_norm_order == ORC_QK_AFTER_ROPE) {
+        orc_rmsnorm_heads(s->q, lw->q_norm, H, HD, m->rms_eps);
+        orc_rmsnorm_heads(krow, lw->k_norm, KVH, HD, m->rms_eps);
+    }
     memcpy(vc + (size_t)pos * s->kv_embd, s->v, sizeof(float) * (size_t)s->kv_embd);
 
     orc_attention(s->attn_out, s->q, kc, vc, pos + 1, H, KVH, HD, s->attn);
@@ -1044,13 +1061,21 @@ void orc_forward_batch(const orc_model* m, orc_state* s, const int32_t* tokens, 
             add_bias(Q + (size_t)t * H * HD, lw->bq, H * HD);
             add_bias(K + (size_t)t * kve, lw->bk, kve);
             add_bias(V + (size_t)t * kve, lw->bv, kve);
+            if (m->qk_norm_order == ORC_QK_BEFORE_ROPE) {  /* :1388-1391 */
+                orc_rmsnorm_heads(Q + (size_t)t * H * HD, lw->q_norm, H, HD, m->rms_eps);
+                orc_rmsnorm_heads(K + (size_t)t * kve, lw->k_norm, KVH, HD, m->rms_eps);
+            }
         }
         for (int t = 0; t < T; t++) {
             const int pos = pos_start + t;
-            orc_rope(Q + (size_t)t * H * HD, Q + (size_t)t * H * HD, pos, H, HD, s->rope_cos,
-                     s->rope_sin);
-            orc_rope(kc + (size_t)pos * kve, K + (size_t)t * kve, pos, KVH, HD, s->rope_cos,
-                     s->rope_sin);
+            float* qrow = Q + (size_t)t * H * HD;
+            float* krow = kc + (size_t)pos * kve;
+            orc_rope(qrow, qrow, pos, H, HD, s->rope_cos, s->rope_sin);
+            orc_rope(krow, K + (size_t)t * kve, pos, KVH, HD, s->rope_cos, s->rope_sin);
+            if (m->qk_norm_order == ORC_QK_AFTER_ROPE) {  /* :1397-1403 */
+                orc_rmsnorm_heads(qrow, lw->q_norm, H, HD, m->rms_eps);
+                orc_rmsnorm_heads(krow, lw->k_norm, KVH, HD, m->rms_eps);
+            }
             memcpy(vc + (size_t)pos * kve, V + (size_t)t * kve, sizeof(float) * (size_t)kve);
         }
         for (int t = 0; t < T; t++)

@@ -103,7 +103,13 @@ typedef struct {
     const float* bq; /* optional biases (Qwen2), may be NULL */
     const float* bk;
     const float* bv;
+    const float* q_norm; /* optional per-head RMSNorm weights (head_dim floats), */
+    const float* k_norm; /* used when orc_model.qk_norm_order != 0; may be NULL */
 } orc_layer;
+
+/* QkNormOrder (llama_model.cpp:955): 0 none, 1 before RoPE (qwen3), 2 after
+ * RoPE (hunyuan-dense) */
+enum { ORC_QK_NONE = 0, ORC_QK_BEFORE_ROPE = 1, ORC_QK_AFTER_ROPE = 2 };
 
 typedef struct {
     int n_layer, n_embd, n_heads, n_kv_heads, ffn_dim, n_vocab, n_ctx;
@@ -112,6 +118,7 @@ typedef struct {
     const float* output_norm;
     orc_wt output;
     const orc_layer* layers; /* n_layer entries */
+    int qk_norm_order;       /* ORC_QK_* */
 } orc_model;
 
 typedef struct orc_state orc_state;
@@ -129,6 +136,10 @@ void orc_forward_token(const orc_model* m, orc_state* s, int token, int pos);
 void orc_forward_layer(const orc_model* m, orc_state* s, int layer, int pos);
 void orc_forward_batch(const orc_model* m, orc_state* s, const int32_t* tokens, int T,
                        int pos_start);
+/* rms_norm_heads_inplace (llama_model.cpp:421-429): rms_norm_avx2 on each of
+ * the n_heads head_dim-float heads of x with the one weight vector w; no-op
+ * when w is NULL. */
+void orc_rmsnorm_heads(float* x, const float* w, int n_heads, int head_dim, float eps);
 int orc_generate_greedy(const orc_model* m, const int32_t* prompt, int n_prompt, int n_gen,
                         int batched_prefill, int32_t* out_tokens, float* out_margins);
 

@@ -61,6 +61,7 @@ def _load_orc() -> C.CDLL:
         "orc_gemv_f16_f32": ([vp, vp, vp, vp, i32, i32, i32], None),
         "orc_dequant_row": ([vp, i32, vp, i32], None),
         "orc_sample": ([vp, i32, i32, f32, f32, f32, C.POINTER(f32)], i32),
+        "orc_rmsnorm_heads": ([vp, vp, i32, i32, f32], None),
         "orc_state_new": ([vp], vp),
         "orc_state_free": ([vp], None),
         "orc_state_logits": ([vp], C.POINTER(C.c_float)),
@@ -174,6 +175,14 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     w = np.ascontiguousarray(w, np.float32)
     y = np.empty_like(x)
     orc.orc_rmsnorm(_ptr(y), _ptr(x), _ptr(w), x.size, eps)
+    return y
+
+
+def rmsnorm_heads(x: np.ndarray, w: np.ndarray, n_heads: int, hd: int, eps: float) -> np.ndarray:
+    """rms_norm_heads_inplace (llama_model.cpp:421-429) on a copy."""
+    y = np.ascontiguousarray(x, np.float32).copy()
+    w = np.ascontiguousarray(w, np.float32)
+    orc.orc_rmsnorm_heads(_ptr(y), _ptr(w), n_heads, hd, eps)
     return y
 
 
@@ -364,14 +373,16 @@ class OrcWt(C.Structure):
 class OrcLayer(C.Structure):
     _fields_ = [("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p)] + [
         (n, OrcWt) for n in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
-    ] + [("bq", C.c_void_p), ("bk", C.c_void_p), ("bv", C.c_void_p)]
+    ] + [("bq", C.c_void_p), ("bk", C.c_void_p), ("bv", C.c_void_p), ("q_norm", C.c_void_p),
+         ("k_norm", C.c_void_p)]
 
 
 class OrcModel(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layer", "n_embd", "n_heads", "n_kv_heads", "ffn_dim",
                                         "n_vocab", "n_ctx")] + [
         ("rms_eps", C.c_float), ("rope_theta", C.c_float), ("tok_embd", OrcWt),
-        ("output_norm", C.c_void_p), ("output", OrcWt), ("layers", C.POINTER(OrcLayer))]
+        ("output_norm", C.c_void_p), ("output", OrcWt), ("layers", C.POINTER(OrcLayer)),
+        ("qk_norm_order", C.c_int)]
 
 
 class OracleModel:
@@ -407,12 +418,14 @@ class OracleModel:
             L.bq = opt(b + "attn_q.bias")
             L.bk = opt(b + "attn_k.bias")
             L.bv = opt(b + "attn_v.bias")
+            L.q_norm = opt(b + "attn_q_norm.weight")
+            L.k_norm = opt(b + "attn_k_norm.weight")
         self._layers = layers
         out_name = "output.weight" if "output.weight" in tensors else "token_embd.weight"
         self.m = OrcModel(hp.n_layer, hp.n_embd, hp.n_heads, hp.n_kv_heads, hp.ffn_dim,
                           hp.n_vocab, hp.n_ctx, hp.rms_eps, hp.rope_theta,
                           wt("token_embd.weight"), arr("output_norm.weight")[1], wt(out_name),
-                          layers)
+                          layers, int(getattr(hp, "qk_norm_order", 0)))
         self.state = orc.orc_state_new(C.byref(self.m))
 
     def close(self):

@@ -77,12 +77,23 @@ def layer_stage_errors(ctx, g, T, hp, layer, pos):
     q = qkv[:qo] + T.get(b + "attn_q.bias", np.zeros(qo, np.float32))
     k = qkv[qo:qo + kvo] + T.get(b + "attn_k.bias", zero)
     v = qkv[qo + kvo:] + T.get(b + "attn_v.bias", zero)
+    # per-head q/k norms (llama_model.cpp:1236-1248): before RoPE (1) or after it (2)
+    order = getattr(hp, "qk_norm_order", 0)
+
+    def finish(x, w, nh):
+        if order == 1 and w is not None:
+            x = O.rmsnorm_heads(x, w, nh, HD, hp.rms_eps)
+        x = O.rope(x, pos, nh, HD, cos_t, sin_t)
+        if order == 2 and w is not None:
+            x = O.rmsnorm_heads(x, w, nh, HD, hp.rms_eps)
+        return x
+
     k_dev, v_dev = g.get_kv(layer, 0, pos + 1)
-    assert np.array_equal(k_dev[pos], O.rope(k, pos, KVH, HD, cos_t, sin_t)), "stored K row"
+    assert np.array_equal(k_dev[pos], finish(k, T.get(b + "attn_k_norm.weight"), KVH)), "stored K row"
     assert np.array_equal(v_dev[pos], v), "stored V row"
     att = g.buffer(_ffi.AXF_LLAMA_BUF_ATTN)
-    rec("attention", att, O.attention(O.rope(q, pos, H, HD, cos_t, sin_t), k_dev, v_dev, pos + 1,
-                                      H, KVH, HD), 1e-5, 1e-6)
+    rec("attention", att, O.attention(finish(q, T.get(b + "attn_q_norm.weight"), H), k_dev, v_dev,
+                                      pos + 1, H, KVH, HD), 1e-5, 1e-6)
     aq = g.buffer(_ffi.AXF_LLAMA_BUF_ATTN_Q8)
     assert np.array_equal(aq, O.quantize_q8_0(att)), "attention Q8_0 blocks"
 

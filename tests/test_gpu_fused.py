@@ -82,6 +82,21 @@ def test_fused_stages_hidden3072(ctx):
     fused_stage_parity(ctx, cfg, 300, True, 5)
 
 
+def test_fused_stages_qk_norm_before_rope(ctx):
+    """Per-head q/k RMSNorm before RoPE (qwen3): bias, norm, RoPE of q and of
+    the stored K row (bit-exact), then the same attention and FFN stages."""
+    cfg = dict(n_embd=2048, n_heads=16, n_kv_heads=8, ffn_dim=6144, rms_eps=1e-6,
+               rope_theta=1e6, qk_norm_order=1)
+    fused_stage_parity(ctx, cfg, 700, True, 6)
+
+
+def test_fused_stages_qk_norm_after_rope(ctx):
+    """Per-head q/k RMSNorm after RoPE (hunyuan-dense)."""
+    cfg = dict(n_embd=1024, n_heads=8, n_kv_heads=2, ffn_dim=3072, rms_eps=1e-5,
+               rope_theta=1e4, qk_norm_order=2)
+    fused_stage_parity(ctx, cfg, 129, False, 7)
+
+
 def test_layer_stage_arguments(ctx):
     from llm_core_amd._ffi import AxfError
     from llm_core_amd.model import Hparams, LlamaHip, SynthLlama

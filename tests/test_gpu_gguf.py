@@ -60,6 +60,29 @@ def test_qwen2_tied_head_no_vocab_array(ctx, tmp_path):
             _same_outputs(ctx, g, ref, np.array([1, 5, 6, 7, 8], np.int32), n_gen=8)
 
 
+@pytest.mark.parametrize("arch,order", [("qwen3", 1), ("hunyuan-dense", 2)])
+def test_qk_norm_architectures(ctx, tmp_path, arch, order):
+    """qwen3 (per-head q/k norms before RoPE) and hunyuan-dense (after RoPE):
+    the order comes from general.architecture (llama_model.cpp:1520-1522), the
+    norm weights from blk.N.attn_{q,k}_norm.weight; the file equals the tensor
+    API model with that order.  (hunyuan-dense files without
+    rope.scaling.alpha keep freq_base unscaled.)"""
+    hp = Hparams(**{**SMALL, "qk_norm_order": order})
+    m = SynthLlama(hp, seed=12, norm_std=0.2)
+    path = G.llama_gguf(m, arch=arch).write(tmp_path / "qk.gguf")
+    with LlamaHip.from_gguf(ctx, path) as g, LlamaHip(ctx, m) as ref:
+        assert g.hp.qk_norm_order == order
+        assert g.device_bytes() == ref.device_bytes()
+        _same_outputs(ctx, g, ref, np.array([1, 33, 7, 920, 4, 61], np.int32), n_gen=8)
+    # the same weights without the order give other logits (the norms matter)
+    plain = copy.copy(m)
+    plain.hp = Hparams(**SMALL)
+    with LlamaHip(ctx, m) as a, LlamaHip(ctx, plain) as b:
+        a.forward_batch(np.array([1, 33, 7], np.int32), 0)
+        b.forward_batch(np.array([1, 33, 7], np.int32), 0)
+        assert not np.allclose(a.logits(), b.logits(), atol=1e-3)
+
+
 def _expect_error(ctx, path, code, text):
     with pytest.raises(AxfError) as e:
         LlamaHip.from_gguf(ctx, path)
@@ -69,12 +92,10 @@ def _expect_error(ctx, path, code, text):
 def test_rejected_files(ctx, tmp_path):
     hp = Hparams(**{**SMALL, "n_layer": 1})
     m = SynthLlama(hp, seed=2)
-    # per-head q/k norms (qwen3 / hunyuan-dense) are not part of this decoder
-    _expect_error(ctx, G.llama_gguf(m, arch="qwen3").write(tmp_path / "a.gguf"),
-                  AXF_ERR_UNSUPPORTED, "needs per-head q/k norms")
-    w = G.llama_gguf(m)
-    w.add_tensor("blk.0.attn_q_norm.weight", np.ones(64, np.float32), G.GGML_F32, (64,))
-    _expect_error(ctx, w.write(tmp_path / "b.gguf"), AXF_ERR_UNSUPPORTED, "attn_q_norm")
+    # a per-head norm weight of the wrong length (qwen3: head_dim floats)
+    w = G.llama_gguf(m, arch="qwen3")
+    w.add_tensor("blk.0.attn_q_norm.weight", np.ones(32, np.float32), G.GGML_F32, (32,))
+    _expect_error(ctx, w.write(tmp_path / "b.gguf"), AXF_ERR_INVALID_ARG, "attn_q_norm")
     # a weight type the decoder does not run (F16 = 1)
     bad = copy.copy(m)
     bad.tensors = dict(m.tensors)

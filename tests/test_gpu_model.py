@@ -411,6 +411,20 @@ def test_forward_batch_qwen25_3b_layer(ctx):
     _check_prefill(gl, ol, max(noise, 1e-3))
 
 
+@pytest.mark.parametrize("order", [1, 2])
+def test_forward_batch_qk_norm(ctx, order):
+    """Per-head q/k RMSNorm before RoPE (qwen3) or after it (hunyuan-dense),
+    q/k/v biases, 2 layers, a prefill of 40 tokens in two calls: last-row
+    logits and residual against the oracle's batch (the decode step's kernels
+    are checked stage by stage in test_gpu_fused)."""
+    cfg = {**SMALL, "qk_norm_order": order}
+    gl, ol, gx, ox, noise = _prefill_case(ctx, cfg, 30 + order, 40, splits=(17,),
+                                          with_bias=True)
+    _check_prefill(gl, ol, noise)
+    rel = np.linalg.norm(gx.astype(np.float64) - ox) / np.linalg.norm(ox)
+    assert rel < 1e-3 or noise > 1e-3, f"final-norm row relative error {rel}"
+
+
 def test_forward_batch_rejects_bad_input(ctx):
     from llm_core_amd._ffi import AxfError
     from llm_core_amd.model import Hparams, LlamaHip, SynthLlama

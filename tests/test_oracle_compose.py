@@ -436,3 +436,122 @@ def test_batch_rows_positions_and_causal_mean():
             m2.close()
     finally:
         m.close()
+
+
+# ---------------------------------------------------------------------------
+# per-head q/k RMSNorm (qwen3: before RoPE; hunyuan-dense: after RoPE;
+# llama_model.cpp:1236-1248, batch :1388-1403; rms_norm_heads_inplace :421-429)
+# ---------------------------------------------------------------------------
+
+def test_rmsnorm_heads_closed_forms():
+    hd, heads, eps = 128, 3, 1e-6
+    rng = np.random.default_rng(21)
+    w = f32(rng.uniform(0.5, 2.0, hd))
+    x = f32(np.concatenate([np.full(hd, 3.0), rng.standard_normal(hd), np.full(hd, -0.25)]))
+    y = O.rmsnorm_heads(x, w, heads, hd, eps)
+    # a constant head c: w * c / sqrt(c^2 + eps), to fp32 rounding
+    for h, c in ((0, 3.0), (2, -0.25)):
+        want = w * (c / np.sqrt(c * c + eps))
+        np.testing.assert_allclose(y[h * hd:(h + 1) * hd], want, rtol=3e-7, atol=0)
+    # each head on its own, with the same weight vector: head 1 equals the
+    # whole-vector RMSNorm of that head alone, bit for bit
+    assert np.array_equal(y[hd:2 * hd], O.rmsnorm(x[hd:2 * hd], w, eps))
+    # scaling one head leaves the others' bits unchanged
+    x2 = x.copy()
+    x2[hd:2 * hd] *= 10.0
+    y2 = O.rmsnorm_heads(x2, w, heads, hd, eps)
+    assert np.array_equal(y2[:hd], y[:hd]) and np.array_equal(y2[2 * hd:], y[2 * hd:])
+    # a slip that normalises over all heads at once gives other values
+    assert not np.allclose(O.rmsnorm(x, np.tile(w, heads), eps), y, atol=1e-3)
+
+
+def qk_norm_case(order: int, seed: int):
+    """A switched-off layer with per-head q/k norm weights at position 6: the
+    cache K row and q after the layer, and their closed forms."""
+    hp = HP(n_ctx=16)
+    hp.qk_norm_order = order
+    t = random_model(hp, seed=seed)
+    switch_off(t, hp)
+    rng = np.random.default_rng(seed + 1)
+    HD, H, KVH, E = hp.head_dim, hp.n_heads, hp.n_kv_heads, hp.n_embd
+    qn, kn = f32(rng.uniform(0.3, 3.0, HD)), f32(rng.uniform(0.3, 3.0, HD))
+    t["blk.0.attn_q_norm.weight"] = (F32, qn)
+    t["blk.0.attn_k_norm.weight"] = (F32, kn)
+    m = O.OracleModel(hp, t)
+    try:
+        pos = 6
+        x = f32(rng.standard_normal(E))
+        m.x_view()[:] = x
+        m.forward_layer(0, pos)
+        k, v = m.kv_view()
+        got_k, got_v, got_q = k[0, pos].copy(), v[0, pos].copy(), m.q_view().copy()
+    finally:
+        m.close()
+    xq = O.quantize_q8_0(O.rmsnorm(x, t["blk.0.attn_norm.weight"][1], hp.rms_eps))
+    qp = gemv(t, "blk.0.attn_q.weight", xq, H * HD, E) + t["blk.0.attn_q.bias"][1]
+    kp = gemv(t, "blk.0.attn_k.weight", xq, KVH * HD, E) + t["blk.0.attn_k.bias"][1]
+    vp = gemv(t, "blk.0.attn_v.weight", xq, KVH * HD, E) + t["blk.0.attn_v.bias"][1]
+    c, s = rope_tab(hp)
+    eps = hp.rms_eps
+    before = (O.rope(O.rmsnorm_heads(qp, qn, H, HD, eps), pos, H, HD, c, s),
+              O.rope(O.rmsnorm_heads(kp, kn, KVH, HD, eps), pos, KVH, HD, c, s))
+    after = (O.rmsnorm_heads(O.rope(qp, pos, H, HD, c, s), qn, H, HD, eps),
+             O.rmsnorm_heads(O.rope(kp, pos, KVH, HD, c, s), kn, KVH, HD, eps))
+    plain = (O.rope(qp, pos, H, HD, c, s), O.rope(kp, pos, KVH, HD, c, s))
+    return (got_q, got_k, got_v), vp, before, after, plain
+
+
+def test_qk_norm_before_rope():
+    (q, k, v), vp, before, after, plain = qk_norm_case(1, seed=31)
+    assert np.array_equal(q, before[0]) and np.array_equal(k, before[1])
+    assert np.array_equal(v, vp)  # V: bias only, no norm
+    # the orders differ once RoPE rotates (position 6) and the weights vary
+    assert not np.allclose(before[1], after[1], atol=1e-3)
+    assert not np.allclose(before[1], plain[1], atol=1e-3)
+
+
+def test_qk_norm_after_rope():
+    (q, k, v), vp, before, after, plain = qk_norm_case(2, seed=33)
+    assert np.array_equal(q, after[0]) and np.array_equal(k, after[1])
+    assert np.array_equal(v, vp)
+    assert not np.allclose(after[0], before[0], atol=1e-3)
+
+
+def test_qk_norm_weights_ignored_without_order():
+    (q, k, v), vp, before, after, plain = qk_norm_case(0, seed=35)
+    assert np.array_equal(q, plain[0]) and np.array_equal(k, plain[1])
+
+
+def test_qk_norm_batch_rows():
+    """llama_forward_batch's order (:1388-1403) on a switched-off layer: every
+    new cache row is the closed form of its own GEMM row, for both orders."""
+    for order in (1, 2):
+        hp = HP(n_ctx=16)
+        hp.qk_norm_order = order
+        t = random_model(hp, seed=41 + order)
+        switch_off(t, hp)
+        rng = np.random.default_rng(50 + order)
+        HD, KVH, E = hp.head_dim, hp.n_kv_heads, hp.n_embd
+        kn = f32(rng.uniform(0.3, 3.0, HD))
+        t["blk.0.attn_q_norm.weight"] = (F32, f32(rng.uniform(0.3, 3.0, HD)))
+        t["blk.0.attn_k_norm.weight"] = (F32, kn)
+        m = O.OracleModel(hp, t)
+        try:
+            pos0, toks = 2, [5, 60, 33]
+            m.forward_batch(toks, pos0)
+            k, _ = m.kv_view()
+            an = t["blk.0.attn_norm.weight"][1]
+            xqs = [O.quantize_q8_0(O.rmsnorm(embed_row(t, tok, E), an, hp.rms_eps)) for tok in toks]
+            K = O.gemm_q4k_q8(t["blk.0.attn_k.weight"][1], np.concatenate(xqs), KVH * HD,
+                              len(toks), E)
+            c, s = rope_tab(hp)
+            for i in range(len(toks)):
+                kp = K[i] + t["blk.0.attn_k.bias"][1]
+                p = pos0 + i
+                if order == 1:
+                    want = O.rope(O.rmsnorm_heads(kp, kn, KVH, HD, hp.rms_eps), p, KVH, HD, c, s)
+                else:
+                    want = O.rmsnorm_heads(O.rope(kp, p, KVH, HD, c, s), kn, KVH, HD, hp.rms_eps)
+                assert np.array_equal(k[0, p], want), (order, i)
+        finally:
+            m.close()
