@@ -230,7 +230,7 @@ PROBES = [(0, "plain_read"), (1, "mfma_operand_layout"), (2, "rows16_x_64B"), (3
           (4, "contiguous_same_lanes"), (5, "contiguous_lds_exchange"), (6, "lds_tile_natural_stride"),
           (7, "lds_tile_rotated"), (8, "sync_none"), (9, "sync_atomic"), (10, "sync_release_fence_atomic"),
           (11, "sync_threadfence_atomic"), (12, "lastarrive_32_counters"),
-          (13, "lastarrive_1_counter")]
+          (13, "lastarrive_1_counter"), (14, "empty_kernel_1_wg"), (15, "empty_kernel_1024_wgs")]
 
 
 def probe_run(ctx, reps=20):

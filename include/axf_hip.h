@@ -276,7 +276,8 @@ int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t byte
  * the atomic, __threadfence and the atomic; 12-13 the last-arriver reduction
  * (write-through partials, an agent-scope atomic per workgroup on one of 32
  * group counters (12) or on one counter (13), the last arriver of a group
- * summing 32 partials) (8-13: bufs unused).  *ms = elapsed
+ * summing 32 partials); 14-15 an empty kernel of 1 or 1024 workgroups (the
+ * cost of a launch in a replayed graph) (8-15: bufs unused).  *ms = elapsed
  * milliseconds of reps passes over the n buffers. */
 int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
                         int reps, float* ms);

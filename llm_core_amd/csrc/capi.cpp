@@ -633,7 +633,7 @@ int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t byte
 int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
                         int reps, float* ms) {
     AXF_CHECK_CTX(ctx);
-    AXF_REQUIRE(probe >= 0 && probe <= 13 && n > 0 && reps > 0 && ms, "bad arguments");
+    AXF_REQUIRE(probe >= 0 && probe <= 15 && n > 0 && reps > 0 && ms, "bad arguments");
     if (probe <= 7) {
         AXF_REQUIRE(bufs && rows >= 16, "probes 0-7 need buffers of rows >= 16 rows");
         for (int i = 0; i < n; i++) AXF_REQUIRE(bufs[i] && aligned(bufs[i], 16), "buffer misaligned");
