@@ -5,6 +5,8 @@ for bit; fp32 reductions within |gpu - ref| <= 1e-4 + 1e-3*|ref| (the
 north-star GEMV tolerance) unless a tighter bound is stated."""
 import ctypes as C
 
+import functools
+
 import numpy as np
 import pytest
 
@@ -180,18 +182,25 @@ def test_gemv_rejects_bad_arguments(ctx):
 # ---------------------------------------------------------------------------
 
 GEMM_CASES = [(11008, 4096, 1), (11008, 4096, 4), (1024, 4096, 16), (512, 4096, 64),
+              (11008, 4096, 16), (11008, 4096, 64),  # config 4 at full size
               (75, 11008, 5), (33, 256, 9), (40, 512, 17), (300, 1024, 33), (64, 768, 130),
               # the fp16 matrix-core kernel (65+ tokens): ragged 128-row and 64-token tiles
               (300, 1024, 200), (520, 2048, 65), (1100, 4096, 96)]
 
 
-@pytest.mark.parametrize("path", [None, 1, 2, 3], ids=["auto", "dot4", "mfma", "stream"])
-@pytest.mark.parametrize("rows,cols,T", GEMM_CASES)
-def test_gemm_q4k_q8(ctx, rows, cols, T, path):
+@functools.lru_cache(maxsize=2)
+def gemm_case_data(rows, cols, T):
+    """Weights, Q8_0 activations and the oracle's product, shared by the four paths."""
     W = weights(Q4K, rows, cols, 4)
     X = np.random.default_rng(T).standard_normal(T * cols).astype(np.float32)
     XQ = O.quantize_q8_0(X)
-    want = O.gemm_q4k_q8(W, XQ, rows, T, cols)
+    return W, XQ, O.gemm_q4k_q8(W, XQ, rows, T, cols)
+
+
+@pytest.mark.parametrize("path", [None, 1, 2, 3], ids=["auto", "dot4", "mfma", "stream"])
+@pytest.mark.parametrize("rows,cols,T", GEMM_CASES)
+def test_gemm_q4k_q8(ctx, rows, cols, T, path):
+    W, XQ, want = gemm_case_data(rows, cols, T)
     dW, dX, dY = ctx.upload(W), ctx.upload(XQ), ctx.alloc(T * rows * 4)
     ctx.write(dY, np.full(T * rows, np.nan, np.float32))  # every output must be written
     ctx.gemm_q4k_q8(dY, dW, dX, rows, T, cols, O.row_bytes(Q4K, cols), path=path)
@@ -233,7 +242,9 @@ GEMM6_CASES = [(4096, 4096, 1), (4096, 11008, 4), (512, 11008, 9), (2048, 2048, 
                (40, 512, 8), (300, 1024, 33), (256, 2048, 64), (64, 768, 130), (75, 512, 12),
                (90, 768, 24), (6, 256, 8),
                # the wider tiles: 64x64 (ragged rows and tokens), 32x32, 16x16
-               (4096, 768, 256), (4100, 768, 250), (2048, 1280, 128), (2040, 1280, 120)]
+               (4096, 768, 256), (4100, 768, 250), (2048, 1280, 128), (2040, 1280, 120),
+               # the 7B down projection at config-4 token counts
+               (4096, 11008, 16), (4096, 11008, 64)]
 
 
 def _gemm6_want(W, XQ, rows, cols, T):
