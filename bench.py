@@ -230,7 +230,10 @@ PROBES = [(0, "plain_read"), (1, "mfma_operand_layout"), (2, "rows16_x_64B"), (3
           (4, "contiguous_same_lanes"), (5, "contiguous_lds_exchange"), (6, "lds_tile_natural_stride"),
           (7, "lds_tile_rotated"), (8, "sync_none"), (9, "sync_atomic"), (10, "sync_release_fence_atomic"),
           (11, "sync_threadfence_atomic"), (12, "lastarrive_32_counters"),
-          (13, "lastarrive_1_counter"), (14, "empty_kernel_1_wg"), (15, "empty_kernel_1024_wgs")]
+          (13, "lastarrive_1_counter"), (14, "empty_kernel_1_wg"), (15, "empty_kernel_1024_wgs"),
+          (16, "nine_lanes_per_block_7rows_16blocks"), (17, "nine_lanes_per_block_7rows_8blocks"),
+          (18, "nine_lanes_per_block_contiguous"), (19, "nine_lanes_per_block_7rows_8blocks_hdr")]
+LOAD_PROBES = set(range(8)) | {16, 17, 18, 19}
 
 
 def probe_run(ctx, reps=20):
@@ -247,7 +250,7 @@ def probe_run(ctx, reps=20):
         reps = 1
     out = {}
     for probe, name in PROBES:
-        seq = bufs * GEMV_ROUNDS if probe <= 7 else [bufs[0]] * 64
+        seq = bufs * GEMV_ROUNDS if probe in LOAD_PROBES else [bufs[0]] * 64
         ctx.bench_probe(probe, seq, rows, 1)
         us = ctx.bench_probe(probe, seq, rows, reps) * 1000.0 / (reps * len(seq))
         out[name] = round(us, 3)

@@ -277,7 +277,11 @@ int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t byte
  * (write-through partials, an agent-scope atomic per workgroup on one of 32
  * group counters (12) or on one counter (13), the last arriver of a group
  * summing 32 partials); 14-15 an empty kernel of 1 or 1024 workgroups (the
- * cost of a launch in a replayed graph) (8-15: bufs unused).  *ms = elapsed
+ * cost of a launch in a replayed graph) (8-15: bufs unused); 16-17 nine lanes
+ * per block (16-byte piece p of the block), block i of seven rows per
+ * instruction, 16 or 8 blocks per lane; 18 nine lanes per block over seven
+ * whole rows (1008 contiguous bytes per instruction); 19 as 17 with each lane
+ * also loading its block's header.  *ms = elapsed
  * milliseconds of reps passes over the n buffers. */
 int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
                         int reps, float* ms);

@@ -343,11 +343,25 @@ __device__ __forceinline__ void rec_put(uint32_t* rec, int b, const uint32_t (&q
     r[18 + slot] = QT == kQ4K ? (uint32_t)(lo + hi) : (((uint32_t)lo & 0xffffu) | ((uint32_t)hi << 16));
 }
 
-// 256-thread staging: one Q8_0 block per thread and step (after the weight loads)
+// Staging: one Q8_0 block per thread and step.  With Q8_0 input the block of
+// the first step (b = threadIdx.x) was loaded into pre[] (d, 8 qs dwords)
+// before the weight loads, so it is staged while the weights stream in (a
+// load issued after them could only be consumed once they had all arrived:
+// loads complete in order); the blocks of later steps (K > 32 * NT) are
+// loaded here.
 template <int QT, int NT, int ACT>
-__device__ __forceinline__ void stage_act(uint32_t* rec, const QGemvArgs& a) {
+__device__ __forceinline__ void stage_act(uint32_t* rec, const QGemvArgs& a,
+                                          const uint32_t (&pre)[9]) {
     const int nblk = a.nb * QK_K / 32;
-    for (int b = threadIdx.x; b < nblk; b += NT) {
+    int b0 = threadIdx.x;
+    if (ACT == (int)QAct::Q8) {
+        if (b0 < nblk) {
+            const uint32_t q[8] = {pre[1], pre[2], pre[3], pre[4], pre[5], pre[6], pre[7], pre[8]};
+            rec_put<QT>(rec, b0, q, __uint_as_float(pre[0]));
+        }
+        b0 += NT;
+    }
+    for (int b = b0; b < nblk; b += NT) {
         uint32_t q[8];
         float d;
         if (ACT == (int)QAct::Q8) {
@@ -552,6 +566,16 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
         dx[4] = make_uint4(ld4(pa), ld4(pb), 0u, 0u);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // Q8_0 input staged through LDS: this thread's first block, ahead of the weights
+    uint32_t pre[9];
+    if constexpr (ACT == (int)QAct::Q8 && !DIRECT) {
+        if ((int)threadIdx.x < a.nb * (QK_K / 32)) {
+            const uint8_t* p = a.xq8 + (size_t)threadIdx.x * Q8_0_BYTES;
+#pragma unroll
+            for (int k = 0; k < 9; k++) pre[k] = ld4(p + 4 * k);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     float4 xv[KPT], wv[KPT];
     const int n4 = a.nb * (QK_K / 4);
@@ -612,7 +636,7 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
         else if constexpr (REG)
             stage_regs<QT, NT, KPT, ACT>(rec, xv, wv, n4, a.eps, red);
         else
-            stage_act<QT, NT, ACT>(rec, a);
+            stage_act<QT, NT, ACT>(rec, a, pre);
         if constexpr (!DIRECT) __syncthreads();
     };
 
@@ -635,6 +659,8 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
         }
         __builtin_amdgcn_sched_barrier(0);
         stage();
+        // nothing that waits for the weights above the workgroup barrier
+        __builtin_amdgcn_sched_barrier(0);
         // every unit is computed on clamped (valid) data and its contribution
         // selected, so no load is sunk into a branch
 #pragma unroll
@@ -696,6 +722,7 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
         }
         __builtin_amdgcn_sched_barrier(0);
         stage();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
             const bool live = rl + i * LPR < nunits;

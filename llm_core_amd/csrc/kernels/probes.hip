@@ -186,6 +186,51 @@ __global__ __launch_bounds__(512) void k_probe_lds(const uint8_t* W, int rows, u
     if (a == kMagic) sink[0] = a;
 }
 
+// Nine lanes per Q4_K block (lane 9b+p loads 16-byte piece p of its block:
+// the header for p = 0, qs bytes 16(p-1).. for p > 0), seven rows per wave
+// (lanes 0-62; lane 63 repeats lane 54's piece).  Each load instruction
+// covers block i of seven rows: 7 x 144 contiguous bytes.  NL blocks per
+// lane; 16 / NL waves share a row set and split its blocks.  H: every lane
+// also loads its block's header (nine lanes per address).
+template <int NL, bool H>
+__global__ __launch_bounds__(256) void k_probe_r7(const uint8_t* W, int rows, uint32_t* sink) {
+    constexpr int WPR = kPrNb / NL, RPW = 7 * 4 / WPR;  // waves per row set, rows per workgroup
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int bl = min(lane / 9, 6), p = lane == 63 ? 0 : lane - 9 * (lane / 9);
+    const int rset = wave / WPR, kpart = wave % WPR;
+    const long row = min((long)blockIdx.x * RPW + rset * 7 + bl, (long)rows - 1);
+    const uint8_t* base = W + row * kPrRow + (long)kpart * NL * Q4K_BYTES;
+    uint4 v[NL], h[H ? NL : 1];
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        v[i] = ld16(base + i * Q4K_BYTES + 16 * p);
+        if constexpr (H) h[i] = ld16(base + i * Q4K_BYTES);
+    }
+    uint32_t a = 0;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        a ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+        if constexpr (H) a += h[i].x ^ h[i].w;
+    }
+    if (a == kMagic) sink[0] = a;
+}
+
+// Nine lanes per block over consecutive blocks: a wave owns 7 rows (16128
+// contiguous bytes); instruction i covers blocks 7i..7i+6, lane l (< 63)
+// loads bytes 1008 i + 16 l of the region
+__global__ __launch_bounds__(256) void k_probe_c7(const uint8_t* W, int rows, uint32_t* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long row0 = min((long)blockIdx.x * 28 + wave * 7, (long)rows - 7);
+    const uint8_t* base = W + row0 * kPrRow + 16 * min(lane, 62);
+    uint4 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = ld16(base + 1008 * i);
+    uint32_t a = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) a ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    if (a == kMagic) sink[0] = a;
+}
+
 // 1024 workgroups each write a 520-byte partial (130 floats); MODE 0: nothing
 // more; 1: one device-scope atomic add per workgroup; 2: an agent-scope
 // release fence, then the atomic; 3: __threadfence, then the atomic.
@@ -248,9 +293,23 @@ size_t probe_scratch_bytes() { return 256 + 4096 + (size_t)1024 * 130 * 4 + 32 *
 hipError_t launch_probe(int probe, const void* buf, int rows, void* scratch, hipStream_t st) {
     const auto* W = static_cast<const uint8_t*>(buf);
     auto* sink = static_cast<uint32_t*>(scratch);
-    if (probe <= 7 && (rows < 16 || !W)) return hipErrorInvalidValue;
+    const bool loads = probe <= 7 || (probe >= 16 && probe <= 19);
+    if (loads && (rows < 16 || !W)) return hipErrorInvalidValue;
     const unsigned tiles = (unsigned)((rows + 15) / 16);
     switch (probe) {
+        case 16:
+            hipLaunchKernelGGL((k_probe_r7<16, false>), dim3((rows + 27) / 28), dim3(256), 0, st, W,
+                               rows, sink);
+            break;
+        case 17:
+            hipLaunchKernelGGL((k_probe_r7<8, false>), dim3((rows + 13) / 14), dim3(256), 0, st, W,
+                               rows, sink);
+            break;
+        case 18: hipLaunchKernelGGL(k_probe_c7, dim3((rows + 27) / 28), dim3(256), 0, st, W, rows, sink); break;
+        case 19:
+            hipLaunchKernelGGL((k_probe_r7<8, true>), dim3((rows + 13) / 14), dim3(256), 0, st, W,
+                               rows, sink);
+            break;
         case 0:
             hipLaunchKernelGGL(k_probe_plain, dim3(2048), dim3(256), 0, st, W,
                                (long)rows * kPrRow / 16, sink);
