@@ -389,10 +389,13 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_mfma_q4k(
 //   * per sub-block: one int8 MFMA (A = token x from LDS, B = the nibbles),
 //     S*sc by a 24-bit multiply, dx by an fp32 FMA, d per block, the min term
 //     by two v_mfma_f32_16x16x4f32 per block, as in the ring kernel above;
+//   * the blocks of the K range are computed in order, each as soon as its
+//     own loads have arrived (the loop is unrolled; a loop that moved the
+//     later blocks' registers down a slot per iteration waited for all of
+//     them before the first block's compute ended);
 //   * with gridDim.y > 1 each workgroup writes its partial tiles to scratch,
-//     and the last of a row group's workgroups to finish (a counter per row
-//     group, reset by that workgroup) sums the partials in K order: results
-//     are deterministic whatever the finishing order.
+//     and k_gemm_splitk_sum adds them in K order: results are deterministic
+//     whatever the finishing order.
 // ---------------------------------------------------------------------------
 template <int RT, int KB, int TT>
 struct Rx {
@@ -474,31 +477,26 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_q4k_rx(
     v4f_t acc[TT], macc[TT];
 #pragma unroll
     for (int w = 0; w < TT; w++) acc[w] = macc[w] = v4f_t{0.f, 0.f, 0.f, 0.f};
-    // One block per iteration (a runtime loop keeps the compiler from
-    // scheduling all blocks' operands at once); block b's weights are in
-    // P[0] / hdr[0], the later blocks' move down one slot per iteration.
-#pragma unroll 1
+    // Blocks in order, unrolled: block b's compute waits only for block b's
+    // loads (and the earlier ones), so it starts while the later blocks are
+    // still arriving.  A scheduling fence between blocks keeps the compiler
+    // from building several blocks' operands at once.
+#pragma unroll
     for (int b = 0; b < KB; b++) {
         // lane g holds chunk g (pieces 0..3 = bytes 8j..8j+7 of qs 32g..32g+31);
         // afterwards Q[c] = bytes 8g..8g+7 of chunk c
         uint32_t Q[4][2];
 #pragma unroll
         for (int e = 0; e < 2; e++) {
-            const auto r02 = __builtin_amdgcn_permlane32_swap(P[0][0][e], P[0][2][e], false, false);
-            const auto r13 = __builtin_amdgcn_permlane32_swap(P[0][1][e], P[0][3][e], false, false);
+            const auto r02 = __builtin_amdgcn_permlane32_swap(P[b][0][e], P[b][2][e], false, false);
+            const auto r13 = __builtin_amdgcn_permlane32_swap(P[b][1][e], P[b][3][e], false, false);
             const auto r01 = __builtin_amdgcn_permlane16_swap(r02[0], r13[0], false, false);
             const auto r23 = __builtin_amdgcn_permlane16_swap(r02[1], r13[1], false, false);
             Q[0][e] = r01[0]; Q[1][e] = r01[1];
             Q[2][e] = r23[0]; Q[3][e] = r23[1];
         }
-        const uint4 h = hdr[0];
+        const uint4 h = hdr[b];
         const bool lv = kb0 + b < nb;
-#pragma unroll
-        for (int k = 0; k + 1 < KB; k++) {
-            hdr[k] = hdr[k + 1];
-#pragma unroll
-            for (int c = 0; c < 4; c++) { P[k][c][0] = P[k + 1][c][0]; P[k][c][1] = P[k + 1][c][1]; }
-        }
         const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
         const uint32_t sc03 = h.y & 0x3f3f3f3fu;
         const uint32_t sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
@@ -534,6 +532,13 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_q4k_rx(
             acc[w] = lv ? a2 : acc[w];
             macc[w] = lv ? m2 : macc[w];
         }
+        // the block's results are final here (not sunk towards the stores)
+#pragma unroll
+        for (int w = 0; w < TT; w++) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) asm volatile("" : "+v"(acc[w][ii]), "+v"(macc[w][ii]));
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (o < rows) {
         float* dst = S == 1 ? Y : part + (size_t)ks * T * rows;
