@@ -232,8 +232,9 @@ PROBES = [(0, "plain_read"), (1, "mfma_operand_layout"), (2, "rows16_x_64B"), (3
           (11, "sync_threadfence_atomic"), (12, "lastarrive_32_counters"),
           (13, "lastarrive_1_counter"), (14, "empty_kernel_1_wg"), (15, "empty_kernel_1024_wgs"),
           (16, "nine_lanes_per_block_7rows_16blocks"), (17, "nine_lanes_per_block_7rows_8blocks"),
-          (18, "nine_lanes_per_block_contiguous"), (19, "nine_lanes_per_block_7rows_8blocks_hdr")]
-LOAD_PROBES = set(range(8)) | {16, 17, 18, 19}
+          (18, "nine_lanes_per_block_contiguous"), (19, "nine_lanes_per_block_7rows_8blocks_hdr"),
+          (20, "four_lanes_per_block_row_per_wave")]
+LOAD_PROBES = set(range(8)) | {16, 17, 18, 19, 20}
 
 
 def probe_run(ctx, reps=20):

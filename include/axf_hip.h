@@ -281,7 +281,8 @@ int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t byte
  * per block (16-byte piece p of the block), block i of seven rows per
  * instruction, 16 or 8 blocks per lane; 18 nine lanes per block over seven
  * whole rows (1008 contiguous bytes per instruction); 19 as 17 with each lane
- * also loading its block's header.  *ms = elapsed
+ * also loading its block's header; 20 four lanes per block, one row per wave
+ * (lane 4q+j: block q's header and qs bytes 16j and 64+16j).  *ms = elapsed
  * milliseconds of reps passes over the n buffers. */
 int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
                         int reps, float* ms);

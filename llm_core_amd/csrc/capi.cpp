@@ -633,7 +633,7 @@ int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t byte
 int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
                         int reps, float* ms) {
     AXF_CHECK_CTX(ctx);
-    AXF_REQUIRE(probe >= 0 && probe <= 19 && n > 0 && reps > 0 && ms, "bad arguments");
+    AXF_REQUIRE(probe >= 0 && probe <= 20 && n > 0 && reps > 0 && ms, "bad arguments");
     const bool loads = probe <= 7 || probe >= 16;  // load-pattern probes read the buffers
     if (loads) {
         AXF_REQUIRE(bufs && rows >= 16, "load probes need buffers of rows >= 16 rows");

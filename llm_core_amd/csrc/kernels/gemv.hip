@@ -99,16 +99,6 @@ __device__ __forceinline__ void stage_q8_q4k(uint32_t* rec, const uint8_t* xq8, 
     }
 }
 
-// F32 activation, padded: element i at float index i + 4*(i >> shift).
-template <int shift, int NT = kThreads>
-__device__ __forceinline__ void stage_f32(float* xs, const float* x, int K) {
-    for (int i4 = threadIdx.x; i4 < K / 4; i4 += NT) {
-        const float4 v = reinterpret_cast<const float4*>(x)[i4];
-        const int i = 4 * i4;
-        *reinterpret_cast<float4*>(xs + i + 4 * (i >> shift)) = v;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // High nibbles of four Q4_K bytes for v_dot4_i32_i8 without a shift: byte
 // (q & 0xf0) ^ 0x80 read as int8 is 16*(h - 8) (one v_bitop3_b32), so a dot4
@@ -202,28 +192,58 @@ __global__ __launch_bounds__(NT) void k_gemv_q4k_f32(float* __restrict__ y,
     const int nchunks = 4 * nb;
     const long row0 = ((long)blockIdx.x * (NT / 64) + wave) * (RPP * NR) + rg;
 
+    // The first PRE float4s of x this thread stages, loaded before the
+    // weights: a load issued after them could only be consumed once they had
+    // all arrived (loads complete in order), and the barrier below would
+    // then wait for the whole weight stream.
+    constexpr int PRE = (16 * LPR * CPL + NT - 1) / NT < 4 ? (16 * LPR * CPL + NT - 1) / NT : 4;
+    const int n4 = nb * (QK_K / 4);
+    // (in a block of its own, so that the loads are not moved down to the
+    // stores that use them)
+    float4 xpre[PRE];
+#pragma unroll
+    for (int k = 0; k < PRE; k++) xpre[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if ((int)threadIdx.x < n4) {
+#pragma unroll
+        for (int k = 0; k < PRE; k++)
+            xpre[k] = reinterpret_cast<const float4*>(x)[min((int)threadIdx.x + NT * k, n4 - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // weight loads from clamped (in-range) addresses, unconditional so that the
+    // compiler's wait counts stay exact; chunks past the row are computed on
+    // those bytes and skipped below, rows past the end are never stored
     uint4 hdr[NR][CPL], qa[NR][CPL], qb[NR][CPL];
 #pragma unroll
     for (int n = 0; n < NR; n++) {
-        const long row = row0 + (long)n * RPP;
+        const long row = min(row0 + (long)n * RPP, (long)rows - 1);
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
-            const int c = rl + i * LPR;
-            if (row < rows && c < nchunks) {
-                const uint8_t* blk = W + row * row_bytes + (long)(c >> 2) * Q4K_BYTES;
-                const int part = c & 3;
-                hdr[n][i] = ld16(blk);
-                qa[n][i] = ld16(blk + 16 + 32 * part);
-                qb[n][i] = ld16(blk + 32 + 32 * part);
-            } else {
-                hdr[n][i] = make_uint4(0, 0, 0, 0);
-                qa[n][i] = qb[n][i] = make_uint4(0, 0, 0, 0);
-            }
+            const int c = min(rl + i * LPR, nchunks - 1);
+            const uint8_t* blk = W + row * row_bytes + (long)(c >> 2) * Q4K_BYTES;
+            const int part = c & 3;
+            hdr[n][i] = ld16(blk);
+            qa[n][i] = ld16(blk + 16 + 32 * part);
+            qb[n][i] = ld16(blk + 32 + 32 * part);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
 
-    stage_f32<6, NT>(xs, x, nb * QK_K);  // 64-float chunk c at float offset 68*c
+    // 64-float chunk c at float offset 68*c (an index past K rewrites the
+    // last float4 with the value loaded for it, clamped above)
+    if ((int)threadIdx.x < n4) {
+#pragma unroll
+        for (int k = 0; k < PRE; k++) {
+            const int i4 = min((int)threadIdx.x + NT * k, n4 - 1);
+            *reinterpret_cast<float4*>(xs + 4 * i4 + 4 * (i4 >> 4)) = xpre[k];
+        }
+    }
+    for (int i4 = (int)threadIdx.x + NT * PRE; i4 < n4; i4 += NT) {
+        const float4 v = reinterpret_cast<const float4*>(x)[i4];
+        *reinterpret_cast<float4*>(xs + 4 * i4 + 4 * (i4 >> 4)) = v;
+    }
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
 
     float acc[NR];
 #pragma unroll
@@ -862,27 +882,48 @@ __global__ __launch_bounds__(kThreads) void k_gemv_q6k_f32(float* __restrict__ y
     const int nchunks = 4 * nb;
     const long row0 = ((long)blockIdx.x * kWaves + wave) * (RPP * NR) + rg;
 
+    // the first PRE float4s of x this thread stages, ahead of the weights (as
+    // in k_gemv_q4k_f32)
+    constexpr int PRE = (16 * LPR * CPL + kThreads - 1) / kThreads < 4
+                            ? (16 * LPR * CPL + kThreads - 1) / kThreads : 4;
+    const int n4 = nb * (QK_K / 4);
+    float4 xpre[PRE];
+#pragma unroll
+    for (int k = 0; k < PRE; k++) xpre[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if ((int)threadIdx.x < n4) {
+#pragma unroll
+        for (int k = 0; k < PRE; k++)
+            xpre[k] = reinterpret_cast<const float4*>(x)[min((int)threadIdx.x + kThreads * k, n4 - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // unconditional loads from clamped addresses (as in k_gemv_q4k_f32)
     Q6Chunk wk[NR][CPL];
 #pragma unroll
     for (int n = 0; n < NR; n++) {
-        const long row = row0 + (long)n * RPP;
+        const long row = min(row0 + (long)n * RPP, (long)rows - 1);
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
-            const int c = rl + i * LPR;
-            if (row < rows && c < nchunks) {
-                load_q6_chunk<LPR == 64>(W + row * row_bytes + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 8; k++) wk[n][i].ql[k] = wk[n][i].qh[k] = 0;
-#pragma unroll
-                for (int k = 0; k < 4; k++) wk[n][i].sc[k] = 0;
-                wk[n][i].dbits = 0;
-            }
+            const int c = min(rl + i * LPR, nchunks - 1);
+            load_q6_chunk<LPR == 64>(W + row * row_bytes + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
         }
     }
 
-    stage_f32<5>(xs, x, nb * QK_K);  // 32-float part p at float offset 36*p
+    __builtin_amdgcn_sched_barrier(0);
+    // 32-float part p at float offset 36*p
+    if ((int)threadIdx.x < n4) {
+#pragma unroll
+        for (int k = 0; k < PRE; k++) {
+            const int i4 = min((int)threadIdx.x + kThreads * k, n4 - 1);
+            *reinterpret_cast<float4*>(xs + 4 * i4 + 4 * (i4 >> 3)) = xpre[k];
+        }
+    }
+    for (int i4 = (int)threadIdx.x + kThreads * PRE; i4 < n4; i4 += kThreads) {
+        const float4 v = reinterpret_cast<const float4*>(x)[i4];
+        *reinterpret_cast<float4*>(xs + 4 * i4 + 4 * (i4 >> 3)) = v;
+    }
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
 
     float acc[NR];
 #pragma unroll

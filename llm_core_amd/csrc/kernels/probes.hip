@@ -231,6 +231,19 @@ __global__ __launch_bounds__(256) void k_probe_c7(const uint8_t* W, int rows, ui
     if (a == kMagic) sink[0] = a;
 }
 
+// Four lanes per block, one row per wave: lane (q = l / 4, j = l % 4) loads
+// block q's header and qs bytes 16j.. and 64+16j.. (adjacent lanes read
+// adjacent 16 bytes: each instruction touches about 28 of the row's 64-byte
+// sectors, against about 64 for the half-block units).  512 threads = 8 rows.
+__global__ __launch_bounds__(512) void k_probe_quad(const uint8_t* W, int rows, uint32_t* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 2, j = lane & 3;
+    const long row = min((long)blockIdx.x * 8 + wave, (long)rows - 1);
+    const uint8_t* blk = W + row * kPrRow + q * Q4K_BYTES;
+    const uint4 h = ld16(blk), a = ld16(blk + 16 + 16 * j), b = ld16(blk + 80 + 16 * j);
+    const uint32_t x = h.x ^ h.y ^ h.z ^ h.w ^ a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w;
+    if (x == kMagic) sink[0] = x;
+}
+
 // 1024 workgroups each write a 520-byte partial (130 floats); MODE 0: nothing
 // more; 1: one device-scope atomic add per workgroup; 2: an agent-scope
 // release fence, then the atomic; 3: __threadfence, then the atomic.
@@ -293,7 +306,7 @@ size_t probe_scratch_bytes() { return 256 + 4096 + (size_t)1024 * 130 * 4 + 32 *
 hipError_t launch_probe(int probe, const void* buf, int rows, void* scratch, hipStream_t st) {
     const auto* W = static_cast<const uint8_t*>(buf);
     auto* sink = static_cast<uint32_t*>(scratch);
-    const bool loads = probe <= 7 || (probe >= 16 && probe <= 19);
+    const bool loads = probe <= 7 || (probe >= 16 && probe <= 20);
     if (loads && (rows < 16 || !W)) return hipErrorInvalidValue;
     const unsigned tiles = (unsigned)((rows + 15) / 16);
     switch (probe) {
@@ -305,6 +318,7 @@ hipError_t launch_probe(int probe, const void* buf, int rows, void* scratch, hip
             hipLaunchKernelGGL((k_probe_r7<8, false>), dim3((rows + 13) / 14), dim3(256), 0, st, W,
                                rows, sink);
             break;
+        case 20: hipLaunchKernelGGL(k_probe_quad, dim3((rows + 7) / 8), dim3(512), 0, st, W, rows, sink); break;
         case 18: hipLaunchKernelGGL(k_probe_c7, dim3((rows + 27) / 28), dim3(256), 0, st, W, rows, sink); break;
         case 19:
             hipLaunchKernelGGL((k_probe_r7<8, true>), dim3((rows + 13) / 14), dim3(256), 0, st, W,
