@@ -79,26 +79,6 @@ static inline bool pair_cfg(int nb) { return nb > 8 && nb <= 16; }
 // Activation staging
 // ---------------------------------------------------------------------------
 
-// Q4_K chunk record c: Q8_0 blocks 2c, 2c+1 -> {qs0[8 dw], qs1[8 dw], d0, d1, sum0, sum1}.
-__device__ __forceinline__ void stage_q8_q4k(uint32_t* rec, const uint8_t* xq8, int nchunks) {
-    for (int c = threadIdx.x; c < nchunks; c += kThreads) {
-        uint32_t* r = rec + 20 * c;
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint8_t* b = xq8 + (size_t)(2 * c + j) * Q8_0_BYTES;
-            int s = 0;
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const uint32_t q = ld4(b + 4 + 4 * k);
-                r[8 * j + k] = q;
-                s = dot4((int)q, 0x01010101, s);
-            }
-            r[16 + j] = ld4(b);
-            r[18 + j] = (uint32_t)s;
-        }
-    }
-}
-
 // ---------------------------------------------------------------------------
 // High nibbles of four Q4_K bytes for v_dot4_i32_i8 without a shift: byte
 // (q & 0xf0) ^ 0x80 read as int8 is 16*(h - 8) (one v_bitop3_b32), so a dot4
@@ -361,6 +341,59 @@ __device__ __forceinline__ void rec_put(uint32_t* rec, int b, const uint32_t (&q
 #pragma unroll
     for (int k = 4; k < 8; k++) hi = dot4((int)q[k], 0x01010101, hi);
     r[18 + slot] = QT == kQ4K ? (uint32_t)(lo + hi) : (((uint32_t)lo & 0xffffu) | ((uint32_t)hi << 16));
+}
+
+// Token-tile staging for the dot4 GEMMs: unit u = (token t = u / nblk, Q8_0
+// block b = u % nblk) of TT tokens (token t0 + min(t, nt - 1): every record
+// valid).  The first PB units of a thread are loaded into registers before the
+// weight loads (q8pre_load, in a block of its own so the loads are not moved
+// down to their stores) and written to LDS after them (q8pre_store), so the
+// workgroup barrier does not wait for the weight stream; the rest are loaded
+// and written in q8pre_store.
+template <int PB>
+struct Q8Pre {
+    uint32_t w[PB][9];  // d, then the 8 qs dwords
+};
+template <int PB>
+__device__ __forceinline__ void q8pre_load(Q8Pre<PB>& p, const uint8_t* XQ8, size_t tok_bytes,
+                                           int t0, int nt, int nblk, int total) {
+#pragma unroll
+    for (int k = 0; k < PB; k++)
+#pragma unroll
+        for (int i = 0; i < 9; i++) p.w[k][i] = 0u;
+    if ((int)threadIdx.x < total) {
+#pragma unroll
+        for (int k = 0; k < PB; k++) {
+            const int u = min((int)threadIdx.x + kThreads * k, total - 1), t = u / nblk;
+            const uint8_t* b8 =
+                XQ8 + (size_t)(t0 + min(t, nt - 1)) * tok_bytes + (size_t)(u - t * nblk) * Q8_0_BYTES;
+#pragma unroll
+            for (int i = 0; i < 9; i++) p.w[k][i] = ld4(b8 + 4 * i);
+        }
+    }
+}
+template <int QT, int PB>
+__device__ __forceinline__ void q8pre_store(const Q8Pre<PB>& p, uint32_t* rec, const uint8_t* XQ8,
+                                            size_t tok_bytes, int t0, int nt, int nblk, int total,
+                                            int nchunks) {
+    if ((int)threadIdx.x < total) {
+#pragma unroll
+        for (int k = 0; k < PB; k++) {
+            const int u = min((int)threadIdx.x + kThreads * k, total - 1), t = u / nblk;
+            const uint32_t q[8] = {p.w[k][1], p.w[k][2], p.w[k][3], p.w[k][4],
+                                   p.w[k][5], p.w[k][6], p.w[k][7], p.w[k][8]};
+            rec_put<QT>(rec + (size_t)t * 20 * nchunks, u - t * nblk, q, __uint_as_float(p.w[k][0]));
+        }
+    }
+    for (int u = (int)threadIdx.x + kThreads * PB; u < total; u += kThreads) {
+        const int t = u / nblk;
+        const uint8_t* b8 =
+            XQ8 + (size_t)(t0 + min(t, nt - 1)) * tok_bytes + (size_t)(u - t * nblk) * Q8_0_BYTES;
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = ld4(b8 + 4 + 4 * i);
+        rec_put<QT>(rec + (size_t)t * 20 * nchunks, u - t * nblk, q, __uint_as_float(ld4(b8)));
+    }
 }
 
 // Staging: one Q8_0 block per thread and step.  With Q8_0 input the block of
@@ -994,31 +1027,31 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q4k_q8(float* __restrict__ Y,
     const int nchunks = 4 * nb;
     const long row0 = ((long)blockIdx.x * kWaves + wave) * (RPP * NR) + rg;
     const size_t tok_bytes = (size_t)nb * 8 * Q8_0_BYTES;
+    const int nblk = 8 * nb, total = TT * nblk;
+    Q8Pre<2> pre;
+    q8pre_load(pre, XQ8, tok_bytes, t0, nt, nblk, total);
+    __builtin_amdgcn_sched_barrier(0);
 
+    // weight loads from clamped addresses, unconditional (exact wait counts);
+    // chunks past the row are skipped below, rows past the end never stored
     uint4 hdr[NR][CPL], qa[NR][CPL], qb[NR][CPL];
 #pragma unroll
     for (int n = 0; n < NR; n++) {
-        const long row = row0 + (long)n * RPP;
+        const long row = min(row0 + (long)n * RPP, (long)rows - 1);
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
-            const int c = rl + i * LPR;
-            if (row < rows && c < nchunks) {
-                const uint8_t* blk = W + row * row_bytes + (long)(c >> 2) * Q4K_BYTES;
-                const int part = c & 3;
-                hdr[n][i] = ld16(blk);
-                qa[n][i] = ld16(blk + 16 + 32 * part);
-                qb[n][i] = ld16(blk + 32 + 32 * part);
-            } else {
-                hdr[n][i] = make_uint4(0, 0, 0, 0);
-                qa[n][i] = qb[n][i] = make_uint4(0, 0, 0, 0);
-            }
+            const int c = min(rl + i * LPR, nchunks - 1);
+            const uint8_t* blk = W + row * row_bytes + (long)(c >> 2) * Q4K_BYTES;
+            const int part = c & 3;
+            hdr[n][i] = ld16(blk);
+            qa[n][i] = ld16(blk + 16 + 32 * part);
+            qb[n][i] = ld16(blk + 32 + 32 * part);
         }
     }
-#pragma unroll
-    for (int t = 0; t < TT; t++)
-        if (t < nt) stage_q8_q4k(rec + (size_t)t * 20 * nchunks, XQ8 + (size_t)(t0 + t) * tok_bytes,
-                                 nchunks);
+    __builtin_amdgcn_sched_barrier(0);
+    q8pre_store<kQ4K>(pre, rec, XQ8, tok_bytes, t0, nt, nblk, total, nchunks);
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
 
     float acc[NR][TT];
 #pragma unroll
@@ -1103,6 +1136,10 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q6k_q8(float* __restrict__ Y,
     const int nchunks = 4 * nb;
     const long row0 = ((long)blockIdx.x * kWaves + wave) * (RPP * NR) + rg;
     const size_t tok_bytes = (size_t)nb * 8 * Q8_0_BYTES;
+    const int nblk = 8 * nb, total = TT * nblk;
+    Q8Pre<2> pre;
+    q8pre_load(pre, XQ8, tok_bytes, t0, nt, nblk, total);
+    __builtin_amdgcn_sched_barrier(0);
 
     Q6Chunk wk[NR][CPL];
 #pragma unroll
@@ -1114,19 +1151,11 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q6k_q8(float* __restrict__ Y,
             load_q6_chunk<LPR == 64>(W + row * row_bytes + (long)(c >> 2) * Q6K_BYTES, c, wk[n][i]);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
     // token records: the clamped token t0 + min(t, nt - 1), so every record is valid
-    for (int t = 0; t < TT; t++) {
-        const uint8_t* xq = XQ8 + (size_t)(t0 + min(t, nt - 1)) * tok_bytes;
-        uint32_t* rt = rec + (size_t)t * 20 * nchunks;
-        for (int b = threadIdx.x; b < nb * 8; b += kThreads) {
-            uint32_t q[8];
-            const uint8_t* p = xq + (size_t)b * Q8_0_BYTES;
-#pragma unroll
-            for (int k = 0; k < 8; k++) q[k] = ld4(p + 4 + 4 * k);
-            rec_put<kQ6K>(rt, b, q, __uint_as_float(ld4(p)));
-        }
-    }
+    q8pre_store<kQ6K>(pre, rec, XQ8, tok_bytes, t0, nt, nblk, total, nchunks);
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
 
     float acc[NR][TT];
 #pragma unroll
