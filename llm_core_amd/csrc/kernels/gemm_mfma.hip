@@ -423,10 +423,11 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_q4k_rx(
     const int cend = min(G::CPT, (nb - kb0) * 18) - 1;
     const int row0 = ((int)blockIdx.x * RT + wave) * kTile;
     const int o = row0 + col;
+    const int t0 = (int)blockIdx.z * kTile * TT;  // first token of this token group
 
     // activations: slot (u, j) with u = 16*tile + t, j < CPT: chunk j of
-    // token u's K range (tokens past T repeat token T-1).  Issued before the
-    // weights, so that they are waited for first.
+    // token t0 + u's K range (tokens past T repeat token T-1).  Issued before
+    // the weights, so that they are waited for first.
     uint4 xr[G::XPW];
 #pragma unroll
     for (int k = 0; k < G::XPW; k++) {
@@ -435,7 +436,7 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_q4k_rx(
             const int slot = piece * 64 + lane;
             const int u = min(slot / G::TSTR, kTile * TT - 1);
             const int j = min(slot - (slot / G::TSTR) * G::TSTR, cend);
-            const int tok = min(u, T - 1);
+            const int tok = min(t0 + u, T - 1);
             xr[k] = ld16(XQ8 + (size_t)tok * tok_bytes + (size_t)kb0 * 8 * Q8_0_BYTES + 16 * j);
         }
     }
@@ -547,7 +548,7 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_q4k_rx(
             const v4f_t v = acc[w] - macc[w];
 #pragma unroll
             for (int ii = 0; ii < 4; ii++) {
-                const int tok = kTile * w + 4 * g + ii;
+                const int tok = t0 + kTile * w + 4 * g + ii;
                 if (tok < T) dst[(size_t)tok * rows + o] = v[ii];
             }
         }
@@ -1266,14 +1267,19 @@ size_t gemm_mfma_scratch_bytes(int T, int nb) {
     return (size_t)nb * 8 * tp * (32 + 4 + 4);
 }
 
-// Register-weights kernel (k_gemm_q4k_rx): 4 row tiles per workgroup; K
-// ranges of 4 blocks for up to 16 tokens, 2 blocks for up to 64 (the LDS holds
-// all token tiles of a K range).
+// Register-weights kernel (k_gemm_q4k_rx): 4 row tiles per workgroup, K
+// ranges of 4 blocks (gridDim.y of them), TT token tiles per workgroup and
+// the token groups over gridDim.z.  Up to 16 tokens one tile; 17-32 two tiles
+// in one group; 33-64 one tile per group (2-4 groups): on the 11008x4096
+// matrix at 64 tokens 27.5 us against 29.5 us for four tiles in one group
+// over 2-block K ranges (twice the split-K partials), the best of the shapes
+// measured (2-8 blocks, 1-4 tiles).
 constexpr int kRxRT = 4;
+constexpr int kRxKB = 4;
 
-static int rx_kb(int T) { return T <= 16 ? 4 : 2; }
+static int rx_tt(int T) { return T > 16 && T <= 32 ? 2 : 1; }
 static int rx_row_groups(int rows) { return (rows + kTile * kRxRT - 1) / (kTile * kRxRT); }
-static int rx_splits(int T, int nb) { return (nb + rx_kb(T) - 1) / rx_kb(T); }
+static int rx_splits(int, int nb) { return (nb + kRxKB - 1) / kRxKB; }
 
 bool gemm_stream_q4k_ok(int T, int nb, int rows) {
     return T >= 1 && T <= kGemmStreamMaxT && nb >= 1 && rows >= 1 &&
@@ -1290,21 +1296,18 @@ hipError_t launch_gemm_stream_q4k_q8(float* Y, const void* W, const void* XQ8, i
     if (!gemm_stream_q4k_ok(T, nb, rows)) return hipErrorInvalidValue;
     // 16-byte loads of weights and activations
     if (((uintptr_t)W | (uintptr_t)XQ8 | (uintptr_t)row_bytes) & 15) return hipErrorInvalidValue;
+    const int TT = rx_tt(T);
     const int S = rx_splits(T, nb);
     if (S > 1 && scratch == nullptr) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)rx_row_groups(rows), (unsigned)rx_splits(T, nb));
+    const int ntg = (T + kTile * TT - 1) / (kTile * TT);
+    const dim3 grid((unsigned)rx_row_groups(rows), (unsigned)S, (unsigned)ntg);
     const auto* w = static_cast<const uint8_t*>(W);
     const auto* x = static_cast<const uint8_t*>(XQ8);
     auto* pt = static_cast<float*>(scratch);
-    const int TT = (T + kTile - 1) / kTile;
     if (TT == 1)
-        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, 4, 1>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
-    else if (TT == 2)
-        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, 2, 2>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
-    else if (TT == 3)
-        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, 2, 3>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
+        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, kRxKB, 1>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
     else
-        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, 2, 4>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
+        hipLaunchKernelGGL((k_gemm_q4k_rx<kRxRT, kRxKB, 2>), grid, dim3(kRxRT * 64), 0, st, Y, w, x, pt, rows, nb, row_bytes, T);
     if (S > 1) {
         const int n = T * rows;
         const bool vec = n % 4 == 0 && ((uintptr_t)Y & 15) == 0 && ((uintptr_t)pt & 15) == 0;

@@ -47,7 +47,7 @@ def test_noalloc_gemm_falls_back_to_the_ring_kernel(ctx):
     from llm_core_amd import _ffi, hip
 
     fn = _ffi.lib.axf_hip_gemm_q4k_q8_noalloc
-    rows, cols, T = 11008, 4096, 64   # split-K partials: 8 x 64 x 11008 x 4 B > 8 MiB
+    rows, cols, T = 11008, 4096, 64   # split-K partials: 4 x 64 x 11008 x 4 B > 8 MiB
     rb = hip.row_bytes(hip.AXF_TYPE_Q4_K, cols)
     W = hip.synth_weight(hip.AXF_TYPE_Q4_K, rows, cols, 71)
     dW = ctx.upload(W)
