@@ -15,8 +15,8 @@
 //                  Splits past the current position exit at once, so the grid
 //                  can be sized for the whole context and replayed.
 //   k_attn_combine grid (n_heads).  out = sum_j o_j e^(m_j - M) / sum_j l_j e^(m_j - M),
-//                  M = max_j m_j, over the non-empty splits, plus the Q8_0
-//                  blocks of out for the next projection.
+//                  M = max_j m_j (found first), over the non-empty splits,
+//                  plus the Q8_0 blocks of out for the next projection.
 // s = dot(q_h, k_t) / sqrt(HD).  The split containing the current position
 // also RoPEs the new key (+ bias), stores it and the new value (+ bias) to the
 // caches, and uses them for that row.
@@ -325,17 +325,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_split(AttnArgs a) {
 }
 
 // One workgroup per query head.  Thread t owns float4 column c = t % (HD/4)
-// and the splits js, js + NJS, ... (js = t / (HD/4)); it loads m, l and o of
-// those splits in one pass and merges them online (running max, rescaled sums).
-// The NJS partial states of a column are then merged in LDS:
-//   out = sum_j o_j e^(m_j - M) / sum_j l_j e^(m_j - M),  M = max_j m_j.
+// and the splits js, js + NJS, ... (js = t / (HD/4)).  The loads of its first
+// U splits (m, l, o) are issued before anything else.  The workgroup first
+// finds M = max_j m_j over the non-empty splits (wave maxima through LDS), so
+// every split's weight e^(m_j - M) is independent of the others: each thread
+// sums w_j o_j and w_j l_j over its splits, and the NJS partial sums of a
+// column are added in a fixed order in LDS:
+//   out = sum_j o_j e^(m_j - M) / sum_j l_j e^(m_j - M).
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(AttnArgs a) {
     constexpr int C4 = HD / 4;
     constexpr int NJS = kAttnThreads / C4;
     constexpr int U = 4;  // splits loaded per step
     __shared__ float4 accs[NJS][C4];
-    __shared__ float ms[NJS], ls[NJS];
+    __shared__ float ls[NJS];
+    __shared__ float wmax[kAttnWaves];
 
     const int h = blockIdx.x, tok = blockIdx.y;
     const int p = (a.pos_dev ? *a.pos_dev : a.pos) + tok;
@@ -343,58 +347,68 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(AttnArgs a) {
     const float* ph = a.part + ((size_t)tok * a.n_heads + h) * a.nsplit * (HD + 2);
     const int c = threadIdx.x % C4, js = threadIdx.x / C4;
 
-    float m = -INFINITY, l = 0.f;
+    // this thread's first U splits; splits past ns re-read split ns-1 (written)
+    // and are dropped below
+    float mj[U], lj[U];
+    float4 oj[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const float* pj = ph + (size_t)min(js + u * NJS, ns - 1) * (HD + 2);
+        mj[u] = pj[0];
+        lj[u] = pj[1];
+        oj[u] = make_float4(pj[2 + 4 * c], pj[3 + 4 * c], pj[4 + 4 * c], pj[5 + 4 * c]);
+    }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (js + u * NJS < ns) mloc = fmaxf(mloc, mj[u]);
+    for (int jj = js + U * NJS; jj < ns; jj += NJS) mloc = fmaxf(mloc, ph[(size_t)jj * (HD + 2)]);
+    const float wm = wave_max_bcast(mloc);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = wm;
+    __syncthreads();
+    float M = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; w++) M = fmaxf(M, wmax[w]);
+
+    float l = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j0 = js; j0 < ns; j0 += U * NJS) {
-        float mj[U], lj[U];
-        float4 oj[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (js + u * NJS < ns) {
+            const float w = expf(mj[u] - M);
+            l = fmaf(lj[u], w, l);
+            acc = fma4(w, oj[u], acc);
+        }
+    }
+    // contexts beyond U * NJS splits
+    for (int j0 = js + U * NJS; j0 < ns; j0 += U * NJS) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int jj = j0 + u * NJS;
-            mj[u] = -INFINITY;
-            lj[u] = 0.f;
-            oj[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (jj < ns) {
-                const float* pj = ph + (size_t)jj * (HD + 2);
-                mj[u] = pj[0];
-                lj[u] = pj[1];
-                oj[u] = make_float4(pj[2 + 4 * c], pj[3 + 4 * c], pj[4 + 4 * c], pj[5 + 4 * c]);
-            }
+            const float* pj = ph + (size_t)min(j0 + u * NJS, ns - 1) * (HD + 2);
+            mj[u] = pj[0];
+            lj[u] = pj[1];
+            oj[u] = make_float4(pj[2 + 4 * c], pj[3 + 4 * c], pj[4 + 4 * c], pj[5 + 4 * c]);
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
             if (j0 + u * NJS < ns) {
-                const float mn = fmaxf(m, mj[u]);
-                const float so = expf(m - mn);  // 0 while m is -inf
-                const float sj = expf(mj[u] - mn);
-                l = fmaf(l, so, lj[u] * sj);
-                acc = make_float4(fmaf(acc.x, so, oj[u].x * sj), fmaf(acc.y, so, oj[u].y * sj),
-                                  fmaf(acc.z, so, oj[u].z * sj), fmaf(acc.w, so, oj[u].w * sj));
-                m = mn;
+                const float w = expf(mj[u] - M);
+                l = fmaf(lj[u], w, l);
+                acc = fma4(w, oj[u], acc);
             }
         }
     }
     accs[js][c] = acc;
-    if (c == 0) {
-        ms[js] = m;
-        ls[js] = l;
-    }
+    if (c == 0) ls[js] = l;
     __syncthreads();
     if (threadIdx.x < C4) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int q = 0; q < NJS; q++) M = fmaxf(M, ms[q]);
         float L = 0.f;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int q = 0; q < NJS; q++) {
-            if (ls[q] > 0.f) {
-                const float w = expf(ms[q] - M);
-                L = fmaf(ls[q], w, L);
-                const float4 aq = accs[q][c];
-                o = make_float4(fmaf(aq.x, w, o.x), fmaf(aq.y, w, o.y), fmaf(aq.z, w, o.z),
-                                fmaf(aq.w, w, o.w));
-            }
+            L += ls[q];
+            const float4 aq = accs[q][c];
+            o = make_float4(o.x + aq.x, o.y + aq.y, o.z + aq.z, o.w + aq.w);
         }
         const float inv = 1.f / L;
         o = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
