@@ -375,15 +375,17 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_mfma_q4k(
 // loads of 8 bytes per lane in the MFMA operand layout do not (8.5 us), and
 // every extra vector-memory instruction per wave and block (activation
 // fragments, dx) costs about 0.35 us.  So:
-//   * a workgroup owns RT row tiles (wave w: 16 rows) and a K range of KB
-//     blocks (split-K over gridDim.y = ceil(nb / KB) workgroups);
+//   * a workgroup owns RT row tiles (wave w: 16 rows), a K range of KB
+//     blocks (split-K over gridDim.y = ceil(nb / KB) workgroups) and TT
+//     token tiles of 16 tokens starting at token 16 * TT * blockIdx.z (the
+//     token groups over gridDim.z);
 //   * lane (col, g) loads its row's block header and qs bytes 32g..32g+31
 //     (chunk g: sub-blocks 2g and 2g+1) as 16-byte loads, all up front;
 //     two rounds of v_permlane32_swap / v_permlane16_swap turn "lane g holds
 //     chunk g" into "lane g holds bytes 8g..8g+7 of every chunk", the B
 //     operand layout of v_mfma_i32_16x16x32_i8;
-//   * the workgroup stages its K range of the activations once, 16 tokens at
-//     a time, into LDS (per token a contiguous run of Q8_0 records, copied by
+//   * the workgroup stages its K range of its tokens' activations once, 16
+//     tokens at a time, into LDS (per token a contiguous run of Q8_0 records, copied by
 //     16-byte loads; one pad chunk per token spreads the tokens over the
 //     banks), then derives dx and dx*bsum per (record, token) from it;
 //   * per sub-block: one int8 MFMA (A = token x from LDS, B = the nibbles),
@@ -394,8 +396,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_mfma_q4k(
 //     later blocks' registers down a slot per iteration waited for all of
 //     them before the first block's compute ended);
 //   * with gridDim.y > 1 each workgroup writes its partial tiles to scratch,
-//     and k_gemm_splitk_sum adds them in K order: results are deterministic
-//     whatever the finishing order.
+//     and k_gemm_splitk_sum(4) adds them in K order: results are
+//     deterministic whatever the finishing order.
 // ---------------------------------------------------------------------------
 template <int RT, int KB, int TT>
 struct Rx {
