@@ -365,7 +365,10 @@ def test_rope_bitexact(ctx, hd, n_heads):
 
 @pytest.mark.parametrize("seq,H,KVH,hd", [(1, 16, 2, 128), (5, 16, 2, 128), (64, 4, 4, 64),
                                           (65, 8, 2, 128), (1024, 16, 2, 128), (2048, 32, 32, 128),
-                                          (300, 4, 1, 256)])
+                                          (300, 4, 1, 256),
+                                          # more splits than one pass of the combine's threads
+                                          # (32 at head dim 128, 64 at 64)
+                                          (3000, 8, 2, 128), (4200, 4, 4, 64)])
 def test_attention(ctx, seq, H, KVH, hd):
     rng = np.random.default_rng(seq + H)
     q = rng.standard_normal(H * hd).astype(np.float32)
