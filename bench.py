@@ -85,6 +85,12 @@ def c5_run(gpu, hp, e2e_too=True):
     prompt (mean of 3 after one untimed), then 512 + 128 greedy tokens timed on
     the host clock (decode from position 512; cache rows re-written)."""
     pf_ms = gpu.bench_prefill(512, reps=3)
+    if e2e_too and under_profiler():
+        # generation captures HIP graphs (the decode step); rocprofv3's kernel
+        # tracing has crashed the host process in that capture, so under it
+        # the prefill is timed alone
+        log("config 5 end-to-end generation skipped under rocprofv3 (it captures HIP graphs)")
+        e2e_too = False
     if not e2e_too:
         log(f"prefill 512 tokens: {pf_ms:.1f} ms ({512 / pf_ms * 1e3:.0f} tok/s)")
         return {"prefill_512_ms": round(pf_ms, 2), "prefill_tok_s": round(512 / pf_ms * 1e3, 1)}
@@ -224,41 +230,6 @@ def read_probe(ctx, nbytes, n_copies, reps=40):
     return {"bytes": nbytes, "n_copies": n_copies, "us": round(us, 3),
             "GBs": round(nbytes / (us * 1e-6) / 1e9, 1), "best_launch": f"{wgs}x256 threads, "
             f"{unroll} x 16 B per thread in flight", "sweep_unroll_wgs_us": sweep}
-
-
-PROBES = [(0, "plain_read"), (1, "mfma_operand_layout"), (2, "rows16_x_64B"), (3, "gemv_halfblock_units"),
-          (4, "contiguous_same_lanes"), (5, "contiguous_lds_exchange"), (6, "lds_tile_natural_stride"),
-          (7, "lds_tile_rotated"), (8, "sync_none"), (9, "sync_atomic"), (10, "sync_release_fence_atomic"),
-          (11, "sync_threadfence_atomic"), (12, "lastarrive_32_counters"),
-          (13, "lastarrive_1_counter"), (14, "empty_kernel_1_wg"), (15, "empty_kernel_1024_wgs"),
-          (16, "nine_lanes_per_block_7rows_16blocks"), (17, "nine_lanes_per_block_7rows_8blocks"),
-          (18, "nine_lanes_per_block_contiguous"), (19, "nine_lanes_per_block_7rows_8blocks_hdr"),
-          (20, "four_lanes_per_block_row_per_wave")]
-LOAD_PROBES = set(range(8)) | {16, 17, 18, 19, 20}
-
-
-def probe_run(ctx, reps=20):
-    """The design probes of axf_hip_bench_probe: load patterns over the 25.4 MB
-    of an 11008x4096 Q4_K matrix (rotating copies, as the GEMV), and the cost of
-    grid-wide synchronisation (1024 workgroups writing 520-byte partials)."""
-    rows = 11008
-    nbytes = rows * 2304
-    n_copies = math.ceil((2 * MALL_BYTES + (96 << 20)) / nbytes)
-    bufs = [ctx.alloc(nbytes) for _ in range(n_copies)]
-    for b in bufs:
-        ctx.write(b, np.zeros(16, np.uint8))
-    if under_profiler():
-        reps = 1
-    out = {}
-    for probe, name in PROBES:
-        seq = bufs * GEMV_ROUNDS if probe in LOAD_PROBES else [bufs[0]] * 64
-        ctx.bench_probe(probe, seq, rows, 1)
-        us = ctx.bench_probe(probe, seq, rows, reps) * 1000.0 / (reps * len(seq))
-        out[name] = round(us, 3)
-        log(f"probe {name}: {us:.3f} us per launch")
-    for b in bufs:
-        b.free()
-    return {"bytes": nbytes, "n_copies": n_copies, "us_per_launch": out}
 
 
 def cpu_model() -> str:
@@ -459,7 +430,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="approximate CPU seconds spent on the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill", "c3", "probes"],
+    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill", "c3"],
                     default="all")
     ap.add_argument("--eager", action="store_true",
                     help="direct launches instead of captured-graph replay in every timing "
@@ -513,9 +484,6 @@ def main() -> int:
             + ("running under rocprofv3" if under_profiler() else "--eager"))
     out: dict = {"launch": "eager" if eager else "hip-graph replay"}
 
-    if args.only == "probes":  # design probes alone (not a bench line)
-        print(json.dumps({"probes": probe_run(ctx)}))
-        return 0
     if args.only == "c3":  # config 3 layer alone (not a bench line)
         print(json.dumps({"c3_qwen25_3b_layer_decode": c3_run(ctx, args.warmup, args.steps)}))
         return 0

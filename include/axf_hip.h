@@ -262,30 +262,6 @@ int axf_hip_bench_gemv(axf_ctx* ctx, int kind, float* y, const void* const* W_li
  * one launch of a given size can read, the ceiling the GEMVs are compared to. */
 int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t bytes, int unroll,
                        int wgs, int reps, float* ms);
-/* Benchmark helper (no reference counterpart): design probes over Q4_K rows of
- * 2304 bytes (K = 4096; each buffer rows * 2304 bytes, 16-byte aligned,
- * rows >= 16), timed as axf_hip_bench_read times its reads.  probe: 0 plain
- * contiguous read; 1 the int8 MFMA operand layout loaded directly (16 rows x
- * 32 bytes per instruction); 2 16 rows x 64 contiguous bytes per instruction;
- * 3 the GEMV's half-block units (32 lanes per row, 16 bytes in every 72); 4 the
- * same bytes loaded contiguously by the same lanes; 5 as 4, then exchanged
- * into the unit layout through LDS; 6 a 16-row tile staged in LDS at its
- * natural stride, read in the MFMA operand layout; 7 as 6 with the rows
- * rotated by chunks; 8-11 1024 workgroups writing 520-byte partials with no
- * synchronisation, a device-scope atomic per workgroup, a release fence and
- * the atomic, __threadfence and the atomic; 12-13 the last-arriver reduction
- * (write-through partials, an agent-scope atomic per workgroup on one of 32
- * group counters (12) or on one counter (13), the last arriver of a group
- * summing 32 partials); 14-15 an empty kernel of 1 or 1024 workgroups (the
- * cost of a launch in a replayed graph) (8-15: bufs unused); 16-17 nine lanes
- * per block (16-byte piece p of the block), block i of seven rows per
- * instruction, 16 or 8 blocks per lane; 18 nine lanes per block over seven
- * whole rows (1008 contiguous bytes per instruction); 19 as 17 with each lane
- * also loading its block's header; 20 four lanes per block, one row per wave
- * (lane 4q+j: block q's header and qs bytes 16j and 64+16j).  *ms = elapsed
- * milliseconds of reps passes over the n buffers. */
-int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
-                        int reps, float* ms);
 /* Benchmark helpers (no reference counterpart): eager != 0 makes
  * axf_hip_bench_gemv, axf_hip_bench_gemm and axf_llama_bench_decode on this
  * context launch every kernel directly instead of capturing and replaying a

@@ -154,7 +154,6 @@ SIGNATURES: dict[str, list] = {
     "axf_hip_bench_gemv": [vp, i32, vp, C.POINTER(vp), i32, vp, i32, i32, sz, i32, C.POINTER(f32)],
     "axf_hip_bench_set_eager": [vp, i32],
     "axf_hip_bench_read": [vp, C.POINTER(vp), i32, sz, i32, i32, i32, C.POINTER(f32)],
-    "axf_hip_bench_probe": [vp, i32, C.POINTER(vp), i32, i32, i32, C.POINTER(f32)],
     "axf_hip_bench_gemm": [vp, i32, vp, C.POINTER(vp), i32, vp, i32, i32, i32, sz, i32, i32,
                            C.POINTER(f32)],
     "axf_synth_normal": [vp, i64, u64, f32, f32],

@@ -36,7 +36,6 @@ SOURCES = [
     "kernels/attention.hip",
     "kernels/sample.hip",
     "kernels/gemv_misc.hip",
-    "kernels/probes.hip",
     "capi.cpp",
     "gemm_noalloc.cpp",
     "host/synth.cpp",

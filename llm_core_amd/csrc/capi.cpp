@@ -630,26 +630,6 @@ int axf_hip_bench_read(axf_ctx* ctx, const void* const* bufs, int n, size_t byte
     });
 }
 
-int axf_hip_bench_probe(axf_ctx* ctx, int probe, const void* const* bufs, int n, int rows,
-                        int reps, float* ms) {
-    AXF_CHECK_CTX(ctx);
-    AXF_REQUIRE(probe >= 0 && probe <= 20 && n > 0 && reps > 0 && ms, "bad arguments");
-    const bool loads = probe <= 7 || probe >= 16;  // load-pattern probes read the buffers
-    if (loads) {
-        AXF_REQUIRE(bufs && rows >= 16, "load probes need buffers of rows >= 16 rows");
-        for (int i = 0; i < n; i++) AXF_REQUIRE(bufs[i] && aligned(bufs[i], 16), "buffer misaligned");
-    }
-    void* scratch = nullptr;
-    int rc = ctx_scratch(ctx, probe_scratch_bytes(), &scratch);  // before any capture
-    if (rc) return rc;
-    // the counters of probes 12-13 start at 0 (each launch adds a multiple of
-    // the group size, so they need no reset afterwards)
-    AXF_HIP(hipMemsetAsync(scratch, 0, 256 + 4096, ctx->stream));
-    return bench_graph(ctx, __func__, n, reps, ms, [&](int i, hipStream_t st) {
-        return launch_probe(probe, loads ? bufs[i] : nullptr, rows, scratch, st);
-    });
-}
-
 int axf_hip_bench_set_eager(axf_ctx* ctx, int eager) {
     AXF_CHECK_CTX(ctx);
     ctx->bench_eager = eager ? 1 : 0;

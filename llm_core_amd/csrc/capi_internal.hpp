@@ -215,8 +215,6 @@ hipError_t launch_mul(float* y, const float* a, const float* b, int n, hipStream
 hipError_t launch_set_int(int* p, int v, hipStream_t st);
 // measurement kernel: read every 16-byte vector of [p, p + bytes) once
 // (unroll 1/2/4/8 vectors in flight per thread, wgs workgroups of 256)
-size_t probe_scratch_bytes();
-hipError_t launch_probe(int probe, const void* buf, int rows, void* scratch, hipStream_t st);
 hipError_t launch_stream_read(const void* p, size_t bytes, int unroll, int wgs, uint32_t* sink,
                               hipStream_t st);
 hipError_t launch_push_token(int* tokens, int* step, const int* tok, hipStream_t st);

@@ -159,6 +159,9 @@ __device__ __forceinline__ void q8_quant32(const float (&v)[32], uint32_t (&q)[8
     for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
     d = amax / 127.f;
     const float id = amax > 0.f ? 127.f / amax : 0.f;
+    // 0 < amax < 127/FLT_MAX: id = +inf, every product +-inf or NaN, which the
+    // reference's cvtps_epi32 turns into INT_MIN and its packs into -128
+    const bool ovf = __builtin_isinf(id);
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         uint32_t w = 0;
@@ -168,7 +171,7 @@ __device__ __forceinline__ void q8_quant32(const float (&v)[32], uint32_t (&q)[8
             r = fminf(fmaxf(r, -128.f), 127.f);
             w |= ((uint32_t)((int)r & 0xff)) << (8 * j);
         }
-        q[k] = w;
+        q[k] = ovf ? 0x80808080u : w;
     }
 }
 
@@ -243,9 +246,11 @@ __device__ __forceinline__ uint32_t rint_mul_bits(float a, float b) {
 
 // Q8_0 of one 32-value block held as float4 by 8 consecutive lanes
 // (sub = lane & 7): returns this lane's 4 packed int8 and, in d, the block scale.
-// Same bits as q8_quant32 on the block (for inputs that are not NaN): |v * id|
-// rounds to at most 127 (|v| <= amax), so the int8 saturation never applies
-// and rint_mul_bits' low byte is the int8 value.
+// Same bits as q8_quant32 on the block (for inputs that are not NaN): for a
+// finite id, |v * id| rounds to at most 127 (|v| <= amax), so the int8
+// saturation never applies and rint_mul_bits' low byte is the int8 value; an
+// infinite id (0 < amax < 127/FLT_MAX) gives -128 for every value, as the
+// reference's cvtps_epi32 + packs.
 __device__ __forceinline__ uint32_t q8_quant4(float4 v, float& d) {
     const float amax =
         max8_nonneg(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -257,7 +262,7 @@ __device__ __forceinline__ uint32_t q8_quant4(float4 v, float& d) {
     // operand's bytes, 4-7 the first's, 0x0c zero)
     const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);
     const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);
-    return lo | hi;
+    return __builtin_isinf(id) ? 0x80808080u : (lo | hi);
 }
 
 // Q4_K scale/min pair for sub-blocks j0 = 2*part and j1 = 2*part + 1 from the

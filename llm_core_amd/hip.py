@@ -197,13 +197,6 @@ class Context:
              reps, C.byref(ms))
         return ms.value
 
-    def bench_probe(self, probe: int, bufs, rows: int, reps: int) -> float:
-        """Milliseconds for reps passes of design probe `probe` (axf_hip_bench_probe)."""
-        arr = (C.c_void_p * len(bufs))(*[int(b) for b in bufs])
-        ms = C.c_float(0)
-        call("axf_hip_bench_probe", self.handle, probe, arr, len(bufs), rows, reps, C.byref(ms))
-        return ms.value
-
     def bench_set_eager(self, eager: bool) -> None:
         """Benchmark helpers launch directly instead of replaying captured graphs."""
         call("axf_hip_bench_set_eager", self.handle, 1 if eager else 0)

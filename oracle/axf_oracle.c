@@ -259,8 +259,18 @@ void orc_quantize_q8_0(orc_block_q8_0* y, const float* x, int k) {
         const float id = (amax > 0.f) ? 127.f / amax : 0.f;
         y[i].d = d;
         for (int j = 0; j < 32; j++) {
-            float r = rintf(src[j] * id);
-            int q = (r > 127.f) ? 127 : (r < -128.f) ? -128 : (int)r;
+            /* _mm256_cvtps_epi32 returns INT_MIN (the integer indefinite) for
+             * a product outside the int32 range, inf or NaN: 0 < amax < 127/FLT_MAX
+             * makes id = +inf and every product +-inf or NaN, so every value of
+             * such a block packs to -128 */
+            const float pr = src[j] * id;
+            int q;
+            if (!(fabsf(pr) < 2147483648.f)) {
+                q = -128;
+            } else {
+                const float r = rintf(pr);
+                q = (r > 127.f) ? 127 : (r < -128.f) ? -128 : (int)r;
+            }
             y[i].qs[j] = (int8_t)q;
         }
     }

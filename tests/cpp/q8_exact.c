@@ -6,7 +6,8 @@
  *      fma(r, RN(1/127), q0)  - every non-negative finite float, exhaustively;
  *   2. the int8 of rint(RN(v*id)) read as the low byte of RN(RN(v*id) + 1.5*2^23),
  *      without saturation - random blocks of several magnitudes, blocks whose
- *      products land on and next to halves, and amax = 0.
+ *      products land on and next to halves, amax = 0, and tiny blocks whose
+ *      127/amax overflows (every value -128, as cvtps_epi32 + packs).
  * Built with -ffp-contract=off so that products and sums round as written.
  * Prints "ok" and exits 0, or prints the first mismatch and exits 1. */
 #include <math.h>
@@ -26,18 +27,28 @@ static float div127(float a) {
 
 static uint32_t lcg(uint64_t* s) { *s = *s * 6364136223846793005ull + 1442695040888963407ull; return (uint32_t)(*s >> 33); }
 
-/* reference and shortcut quantisation of one block; returns 0 when equal */
+/* reference and shortcut quantisation of one block; returns 0 when equal.
+ * The reference's _mm256_cvtps_epi32 gives INT_MIN for a product that is not
+ * a finite int32 (the packs then give -128): with 0 < amax < 127/FLT_MAX the
+ * reciprocal overflows to +inf and every product is +-inf or NaN.  The
+ * shortcut selects -128 for the whole block when id is infinite. */
 static int block_check(const float* v) {
     float amax = 0.f;
     for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
     const float id = amax > 0.f ? 127.f / amax : 0.f;
     if (div127(amax) != amax / 127.f) return 1;
     for (int i = 0; i < 32; i++) {
-        float r = rintf(v[i] * id);
-        r = fminf(fmaxf(r, -128.f), 127.f);
-        const uint8_t want = (uint8_t)((int)r & 0xff);
+        const float pr = v[i] * id;
+        uint8_t want;
+        if (!(fabsf(pr) < 2147483648.f)) {
+            want = 0x80;
+        } else {
+            float r = rintf(pr);
+            r = fminf(fmaxf(r, -128.f), 127.f);
+            want = (uint8_t)((int)r & 0xff);
+        }
         const float p = v[i] * id;
-        const uint8_t got = (uint8_t)(bitsf(p + 12582912.f) & 0xff);
+        const uint8_t got = isinf(id) ? 0x80 : (uint8_t)(bitsf(p + 12582912.f) & 0xff);
         if (want != got) {
             printf("block mismatch: v=%a id=%a want %d got %d\n", v[i], id, (int8_t)want, (int8_t)got);
             return 1;
@@ -77,6 +88,15 @@ int main(void) {
     }
     for (int i = 0; i < 32; i++) v[i] = 0.f;
     if (block_check(v)) return 1;
+    /* tiny blocks: amax around 127/FLT_MAX (id overflows below it), subnormal
+     * values, and zeros beside them */
+    const float lim = 127.f / 3.40282347e38f;
+    const float tiny[] = {lim, nextafterf(lim, 0.f), nextafterf(lim, 1.f), lim * 0.5f,
+                          1.17549435e-38f, 1e-39f, 1.4e-45f, 2.8e-45f};
+    for (unsigned t = 0; t < sizeof tiny / sizeof tiny[0]; t++) {
+        for (int i = 0; i < 32; i++) v[i] = (i % 3 == 0) ? 0.f : (i % 3 == 1 ? tiny[t] : -tiny[t] * 0.5f);
+        if (block_check(v)) return 1;
+    }
     printf("ok\n");
     return 0;
 }

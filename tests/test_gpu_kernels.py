@@ -74,6 +74,16 @@ def test_quantize_q8_0_bitexact(ctx):
     x[63] = 127.0
     x[64:96] = 1e-3
     x[64] = 1e6
+    # tiny blocks: 127/amax overflows to +inf below amax = 127/FLT_MAX (every
+    # value -128, as the reference's cvtps_epi32 + packs), just above it, and
+    # subnormal values, each with zeros beside them
+    lim = np.float32(127.0) / np.finfo(np.float32).max
+    for b, m in enumerate([lim * np.float32(0.5), np.nextafter(lim, np.float32(1)),
+                           np.float32(1e-39), np.float32(3e-37)]):
+        blk = x[96 + 32 * b:128 + 32 * b]
+        blk[:] = 0
+        blk[1::3] = m
+        blk[2::3] = -m * np.float32(0.5)
     xd = ctx.upload(x)
     q = ctx.alloc(4096 // 32 * 36)
     ctx.quantize_q8_0(q, xd, 4096)

@@ -56,6 +56,27 @@ def test_quantize_q8_0(n):
     assert np.array_equal(O.quantize_q8_0(x), want)
 
 
+def test_quantize_q8_0_tiny_blocks():
+    """Blocks whose amax is near 127/FLT_MAX (127/amax overflows to +inf below
+    it), subnormal blocks, and zeros beside them: the reference's cvtps_epi32
+    returns INT_MIN for +-inf and NaN products, which its packs turn into -128."""
+    lim = np.float32(127.0) / np.finfo(np.float32).max
+    mags = [lim, np.nextafter(lim, np.float32(0)), np.nextafter(lim, np.float32(1)),
+            lim * np.float32(0.5), np.float32(1.17549435e-38), np.float32(1e-39),
+            np.float32(1.4e-45), np.float32(3e-37), np.float32(5e-37)]
+    x = np.zeros(32 * len(mags), np.float32)
+    for b, m in enumerate(mags):
+        blk = x[32 * b:32 * (b + 1)]
+        blk[1::3] = m
+        blk[2::3] = -np.float32(m) * np.float32(0.5)
+    want = np.empty(x.size // 32 * 36, np.uint8)
+    R.ref_quantize_q8_0(p(want), p(x), x.size)
+    got = O.quantize_q8_0(x)
+    assert np.array_equal(got, want)
+    q = want.reshape(-1, 36)[:, 4:].view(np.int8)
+    assert (q[3] == -128).all()  # lim / 2: the reciprocal overflows
+
+
 @pytest.mark.parametrize("rows,cols", SHAPES)
 def test_gemv_q4k_q8_all_reference_variants(rows, cols):
     W = blocks(O.Q4K, rows * cols // 256, 3 * rows + cols)
