@@ -199,7 +199,58 @@ def gemm_case(ctx, M, rows=11008, cols=4096, reps=20, seed=4, min_bytes=2 * MALL
     return res
 
 
-def read_probe(ctx, nbytes, n_copies, reps=40):
+def stage_bytes(model) -> dict:
+    """Algorithmic bytes of each decode stage of one layer (layer 0's tensors;
+    every layer has the same shapes) and of the head: weights, norm weights,
+    and for the attention the K and V rows read at the full context."""
+    hp = model.hp
+    t = model.tensors
+    nb = lambda name: t[name][1].nbytes if name in t else 0
+    b = "blk.0."
+    kve = hp.n_kv_heads * (hp.n_embd // hp.n_heads)
+    E = hp.n_embd
+    return {
+        1: nb(b + "attn_q.weight") + nb(b + "attn_k.weight") + nb(b + "attn_v.weight") + 8 * E,
+        2: 2 * hp.n_ctx * kve * 4,
+        3: nb(b + "attn_output.weight") + E // 32 * 36 + 8 * E,
+        4: nb(b + "ffn_gate.weight") + nb(b + "ffn_up.weight") + 8 * E + 4 * hp.ffn_dim,
+        5: nb(b + "ffn_down.weight") + 4 * hp.ffn_dim + 8 * E,
+        6: nb("output.weight") + 8 * E + 4 * hp.n_vocab,
+    }
+
+
+STAGE_NAMES = {1: "q|k|v (RMSNorm prologue)", 2: "attention split + combine",
+               3: "o (x +=)", 4: "gate|up (RMSNorm prologue, SwiGLU epilogue)",
+               5: "down (Q8_0 prologue, x +=)", 6: "head (RMSNorm prologue, argmax)"}
+
+
+def decode_stages(ctx, gpu, model, pos, reps=20):
+    """Each decode stage over all 32 layers (axf_llama_bench_stage: one graph,
+    the stage of layer 0, 1, ..., so consecutive launches stream different
+    weights), beside a plain read of the same byte count over rotating copies
+    measured in the same run."""
+    nbytes = stage_bytes(model)
+    if under_profiler():
+        reps = 1
+    out = {}
+    for st in range(1, 7):
+        ms = gpu.bench_stage(st, pos, 2)
+        ms = gpu.bench_stage(st, pos, reps)
+        us = ms * 1000.0 / (reps * model.hp.n_layer)
+        nb = nbytes[st]
+        rd = read_probe(ctx, nb // 16 * 16, max(1, math.ceil((2 * MALL_BYTES + (96 << 20)) / nb)),
+                        quick=True)
+        out[STAGE_NAMES[st]] = {"us": round(us, 3), "bytes": int(nb),
+                                "GBs": round(nb / (us * 1e-6) / 1e9, 1),
+                                "frac_of_peak": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                "read_us": rd["us"], "vs_read": round(rd["us"] / us, 4)}
+        log(f"decode stage {STAGE_NAMES[st]}: {us:.2f} us per layer, "
+            f"{nb / (us * 1e-6) / 1e9:.0f} GB/s over {nb / 1e6:.1f} MB; same-size read "
+            f"{rd['us']:.2f} us ({rd['GBs']:.0f} GB/s) -> {rd['us'] / us:.3f} of it")
+    return out
+
+
+def read_probe(ctx, nbytes, n_copies, reps=40, quick=False):
     """The plain streaming read (axf_hip_bench_read) of nbytes per launch over
     n_copies rotating buffers, swept over launch shapes (16-byte loads in
     flight per thread x workgroups of 256); the fastest shape is the read
@@ -209,12 +260,14 @@ def read_probe(ctx, nbytes, n_copies, reps=40):
     for b in bufs:  # contents do not matter; make them defined
         ctx.write(b, np.zeros(16, np.uint8))
     seq = bufs * GEMV_ROUNDS
+    if quick:  # about 20 ms of reads per shape
+        reps = int(min(40, max(3, 0.02 / (nbytes * len(seq) / 5e12))))
     if under_profiler():  # counters and traces need a few dispatches per shape, not timings
         reps = 1
     best, sweep = None, []
     one_each = -(-nbytes // (16 * 256))  # workgroups giving one vector per thread
     for unroll in (1, 2, 4, 8):
-        for wgs in (512, 1024, 2048, 4096, one_each):
+        for wgs in (512, 1024, 2048, 4096, 8192, one_each):
             if wgs * 256 * unroll * 16 > 2 * nbytes and wgs != one_each:
                 continue
             if wgs == one_each and unroll > 1:
@@ -442,6 +495,8 @@ def main() -> int:
                     help="leave out the config-3 layer and config-4 GEMM timings (shorter profiling runs)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="--only prefill: time the prefill alone (no graph-replayed generation)")
+    ap.add_argument("--skip-stages", action="store_true",
+                    help="leave out the per-stage decode timings and their same-size reads")
     ap.add_argument("--skip-c5", action="store_true",
                     help="leave out the config-5 prefill and end-to-end timing")
     ap.add_argument("--no-mall-warm", dest="mall_warm", action="store_false",
@@ -519,6 +574,11 @@ def main() -> int:
         log(f"gemv q4k x f32 4096x4096 (config 1): {c1['us_per_launch']:.2f} us, {c1['gbs']:.0f} GB/s")
         c2, _, _ = gemv_case(ctx, 1, hip.AXF_TYPE_Q6_K, 151936, 2048, max(4, args.gemv_reps // 4), 2)
         log(f"gemv q6k 151936x2048 (config 2 head): {c2['us_per_launch']:.2f} us, {c2['gbs']:.0f} GB/s")
+        rd1 = read_probe(ctx, c1["algorithmic_bytes"] // 16 * 16, c1["n_copies"], quick=True)
+        rd2 = read_probe(ctx, c2["algorithmic_bytes"] // 16 * 16, c2["n_copies"], quick=True)
+        for name, c, r in (("config 1", c1, rd1), ("config 2", c2, rd2)):
+            log(f"plain read of {r['bytes'] / 1e6:.1f} MB ({r['best_launch']}): {r['us']:.2f} us, "
+                f"{r['GBs']:.0f} GB/s; {name} GEMV at {r['us'] / c['us_per_launch']:.3f} of it")
         roof = {
             "bound": "hbm",
             "kernel": ROOF_KERNEL_ID,
@@ -545,8 +605,13 @@ def main() -> int:
             "copy_256MiB_d2d": cp,
             "c4_q4k_q8_gemm_11008x4096": c4,
             "q6k_q8_gemm_4096x11008": g6,
-            "c1_q4k_f32_4096x4096": {"us": round(c1["us_per_launch"], 3), "GBs": round(c1["gbs"], 1)},
-            "c2_q6k_q8_151936x2048": {"us": round(c2["us_per_launch"], 3), "GBs": round(c2["gbs"], 1)},
+            "c1_q4k_f32_4096x4096": {"us": round(c1["us_per_launch"], 3), "GBs": round(c1["gbs"], 1),
+                                     "read_us": rd1["us"],
+                                     "vs_read": round(rd1["us"] / c1["us_per_launch"], 4)},
+            "c2_q6k_q8_151936x2048": {"us": round(c2["us_per_launch"], 3), "GBs": round(c2["gbs"], 1),
+                                      "frac_of_peak": round(c2["gbs"] / HBM_PEAK_GBS, 4),
+                                      "read_us": rd2["us"],
+                                      "vs_read": round(rd2["us"] / c2["us_per_launch"], 4)},
             "c3_qwen25_3b_layer_decode": None if args.skip_c4 else c3_run(ctx),
         }
         if not args.no_cpu and not args.skip_c4:
@@ -595,6 +660,8 @@ def main() -> int:
         log(f"decode step @ctx {n_ctx}: {ms_step:.3f} ms -> {tok_s:.1f} tok/s; "
             f"{(w_bytes + kv_bytes) / (ms_step * 1e-3) / 1e9:.0f} GB/s over {(w_bytes + kv_bytes) / 1e9:.2f} GB")
         result = dict(ms_step=ms_step, tok_s=tok_s, w_bytes=w_bytes, kv_bytes=kv_bytes)
+        if not args.skip_stages:
+            result["stages"] = decode_stages(ctx, gpu, model, pos)
         # config 5 end to end: batched prefill of a 512-token prompt, then 128
         # greedy tokens (decode from position 512; rows of the cache re-written)
         if not args.skip_c5 and under_profiler():
@@ -666,6 +733,7 @@ def main() -> int:
             "roofline": roof,
             "cpu_baseline": result.get("cpu"),
             "c5_prefill_and_e2e": result.get("c5"),
+            "decode_stages_per_layer": result.get("stages"),
         }
         line.update(out)
     else:

@@ -468,6 +468,15 @@ int axf_llama_generate_sampled(axf_llama* m, const int32_t* prompt, int n_prompt
  * axf_llama_forward_batch calls on T synthetic tokens at positions 0..T-1,
  * after one untimed call (HIP events on the context stream). */
 int axf_llama_bench_prefill(axf_llama* m, int T, int reps, float* ms);
+/* Benchmark helper (no reference counterpart): one stage of the decode step
+ * (1 q|k|v GEMV with the RMSNorm prologue, 2 attention split + combine, 3 o
+ * GEMV with x +=, 4 gate|up GEMV with SwiGLU, 5 down GEMV with x +=, 6 the head
+ * with the greedy pick) enqueued for layers 0..n_layer-1 in turn (stage 6:
+ * n_layer times) at position `pos`, captured as one graph, replayed once
+ * untimed and `reps` times between HIP events (direct launches under
+ * axf_hip_bench_set_eager).  *ms = elapsed milliseconds of the reps passes.
+ * The buffers the stages read hold whatever the last step left. */
+int axf_llama_bench_stage(axf_llama* m, int stage, int pos, int reps, float* ms);
 /* Time `steps` graph-replayed decode steps, each at position `pos` (the
  * attention reads KV rows 0..pos; rows below pos must already be filled, row
  * pos is rewritten by every step), after `warmup` untimed steps; each step

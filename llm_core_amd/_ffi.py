@@ -209,6 +209,7 @@ SIGNATURES: dict[str, list] = {
     "axf_llama_forward_batch": [vp, vp, i32, i32],
     "axf_llama_bench_prefill": [vp, i32, i32, C.POINTER(f32)],
     "axf_llama_bench_decode": [vp, i32, i32, i32, C.POINTER(f32)],
+    "axf_llama_bench_stage": [vp, i32, i32, i32, C.POINTER(f32)],
 }
 
 _RESTYPES = {

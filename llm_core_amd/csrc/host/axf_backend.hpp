@@ -3,6 +3,7 @@
 // registry slot:
 //   IKernel / IBackend / BackendRegistry : include/axonforge/backend.hpp:18-104
 //   DType values (GGUF-compatible)        : include/axonforge/dtype.hpp:8-31
+//   dtype_element_size                    : dtype.hpp:34-51
 //   DeviceId / TensorStorage / Tensor     : common.hpp:9-33, memory.hpp:12-24, tensor.hpp
 //   OpType subset, AttributeMap           : graph.hpp:17-80
 // Only what the quantized decode path needs is declared here; names, argument
@@ -40,9 +41,29 @@ enum class DType : uint8_t {
     UNKNOWN = 255,
 };
 
-// Exact byte size of `numel` elements (gguf_tensor_nbytes, dtype.hpp:136-155;
-// Q8_0 here is the 36-byte activation block of q8_block.hpp).
-size_t tensor_nbytes(DType dtype, int64_t numel);
+// Bytes per element as the reference counts them (dtype_element_size,
+// dtype.hpp:34-51): exact for the plain types, 1 ("approx") for the
+// block-quantized Q8_0 / Q4_0 / Q5_0 / Q4_K_M / Q3_K_M / Q2_K and 0 for the
+// others (Q6_K included).  Tensor::nbytes() is numel times this; block
+// tensors carry their real size in their storage (Tensor::from_raw_blob).
+constexpr size_t dtype_element_size(DType dtype) noexcept {
+    switch (dtype) {
+        case DType::F32: return 4;
+        case DType::F16: return 2;
+        case DType::BF16: return 2;
+        case DType::Q8_0: return 1;
+        case DType::Q4_0: return 1;
+        case DType::Q5_0: return 1;
+        case DType::Q4_K_M: return 1;
+        case DType::Q3_K_M: return 1;
+        case DType::Q2_K: return 1;
+        case DType::I32: return 4;
+        case DType::I16: return 2;
+        case DType::I8: return 1;
+        case DType::BOOL: return 1;
+        default: return 0;
+    }
+}
 
 enum class DeviceType : uint8_t { CPU = 0, CUDA = 1, Vulkan = 2, Metal = 3, NPU = 4, HIP = 5 };
 
@@ -51,9 +72,7 @@ struct DeviceId {
     int32_t index{0};
     constexpr bool operator==(const DeviceId&) const noexcept = default;
     constexpr bool is_cpu() const noexcept { return type == DeviceType::CPU; }
-    constexpr bool is_hip() const noexcept { return type == DeviceType::HIP; }
     static constexpr DeviceId cpu(int i = 0) { return {DeviceType::CPU, i}; }
-    static constexpr DeviceId hip(int i = 0) { return {DeviceType::HIP, i}; }
 };
 
 class TensorStorage {
@@ -90,13 +109,15 @@ public:
     Tensor() = default;
     static Tensor zeros(Shape shape, DType dtype);
     static Tensor from_blob(void* data, Shape shape, DType dtype);
+    // block-quantized data whose size is not numel * dtype_element_size
+    static Tensor from_raw_blob(void* data, size_t nbytes, Shape shape, DType dtype);
     static Tensor from_storage(std::shared_ptr<TensorStorage> storage, Shape shape, DType dtype);
 
     const Shape& shape() const noexcept { return shape_; }
     DType dtype() const noexcept { return dtype_; }
     DeviceId device() const noexcept { return storage_ ? storage_->device() : DeviceId::cpu(); }
     int64_t numel() const noexcept;
-    size_t nbytes() const noexcept { return tensor_nbytes(dtype_, numel()); }
+    size_t nbytes() const noexcept { return (size_t)numel() * dtype_element_size(dtype_); }
     void* raw_data() noexcept { return storage_ ? storage_->data() : nullptr; }
     const void* raw_data() const noexcept { return storage_ ? storage_->data() : nullptr; }
     template <class T>

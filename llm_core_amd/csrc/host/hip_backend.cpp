@@ -35,24 +35,6 @@ using namespace axf_api;
 #if !defined(AXF_AXONFORGE_HEADERS)
 // ---- core types ----------------------------------------------------------
 
-size_t tensor_nbytes(DType dtype, int64_t numel) {
-    if (numel <= 0) return 0;
-    const auto n = static_cast<size_t>(numel);
-    switch (dtype) {
-        case DType::F32:
-        case DType::I32: return n * 4;
-        case DType::F16:
-        case DType::BF16:
-        case DType::I16: return n * 2;
-        case DType::I8:
-        case DType::BOOL: return n;
-        case DType::Q8_0: return ((n + 31) / 32) * 36;
-        case DType::Q4_K_M: return ((n + 255) / 256) * 144;
-        case DType::Q6_K: return ((n + 255) / 256) * 210;
-        default: return 0;
-    }
-}
-
 CpuTensorStorage::CpuTensorStorage(size_t bytes) : bytes_(bytes) {
     if (bytes_) {
         ptr_ = std::aligned_alloc(64, (bytes_ + 63) / 64 * 64);
@@ -77,7 +59,7 @@ Tensor Tensor::zeros(Shape shape, DType dtype) {
     Tensor t;
     t.shape_ = std::move(shape);
     t.dtype_ = dtype;
-    t.storage_ = std::make_shared<CpuTensorStorage>(tensor_nbytes(dtype, t.numel()));
+    t.storage_ = std::make_shared<CpuTensorStorage>(t.nbytes());
     return t;
 }
 
@@ -85,7 +67,15 @@ Tensor Tensor::from_blob(void* data, Shape shape, DType dtype) {
     Tensor t;
     t.shape_ = std::move(shape);
     t.dtype_ = dtype;
-    t.storage_ = std::make_shared<CpuTensorStorage>(data, tensor_nbytes(dtype, t.numel()));
+    t.storage_ = std::make_shared<CpuTensorStorage>(data, t.nbytes());
+    return t;
+}
+
+Tensor Tensor::from_raw_blob(void* data, size_t nbytes, Shape shape, DType dtype) {
+    Tensor t;
+    t.shape_ = std::move(shape);
+    t.dtype_ = dtype;
+    t.storage_ = std::make_shared<CpuTensorStorage>(data, nbytes);
     return t;
 }
 
@@ -359,14 +349,35 @@ public:
         return std::make_shared<HipTensorStorage>(ctx_, bytes);
     }
 
+    // Bytes a contiguous tensor's data spans.  The reference's Tensor::nbytes()
+    // counts block-quantized elements as 1 byte (Q6_K as 0), so block types take
+    // their block sizes here: Q4_K 144 and Q6_K 210 bytes per 256 weights, Q5_0
+    // 22 per 32, and Q8_0 the 36-byte activation block of q8_block.hpp:8-15.
+    static size_t span_bytes(const Tensor& t) {
+        const auto n = static_cast<size_t>(t.numel());
+        switch (t.dtype()) {
+            case DType::Q4_K_M: return n / 256 * 144;
+            case DType::Q6_K: return n / 256 * 210;
+            case DType::Q5_0: return n / 32 * 22;
+            case DType::Q8_0: return n / 32 * 36;
+            default: return t.nbytes();
+        }
+    }
+
+    // Synchronous copy, as CudaBackend::transfer (cuda_backend.cu:170-178);
+    // both storages must hold the span.
     void transfer(const Tensor& src, Tensor& dst) override {
         require_init();
-        if (src.nbytes() != dst.nbytes())
+        const size_t n = span_bytes(src);
+        if (src.dtype() != dst.dtype() || src.numel() != dst.numel() || n != span_bytes(dst))
             throw std::runtime_error("HipBackend::transfer: size mismatch");
-        const size_t n = src.nbytes();
+        if (!src.storage() || !dst.storage() || src.storage()->byte_size() < n ||
+            dst.storage()->byte_size() < n)
+            throw std::runtime_error("HipBackend::transfer: storage smaller than the tensor");
         void* d = dst.raw_data();
         const void* s = src.raw_data();
-        const bool sh = src.device().is_hip(), dh = dst.device().is_hip();
+        const bool sh = src.device().type == DeviceType::HIP,
+                   dh = dst.device().type == DeviceType::HIP;
         if (sh && dh)
             check(axf_hip_memcpy_d2d(ctx_, d, s, n), "HipBackend::transfer");
         else if (dh)

@@ -539,6 +539,15 @@ hipError_t enqueue_pick(axf_llama* m, bool record, bool advance_pos, const axf_s
                          m->d_hist, m->d_hist_n, st);
 }
 
+// The step's head: logits and the greedy pick (the fused argmax where it applies).
+hipError_t head_pass(axf_llama* m, hipStream_t st) {
+    int t, sh, parts;
+    if (head_argmax_shape(m, &t, &sh, &parts)) return head_argmax(m, false, false, st);
+    const hipError_t e = head_logits(m, m->x, m->attn_out, st);
+    if (e != hipSuccess) return e;
+    return enqueue_pick(m, false, false, nullptr);
+}
+
 hipError_t enqueue_step(axf_llama* m, bool device_state, int token, int pos, bool record,
                         const axf_sampling* smp = nullptr) {
     const auto& hp = m->hp;
@@ -1234,6 +1243,53 @@ int axf_llama_generate_sampled(axf_llama* m, const int32_t* prompt, int n_prompt
             break;
         }
     *n_out = n;
+    return AXF_OK;
+}
+
+int axf_llama_bench_stage(axf_llama* m, int stage, int pos, int reps, float* ms) {
+    LL_LOADED(m);
+    if (!ms || stage < 1 || stage > 6 || pos < 0 || pos >= m->hp.n_ctx || reps <= 0)
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_bench_stage: bad arguments");
+    hipStream_t st = m->ctx->stream;
+    LL_HIP(launch_set_int(m->d_pos, pos, st));
+    LL_HIP(launch_set_int(m->d_token, 1, st));
+    // one pass: the stage of every layer in turn (each layer's weights are
+    // their own memory, so consecutive launches stream different bytes), or
+    // n_layer head launches
+    auto pass = [&]() -> hipError_t {
+        for (int l = 0; l < m->hp.n_layer; l++) {
+            const hipError_t e = stage == 6 ? head_pass(m, st)
+                                            : enqueue_layer(m, l, m->d_pos, 0, stage, stage);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    };
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ex = nullptr;
+    if (!m->ctx->bench_eager) {
+        LL_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        const hipError_t e = pass();
+        const hipError_t e2 = hipStreamEndCapture(st, &g);
+        if (e != hipSuccess || e2 != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return hip_fail(e != hipSuccess ? e : e2, "axf_llama_bench_stage");
+        }
+        const hipError_t e3 = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        if (e3 != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            return hip_fail(e3, "axf_llama_bench_stage");
+        }
+    }
+    auto run = [&]() -> hipError_t { return ex ? hipGraphLaunch(ex, st) : pass(); };
+    hipError_t e = run();  // untimed
+    if (e == hipSuccess) e = hipEventRecord(m->ctx->ev0, st);
+    for (int r = 0; r < reps && e == hipSuccess; r++) e = run();
+    if (e == hipSuccess) e = hipEventRecord(m->ctx->ev1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(m->ctx->ev1);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, m->ctx->ev0, m->ctx->ev1);
+    if (ex) (void)hipGraphExecDestroy(ex);
+    if (g) (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "axf_llama_bench_stage");
     return AXF_OK;
 }
 

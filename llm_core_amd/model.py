@@ -301,3 +301,10 @@ class LlamaHip:
         ms = C.c_float(0)
         call("axf_llama_bench_decode", self.handle, pos, warmup, steps, C.byref(ms))
         return ms.value
+
+    def bench_stage(self, stage: int, pos: int, reps: int) -> float:
+        """Milliseconds for `reps` passes of decode stage `stage` (1 q|k|v, 2
+        attention, 3 o, 4 gate|up, 5 down, 6 head) over every layer."""
+        ms = C.c_float(0)
+        call("axf_llama_bench_stage", self.handle, stage, pos, reps, C.byref(ms))
+        return ms.value

@@ -41,7 +41,7 @@ static void test_registry_and_transfer() {
 
     auto b = reg.create("hip");
     REQUIRE(b->initialize());
-    REQUIRE(b->device_id().is_hip());
+    REQUIRE(b->device_id().type == DeviceType::HIP);
     auto h = Tensor::zeros({4}, DType::F32);
     auto hd = h.data_as<float>();
     for (int i = 0; i < 4; ++i) hd[i] = static_cast<float>(i + 1);
@@ -99,9 +99,11 @@ static void test_matmul_q4k() {
     std::vector<float> xv(cols), wf((size_t)rows * cols);
     REQUIRE(axf_synth_normal(xv.data(), cols, 8, 0.f, 1.f) == AXF_OK);
     // scalar reference from the device dequant of the same bytes
-    auto wh = Tensor::from_blob(wq.data(), {rows, cols}, DType::Q4_K_M);
+    // block-quantized host data carries its real size (from_raw_blob, as the
+    // reference's GGUF tensors)
+    auto wh = Tensor::from_raw_blob(wq.data(), wq.size(), {rows, cols}, DType::Q4_K_M);
     auto xh = Tensor::from_blob(xv.data(), {cols}, DType::F32);
-    auto W = Tensor::from_storage(b->allocate(wh.nbytes(), 256), {rows, cols}, DType::Q4_K_M);
+    auto W = Tensor::from_storage(b->allocate(wq.size(), 256), {rows, cols}, DType::Q4_K_M);
     auto X = Tensor::from_storage(b->allocate(xh.nbytes(), 256), {cols}, DType::F32);
     auto Y = Tensor::from_storage(b->allocate((size_t)rows * 4, 256), {rows}, DType::F32);
     auto WF = Tensor::from_storage(b->allocate(wf.size() * 4, 256), {rows * cols}, DType::F32);
