@@ -5,6 +5,8 @@
 Outputs
   llm_core_amd/lib/libaxf_hip.so          HIP kernels + C-ABI + C++ backend/decoder
   llm_core_amd/_build/test_backend_hip    C++ backend test program (tests/cpp)
+  llm_core_amd/_build/test_backend_dropin the same test against the reference's own
+                                          backend API (where /root/reference exists)
   oracle/liboracle.so, oracle/_ref/...    CPU checker (via oracle/Makefile)
 
 hipcc cross-compiles for gfx950 without a GPU.  Every HIP translation unit is
@@ -102,6 +104,17 @@ def build_cpp_tests() -> Path:
     return exe
 
 
+def build_dropin_test() -> Path | None:
+    """The plugin built against the reference's own headers, registry and
+    Tensor where the reference tree exists (tests/cpp/build_dropin.py)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "axf_build_dropin", ROOT / "tests" / "cpp" / "build_dropin.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.build()
+
+
 def build_oracle() -> None:
     make = shutil.which("make")
     if make is None:
@@ -112,6 +125,7 @@ def build_oracle() -> None:
 def build_all(jobs: int = 8) -> Path:
     lib = build_library(jobs)
     build_cpp_tests()
+    build_dropin_test()
     build_oracle()
     return lib
 

@@ -3,6 +3,13 @@
 // (registry, H2D/D2H round trip, RMSNorm against a scalar reference) plus the
 // quantized MATMUL path and the error behaviour of the registry
 // (tests/test_backend_x86.cpp:25-29).  Exit code 0 = all checks passed.
+//
+// Built twice: against this tree's restatement of the interface
+// (axf_backend.hpp), and with AXF_AXONFORGE_HEADERS against the reference's
+// own headers, registry and Tensor (tests/cpp/build_dropin.py), linked with the
+// plugin compiled in its drop-in mode.  `--no-device` checks what holds on a
+// host without a GPU: the backend is registered, initialize() reports no
+// device, and device work throws std::runtime_error.
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -10,10 +17,14 @@
 #include <string>
 #include <vector>
 
+#if defined(AXF_AXONFORGE_HEADERS)
+#include "axonforge/backend.hpp"
+using namespace axonforge;
+#else
 #include "axf_backend.hpp"
-#include "axf_hip.h"
-
 using namespace axf;
+#endif
+#include "axf_hip.h"
 
 static int g_fail = 0;
 #define REQUIRE(cond)                                                        \
@@ -150,7 +161,58 @@ static void test_matmul_q4k() {
     std::printf("matmul q4k: done\n");
 }
 
-int main() {
+static void test_no_device() {
+    auto& reg = BackendRegistry::instance();
+    REQUIRE(reg.has_backend("hip"));
+    bool listed = false;
+    for (const auto& id : reg.available_backends()) listed = listed || id == "hip";
+    REQUIRE(listed);
+    bool threw = false;
+    try {
+        (void)reg.create("no_such_backend");
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    REQUIRE(threw);
+    auto b = reg.create("hip");
+    REQUIRE(b->name() == "hip");
+    REQUIRE(b->device_id().type == DeviceType::HIP);
+    bool init = true;
+    try {
+        init = b->initialize();
+    } catch (const std::runtime_error&) {
+        init = false;
+    }
+    REQUIRE(!init);
+    threw = false;
+    try {
+        (void)b->allocate(256, 256);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    REQUIRE(threw);
+    threw = false;
+    try {
+        std::vector<DType> dt = {DType::Q4_K_M, DType::F32};
+        (void)b->get_kernel(OpType::MATMUL, dt, AttributeMap{});
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    REQUIRE(threw);
+    std::printf("no device: done\n");
+}
+
+int main(int argc, char** argv) {
+    if (argc > 1 && std::strcmp(argv[1], "--no-device") == 0) {
+        try {
+            test_no_device();
+        } catch (const std::exception& e) {
+            std::printf("EXCEPTION: %s\n", e.what());
+            return 2;
+        }
+        std::printf("%s (%d failures)\n", g_fail ? "FAILED" : "PASSED", g_fail);
+        return g_fail ? 1 : 0;
+    }
     try {
         test_registry_and_transfer();
         test_rmsnorm();

@@ -4,20 +4,28 @@ llm_core_amd/csrc/host/hip_backend.cpp takes its interface from one include
 switch: axf_backend.hpp (namespace axf) in this tree, or, built with
 AXF_AXONFORGE_HEADERS inside the reference tree, the reference's own
 include/axonforge/backend.hpp (namespace axonforge, through the alias
-axf_api).  A compile against the reference's real headers needs its
-configure-generated axonforge/version.hpp (common.hpp includes it), which this
-image cannot produce without running the reference's build, so the drop-in is
-checked here in two parts:
+axf_api).  Checked here (the reference parts skipped where /root/reference is
+absent):
 
-  * against the reference's header text (skipped where /root/reference is
-    absent): every enumerator the plugin uses has the reference's value
-    (DType, dtype.hpp; OpType, graph.hpp), DeviceType differs by exactly the
-    one added enumerator HIP = 5 (common.hpp), IKernel / IBackend declare the
-    same pure-virtual signatures (backend.hpp:18-69), and every Tensor member
-    and factory the plugin calls is declared in tensor.hpp;
-  * the drop-in mode itself compiles (against a header that maps namespace
-    axonforge onto this tree's restatement) and then defines none of the core
-    types the reference supplies (Tensor, CpuTensorStorage, BackendRegistry).
+  * the real build: tests/cpp/build_dropin.py compiles the plugin in its
+    drop-in mode against a copy of the reference's include tree (version.hpp
+    configured from its own template, the one DeviceType::HIP edit applied),
+    links it with the reference's own BackendRegistry, Tensor and AttributeMap
+    compiled from source and the C++ backend test, and the program runs: the
+    backend is registered under "hip", unknown ids throw std::runtime_error,
+    and on a host without a GPU initialize() reports no device and device
+    work throws std::runtime_error (the GPU test runs the same program's
+    device checks through IKernel::execute);
+  * the configured version.hpp equals what CMake's configure_file(@ONLY)
+    writes from the same template and version (cmake -P);
+  * against the reference's header text: every enumerator the plugin uses has
+    the reference's value (DType, dtype.hpp; OpType, graph.hpp), DeviceType
+    differs by exactly the one added enumerator HIP = 5 (common.hpp), IKernel
+    / IBackend declare the same pure-virtual signatures (backend.hpp:18-69),
+    and every Tensor member and factory the plugin calls is declared in
+    tensor.hpp;
+  * the drop-in mode defines none of the core types the reference supplies
+    (Tensor, CpuTensorStorage, BackendRegistry).
 """
 import os
 import re
@@ -141,3 +149,66 @@ def test_dropin_mode_compiles_without_the_core_type_definitions(tmp_path):
                  "tensor_nbytes"):
         assert core not in syms, f"drop-in mode still defines {core}"
     assert "HipBackend" in syms
+
+
+def _build_dropin_module():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("axf_build_dropin",
+                                                  ROOT / "tests" / "cpp" / "build_dropin.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@need_ref
+def test_plugin_builds_and_registers_against_the_reference_backend_api(tmp_path):
+    if shutil.which("g++") is None or not Path(os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")).exists():
+        pytest.skip("g++ / hipcc not available")
+    if not (ROOT / "llm_core_amd" / "lib" / "libaxf_hip.so").exists():
+        pytest.skip("libaxf_hip.so not built")
+    exe = _build_dropin_module().build(out=tmp_path / "test_backend_dropin")
+    assert exe is not None and exe.exists()
+    if Path("/dev/kfd").exists():
+        pytest.skip("a GPU is visible: the device checks run in the gpu test")
+    proc = subprocess.run([str(exe), "--no-device"], capture_output=True, text=True, timeout=60)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "no device: done" in proc.stdout and "PASSED (0 failures)" in proc.stdout
+
+
+@need_ref
+def test_configured_version_header_equals_cmake_configure_file(tmp_path):
+    cmake = shutil.which("cmake")
+    if cmake is None:
+        pytest.skip("cmake not available")
+    mod = _build_dropin_module()
+    ref = Path("/root/reference")
+    m = re.search(r"project\(\s*\w+\s+VERSION\s+([\d.]+)", (ref / "CMakeLists.txt").read_text())
+    major, minor, patch = m.group(1).split(".")
+    script = tmp_path / "configure.cmake"
+    out = tmp_path / "version.hpp"
+    script.write_text(
+        f'set(PROJECT_VERSION "{m.group(1)}")\nset(PROJECT_VERSION_MAJOR {major})\n'
+        f"set(PROJECT_VERSION_MINOR {minor})\nset(PROJECT_VERSION_PATCH {patch})\n"
+        f'configure_file("{ref / "include" / "axonforge" / "version.hpp.in"}" "{out}" @ONLY)\n')
+    subprocess.run([cmake, "-P", str(script)], check=True, capture_output=True, timeout=60)
+    assert mod.configured_version_header(ref) == out.read_text()
+
+
+@need_ref
+def test_hip_device_type_edit_is_the_one_documented_line():
+    mod = _build_dropin_module()
+    ref = (REF / "common.hpp").read_text()
+    edited = mod.add_hip_device_type(ref)
+    assert enum_values(edited, "DeviceType") == {**enum_values(ref, "DeviceType"), "HIP": 5}
+    added = [ln for ln in edited.splitlines() if ln not in ref.splitlines()]
+    assert len(added) == 2 and "HIP    = 5," in added[0] and 'return "hip";' in added[1]
+
+
+def test_cpp_backend_program_without_a_device():
+    exe = ROOT / "llm_core_amd" / "_build" / "test_backend_hip"
+    if not exe.exists():
+        pytest.skip("test_backend_hip not built")
+    if Path("/dev/kfd").exists():
+        pytest.skip("a GPU is visible: the device checks run in the gpu test")
+    proc = subprocess.run([str(exe), "--no-device"], capture_output=True, text=True, timeout=60)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
