@@ -924,41 +924,60 @@ static size_t wt_row_bytes(const orc_wt* w, int in) {
     return (size_t)(in / ORC_QK_K) * (w->type == ORC_TYPE_Q6_K ? ORC_Q6K_BYTES : ORC_Q4K_BYTES);
 }
 
-/* The head's gemv_wt_q8 (llama_model.cpp:767-831): Q8_0 weights take the Q8_0
- * activations (q8_fast branch), Q5_0 and F16 fall back to gemv_wt with the fp32
- * row (:701-724, the F16 kernel at :660-680); Q4_K / Q6_K as in the layers. */
-static void head_gemv(float* y, const orc_wt* w, const orc_block_q8_0* xq8, const float* x,
-                      int out, int in);
-
-/* gemv_wt_q8, llama_model.cpp:767-831 (Q4_K and Q6_K branches). */
-static void gemv_wt_q8(float* y, const orc_wt* w, const orc_block_q8_0* xq8, int out, int in) {
-    if (w->type == ORC_TYPE_Q6_K)
-        orc_gemv_q6k_q8(y, w->data, xq8, 0, out, in, wt_row_bytes(w, in));
+/* gemv_wt, llama_model.cpp:670-731: fp32 activations. F16 -> the F16 GEMV
+ * (:672-680), Q4_K / Q6_K -> the fp32-activation K-quant GEMVs (:681-700),
+ * Q8_0 -> q8_0_weight_dot_row (:701-712), Q5_0 -> q5_0_dot_row (:713-724). */
+static void gemv_wt(float* y, const orc_wt* w, const float* x, int out, int in) {
+    const size_t rb = wt_row_bytes(w, in);
+    if (w->type == 1)
+        orc_gemv_f16_f32(y, (const uint16_t*)w->data, x, NULL, 0, out, in);
+    else if (w->type == ORC_TYPE_Q4_K)
+        orc_gemv_q4k_f32(y, w->data, x, 0, out, in, rb);
+    else if (w->type == ORC_TYPE_Q6_K)
+        orc_gemv_q6k_f32(y, w->data, x, 0, out, in, rb);
+    else if (w->type == 8)
+        orc_gemv_q8_0w_f32(y, w->data, x, 0, out, in, rb);
     else
-        orc_gemv_q4k_q8(y, w->data, xq8, 0, out, in, wt_row_bytes(w, in));
+        orc_gemv_q5_0_f32(y, w->data, x, 0, out, in, rb);
 }
 
-/* gemm_wt_q8, llama_model.cpp:837-879: Q4_K -> GEMM kernel; Q6_K -> per-token GEMV. */
-static void gemm_wt_q8(float* Y, const orc_wt* w, const orc_block_q8_0* XQ8, int M, int T, int in) {
+/* gemv_wt_q8, llama_model.cpp:767-831 (the decode step's GEMV; q8_fast and AVX2,
+ * as the reference builds every layer, :986-1006): Q4_K and Q6_K -> the Q8_0
+ * GEMVs, Q8_0 -> gemv_q8_0_weight_q8 (:825-828), everything else -> gemv_wt
+ * with the fp32 activation xf32 (:830). */
+static void gemv_wt_q8(float* y, const orc_wt* w, const orc_block_q8_0* xq8, const float* xf32,
+                       int out, int in) {
+    const size_t rb = wt_row_bytes(w, in);
+    if (w->type == ORC_TYPE_Q6_K)
+        orc_gemv_q6k_q8(y, w->data, xq8, 0, out, in, rb);
+    else if (w->type == ORC_TYPE_Q4_K)
+        orc_gemv_q4k_q8(y, w->data, xq8, 0, out, in, rb);
+    else if (w->type == 8)
+        orc_gemv_q8_0w_q8(y, w->data, xq8, 0, out, in, rb);
+    else
+        gemv_wt(y, w, xf32, out, in);
+}
+
+/* gemm_wt_q8, llama_model.cpp:837-879: Q4_K -> GEMM kernel; Q6_K -> per-token
+ * Q8_0 GEMV; every other type (Q8_0 included: the batched path has no Q8_0
+ * branch) -> gemv_wt per token with the fp32 rows XF32 (:876-879). */
+static void gemm_wt_q8(float* Y, const orc_wt* w, const orc_block_q8_0* XQ8, const float* XF32,
+                       int M, int T, int in) {
     const size_t rb = wt_row_bytes(w, in);
     if (w->type == ORC_TYPE_Q6_K) {
         for (int t = 0; t < T; t++)
             orc_gemv_q6k_q8(Y + (size_t)t * M, w->data, XQ8 + (size_t)t * (in / 32), 0, M, in, rb);
-    } else {
+    } else if (w->type == ORC_TYPE_Q4_K) {
         orc_gemm_q4k_q8(Y, w->data, XQ8, M, T, in, rb, 0, M);
+    } else {
+        for (int t = 0; t < T; t++) gemv_wt(Y + (size_t)t * M, w, XF32 + (size_t)t * in, M, in);
     }
 }
 
+/* The head's gemv_wt_q8 (llama_model.cpp:1330-1332): the same dispatch. */
 static void head_gemv(float* y, const orc_wt* w, const orc_block_q8_0* xq8, const float* x,
                       int out, int in) {
-    if (w->type == 8)
-        orc_gemv_q8_0w_q8(y, w->data, xq8, 0, out, in, wt_row_bytes(w, in));
-    else if (w->type == 6)
-        orc_gemv_q5_0_f32(y, w->data, x, 0, out, in, wt_row_bytes(w, in));
-    else if (w->type == 1)
-        orc_gemv_f16_f32(y, (const uint16_t*)w->data, x, NULL, 0, out, in);
-    else
-        gemv_wt_q8(y, w, xq8, out, in);
+    gemv_wt_q8(y, w, xq8, x, out, in);
 }
 
 /* emb_lookup, llama_model.cpp:882-934. */
@@ -989,9 +1008,9 @@ void orc_forward_layer(const orc_model* m, orc_state* s, int l, int pos) {
 
     orc_rmsnorm(s->xb, s->x, lw->attn_norm, E, m->rms_eps);
     orc_quantize_q8_0(s->xq8, s->xb, E);
-    gemv_wt_q8(s->q, &lw->wq, s->xq8, H * HD, E);
-    gemv_wt_q8(s->k, &lw->wk, s->xq8, KVH * HD, E);
-    gemv_wt_q8(s->v, &lw->wv, s->xq8, KVH * HD, E);
+    gemv_wt_q8(s->q, &lw->wq, s->xq8, s->xb, H * HD, E);
+    gemv_wt_q8(s->k, &lw->wk, s->xq8, s->xb, KVH * HD, E);
+    gemv_wt_q8(s->v, &lw->wv, s->xq8, s->xb, KVH * HD, E);
     add_bias(s->q, lw->bq, H * HD);
     add_bias(s->k, lw->bk, KVH * HD);
     add_bias(s->v, lw->bv, KVH * HD);
@@ -1013,16 +1032,16 @@ void orc_forward_layer(const orc_model* m, orc_state* s, int l, int pos) {
     orc_attention(s->attn_out, s->q, kc, vc, pos + 1, H, KVH, HD, s->attn);
 
     orc_quantize_q8_0(s->xq8, s->attn_out, E);
-    gemv_wt_q8(s->xb, &lw->wo, s->xq8, E, E);
+    gemv_wt_q8(s->xb, &lw->wo, s->xq8, s->attn_out, E, E);
     for (int i = 0; i < E; i++) s->x[i] += s->xb[i];
 
     orc_rmsnorm(s->xb, s->x, lw->ffn_norm, E, m->rms_eps);
     orc_quantize_q8_0(s->xq8, s->xb, E);
-    gemv_wt_q8(s->gate, &lw->wgate, s->xq8, FD, E);
-    gemv_wt_q8(s->up, &lw->wup, s->xq8, FD, E);
+    gemv_wt_q8(s->gate, &lw->wgate, s->xq8, s->xb, FD, E);
+    gemv_wt_q8(s->up, &lw->wup, s->xq8, s->xb, FD, E);
     orc_swiglu(s->gate, s->up, FD);
     orc_quantize_q8_0(s->xq8, s->gate, FD);
-    gemv_wt_q8(s->ffn, &lw->wdown, s->xq8, E, FD);
+    gemv_wt_q8(s->ffn, &lw->wdown, s->xq8, s->gate, E, FD);
     for (int i = 0; i < E; i++) s->x[i] += s->ffn[i];
 }
 
@@ -1064,9 +1083,9 @@ void orc_forward_batch(const orc_model* m, orc_state* s, const int32_t* tokens, 
             orc_rmsnorm(XB + (size_t)t * E, X + (size_t)t * E, lw->attn_norm, E, m->rms_eps);
             orc_quantize_q8_0(XQE + (size_t)t * (E / 32), XB + (size_t)t * E, E);
         }
-        gemm_wt_q8(Q, &lw->wq, XQE, H * HD, T, E);
-        gemm_wt_q8(K, &lw->wk, XQE, KVH * HD, T, E);
-        gemm_wt_q8(V, &lw->wv, XQE, KVH * HD, T, E);
+        gemm_wt_q8(Q, &lw->wq, XQE, XB, H * HD, T, E);
+        gemm_wt_q8(K, &lw->wk, XQE, XB, KVH * HD, T, E);
+        gemm_wt_q8(V, &lw->wv, XQE, XB, KVH * HD, T, E);
         for (int t = 0; t < T; t++) {
             add_bias(Q + (size_t)t * H * HD, lw->bq, H * HD);
             add_bias(K + (size_t)t * kve, lw->bk, kve);
@@ -1093,19 +1112,19 @@ void orc_forward_batch(const orc_model* m, orc_state* s, const int32_t* tokens, 
                           KVH, HD, s->attn);
         for (int t = 0; t < T; t++)
             orc_quantize_q8_0(XQE + (size_t)t * (E / 32), AO + (size_t)t * E, E);
-        gemm_wt_q8(XB, &lw->wo, XQE, E, T, E);
+        gemm_wt_q8(XB, &lw->wo, XQE, AO, E, T, E);
         for (size_t i = 0; i < (size_t)T * E; i++) X[i] += XB[i];
         for (int t = 0; t < T; t++) {
             orc_rmsnorm(XB + (size_t)t * E, X + (size_t)t * E, lw->ffn_norm, E, m->rms_eps);
             orc_quantize_q8_0(XQE + (size_t)t * (E / 32), XB + (size_t)t * E, E);
         }
-        gemm_wt_q8(GATE, &lw->wgate, XQE, FD, T, E);
-        gemm_wt_q8(UP, &lw->wup, XQE, FD, T, E);
+        gemm_wt_q8(GATE, &lw->wgate, XQE, XB, FD, T, E);
+        gemm_wt_q8(UP, &lw->wup, XQE, XB, FD, T, E);
         for (int t = 0; t < T; t++) {
             orc_swiglu(GATE + (size_t)t * FD, UP + (size_t)t * FD, FD);
             orc_quantize_q8_0(XQF + (size_t)t * (FD / 32), GATE + (size_t)t * FD, FD);
         }
-        gemm_wt_q8(FFN, &lw->wdown, XQF, E, T, FD);
+        gemm_wt_q8(FFN, &lw->wdown, XQF, GATE, E, T, FD);
         for (size_t i = 0; i < (size_t)T * E; i++) X[i] += FFN[i];
     }
     float* xl = X + (size_t)(T - 1) * E;

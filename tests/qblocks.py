@@ -82,3 +82,49 @@ def dequant_q8(b) -> np.ndarray:
     """d*q per element, one fp32 rounding (what an identity-weight GEMV returns)."""
     d, q = unpack_q8(b)
     return (d[:, None] * q.astype(np.float32)).astype(np.float32).reshape(-1)
+
+
+Q8_0W, Q5_0W, F16W = 8, 6, 1  # GGUF type ids of the other weight types
+
+
+def misc_identity(qtype: int, rows: int, cols: int, c: int = 1) -> np.ndarray:
+    """Matrix with weight c at (r, r) for r < min(rows, cols), 0 elsewhere, in
+    Q8_0 (d = 1, q = c), Q5_0 (d = 1, q5 = 16 + c: every other value 16, i.e. 0)
+    or F16 layout (dtype.hpp:130-133 block sizes: 34, 22 bytes per 32; F16 2 per
+    element)."""
+    if qtype == F16W:
+        w = np.zeros((rows, cols), np.float16)
+        for r in range(min(rows, cols)):
+            w[r, r] = c
+        return w.reshape(-1).view(np.uint8)
+    nb = cols // 32
+    if qtype == Q8_0W:
+        out = np.zeros((rows, nb, 34), np.uint8)
+        out[:, :, 0:2] = np.array([F16_ONE], np.uint16).view(np.uint8)
+        for r in range(min(rows, cols)):
+            out[r, r // 32, 2 + r % 32] = c & 0xff
+        return out.reshape(-1)
+    assert qtype == Q5_0W and 0 <= c <= 15
+    out = np.zeros((rows, nb, 22), np.uint8)
+    out[:, :, 0:2] = np.array([F16_ONE], np.uint16).view(np.uint8)
+    out[:, :, 2:6] = 0xFF                    # the fifth bit of every value: 16 + nibble
+    for r in range(min(rows, cols)):
+        e = r % 32                           # element e < 16: low nibble of qs[e], else high of qs[e-16]
+        if e < 16:
+            out[r, r // 32, 6 + e] |= c
+        else:
+            out[r, r // 32, 6 + e - 16] |= c << 4
+    return out.reshape(-1)
+
+
+def misc_random(rng, qtype: int, rows: int, cols: int, scale: float = 1e-3) -> np.ndarray:
+    """Random blocks of the other types: any int8 / 5-bit values, fp16 d in
+    scale*[0.5, 1.5); F16 weights N(0, 0.02)."""
+    if qtype == F16W:
+        return (rng.standard_normal((rows, cols)) * 0.02).astype(np.float16).reshape(-1).view(np.uint8)
+    nb = cols // 32
+    bb = 34 if qtype == Q8_0W else 22
+    b = rng.integers(0, 256, (rows, nb, bb), dtype=np.uint8)
+    d = (rng.uniform(0.5, 1.5, (rows, nb)) * scale).astype(np.float16)
+    b[:, :, 0:2] = d.view(np.uint8).reshape(rows, nb, 2)
+    return b.reshape(-1)
