@@ -119,14 +119,16 @@ bool gemm_mfma_q6k_ok(const void* W, int rows, int nb, long row_bytes);
 hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
                                    int nb, long row_bytes, void* scratch, hipStream_t st);
 // Other weight types (kernels/gemv_misc.hip): nb = 32-element blocks per row.
+// T tokens (T <= 65535): activation rows and y rows of token t follow each
+// other (x + t*cols, xq8 + t*nb blocks, y + t*rows); accumulate adds to y.
 hipError_t launch_gemv_q8w_q8(float* y, const void* W, const void* xq8, int rows, int nb,
-                              long row_bytes, int accumulate, hipStream_t st);
+                              long row_bytes, int accumulate, hipStream_t st, int T = 1);
 hipError_t launch_gemv_q8w_f32(float* y, const void* W, const float* x, int rows, int nb,
-                               long row_bytes, hipStream_t st);
+                               long row_bytes, hipStream_t st, int accumulate = 0, int T = 1);
 hipError_t launch_gemv_q5_0_f32(float* y, const void* W, const float* x, int rows, int nb,
-                                long row_bytes, hipStream_t st);
+                                long row_bytes, hipStream_t st, int accumulate = 0, int T = 1);
 hipError_t launch_gemv_f16_f32(float* y, const void* W, const float* x, const float* bias,
-                               int rows, int cols, hipStream_t st);
+                               int rows, int cols, hipStream_t st, int accumulate = 0, int T = 1);
 hipError_t launch_embed_misc(int qtype, float* out, const void* W, const int* tok_dev, int tok,
                              int T, int cols, long row_bytes, hipStream_t st);
 hipError_t launch_dequant_q4k(float* y, const void* W, long nblocks, hipStream_t st);
@@ -141,7 +143,8 @@ hipError_t launch_rope_kv_rows(const float* k, int k_ld, const float* v, int v_l
                                const float* bk, const float* bv, float* kcache, float* vcache,
                                int pos0, int T, int n_kv_heads, int hd, const float* cos_t,
                                const float* sin_t, hipStream_t st);
-hipError_t launch_swiglu_gu(void* outq8, const float* gu, int T, int n, int B, hipStream_t st);
+hipError_t launch_swiglu_gu(void* outq8, const float* gu, int T, int n, int B, hipStream_t st,
+                            float* out = nullptr);
 hipError_t launch_embed_rows(int qtype, float* out, const void* W, const int* toks_dev, int T,
                              int nb, long row_bytes, hipStream_t st);
 hipError_t launch_rope(float* dst, const float* src, const int* pos_dev, int pos, int n_heads,

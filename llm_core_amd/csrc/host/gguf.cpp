@@ -479,17 +479,14 @@ int axf_llama_load_gguf(axf_llama* m, const axf_gguf* g) {
                                   t.name == "output_norm.weight" ||
                                   t.name.compare(0, 4, "blk.") == 0;
         if (!model_tensor) continue;
-        // Q8_0 / Q5_0 / F16 only for the embedding and the head (the layer
-        // matrices run the fused Q4_K / Q6_K kernels)
-        const bool head = t.name == "token_embd.weight" || t.name == "output.weight";
-        const bool other = t.ggml_type == AXF_TYPE_Q8_0 || t.ggml_type == AXF_TYPE_Q5_0 ||
-                           t.ggml_type == AXF_TYPE_F16;
+        // the weight types of the reference's gemv_wt / gemv_wt_q8 dispatch
+        // (llama_model.cpp:670-831); axf_llama_load checks each tensor's shape
         if (t.ggml_type != AXF_TYPE_F32 && t.ggml_type != AXF_TYPE_Q4_K &&
-            t.ggml_type != AXF_TYPE_Q6_K && !(head && other))
+            t.ggml_type != AXF_TYPE_Q6_K && t.ggml_type != AXF_TYPE_Q8_0 &&
+            t.ggml_type != AXF_TYPE_Q5_0 && t.ggml_type != AXF_TYPE_F16)
             return fail(AXF_ERR_UNSUPPORTED, "axf_llama_load_gguf: " + t.name + " has GGML type " +
                                                  std::to_string(t.ggml_type) +
-                                                 (head ? " (supported: Q4_K, Q6_K, Q8_0, Q5_0, F16)"
-                                                       : " (supported: F32, Q4_K, Q6_K)"));
+                                                 " (supported: F32, F16, Q8_0, Q5_0, Q4_K, Q6_K)");
         const uint8_t* p = g->data(t);
         if (!p || t.nbytes == 0)
             return fail(AXF_ERR_INVALID_ARG,

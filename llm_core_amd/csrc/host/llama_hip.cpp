@@ -77,6 +77,7 @@ struct axf_llama {
 
     float *kv_k = nullptr, *kv_v = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
     float *x = nullptr, *qkv = nullptr, *attn_out = nullptr, *gateup = nullptr, *logits = nullptr;
+    float* xb = nullptr;  // RMSNorm(x) * norm weight in fp32 (layers with Q5_0 / F16 matrices)
     float* h = nullptr;  // SwiGLU output, FD floats
     uint8_t* xq8 = nullptr;
     float* attn_part = nullptr;
@@ -92,6 +93,7 @@ struct axf_llama {
     int* pf_tok = nullptr;
     float *pf_x = nullptr, *pf_qk = nullptr, *pf_v = nullptr, *pf_ao = nullptr, *pf_tmp = nullptr,
           *pf_gu = nullptr, *pf_part = nullptr;
+    float *pf_xb = nullptr, *pf_h = nullptr;  // fp32 normalised rows and SwiGLU rows
     uint8_t *pf_q8 = nullptr, *pf_gemm = nullptr;
     // prefill attention: the matrix-core kernel, or (testing) the decode
     // split/combine kernels over a token grid
@@ -117,6 +119,7 @@ namespace {
 bool misc_type(int qtype) {
     return qtype == AXF_TYPE_Q8_0 || qtype == AXF_TYPE_Q5_0 || qtype == AXF_TYPE_F16;
 }
+bool kquant(int qtype) { return qtype == AXF_TYPE_Q4_K || qtype == AXF_TYPE_Q6_K; }
 
 int dalloc(axf_llama* m, size_t bytes, void** p) {
     *p = nullptr;
@@ -172,29 +175,41 @@ int upload_f32(axf_llama* m, const std::string& name, int n, float** out, bool r
     return AXF_OK;
 }
 
+// A layer matrix: Q4_K / Q6_K (rows of whole 256-weight super-blocks), or the
+// types the reference's gemv_wt / gemv_wt_q8 also take (llama_model.cpp:670-831):
+// Q8_0 and Q5_0 (32-weight blocks), F16 (rows of a multiple of 8 here: the
+// kernel reads 16 bytes at a time).
+int check_q(const std::string& name, const HostTensor* t, int rows, int cols) {
+    if (kquant(t->qtype)) {
+        if (cols % QK_K)
+            return fail(AXF_ERR_UNSUPPORTED, "axf_llama_load: " + name +
+                                                 " is Q4_K/Q6_K with rows that are not whole super-blocks");
+    } else if (t->qtype == AXF_TYPE_Q8_0 || t->qtype == AXF_TYPE_Q5_0) {
+        if (cols % 32)
+            return fail(AXF_ERR_UNSUPPORTED, "axf_llama_load: " + name + " rows must be whole 32-blocks");
+    } else if (t->qtype == AXF_TYPE_F16) {
+        if (cols % 8)
+            return fail(AXF_ERR_UNSUPPORTED, "axf_llama_load: " + name + " F16 rows must be a multiple of 8");
+    } else {
+        return fail(AXF_ERR_UNSUPPORTED,
+                    "axf_llama_load: " + name + " must be Q4_K, Q6_K, Q8_0, Q5_0 or F16");
+    }
+    if (t->bytes != (size_t)rows * axf_row_bytes(t->qtype, cols))
+        return fail(AXF_ERR_INVALID_ARG, "axf_llama_load: " + name + " has wrong byte size");
+    return AXF_OK;
+}
+
 // token_embd / output: also the other GGUF weight types of the reference's
 // head and embedding paths (Q8_0, Q5_0, F16)
 int upload_head(axf_llama* m, const std::string& name, int rows, int cols, DevW* w) {
     const HostTensor* t;
     LL_TRY(need(m, name, &t));
-    if (t->qtype != AXF_TYPE_Q4_K && t->qtype != AXF_TYPE_Q6_K && !misc_type(t->qtype))
-        return fail(AXF_ERR_UNSUPPORTED,
-                    "axf_llama_load: " + name + " must be Q4_K, Q6_K, Q8_0, Q5_0 or F16");
+    LL_TRY(check_q(name, t, rows, cols));
     const size_t rb = axf_row_bytes(t->qtype, cols);
-    if (t->bytes != (size_t)rows * rb)
-        return fail(AXF_ERR_INVALID_ARG, "axf_llama_load: " + name + " has wrong byte size");
     void* p;
     LL_TRY(dalloc(m, t->bytes, &p));
     LL_TRY(upload(m, p, t->host, t->bytes));
     *w = DevW{t->qtype, static_cast<uint8_t*>(p), rb};
-    return AXF_OK;
-}
-
-int check_q(const std::string& name, const HostTensor* t, int rows, int cols) {
-    if (t->qtype != AXF_TYPE_Q4_K && t->qtype != AXF_TYPE_Q6_K)
-        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_load: " + name + " must be Q4_K or Q6_K");
-    if (t->bytes != (size_t)rows * axf_row_bytes(t->qtype, cols))
-        return fail(AXF_ERR_INVALID_ARG, "axf_llama_load: " + name + " has wrong byte size");
     return AXF_OK;
 }
 
@@ -246,8 +261,8 @@ int upload_gate_up(axf_llama* m, int l, Layer& L) {
     LL_TRY(check_q(b + "ffn_gate.weight", tg, FD, E));
     LL_TRY(need(m, b + "ffn_up.weight", &tu));
     LL_TRY(check_q(b + "ffn_up.weight", tu, FD, E));
-    const int B = qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2;
-    L.gu_interleaved = tg->qtype == tu->qtype && FD % B == 0;
+    const int B = kquant(tg->qtype) ? qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2 : 1;
+    L.gu_interleaved = kquant(tg->qtype) && tg->qtype == tu->qtype && FD % B == 0;
     if (!L.gu_interleaved) {
         LL_TRY(upload_pair(m, b + "ffn_gate.weight", FD, "", 0, E, &L.wgate, nullptr, nullptr));
         LL_TRY(upload_pair(m, b + "ffn_up.weight", FD, "", 0, E, &L.wup, nullptr, nullptr));
@@ -303,6 +318,20 @@ hipError_t gemv_q8(const DevW& w, float* y, const void* xq8, int rows, int cols,
     return launch_qgemv(w.qtype, QAct::Q8, false, a, threads, st);
 }
 
+// y (+)= W * activation by the reference's gemv_wt_q8 dispatch
+// (llama_model.cpp:767-831): Q4_K, Q6_K and Q8_0 weights take the Q8_0
+// activation xq8 (Q8_0: gemv_q8_0_weight_q8, :825-828), Q5_0 and F16 weights
+// the fp32 activation xf through gemv_wt (:830).
+hipError_t gemv_any(const DevW& w, float* y, const uint8_t* xq8, const float* xf, int rows,
+                    int cols, bool acc, hipStream_t st) {
+    if (kquant(w.qtype)) return gemv_q8(w, y, xq8, rows, cols, acc, st);
+    if (w.qtype == AXF_TYPE_Q8_0)
+        return launch_gemv_q8w_q8(y, w.d, xq8, rows, cols / 32, (long)w.row_bytes, acc ? 1 : 0, st);
+    if (w.qtype == AXF_TYPE_Q5_0)
+        return launch_gemv_q5_0_f32(y, w.d, xf, rows, cols / 32, (long)w.row_bytes, st, acc ? 1 : 0);
+    return launch_gemv_f16_f32(y, w.d, xf, nullptr, rows, cols, st, acc ? 1 : 0);
+}
+
 // y = W * Q8_0(RMSNorm(x) * nw), the normalisation in the GEMV prologue;
 // the SwiGLU variant (gate|up interleaved) runs 512-thread workgroups
 hipError_t gemv_norm(const DevW& w, float* y, const float* x, const float* nw, float eps,
@@ -347,7 +376,8 @@ hipError_t head_logits(axf_llama* m, const float* x, float* scratch, hipStream_t
 bool head_argmax_shape(const axf_llama* m, int* threads, int* shape, int* parts) {
     const auto& hp = m->hp;
     const int nb = hp.n_embd / QK_K;
-    if (misc_type(m->output.qtype) || !qgemv_threads_ok(QAct::Norm, nb, 512)) return false;
+    if (misc_type(m->output.qtype) || hp.n_embd % QK_K || !qgemv_threads_ok(QAct::Norm, nb, 512))
+        return false;
     *threads = decode_gemv_threads(QAct::Norm, hp.n_vocab, nb, shape);
     *parts = qgemv_wgs(hp.n_vocab, nb, *threads, *shape);
     return true;
@@ -431,7 +461,7 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int f
         }
         const int threads = decode_gemv_threads(QAct::Norm, a.rows0 + a.rows1, a.nb, &a.shape);
         ST(launch_qgemv2(QAct::Norm, a, threads, st));
-    } else {
+    } else if (kquant(L.wq.qtype) && kquant(L.wk.qtype) && kquant(L.wv.qtype)) {
         if (L.qk_fused) {
             ST(gemv_norm(L.wq, q, m->x, L.attn_norm, hp.rms_eps, qo + kvo, E, false, st));
         } else {
@@ -439,6 +469,17 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int f
             ST(gemv_norm(L.wk, k, m->x, L.attn_norm, hp.rms_eps, kvo, E, false, st));
         }
         ST(gemv_norm(L.wv, v, m->x, L.attn_norm, hp.rms_eps, kvo, E, false, st));
+    } else {
+        // Q8_0 / Q5_0 / F16 projections: RMSNorm once (fp32 and Q8_0), then each
+        // GEMV on the activation its type takes
+        ST(launch_rmsnorm(m->xb, m->xq8, m->x, L.attn_norm, E, hp.rms_eps, st));
+        if (L.qk_fused) {
+            ST(gemv_any(L.wq, q, m->xq8, m->xb, qo + kvo, E, false, st));
+        } else {
+            ST(gemv_any(L.wq, q, m->xq8, m->xb, qo, E, false, st));
+            ST(gemv_any(L.wk, k, m->xq8, m->xb, kvo, E, false, st));
+        }
+        ST(gemv_any(L.wv, v, m->xq8, m->xb, kvo, E, false, st));
     }
     // 2./3. attention -> Q8_0 of its output
     if (stage(2)) {
@@ -491,18 +532,27 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int f
         ST(launch_attention_fused(a, HD, st));
     }
     // 4. x += o
-    if (stage(3)) ST(gemv_q8(L.wo, m->x, m->xq8, E, qo, true, st));
+    if (stage(3)) ST(gemv_any(L.wo, m->x, m->xq8, m->attn_out, E, qo, true, st));
     // 5. h = SwiGLU(gate, up) from RMSNorm(x) * ffn_norm
     if (!stage(4)) {
     } else if (L.gu_interleaved) {
         ST(gemv_norm(L.wgate, m->h, m->x, L.ffn_norm, hp.rms_eps, 2 * FD, E, true, st));
-    } else {
+    } else if (kquant(L.wgate.qtype) && kquant(L.wup.qtype)) {
         ST(gemv_norm(L.wgate, m->gateup, m->x, L.ffn_norm, hp.rms_eps, FD, E, false, st));
         ST(gemv_norm(L.wup, m->gateup + FD, m->x, L.ffn_norm, hp.rms_eps, FD, E, false, st));
         ST(launch_swiglu(m->h, nullptr, m->gateup, m->gateup + FD, FD, st));
+    } else {
+        ST(launch_rmsnorm(m->xb, m->xq8, m->x, L.ffn_norm, E, hp.rms_eps, st));
+        ST(gemv_any(L.wgate, m->gateup, m->xq8, m->xb, FD, E, false, st));
+        ST(gemv_any(L.wup, m->gateup + FD, m->xq8, m->xb, FD, E, false, st));
+        ST(launch_swiglu(m->h, nullptr, m->gateup, m->gateup + FD, FD, st));
     }
     // 6. x += down(Q8_0(h))
-    if (stage(5)) {
+    if (stage(5) && !kquant(L.wdown.qtype)) {
+        // Q8_0 weights take Q8_0(h), Q5_0 / F16 the fp32 h
+        if (L.wdown.qtype == AXF_TYPE_Q8_0) ST(launch_quantize_q8_0(m->xq8, m->h, FD, st));
+        ST(gemv_any(L.wdown, m->x, m->xq8, m->h, E, FD, true, st));
+    } else if (stage(5)) {
         QGemvArgs a = weights(L.wdown, E, m->x, FD);
         a.x = m->h;
         a.accumulate = 1;
@@ -610,6 +660,10 @@ int prefill_alloc(axf_llama* m) {
     m->pf_tmp = static_cast<float*>(p);
     LL_TRY(dalloc(m, C * 2 * FD * 4, &p));
     m->pf_gu = static_cast<float*>(p);
+    LL_TRY(dalloc(m, C * E * 4, &p));
+    m->pf_xb = static_cast<float*>(p);
+    LL_TRY(dalloc(m, C * FD * 4, &p));
+    m->pf_h = static_cast<float*>(p);
     if (m->pf_attn_split) {
         LL_TRY(dalloc(m, C * part_per_tok, &p));
         m->pf_part = static_cast<float*>(p);
@@ -642,6 +696,19 @@ hipError_t gemm_rows(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, 
                               GemmPath::Auto, m->pf_gemm, st);
 }
 
+// Y[T][rows] by gemm_wt_q8's dispatch (llama_model.cpp:837-879): Q4_K and Q6_K
+// on the Q8_0 rows; every other type, Q8_0 included (the batched path has no
+// Q8_0 branch), on the fp32 rows XF through gemv_wt per token (:876-879).
+hipError_t gemm_any(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, const float* xf,
+                    int rows, int T, int cols, hipStream_t st) {
+    if (kquant(w.qtype)) return gemm_rows(m, w, Y, xq8, rows, T, cols, st);
+    if (w.qtype == AXF_TYPE_Q8_0)
+        return launch_gemv_q8w_f32(Y, w.d, xf, rows, cols / 32, (long)w.row_bytes, st, 0, T);
+    if (w.qtype == AXF_TYPE_Q5_0)
+        return launch_gemv_q5_0_f32(Y, w.d, xf, rows, cols / 32, (long)w.row_bytes, st, 0, T);
+    return launch_gemv_f16_f32(Y, w.d, xf, nullptr, rows, cols, st, 0, T);
+}
+
 hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     const auto& hp = m->hp;
     const int E = hp.n_embd, H = hp.n_heads, KVH = hp.n_kv_heads, HD = m->hd, FD = hp.ffn_dim;
@@ -652,8 +719,11 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     hipError_t e;
 #define ST(call)               \
     if ((e = (call)) != hipSuccess) return e;
-    // q|k and v projections of RMSNorm(x) * attn_norm
-    ST(launch_rmsnorm_rows(nullptr, m->pf_q8, m->pf_x, L.attn_norm, E, hp.rms_eps, T, st));
+    // q|k and v projections of RMSNorm(x) * attn_norm (fp32 rows too where a
+    // projection of another type takes them)
+    const bool f_qkv = !kquant(L.wq.qtype) || !kquant(L.wk.qtype) || !kquant(L.wv.qtype);
+    ST(launch_rmsnorm_rows(f_qkv ? m->pf_xb : nullptr, m->pf_q8, m->pf_x, L.attn_norm, E,
+                           hp.rms_eps, T, st));
     float* q = m->pf_qk;
     float* k;
     int q_ld, k_ld;
@@ -665,10 +735,10 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
         k = q + (size_t)T * qo;
         q_ld = qo;
         k_ld = kvo;
-        ST(gemm_rows(m, L.wq, q, m->pf_q8, qo, T, E, st));
-        ST(gemm_rows(m, L.wk, k, m->pf_q8, kvo, T, E, st));
+        ST(gemm_any(m, L.wq, q, m->pf_q8, m->pf_xb, qo, T, E, st));
+        ST(gemm_any(m, L.wk, k, m->pf_q8, m->pf_xb, kvo, T, E, st));
     }
-    ST(gemm_rows(m, L.wv, m->pf_v, m->pf_q8, kvo, T, E, st));
+    ST(gemm_any(m, L.wv, m->pf_v, m->pf_q8, m->pf_xb, kvo, T, E, st));
     // K, V rows into the cache, then attention of every row -> Q8_0
     const bool qkn = hp.qk_norm_order != 0;
     if (qkn) {  // per-head q/k norms: q rows finished in place, K/V rows stored
@@ -721,22 +791,27 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
         ST(m->pf_attn_split ? launch_attention_fused(a, HD, st)
                             : launch_attention_prefill(a, HD, st));
     }
-    // x += o
-    ST(gemm_rows(m, L.wo, m->pf_tmp, m->pf_q8, E, T, qo, st));
+    // x += o (the attention's fp32 rows pf_ao and their Q8_0 pf_q8)
+    ST(gemm_any(m, L.wo, m->pf_tmp, m->pf_q8, m->pf_ao, E, T, qo, st));
     ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
-    // SwiGLU(gate, up) of RMSNorm(x) * ffn_norm -> Q8_0
-    ST(launch_rmsnorm_rows(nullptr, m->pf_q8, m->pf_x, L.ffn_norm, E, hp.rms_eps, T, st));
+    // SwiGLU(gate, up) of RMSNorm(x) * ffn_norm -> Q8_0 (and fp32 rows of h
+    // where the down projection is of another type)
+    const bool f_gu = !kquant(L.wgate.qtype) || !kquant(L.wup.qtype);
+    const bool f_down = !kquant(L.wdown.qtype);
+    ST(launch_rmsnorm_rows(f_gu ? m->pf_xb : nullptr, m->pf_q8, m->pf_x, L.ffn_norm, E,
+                           hp.rms_eps, T, st));
     if (L.gu_interleaved) {
         ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, 2 * FD, T, E, st));
         const int B = qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2;
-        ST(launch_swiglu_gu(m->pf_q8, m->pf_gu, T, FD, B, st));
+        ST(launch_swiglu_gu(m->pf_q8, m->pf_gu, T, FD, B, st, f_down ? m->pf_h : nullptr));
     } else {
-        ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, FD, T, E, st));
-        ST(gemm_rows(m, L.wup, m->pf_gu + (size_t)T * FD, m->pf_q8, FD, T, E, st));
-        ST(launch_swiglu(nullptr, m->pf_q8, m->pf_gu, m->pf_gu + (size_t)T * FD, T * FD, st));
+        ST(gemm_any(m, L.wgate, m->pf_gu, m->pf_q8, m->pf_xb, FD, T, E, st));
+        ST(gemm_any(m, L.wup, m->pf_gu + (size_t)T * FD, m->pf_q8, m->pf_xb, FD, T, E, st));
+        ST(launch_swiglu(f_down ? m->pf_h : nullptr, m->pf_q8, m->pf_gu,
+                         m->pf_gu + (size_t)T * FD, T * FD, st));
     }
     // x += down
-    ST(gemm_rows(m, L.wdown, m->pf_tmp, m->pf_q8, E, T, FD, st));
+    ST(gemm_any(m, L.wdown, m->pf_tmp, m->pf_q8, m->pf_h, E, T, FD, st));
     ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
 #undef ST
     return hipSuccess;
@@ -844,9 +919,11 @@ int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out)
         return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: n_ctx above 32768");
     if (hd != 64 && hd != 128 && hd != 256)
         return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: head_dim must be 64, 128 or 256");
-    if (h.n_embd % QK_K || h.ffn_dim % QK_K)
-        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: n_embd and ffn_dim must be multiples of 256");
-    if (h.n_embd / QK_K > kMaxBlocksPerRow || h.ffn_dim / QK_K > kMaxBlocksPerRow)
+    // Q8_0 activation blocks of 32; matrices of whole super-blocks (Q4_K / Q6_K)
+    // are checked per tensor at load
+    if (h.n_embd % 32 || h.ffn_dim % 32)
+        return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: n_embd and ffn_dim must be multiples of 32");
+    if (h.n_embd > kMaxBlocksPerRow * QK_K || h.ffn_dim > kMaxBlocksPerRow * QK_K)
         return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: dimension above 32768");
     if (h.n_embd > 8192)  // the GEMVs that fuse RMSNorm take K <= 8192
         return fail(AXF_ERR_UNSUPPORTED, "axf_llama_create: n_embd above 8192");
@@ -941,6 +1018,8 @@ int axf_llama_load(axf_llama* m) {
     }
     LL_TRY(dalloc(m, (size_t)E * 4, &p));
     m->x = static_cast<float*>(p);
+    LL_TRY(dalloc(m, (size_t)E * 4, &p));
+    m->xb = static_cast<float*>(p);
     LL_TRY(dalloc(m, (size_t)(qo + 2 * kvo) * 4, &p));
     m->qkv = static_cast<float*>(p);
     LL_TRY(dalloc(m, (size_t)qo * 4, &p));

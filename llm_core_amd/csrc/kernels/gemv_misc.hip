@@ -13,7 +13,9 @@
 // These are HBM-bound streams.  LPR lanes share a row and stride over its
 // 32-element blocks (F16: 8-element groups); the lane partials are reduced with
 // shuffles, so the fp32 sums differ from the reference's sequential order
-// only by reassociation.  The 34- and 22-byte blocks are 2-byte aligned and
+// only by reassociation.  gridDim.y tokens (the batched prefill): token t reads
+// activation row t (cols floats, or cols/32 Q8_0 blocks) and writes y row t
+// (rows floats); accumulate != 0 adds to y (the residual projections).  The 34- and 22-byte blocks are 2-byte aligned and
 // read as 16-bit words; F16 rows are read 16 bytes at a time (the entry points
 // require 16-byte aligned rows).
 #include "common.hpp"
@@ -50,6 +52,8 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_q8w_q8(float* __restrict_
                                                               const uint8_t* __restrict__ xq8,
                                                               int rows, int nb, long row_bytes,
                                                               int accumulate) {
+    y += (size_t)blockIdx.y * rows;
+    xq8 += (size_t)blockIdx.y * nb * Q8_0_BYTES;
     const long row = misc_row<LPR>();
     const int rl = threadIdx.x % LPR;
     float acc = 0.f;
@@ -73,7 +77,10 @@ template <int LPR>
 __global__ __launch_bounds__(kMiscThreads) void k_gemv_q8w_f32(float* __restrict__ y,
                                                                const uint8_t* __restrict__ W,
                                                                const float* __restrict__ x,
-                                                               int rows, int nb, long row_bytes) {
+                                                               int rows, int nb, long row_bytes,
+                                                               int accumulate) {
+    y += (size_t)blockIdx.y * rows;
+    x += (size_t)blockIdx.y * nb * 32;
     const long row = misc_row<LPR>();
     const int rl = threadIdx.x % LPR;
     float acc = 0.f;
@@ -95,14 +102,17 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_q8w_f32(float* __restrict
         }
     }
     acc = lanes_sum<LPR>(acc);
-    if (row < rows && rl == 0) y[row] = acc;
+    if (row < rows && rl == 0) y[row] = accumulate ? y[row] + acc : acc;
 }
 
 template <int LPR>
 __global__ __launch_bounds__(kMiscThreads) void k_gemv_q5_0_f32(float* __restrict__ y,
                                                                 const uint8_t* __restrict__ W,
                                                                 const float* __restrict__ x,
-                                                                int rows, int nb, long row_bytes) {
+                                                                int rows, int nb, long row_bytes,
+                                                                int accumulate) {
+    y += (size_t)blockIdx.y * rows;
+    x += (size_t)blockIdx.y * nb * 32;
     const long row = misc_row<LPR>();
     const int rl = threadIdx.x % LPR;
     float acc = 0.f;
@@ -129,7 +139,7 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_q5_0_f32(float* __restric
         }
     }
     acc = lanes_sum<LPR>(acc);
-    if (row < rows && rl == 0) y[row] = acc;
+    if (row < rows && rl == 0) y[row] = accumulate ? y[row] + acc : acc;
 }
 
 template <int LPR>
@@ -137,7 +147,9 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_f16_f32(float* __restrict
                                                                const uint16_t* __restrict__ W,
                                                                const float* __restrict__ x,
                                                                const float* __restrict__ bias,
-                                                               int rows, int cols) {
+                                                               int rows, int cols, int accumulate) {
+    y += (size_t)blockIdx.y * rows;
+    x += (size_t)blockIdx.y * cols;
     const long row = misc_row<LPR>();
     const int rl = threadIdx.x % LPR;
     float acc = 0.f;
@@ -159,7 +171,10 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_f16_f32(float* __restrict
         }
     }
     acc = lanes_sum<LPR>(acc);
-    if (row < rows && rl == 0) y[row] = acc + (bias ? bias[row] : 0.f);
+    if (row < rows && rl == 0) {
+        const float v = acc + (bias ? bias[row] : 0.f);
+        y[row] = accumulate ? y[row] + v : v;
+    }
 }
 
 // Embedding row (rows of T tokens when tok_dev lists them): exact dequant.
@@ -197,7 +212,7 @@ int misc_lpr(int units) { return units >= 64 ? 64 : (units >= 32 ? 32 : 16); }
 #define AXF_MISC_LAUNCH(KERNEL, LPR_, ROWS, ...)                                           \
     do {                                                                                   \
         const dim3 grid_((unsigned)(((long)(ROWS) + (kMiscThreads / LPR_) - 1) /           \
-                                    (kMiscThreads / LPR_)));                              \
+                                    (kMiscThreads / LPR_)), (unsigned)T);                 \
         hipLaunchKernelGGL((KERNEL<LPR_>), grid_, dim3(kMiscThreads), 0, st, __VA_ARGS__); \
     } while (0)
 
@@ -210,30 +225,34 @@ int misc_lpr(int units) { return units >= 64 ? 64 : (units >= 32 ? 32 : 16); }
     } while (0)
 
 hipError_t launch_gemv_q8w_q8(float* y, const void* W, const void* xq8, int rows, int nb,
-                              long row_bytes, int accumulate, hipStream_t st) {
+                              long row_bytes, int accumulate, hipStream_t st, int T) {
+    if (T <= 0 || T > 65535) return hipErrorInvalidValue;
     AXF_MISC_DISPATCH(k_gemv_q8w_q8, nb, rows, y, static_cast<const uint8_t*>(W),
                       static_cast<const uint8_t*>(xq8), rows, nb, row_bytes, accumulate);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_q8w_f32(float* y, const void* W, const float* x, int rows, int nb,
-                               long row_bytes, hipStream_t st) {
+                               long row_bytes, hipStream_t st, int accumulate, int T) {
+    if (T <= 0 || T > 65535) return hipErrorInvalidValue;
     AXF_MISC_DISPATCH(k_gemv_q8w_f32, nb, rows, y, static_cast<const uint8_t*>(W), x, rows, nb,
-                      row_bytes);
+                      row_bytes, accumulate);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_q5_0_f32(float* y, const void* W, const float* x, int rows, int nb,
-                                long row_bytes, hipStream_t st) {
+                                long row_bytes, hipStream_t st, int accumulate, int T) {
+    if (T <= 0 || T > 65535) return hipErrorInvalidValue;
     AXF_MISC_DISPATCH(k_gemv_q5_0_f32, nb, rows, y, static_cast<const uint8_t*>(W), x, rows, nb,
-                      row_bytes);
+                      row_bytes, accumulate);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_f16_f32(float* y, const void* W, const float* x, const float* bias,
-                               int rows, int cols, hipStream_t st) {
+                               int rows, int cols, hipStream_t st, int accumulate, int T) {
+    if (T <= 0 || T > 65535) return hipErrorInvalidValue;
     AXF_MISC_DISPATCH(k_gemv_f16_f32, cols / 8, rows, y, static_cast<const uint16_t*>(W), x, bias,
-                      rows, cols);
+                      rows, cols, accumulate);
     return hipGetLastError();
 }
 

@@ -259,8 +259,8 @@ __global__ void k_rope_kv_rows(const float* __restrict__ k, int k_ld, const floa
 
 // SwiGLU of T rows whose gate and up halves are interleaved by row blocks of B
 // ([gate B][up B] ... per row of 2*n), into Q8_0 blocks of the [T][n] result.
-__global__ void k_swiglu_gu(uint8_t* __restrict__ outq8, const float* __restrict__ gu, int T,
-                            int n, int B) {
+__global__ void k_swiglu_gu(uint8_t* __restrict__ outq8, float* __restrict__ out,
+                            const float* __restrict__ gu, int T, int n, int B) {
     const int n4 = n / 4;
     for (long q = (long)blockIdx.x * blockDim.x + threadIdx.x; q < (long)T * n4;
          q += (long)gridDim.x * blockDim.x) {
@@ -275,6 +275,7 @@ __global__ void k_swiglu_gu(uint8_t* __restrict__ outq8, const float* __restrict
         o.y = swiglu1(g.y, u.y);
         o.z = swiglu1(g.z, u.z);
         o.w = swiglu1(g.w, u.w);
+        if (out) reinterpret_cast<float4*>(out)[q] = o;  // [T][n] fp32 rows
         q8_block_store(outq8 + (size_t)(q >> 3) * Q8_0_BYTES, (int)(q & 7), o);
     }
 }
@@ -483,10 +484,11 @@ hipError_t launch_rope_kv_rows(const float* k, int k_ld, const float* v, int v_l
                        sin_t);
     return hipGetLastError();
 }
-hipError_t launch_swiglu_gu(void* outq8, const float* gu, int T, int n, int B, hipStream_t st) {
+hipError_t launch_swiglu_gu(void* outq8, const float* gu, int T, int n, int B, hipStream_t st,
+                            float* out) {
     if (n % 32 || B % 4 || n % B) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_swiglu_gu, dim3(grid_for((long)T * n / 4, 256)), dim3(256), 0, st,
-                       static_cast<uint8_t*>(outq8), gu, T, n, B);
+                       static_cast<uint8_t*>(outq8), out, gu, T, n, B);
     return hipGetLastError();
 }
 hipError_t launch_embed_rows(int qtype, float* out, const void* W, const int* toks_dev, int T,

@@ -49,6 +49,10 @@ LLAMA2_7B = dict(n_layer=32, n_embd=4096, n_heads=32, n_kv_heads=32, ffn_dim=110
 QWEN25_3B_LAYER = dict(n_layer=1, n_embd=2048, n_heads=16, n_kv_heads=2, ffn_dim=11008,
                        n_vocab=151936, rms_eps=1e-6, rope_theta=1e6)
 
+# Qwen2.5-0.5B shape (qwen2 architecture: q/k/v biases, tied embeddings)
+QWEN25_05B = dict(n_layer=24, n_embd=896, n_heads=14, n_kv_heads=2, ffn_dim=4864,
+                  n_vocab=151936, rms_eps=1e-6, rope_theta=1e6)
+
 Q4K_M_TYPES = {
     "attn_q": AXF_TYPE_Q4_K,
     "attn_k": AXF_TYPE_Q4_K,
@@ -58,6 +62,19 @@ Q4K_M_TYPES = {
     "ffn_up": AXF_TYPE_Q4_K,
     "ffn_down": AXF_TYPE_Q6_K,
 }
+
+
+def q4k_m_fallback_types(layer: int, n_layer: int) -> dict:
+    """The weight types llama.cpp's Q4_K_M mix gives a model whose hidden size
+    is not a multiple of 256 (Qwen2.5-0.5B: 896): matrices with 896-wide rows
+    fall back from Q4_K to Q5_0 and from Q6_K to Q8_0; ffn_down (4864-wide rows)
+    keeps Q6_K on the layers that get more bits (the first and last eighth and
+    every third layer between), Q4_K elsewhere."""
+    more = layer < n_layer // 8 or layer >= 7 * n_layer // 8 or (layer - n_layer // 8) % 3 == 2
+    return {"attn_q": AXF_TYPE_Q5_0, "attn_k": AXF_TYPE_Q5_0,
+            "attn_v": AXF_TYPE_Q8_0 if more else AXF_TYPE_Q5_0,
+            "attn_output": AXF_TYPE_Q5_0, "ffn_gate": AXF_TYPE_Q5_0, "ffn_up": AXF_TYPE_Q5_0,
+            "ffn_down": AXF_TYPE_Q6_K if more else AXF_TYPE_Q4_K}
 
 
 def synth_other(qtype: int, rows: int, cols: int, seed: int, std: float = 0.02) -> np.ndarray:
@@ -98,7 +115,8 @@ class SynthLlama:
     norm_std: float = 0.0
     with_bias: bool = False
     embd_type: int = AXF_TYPE_Q4_K   # token_embd.weight
-    head_type: int = AXF_TYPE_Q6_K   # output.weight
+    head_type: int = AXF_TYPE_Q6_K   # output.weight; None: tied to token_embd (no output.weight)
+    layer_types: object = None       # {base: qtype} or layer -> {base: qtype}; default Q4K_M_TYPES
     tensors: dict = field(default_factory=dict)  # name -> (qtype, ndarray)
 
     def __post_init__(self) -> None:
@@ -127,7 +145,8 @@ class SynthLlama:
             self.tensors[name] = (AXF_TYPE_F32, v)
 
         qw("token_embd.weight", self.embd_type, hp.n_vocab, E)
-        qw("output.weight", self.head_type, hp.n_vocab, E)
+        if self.head_type is not None:
+            qw("output.weight", self.head_type, hp.n_vocab, E)
         norm("output_norm.weight", E)
         shapes = {"attn_q": (qo, E), "attn_k": (kvo, E), "attn_v": (kvo, E),
                   "attn_output": (E, qo), "ffn_gate": (FD, E), "ffn_up": (FD, E),
@@ -135,8 +154,9 @@ class SynthLlama:
         for layer in range(hp.n_layer):
             norm(f"blk.{layer}.attn_norm.weight", E)
             norm(f"blk.{layer}.ffn_norm.weight", E)
+            lt = self.layer_types(layer) if callable(self.layer_types) else self.layer_types
             for base, (rows, cols) in shapes.items():
-                qw(f"blk.{layer}.{base}.weight", Q4K_M_TYPES[base], rows, cols)
+                qw(f"blk.{layer}.{base}.weight", (lt or {}).get(base, Q4K_M_TYPES[base]), rows, cols)
             if self.with_bias:
                 for base, n in (("attn_q", qo), ("attn_k", kvo), ("attn_v", kvo)):
                     self.tensors[f"blk.{layer}.{base}.bias"] = (
@@ -151,6 +171,8 @@ class SynthLlama:
         for name, (qt, arr) in self.tensors.items():
             if name == "token_embd.weight":
                 total += hip.row_bytes(qt, self.hp.n_embd)
+                if "output.weight" not in self.tensors:  # tied head: the whole matrix
+                    total += arr.nbytes
             else:
                 total += arr.nbytes
         return total

@@ -96,13 +96,13 @@ def test_rejected_files(ctx, tmp_path):
     w = G.llama_gguf(m, arch="qwen3")
     w.add_tensor("blk.0.attn_q_norm.weight", np.ones(32, np.float32), G.GGML_F32, (32,))
     _expect_error(ctx, w.write(tmp_path / "b.gguf"), AXF_ERR_INVALID_ARG, "attn_q_norm")
-    # a weight type the decoder does not run (F16 = 1)
+    # a weight type the decoder does not run (Q4_0 = 2: 18-byte blocks of 32)
     bad = copy.copy(m)
     bad.tensors = dict(m.tensors)
     w = G.llama_gguf(bad)
     w.infos = [i for i in w.infos if b"blk.0.attn_output.weight" not in i]
-    w.add_tensor("blk.0.attn_output.weight", np.zeros(512 * 512, np.float16), 1, (512, 512))
-    _expect_error(ctx, w.write(tmp_path / "c.gguf"), AXF_ERR_UNSUPPORTED, "GGML type 1")
+    w.add_tensor("blk.0.attn_output.weight", np.zeros(512 * 512 // 32 * 18, np.uint8), 2, (512, 512))
+    _expect_error(ctx, w.write(tmp_path / "c.gguf"), AXF_ERR_UNSUPPORTED, "GGML type 2")
     # tokenizer vocabulary and token_embd disagree
     w = G.llama_gguf(m, tokens=False)
     w.add_array("tokenizer.ggml.tokens", G.STRING, ["x"] * 999)

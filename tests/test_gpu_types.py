@@ -1,0 +1,219 @@
+"""Layer matrices of the other GGUF weight types (Q8_0, Q5_0, F16) and hidden
+sizes that are not a multiple of 256, on the device decoder.
+
+The reference's decode step routes every layer matrix through gemv_wt_q8
+(/root/reference/src/models/llama_model.cpp:767-831): Q8_0 weights take the
+Q8_0 activation, Q5_0 and F16 weights the fp32 one (the normalised row, the
+attention output or the SwiGLU output).  Its batched prefill (gemm_wt_q8,
+:837-879) gives Q8_0 weights the fp32 rows too.  A Q4_K_M file of a model
+whose hidden size is not a multiple of 256 (Qwen2.5-0.5B: 896) holds such
+matrices: llama.cpp falls back from Q4_K to Q5_0 and from Q6_K to Q8_0 for
+rows that are not whole super-blocks.
+
+The toy model here (hidden 384 = 6 heads of 64, GQA 6/2, FFN 1024, biases,
+Q8_0 embedding, tied head) has five layers with every type in every
+position: layer 0 the Q4_K_M fall-back mix (Q5_0 q/k/o/gate/up, Q8_0 v, Q6_K
+down), layers 1-4 F16/Q8_0/Q5_0 mixes whose down projections are Q8_0,
+Q4_K, F16 and Q5_0.  Checked against the oracle:
+  * each decode stage on the device's own inputs (K/V rows and the attention
+    output's Q8_0 blocks bit-exact, the rest within |gpu - ref| <= 1e-4 +
+    1e-3 |ref|);
+  * 32 greedy tokens identical to the oracle's under both prefill schemes
+    (seeds whose oracle top-2 margins stay above the Q8_0-flip bound), and
+    graph replay = eager launches;
+  * the batched prefill's last-row logits against the oracle's batch;
+  * the model from a GGUF file equals the tensor-API model bit for bit;
+  * the Qwen2.5-0.5B shape (24 layers, hidden 896, 14/2 heads, FFN 4864,
+    vocabulary 151936) decodes with per-step logits against the oracle.
+"""
+import numpy as np
+import pytest
+
+from gpu_helpers import layer_stage_errors, within
+from llm_core_amd._ffi import (AXF_TYPE_F16 as F16, AXF_TYPE_Q4_K as Q4K, AXF_TYPE_Q5_0 as Q5,
+                               AXF_TYPE_Q6_K as Q6K, AXF_TYPE_Q8_0 as Q8)
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOY = dict(n_layer=5, n_embd=384, n_heads=6, n_kv_heads=2, ffn_dim=1024, n_vocab=512, n_ctx=64,
+           rms_eps=1e-6, rope_theta=1e6)
+LAYER_TYPES = [
+    dict(attn_q=Q5, attn_k=Q5, attn_v=Q8, attn_output=Q5, ffn_gate=Q5, ffn_up=Q5, ffn_down=Q6K),
+    dict(attn_q=F16, attn_k=Q8, attn_v=Q5, attn_output=Q8, ffn_gate=Q8, ffn_up=F16, ffn_down=Q8),
+    dict(attn_q=Q8, attn_k=Q8, attn_v=F16, attn_output=F16, ffn_gate=F16, ffn_up=Q5, ffn_down=Q4K),
+    dict(attn_q=Q5, attn_k=F16, attn_v=Q5, attn_output=Q8, ffn_gate=Q8, ffn_up=Q8, ffn_down=F16),
+    dict(attn_q=Q8, attn_k=Q5, attn_v=Q8, attn_output=F16, ffn_gate=Q5, ffn_up=Q8, ffn_down=Q5),
+]
+# oracle top-2 margins of these seeds' 32 greedy tokens stay >= 0.05 under
+# both prefill schemes (a Q8_0 rounding flip moves these logits by ~1e-2)
+GREEDY_SEEDS = [2, 15, 22]
+
+
+def toy_model(seed, n_ctx=None):
+    from llm_core_amd.model import Hparams, SynthLlama
+
+    hp = Hparams(**{**TOY, **({"n_ctx": n_ctx} if n_ctx else {})})
+    return SynthLlama(hp, seed=seed, norm_std=0.1, with_bias=True, embd_type=Q8, head_type=None,
+                      layer_types=lambda layer: LAYER_TYPES[layer])
+
+
+@pytest.mark.parametrize("layer", [0, 1, 2, 3, 4])
+def test_decode_stages_every_type(ctx, layer):
+    from llm_core_amd import hip
+    from llm_core_amd.model import LlamaHip
+
+    m = toy_model(3, n_ctx=40)
+    hp = m.hp
+    T = {k: v[1] for k, v in m.tensors.items()}
+    kvo, prior = hp.n_kv_heads * hp.head_dim, 37
+    kc = hip.synth_normal(prior * kvo, 51).reshape(prior, kvo)
+    vc = hip.synth_normal(prior * kvo, 52).reshape(prior, kvo)
+    with LlamaHip(ctx, m) as g:
+        g.set_kv(layer, kc, vc, prior)
+        x0 = hip.synth_normal(hp.n_embd, 53)
+        g.set_x(x0)
+        for tag, err, nbad, rel in layer_stage_errors(ctx, g, T, hp, layer, prior,
+                                                      types=LAYER_TYPES[layer]):
+            print(f"  layer {layer} {tag}: max |err| {err:.3e}, norm-wise {rel:.2e}", flush=True)
+            assert nbad == 0, f"{tag}: {nbad} elements outside tolerance, max |err| {err:.3e}"
+        x2 = g.get_x()
+        g.set_kv(layer, kc, vc, prior)
+        g.set_x(x0)
+        g.forward_layer(layer, prior)  # the whole layer in one call: the same bits
+        assert np.array_equal(g.get_x(), x2)
+
+
+@pytest.mark.parametrize("seed", GREEDY_SEEDS)
+def test_greedy_32_tokens_every_type(ctx, seed):
+    from llm_core_amd.model import LlamaHip
+
+    m = toy_model(seed)
+    rng = np.random.default_rng(seed)
+    prompt = np.concatenate([[1], rng.integers(0, m.hp.n_vocab, 7)]).astype(np.int32)
+    with LlamaHip(ctx, m) as g:
+        graph = g.generate(prompt, 32, use_graph=True)
+        eager = g.generate(prompt, 32, use_graph=False)
+        tbt = g.generate(prompt, 32, use_graph=True, batched_prefill=False)
+    om = O.OracleModel(m.hp, m.tensors)
+    try:
+        bat, mb = om.generate(prompt, 32, batched_prefill=True)
+        seq, ms = om.generate(prompt, 32, batched_prefill=False)
+    finally:
+        om.close()
+    assert min(mb.min(), ms.min()) >= 0.05, (mb.min(), ms.min())
+    assert np.array_equal(graph, eager), "graph replay and eager launches disagree"
+    assert np.array_equal(graph, bat), (graph, bat)
+    assert np.array_equal(tbt, seq), (tbt, seq)
+
+
+# A single Q8_0 rounding flip of one activation moves these logits by up to
+# ~2e-2 (the teacher-forced bound of test_gpu_model.py); the prefill's K-quant
+# GEMMs (matrix cores) and RMSNorm rows sum in other orders than the oracle's
+# per-token kernels, so a flip can occur anywhere in the five layers.
+ONE_FLIP = 3e-2
+
+
+@pytest.mark.parametrize("seed,T", [(4, 24), (9, 40)])
+def test_forward_batch_every_type(ctx, seed, T):
+    """Batched prefill (Q8_0 layer matrices on the fp32 rows, as gemm_wt_q8):
+    last-row logits within the tolerance of the oracle's single batch, or
+    within one Q8_0 flip's worth where the summation orders diverge; the
+    greedy pick agrees wherever the oracle's margin exceeds twice the
+    difference.  A wiring slip (a Q8_0 matrix on the Q8_0 rows, a dropped
+    bias) moves them by far more."""
+    from llm_core_amd.model import LlamaHip
+
+    m = toy_model(seed)
+    rng = np.random.default_rng(seed)
+    toks = np.concatenate([[1], rng.integers(0, m.hp.n_vocab, T - 1)]).astype(np.int32)
+    om = O.OracleModel(m.hp, m.tensors)
+    om.forward_batch(toks, 0)
+    ol = om.logits().copy()
+    om.close()
+    with LlamaHip(ctx, m) as g:
+        g.forward_batch(toks[:5], 0)  # two chunks: positions 0 and 5
+        g.forward_batch(toks[5:], 5)
+        gl = g.logits()
+    ok, err, nbad = within(gl, ol)
+    print(f"  prefill {T} tokens: max |err| {err:.3e} ({nbad} outside the tolerance), "
+          f"logit scale {np.max(np.abs(ol)):.3f}", flush=True)
+    assert ok or err < ONE_FLIP, f"{nbad} logits outside tolerance, max |err| {err:.3e}"
+    if O.top2_margin(ol) > 2 * err:
+        assert int(np.argmax(gl)) == O.argmax(ol)
+
+
+def test_gguf_file_every_type(ctx, tmp_path):
+    """The toy model as a qwen2 GGUF file (tied head) against the same tensors
+    registered one by one: identical logits and greedy tokens."""
+    from llm_core_amd import gguf as G
+    from llm_core_amd.model import LlamaHip
+
+    m = toy_model(6)
+    path = G.llama_gguf(m, arch="qwen2", tied=True).write(tmp_path / "types.gguf")
+    prompt = np.array([1, 44, 300, 7, 511, 2], np.int32)
+    with LlamaHip.from_gguf(ctx, path) as a, LlamaHip(ctx, m) as b:
+        assert a.device_bytes() == b.device_bytes()
+        a.forward_batch(prompt, 0)
+        b.forward_batch(prompt, 0)
+        assert np.array_equal(a.logits(), b.logits())
+        assert np.array_equal(a.generate(prompt, 10), b.generate(prompt, 10))
+
+
+def test_rejects_kquant_rows_of_partial_superblocks(ctx):
+    """A Q4_K matrix whose rows are not whole 256-weight super-blocks (hidden
+    384) is refused at load with AXF_ERR_UNSUPPORTED."""
+    from llm_core_amd._ffi import AXF_ERR_UNSUPPORTED, AxfError
+    from llm_core_amd.model import LlamaHip
+
+    m = toy_model(2)
+    qt, w = m.tensors["blk.0.attn_q.weight"]
+    rows = m.hp.n_heads * m.hp.head_dim
+    m.tensors["blk.0.attn_q.weight"] = (Q4K, np.zeros(rows * 144, np.uint8))  # one block per row
+    with pytest.raises(AxfError) as e:
+        LlamaHip(ctx, m)
+    assert e.value.code == AXF_ERR_UNSUPPORTED and "super-blocks" in str(e.value)
+
+
+def test_qwen25_05b_shape_decode(ctx):
+    """Qwen2.5-0.5B shape with the Q4_K_M fall-back mix (24 layers, hidden
+    896, 14/2 heads of 64, FFN 4864, vocabulary 151936, q/k/v biases, Q8_0
+    embedding tied to the head): a 6-token batched prefill and four decode
+    steps teacher-forced on the oracle's cache; per step the logits agree
+    within a few Q8_0 flips' worth and the greedy pick agrees wherever the
+    oracle's margin exceeds twice the difference."""
+    from llm_core_amd.model import QWEN25_05B, Hparams, LlamaHip, SynthLlama, q4k_m_fallback_types
+
+    hp = Hparams(n_ctx=64, **QWEN25_05B)
+    m = SynthLlama(hp, seed=8, norm_std=0.1, with_bias=True, embd_type=Q8, head_type=None,
+                   layer_types=lambda layer: q4k_m_fallback_types(layer, hp.n_layer))
+    prompt = np.array([1, 300, 7000, 151000, 42, 99], np.int32)
+    om = O.OracleModel(hp, m.tensors)
+    g = LlamaHip(ctx, m)
+    try:
+        om.forward_batch(prompt, 0)
+        g.forward_batch(prompt, 0)
+        ol, gl = om.logits(), g.logits()
+        err = float(np.max(np.abs(gl.astype(np.float64) - ol)))
+        print(f"  prefill: max |err| {err:.3e} (logit scale {np.max(np.abs(ol)):.3f})", flush=True)
+        assert err < 0.05 * max(1.0, float(np.max(np.abs(ol))))
+        toks = list(prompt)
+        for step in range(4):
+            pos = len(toks)
+            nxt = O.argmax(om.logits())
+            kk, vv = om.kv_view()
+            for layer in range(hp.n_layer):
+                g.set_kv(layer, kk[layer, :pos], vv[layer, :pos], pos)
+            om.forward_token(nxt, pos)
+            g.forward_token(nxt, pos)
+            ol, gl = om.logits(), g.logits()
+            diff = float(np.max(np.abs(gl.astype(np.float64) - ol)))
+            print(f"  step {step} pos {pos}: max |err| {diff:.3e}, margin {O.top2_margin(ol):.3e}",
+                  flush=True)
+            assert diff < 0.05 * max(1.0, float(np.max(np.abs(ol))))
+            if O.top2_margin(ol) > 2 * diff:
+                assert int(np.argmax(gl)) == O.argmax(ol)
+            toks.append(nxt)
+    finally:
+        g.close()
+        om.close()
