@@ -136,6 +136,41 @@ def c3_run(ctx, warmup=10, steps=100):
                     "1024: the layer plus embedding, a 512-row head and argmax"}
 
 
+def qwen05b_run(ctx, warmup=10, steps=50, n_ctx=2048):
+    """A Qwen2.5-0.5B-shape model (24 layers, hidden 896, 14/2 heads of 64,
+    FFN 4864, vocabulary 151936, q/k/v biases, head tied to a Q8_0 embedding)
+    with llama.cpp's Q4_K_M types for its widths: Q5_0 / Q8_0 for the
+    896-wide rows, Q4_K / Q6_K for ffn_down.  Decode step at context n_ctx
+    (KV rows 0..n_ctx-2 filled N(0,1)), graph-replayed.  The reference
+    publishes ~30.8 tok/s for this model on an i9-12900K (README.md:325)."""
+    from llm_core_amd import _ffi, hip
+    from llm_core_amd.model import (QWEN25_05B, Hparams, LlamaHip, SynthLlama,
+                                    q4k_m_fallback_types)
+
+    hp = Hparams(n_ctx=n_ctx, **QWEN25_05B)
+    t0 = time.time()
+    model = SynthLlama(hp, seed=5, with_bias=True, embd_type=_ffi.AXF_TYPE_Q8_0, head_type=None,
+                       layer_types=lambda layer: q4k_m_fallback_types(layer, hp.n_layer))
+    kve = hp.n_kv_heads * hp.head_dim
+    pos = n_ctx - 1
+    with LlamaHip(ctx, model) as gpu:
+        for layer in range(hp.n_layer):
+            gpu.set_kv(layer, hip.synth_normal(pos * kve, 600 + layer).reshape(pos, kve),
+                       hip.synth_normal(pos * kve, 700 + layer).reshape(pos, kve), pos)
+        ms = gpu.bench_decode(pos, warmup, steps) / steps
+        pf = gpu.bench_prefill(512, reps=3)
+    nbytes = model.weight_bytes_per_token() + 2 * hp.n_layer * n_ctx * kve * 4
+    log(f"qwen2.5-0.5b shape (Q5_0/Q8_0/Q4_K/Q6_K, tied Q8_0 head) decode step @ctx {n_ctx}: "
+        f"{ms * 1e3:.1f} us -> {1e3 / ms:.0f} tok/s, {nbytes / (ms * 1e-3) / 1e9:.0f} GB/s over "
+        f"{nbytes / 1e6:.1f} MB; prefill 512: {pf:.2f} ms (built in {time.time() - t0:.1f} s)")
+    return {"us_per_step": round(ms * 1e3, 2), "tok_s": round(1e3 / ms, 1),
+            "bytes_per_step": int(nbytes), "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "prefill_512_ms": round(pf, 2), "context": n_ctx,
+            "published_reference_tok_s": 30.8,
+            "what": "Qwen2.5-0.5B-shape synthetic model, llama.cpp Q4_K_M types for hidden 896 "
+                    "(reference figure: i9-12900K, README.md:325)"}
+
+
 def c4_sweep(ctx, Ms=(1, 2, 4, 8, 16, 32, 64)):
     res = [gemm_case(ctx, M) for M in Ms]
     for g4 in res:
@@ -483,7 +518,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="approximate CPU seconds spent on the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill", "c3"],
+    ap.add_argument("--only", choices=["all", "gemv", "decode", "gemm", "prefill", "c3", "qwen05b"],
                     default="all")
     ap.add_argument("--eager", action="store_true",
                     help="direct launches instead of captured-graph replay in every timing "
@@ -539,6 +574,9 @@ def main() -> int:
             + ("running under rocprofv3" if under_profiler() else "--eager"))
     out: dict = {"launch": "eager" if eager else "hip-graph replay"}
 
+    if args.only == "qwen05b":  # Qwen2.5-0.5B-shape decode alone (not a bench line)
+        print(json.dumps({"qwen25_05b_q4km": qwen05b_run(ctx)}))
+        return 0
     if args.only == "c3":  # config 3 layer alone (not a bench line)
         print(json.dumps({"c3_qwen25_3b_layer_decode": c3_run(ctx, args.warmup, args.steps)}))
         return 0
@@ -613,6 +651,7 @@ def main() -> int:
                                       "read_us": rd2["us"],
                                       "vs_read": round(rd2["us"] / c2["us_per_launch"], 4)},
             "c3_qwen25_3b_layer_decode": None if args.skip_c4 else c3_run(ctx),
+            "qwen25_05b_q4km": None if args.skip_c4 else qwen05b_run(ctx),
         }
         if not args.no_cpu and not args.skip_c4:
             from oracle import oracle as O

@@ -368,6 +368,10 @@ typedef struct {
     int qk_norm_order;
 } axf_llama_hparams;
 
+/* n_embd and ffn_dim multiples of 32 (n_embd <= 8192, ffn_dim <= 32768),
+ * head_dim = n_embd / n_heads of 64, 128 or 256, at most 8 query heads per
+ * KV head, n_ctx <= 32768; otherwise AXF_ERR_UNSUPPORTED (or
+ * AXF_ERR_INVALID_ARG for inconsistent values). */
 int axf_llama_create(axf_ctx* ctx, const axf_llama_hparams* hp, axf_llama** out);
 int axf_llama_destroy(axf_llama* m);
 /* Register a host tensor by its GGUF name (token_embd.weight, output_norm.weight,
@@ -377,11 +381,17 @@ int axf_llama_destroy(axf_llama* m);
  * buffer must stay valid until axf_llama_load returns. */
 int axf_llama_set_tensor(axf_llama* m, const char* name, int qtype, const void* host,
                          size_t bytes);
-/* Upload all registered tensors once and allocate the KV cache and buffers. */
+/* Upload all registered tensors once and allocate the KV cache and buffers.
+ * Every matrix may be Q4_K or Q6_K (rows of whole 256-weight super-blocks),
+ * Q8_0 or Q5_0 (rows of whole 32-blocks) or F16 (rows a multiple of 8), in
+ * any mix: the decode step multiplies Q4_K / Q6_K / Q8_0 matrices with the
+ * Q8_0 activation and Q5_0 / F16 ones with the fp32 activation (gemv_wt_q8,
+ * llama_model.cpp:767-831); the batched prefill gives Q8_0 / Q5_0 / F16 the
+ * fp32 rows (gemm_wt_q8, :837-879).  Another type: AXF_ERR_UNSUPPORTED. */
 int axf_llama_load(axf_llama* m);
 /* Register every model tensor of an open GGUF file (the names build_weights
- * reads, llama_model.cpp:975-1006) straight from the mapping and load.  F32,
- * Q4_K and Q6_K tensors (and Q8_0 / Q5_0 / F16 for the embedding and head). */
+ * reads, llama_model.cpp:975-1006) straight from the mapping and load.  F32
+ * vectors; F16, Q8_0, Q5_0, Q4_K and Q6_K matrices (as axf_llama_load). */
 int axf_llama_load_gguf(axf_llama* m, const axf_gguf* g);
 /* Engine::from_gguf + the model construction of llama_generate_cpu_impl
  * (llama_model.cpp:1508-1522): hyperparameters from the file's metadata with
