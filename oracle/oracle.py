@@ -109,6 +109,7 @@ def _load_ref() -> C.CDLL | None:
                                C.POINTER(i32)], C.c_double),
         "ref_time_head_argmax": ([C.POINTER(vp), i32, i32, i32, vp, vp, i32, i32, C.POINTER(i32),
                                   C.POINTER(i32)], C.c_double),
+        "ref_generate_greedy": ([vp, vp, i32, i32, i32, vp, vp, i32, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -298,6 +299,27 @@ def ref_time_decode_step(model: "OracleModel", kv_k: np.ndarray, kv_v: np.ndarra
     t = ref.ref_time_decode_step(C.byref(model.m), _ptr(kv_k), _ptr(kv_v), pos, warmup, steps,
                                  n_threads, C.byref(used), C.byref(last))
     return t, used.value, last.value
+
+
+def ref_generate_greedy(model: "OracleModel", prompt, n_gen: int, n_threads: int = 0, top_k: int = 0):
+    """Greedy generation of llama_generate_cpu_impl (batched prefill of the
+    prompt as given, then one decode step per token) on the reference's
+    compiled kernels and ThreadPool (ref_shim.cpp): (ids, top-1 minus top-2
+    margins of the logits each id was taken from), and with top_k > 0 also
+    each step's top_k (ids, logits), largest first.  Q4_K / Q6_K layer
+    matrices."""
+    assert ref is not None, "oracle/_ref not built"
+    p = np.ascontiguousarray(prompt, np.int32)
+    toks = np.zeros(max(n_gen, 1), np.int32)
+    margins = np.zeros(max(n_gen, 1), np.float32)
+    tk = max(top_k, 1)
+    tids = np.zeros((max(n_gen, 1), tk), np.int32)
+    tvals = np.zeros((max(n_gen, 1), tk), np.float32)
+    n = ref.ref_generate_greedy(C.byref(model.m), _ptr(p), p.size, n_gen, n_threads, _ptr(toks),
+                                _ptr(margins), top_k, _ptr(tids), _ptr(tvals))
+    if top_k > 0:
+        return toks[:n], margins[:n], tids[:n], tvals[:n]
+    return toks[:n], margins[:n]
 
 
 MISC_BLOCK = {8: 34, 6: 22}  # bytes per 32 elements: Q8_0, Q5_0

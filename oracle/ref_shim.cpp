@@ -10,6 +10,7 @@
 // the reference's header src/core/thread_pool.hpp, included where it lies.
 #include <algorithm>
 #include <chrono>
+#include <cmath>
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
@@ -445,4 +446,209 @@ extern "C" double ref_time_decode_step(const orc_model* m, float* kv_k, float* k
     if (last_token) *last_token = token;
     std::sort(t.begin(), t.begin() + steps);
     return steps > 0 ? t[steps / 2] : 0.0;
+}
+
+// ---------------------------------------------------------------------------
+// Greedy generation of llama_generate_cpu_impl (llama_model.cpp:1502-1631)
+// with temperature 0, no repetition penalty and no EOS stop, on the
+// reference's compiled kernels: the prompt (used as given: the caller starts
+// it with BOS) prefilled as one llama_forward_batch (:1339-1462: Q8_0 rows,
+// the Q4_K GEMM over all tokens, Q6_K per token, causal attention of every
+// row), then llama_forward_token per generated token (:1207-1333, the r8 /
+// 4-row Q8_0 GEMVs and the fused gate+up) - the GEMMs and GEMVs split over
+// the reference ThreadPool by rows, which does not change any result (each
+// output is computed by one thread).  The glue ops are the oracle's
+// restatement.  out_tokens[i] = the i-th generated id; out_margins[i] = the
+// top-1 minus top-2 logit it was taken from.  Returns the number generated
+// (stops at the context end).
+// ---------------------------------------------------------------------------
+namespace {
+
+void gemm_wt_q8_ref(float* Y, const WtR& W, const block_q8_0* XQ8, int M, int T, int K,
+                    axonforge::ThreadPool* pool, bool vnni) {
+    const size_t rb = (size_t)(K / 256) * (W.w->type == ORC_TYPE_Q6_K ? 210 : 144);
+    auto fn = [&](int s, int e) {
+        if (W.w->type == ORC_TYPE_Q6_K) {
+            for (int t = 0; t < T; t++)
+                cx::gemv_q6k_q8_avx2_range(Y + (size_t)t * M, W.w->data, XQ8 + (size_t)t * (K / 32),
+                                           s, e, K, rb);
+        } else if (vnni) {
+            cx::gemm_q4k_q8_avxvnni_range(Y, W.w->data, XQ8, M, T, K, rb, s, e);
+        } else {
+            cx::gemm_q4k_q8_avx2_range(Y, W.w->data, XQ8, M, T, K, rb, s, e);
+        }
+    };
+    if (pool && M >= 32) pool->parallel_for(M, fn); else fn(0, M);
+}
+
+}  // namespace
+
+extern "C" int ref_generate_greedy(const orc_model* m, const int32_t* prompt, int n_prompt,
+                                   int n_gen, int n_threads, int32_t* out_tokens,
+                                   float* out_margins, int top_k, int32_t* top_ids,
+                                   float* top_vals) {
+    if (n_threads <= 0) n_threads = std::min(16, (int)std::thread::hardware_concurrency());
+    const int E = m->n_embd, H = m->n_heads, KVH = m->n_kv_heads, HD = E / H, FD = m->ffn_dim;
+    const int kve = KVH * HD, L = m->n_layer, NC = m->n_ctx, V = m->n_vocab, T = n_prompt;
+    if (T < 1 || T > NC) return 0;
+    const bool vnni = cx::cpu_features().avxvnni;
+    std::vector<WtR> wq, wk, wv, wo, wg, wu, wd;
+    for (int l = 0; l < L; l++) {
+        const orc_layer& lw = m->layers[l];
+        wq.push_back(make_wt(&lw.wq, H * HD, E));
+        wk.push_back(make_wt(&lw.wk, kve, E));
+        wv.push_back(make_wt(&lw.wv, kve, E));
+        wo.push_back(make_wt(&lw.wo, E, H * HD));
+        wg.push_back(make_wt(&lw.wgate, FD, E));
+        wu.push_back(make_wt(&lw.wup, FD, E));
+        wd.push_back(make_wt(&lw.wdown, E, FD));
+    }
+    WtR head = make_wt(&m->output, V, E);
+    cpu_set_t orig_aff;
+    sched_getaffinity(0, sizeof(orig_aff), &orig_aff);
+    const int nw = n_threads - 1;
+    std::unique_ptr<axonforge::ThreadPool> pool;
+    if (nw > 0) {
+        pool = std::make_unique<axonforge::ThreadPool>(nw);
+        axonforge::ThreadPool::pin_caller(nw);
+    }
+    std::vector<float> kv_k((size_t)L * NC * kve), kv_v(kv_k.size());
+    std::vector<float> rc((size_t)NC * HD / 2), rs(rc.size()), logits(V);
+    orc_rope_table(rc.data(), rs.data(), HD, m->rope_theta, NC);
+    const size_t rbe = (size_t)(E / 256) * (m->tok_embd.type == ORC_TYPE_Q6_K ? 210 : 144);
+    auto embed = [&](float* out, int tok) {
+        if (m->tok_embd.type == ORC_TYPE_Q6_K)
+            orc_dequant_q6k(out, m->tok_embd.data + (size_t)tok * rbe, E / 256);
+        else
+            orc_dequant_q4k(out, m->tok_embd.data + (size_t)tok * rbe, E / 256);
+    };
+    auto add_rows = [](float* y, const float* b, int rows, int n) {
+        if (!b) return;
+        for (int t = 0; t < rows; t++)
+            for (int i = 0; i < n; i++) y[(size_t)t * n + i] += b[i];
+    };
+
+    // ---- batched prefill (llama_forward_batch) ----
+    std::vector<float> X((size_t)T * E), XB((size_t)T * E), Q((size_t)T * H * HD), K((size_t)T * kve),
+        Vv((size_t)T * kve), AO((size_t)T * E), GATE((size_t)T * FD), UP((size_t)T * FD),
+        FFN((size_t)T * E);
+    std::vector<block_q8_0> XQE((size_t)T * (E / 32)), XQF((size_t)T * (FD / 32));
+    std::vector<float> attn_scratch((size_t)(nw + 1) * NC);
+    for (int t = 0; t < T; t++) embed(X.data() + (size_t)t * E, prompt[t]);
+    for (int l = 0; l < L; l++) {
+        const orc_layer& lw = m->layers[l];
+        float* kc = kv_k.data() + (size_t)l * NC * kve;
+        float* vc = kv_v.data() + (size_t)l * NC * kve;
+        for (int t = 0; t < T; t++) {
+            orc_rmsnorm(XB.data() + (size_t)t * E, X.data() + (size_t)t * E, lw.attn_norm, E, m->rms_eps);
+            cx::quantize_q8_avx2(XQE.data() + (size_t)t * (E / 32), XB.data() + (size_t)t * E, E);
+        }
+        gemm_wt_q8_ref(Q.data(), wq[l], XQE.data(), H * HD, T, E, pool.get(), vnni);
+        gemm_wt_q8_ref(K.data(), wk[l], XQE.data(), kve, T, E, pool.get(), vnni);
+        gemm_wt_q8_ref(Vv.data(), wv[l], XQE.data(), kve, T, E, pool.get(), vnni);
+        add_rows(Q.data(), lw.bq, T, H * HD);
+        add_rows(K.data(), lw.bk, T, kve);
+        add_rows(Vv.data(), lw.bv, T, kve);
+        for (int t = 0; t < T; t++) {
+            orc_rope(Q.data() + (size_t)t * H * HD, Q.data() + (size_t)t * H * HD, t, H, HD, rc.data(),
+                     rs.data());
+            orc_rope(kc + (size_t)t * kve, K.data() + (size_t)t * kve, t, KVH, HD, rc.data(), rs.data());
+            std::memcpy(vc + (size_t)t * kve, Vv.data() + (size_t)t * kve, sizeof(float) * kve);
+        }
+        // causal attention: row t over positions 0..t (rows split over threads;
+        // each row's arithmetic is the sequential one of :1410-1426)
+        auto att = [&](int s, int e) {
+            static thread_local std::vector<float> scratch;
+            if ((int)scratch.size() < NC) scratch.resize(NC);
+            for (int t = s; t < e; t++)
+                orc_attention(AO.data() + (size_t)t * E, Q.data() + (size_t)t * H * HD, kc, vc, t + 1,
+                              H, KVH, HD, scratch.data());
+        };
+        if (pool) pool->parallel_for(T, att); else att(0, T);
+        for (int t = 0; t < T; t++)
+            cx::quantize_q8_avx2(XQE.data() + (size_t)t * (E / 32), AO.data() + (size_t)t * E, E);
+        gemm_wt_q8_ref(XB.data(), wo[l], XQE.data(), E, T, E, pool.get(), vnni);
+        for (size_t i = 0; i < (size_t)T * E; i++) X[i] += XB[i];
+        for (int t = 0; t < T; t++) {
+            orc_rmsnorm(XB.data() + (size_t)t * E, X.data() + (size_t)t * E, lw.ffn_norm, E, m->rms_eps);
+            cx::quantize_q8_avx2(XQE.data() + (size_t)t * (E / 32), XB.data() + (size_t)t * E, E);
+        }
+        gemm_wt_q8_ref(GATE.data(), wg[l], XQE.data(), FD, T, E, pool.get(), vnni);
+        gemm_wt_q8_ref(UP.data(), wu[l], XQE.data(), FD, T, E, pool.get(), vnni);
+        for (int t = 0; t < T; t++) {
+            orc_swiglu(GATE.data() + (size_t)t * FD, UP.data() + (size_t)t * FD, FD);
+            cx::quantize_q8_avx2(XQF.data() + (size_t)t * (FD / 32), GATE.data() + (size_t)t * FD, FD);
+        }
+        gemm_wt_q8_ref(FFN.data(), wd[l], XQF.data(), E, T, FD, pool.get(), vnni);
+        for (size_t i = 0; i < (size_t)T * E; i++) X[i] += FFN[i];
+    }
+    std::vector<float> x(X.begin() + (size_t)(T - 1) * E, X.begin() + (size_t)T * E);
+    std::vector<block_q8_0> xq8((size_t)std::max(E, FD) / 32);
+    orc_rmsnorm(x.data(), x.data(), m->output_norm, E, m->rms_eps);
+    cx::quantize_q8_avx2(xq8.data(), x.data(), E);
+    gemv_wt_q8(logits.data(), head, xq8.data(), V, E, pool.get(), vnni);
+    X.clear(); XB.clear(); Q.clear(); K.clear(); Vv.clear(); AO.clear(); GATE.clear(); UP.clear();
+    FFN.clear();
+
+    // ---- decode loop (llama_forward_token per generated token) ----
+    std::vector<float> xb(E), q(H * HD), k(kve), v(kve), attn(NC), ao(E), gate(FD), up(FD), ffn(E);
+    int n = 0, n_past = T;
+    for (int step = 0; step < n_gen; step++) {
+        if (n_past >= NC) break;
+        const int tok = orc_argmax(logits.data(), V);
+        out_tokens[n] = tok;
+        out_margins[n] = orc_top2_margin(logits.data(), V);
+        if (top_k > 0 && top_ids && top_vals) {
+            // the top_k logits of this step, largest first (ties: lower id first)
+            std::vector<int32_t> idx(V);
+            for (int i = 0; i < V; i++) idx[i] = i;
+            const int kk = std::min(top_k, V);
+            std::partial_sort(idx.begin(), idx.begin() + kk, idx.end(), [&](int32_t a, int32_t b) {
+                return logits[a] > logits[b] || (logits[a] == logits[b] && a < b);
+            });
+            for (int i = 0; i < kk; i++) {
+                top_ids[(size_t)n * top_k + i] = idx[i];
+                top_vals[(size_t)n * top_k + i] = logits[idx[i]];
+            }
+        }
+        n++;
+        const int pos = n_past;
+        embed(x.data(), tok);
+        block_q8_0* xq = xq8.data();
+        for (int l = 0; l < L; l++) {
+            const orc_layer& lw = m->layers[l];
+            float* kc = kv_k.data() + (size_t)l * NC * kve;
+            float* vc = kv_v.data() + (size_t)l * NC * kve;
+            orc_rmsnorm(xb.data(), x.data(), lw.attn_norm, E, m->rms_eps);
+            cx::quantize_q8_avx2(xq, xb.data(), E);
+            gemv_wt_q8(q.data(), wq[l], xq, H * HD, E, pool.get(), vnni);
+            gemv_wt_q8(k.data(), wk[l], xq, kve, E, pool.get(), vnni);
+            gemv_wt_q8(v.data(), wv[l], xq, kve, E, pool.get(), vnni);
+            for (int i = 0; lw.bq && i < H * HD; i++) q[i] += lw.bq[i];
+            for (int i = 0; lw.bk && i < kve; i++) k[i] += lw.bk[i];
+            for (int i = 0; lw.bv && i < kve; i++) v[i] += lw.bv[i];
+            orc_rope(q.data(), q.data(), pos, H, HD, rc.data(), rs.data());
+            orc_rope(kc + (size_t)pos * kve, k.data(), pos, KVH, HD, rc.data(), rs.data());
+            std::memcpy(vc + (size_t)pos * kve, v.data(), sizeof(float) * kve);
+            orc_attention(ao.data(), q.data(), kc, vc, pos + 1, H, KVH, HD, attn.data());
+            cx::quantize_q8_avx2(xq, ao.data(), E);
+            gemv_wt_q8(xb.data(), wo[l], xq, E, E, pool.get(), vnni);
+            for (int i = 0; i < E; i++) x[i] += xb[i];
+            orc_rmsnorm(xb.data(), x.data(), lw.ffn_norm, E, m->rms_eps);
+            cx::quantize_q8_avx2(xq, xb.data(), E);
+            gemv_wt_q8(gate.data(), wg[l], xq, FD, E, pool.get(), vnni);
+            gemv_wt_q8(up.data(), wu[l], xq, FD, E, pool.get(), vnni);
+            orc_swiglu(gate.data(), up.data(), FD);
+            cx::quantize_q8_avx2(xq, gate.data(), FD);
+            gemv_wt_q8(ffn.data(), wd[l], xq, E, FD, pool.get(), vnni);
+            for (int i = 0; i < E; i++) x[i] += ffn[i];
+        }
+        orc_rmsnorm(x.data(), x.data(), m->output_norm, E, m->rms_eps);
+        cx::quantize_q8_avx2(xq, x.data(), E);
+        gemv_wt_q8(logits.data(), head, xq, V, E, pool.get(), vnni);
+        n_past++;
+    }
+    pool.reset();
+    sched_setaffinity(0, sizeof(orig_aff), &orig_aff);
+    return n;
 }

@@ -21,13 +21,24 @@ and the head), a 512-token uniform-random prompt, greedy decode, context 2048
     through the later layers.  The test prints that growth (the batched
     prefill's row 511 against the decode path's row over the same cache, per
     layer) and requires layer 0, where nothing has grown yet, to agree to fp32
-    rounding.
+    rounding;
+  * against the reference itself: tests/golden/c5_greedy.json holds the 32
+    greedy ids of the same model on the reference's compiled x86 kernels
+    (tests/golden/make_c5_greedy.py; a 512-token prompt starting with BOS) and
+    the reference's top-2 margin at each; the device's ids must equal them up
+    to the first step whose reference margin is within the device's measured
+    prefill-path noise (where fp32 summation order can decide the token).
 """
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 
 from gpu_helpers import device_norm_q8, layer_stage_errors, within
 from oracle import oracle as O
+
+FIXTURE = Path(__file__).resolve().parent / "golden" / "c5_greedy.json"
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
@@ -136,3 +147,62 @@ def test_config5_full_size(ctx):
         assert growth[0] < 1e-5, "layer 0 K rows of the two paths differ beyond fp32 rounding"
     finally:
         g.close()
+
+
+@pytest.mark.timeout(900)
+def test_config5_against_the_reference(ctx):
+    """The device against the reference's own generation on the same config-5
+    model and prompt, teacher-forced: the device prefills the prompt (batched)
+    and then decodes the reference's ids one by one, so that
+    both sides hold the same history at every step.  Per step, the device's
+    logits at the reference's 8 largest are compared with the reference's
+    values.  The bound for that difference is twice the largest logit
+    difference between the device's own two prefill paths on this prompt
+    (batched, and token by token through the decode kernels): both are fp32
+    summation-order effects (a Q8_0 requantisation that lands across a
+    rounding boundary moves a layer's update, and such moves grow through 32
+    random layers).  The device's argmax must be the reference's id at every
+    step where the reference's top-2 margin exceeds twice that step's
+    measured difference.  Free-running greedy ids are reported, not asserted:
+    the reference's third step is a near-tie (margin 1e-3), which any other
+    summation order may decide the other way."""
+    from llm_core_amd.model import LLAMA2_7B, Hparams, LlamaHip, SynthLlama
+
+    fx = json.loads(FIXTURE.read_text())
+    hp = Hparams(n_ctx=fx["model"]["n_ctx"], **LLAMA2_7B)
+    prompt = np.array(fx["prompt"], np.int32)
+    rule = np.concatenate([[1], np.random.default_rng(5).integers(0, hp.n_vocab, prompt.size - 1)])
+    assert np.array_equal(prompt, rule), "fixture prompt does not follow its rule"
+    ref_ids, ref_m = np.array(fx["ids"]), np.array(fx["margins"])
+    top_ids, top_v = np.array(fx["top_ids"]), np.array(fx["top_logits"], np.float64)
+    assert np.array_equal(top_ids[:, 0], ref_ids)
+    n = ref_ids.size
+    model = SynthLlama(hp, seed=5)
+    with LlamaHip(ctx, model) as g:
+        free = g.generate(prompt, n, use_graph=True)
+        g.forward_batch(prompt, 0)
+        lb = g.logits().astype(np.float64)
+        err, agree = np.zeros(n), np.zeros(n, bool)
+        dev_m = np.zeros(n)
+        for t in range(n):
+            lg = g.logits().astype(np.float64) if t else lb
+            err[t] = np.max(np.abs(lg[top_ids[t]] - top_v[t]))
+            agree[t] = int(np.argmax(lg)) == ref_ids[t]
+            s2 = np.sort(lg)[-2:]
+            dev_m[t] = s2[1] - s2[0]
+            g.forward_token(int(ref_ids[t]), prompt.size + t)
+        for t, tok in enumerate(prompt):
+            g.forward_token(int(tok), t)
+        noise = float(np.max(np.abs(g.logits().astype(np.float64) - lb)))
+    lead = int(np.argmax(free != ref_ids)) if np.any(free != ref_ids) else n
+    scale = float(np.mean(np.abs(top_v[:, 0])))
+    print(f"\n  free-running: {lead} of {n} leading ids equal the reference's (its step-{lead} margin "
+          f"{ref_m[min(lead, n - 1)]:.3e})\n  teacher-forced: device argmax = reference id at {int(agree.sum())} "
+          f"of {n} steps; top-8 logit |diff| max {err.max():.3e}, median {np.median(err):.3e} "
+          f"(top logit ~{scale:.2f}); device two-path prefill noise {noise:.3e}", flush=True)
+    for t in np.nonzero(~agree)[0]:
+        print(f"    step {t}: reference margin {ref_m[t]:.3e}, device margin {dev_m[t]:.3e}, "
+              f"step |diff| {err[t]:.3e}", flush=True)
+    assert err.max() <= 2 * noise, f"top-8 logits differ by {err.max():.3e} > 2 x path noise {noise:.3e}"
+    bad = [int(t) for t in np.nonzero(~agree & (ref_m > 2 * err))[0]]
+    assert not bad, f"argmax differs at steps {bad} where the reference's margin exceeds twice the step's difference"

@@ -140,3 +140,32 @@ def test_dequant_via_onehot_reference_gemv():
             e[j] = 1
             fn(p(y), p(W), p(e), 0, rows, cols, O.row_bytes(qt, cols))
             assert np.array_equal(y, D[:, j])
+
+
+@pytest.mark.parametrize("seed,kvh", [(3, 4), (7, 8)])
+def test_reference_kernel_generation_equals_the_oracle_loop(seed, kvh):
+    """ref_generate_greedy (the reference's compiled GEMM / GEMVs on its
+    ThreadPool, the generator of tests/golden/c5_greedy.json) against the
+    oracle's orc_generate_greedy on the same model: the same ids and the same
+    margins, bit for bit (batched prefill, then decode steps; biases, GQA)."""
+    from llm_core_amd.model import Hparams, SynthLlama
+
+    hp = Hparams(n_layer=2, n_embd=512, n_heads=8, n_kv_heads=kvh, ffn_dim=1024, n_vocab=1000,
+                 n_ctx=48, rms_eps=1e-5, rope_theta=10000.0)
+    m = SynthLlama(hp, seed=seed, norm_std=0.1, with_bias=True)
+    om = O.OracleModel(hp, m.tensors)
+    try:
+        prompt = np.concatenate([[1], np.random.default_rng(seed).integers(0, 1000, 20)]).astype(np.int32)
+        a, ma = om.generate(prompt, 40, batched_prefill=True)
+        b, mb = O.ref_generate_greedy(om, prompt, 40, 4)
+        assert len(a) == len(b) == hp.n_ctx - prompt.size  # both stop at the context end
+        assert np.array_equal(a, b)
+        assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
+        c, mc, tid, tv = O.ref_generate_greedy(om, prompt, 40, 4, top_k=5)
+        assert np.array_equal(c, b) and np.array_equal(mc, mb)
+        assert np.array_equal(tid[:, 0], b), "top-1 id is the greedy id"
+        assert np.array_equal((tv[:, 0] - tv[:, 1]).view(np.uint32), mb.view(np.uint32)), "top-2 gap is the margin"
+        assert np.all(np.diff(tv, axis=1) <= 0), "top-k logits sorted"
+        assert all(np.unique(r).size == 5 for r in tid), "top-k ids distinct"
+    finally:
+        om.close()
