@@ -10,12 +10,15 @@ cpu_baseline leg.  Never used by llm_core_amd.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-ORC_PATH = HERE / "liboracle.so"
+# AXF_ORACLE_LIB: another build of axf_oracle.c (the mutation test's planted
+# slips, tests/test_oracle_mutations.py); by default the one built here
+ORC_PATH = Path(os.environ["AXF_ORACLE_LIB"]) if os.environ.get("AXF_ORACLE_LIB") else HERE / "liboracle.so"
 REF_PATH = HERE / "_ref" / "libaxf_ref.so"
 
 Q4K, Q6K, F32 = 12, 14, 0
