@@ -592,11 +592,13 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
     // activation built from registers: the fused normalisation, and fp32 at 512+ threads
     constexpr bool REG = ACT == (int)QAct::Norm || (NT >= kWide && ACT == (int)QAct::F32);
     // the one-chunk Q6_K rows with an fp32 activation at 512+ threads (the
-    // decode down-projection): the activation is staged before the weight
-    // loads are issued, so its registers are free before the weights' go live:
-    // 111 -> 94 VGPRs, two 512-thread workgroups resident per CU instead of
-    // one; 7B down 14.05 -> 13.85 us, decode step 1.783 -> 1.779 ms (1024-thread
-    // workgroups at 94 VGPRs: 1.787 ms)
+    // decode down-projection): only the first unit's weights are issued before
+    // the activation is staged, the rest after, so the activation's registers
+    // are free before most of the weights' go live: 111 -> 94 VGPRs, two
+    // 512-thread workgroups resident per CU instead of one.  7B down 14.05 ->
+    // 12.95 us, decode step 1.783 -> 1.771 ms, config-3 step 41.6 -> 41.2 us
+    // (staging before any weight load: 13.85 us, 1.779 ms; that with
+    // 1024-thread workgroups: 1.787 ms)
     constexpr bool SFIRST = QT == kQ6K && ACT == (int)QAct::F32 && NT >= kWide && !PAIR;
     // float4s of x per thread: K / 4 <= 16 * LPR * CPL * UC
     constexpr int KPT = (16 * LPR * CPL * UC + NT - 1) / NT;
@@ -752,48 +754,57 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
             }
         }
     } else {
-        if constexpr (SFIRST) {
-            stage();
-            __builtin_amdgcn_sched_barrier(0);
-        }
         // unit (n, i): ql (8 dwords per chunk), the half's qh (8 dwords), scales, d
         uint32_t ql[NR][CPL][8 * UC], qh[NR][CPL][8], sc[NR][CPL][4], db[NR][CPL];
-#pragma unroll
-        for (int n = 0; n < NR; n++) {
+        auto load6 = [&](int n, int i) {
             const long row = min(row0 + (long)n * RPP, (long)rows - 1);
-#pragma unroll
-            for (int i = 0; i < CPL; i++) {
-                const int u = min(rl + i * LPR, nunits - 1);
-                const int c0 = u * UC;  // first chunk of the unit
-                const int h = (c0 >> 1) & 1, t = c0 & 1;
-                const uint8_t* blk = W + row * rb + (long)(c0 >> 2) * Q6K_BYTES;
-                if constexpr (PAIR) {
-                    // 64 ql bytes, 32 qh bytes, 8 scale bytes of half h, and d, as
-                    // aligned dwords + v_alignbyte: against 16-byte vectors at the
-                    // 2-byte aligned addresses, 9.4 -> 9.2 us for the 7B q|k|v
-                    // launch and 26.7 -> 24.9 us for the 32000 x 4096 head (the
-                    // K = 11008 one-chunk rows measured the other way: 14.0 -> 14.7 us)
-                    load_u2<16, false>(blk + 64 * h, ql[n][i]);
-                    load_u2<8, false>(blk + 128 + 32 * h, qh[n][i]);
-                    {
-                        // 8 bytes at blk + 192 + 8h; the third dword is read only when
-                        // the field is 2 bytes past a dword (it then ends at blk + 210)
-                        const uint8_t* p = blk + 192 + 8 * h;
-                        const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);
-                        const uint8_t* base = p - sh;
-                        const uint32_t w0 = ld4(base), w1 = ld4(base + 4);
-                        const uint32_t w2 = ld4(base + (sh ? 8 : 4));
-                        sc[n][i][0] = alignbyte(w1, w0, sh);
-                        sc[n][i][1] = alignbyte(w2, w1, sh);
-                    }
-                    sc[n][i][2] = sc[n][i][3] = 0u;
-                    db[n][i] = ld2(blk + 208);
-                } else {
-                    load_u2<8, LPR == 64>(blk + 64 * h + 32 * t, ql[n][i]);
-                    load_u2<8, LPR == 64>(blk + 128 + 32 * h, qh[n][i]);
-                    load_q6_tail<LPR == 64>(blk, sc[n][i], db[n][i]);
+            const int u = min(rl + i * LPR, nunits - 1);
+            const int c0 = u * UC;  // first chunk of the unit
+            const int h = (c0 >> 1) & 1, t = c0 & 1;
+            const uint8_t* blk = W + row * rb + (long)(c0 >> 2) * Q6K_BYTES;
+            if constexpr (PAIR) {
+                // 64 ql bytes, 32 qh bytes, 8 scale bytes of half h, and d, as
+                // aligned dwords + v_alignbyte: against 16-byte vectors at the
+                // 2-byte aligned addresses, 9.4 -> 9.2 us for the 7B q|k|v
+                // launch and 26.7 -> 24.9 us for the 32000 x 4096 head (the
+                // K = 11008 one-chunk rows measured the other way: 14.0 -> 14.7 us)
+                load_u2<16, false>(blk + 64 * h, ql[n][i]);
+                load_u2<8, false>(blk + 128 + 32 * h, qh[n][i]);
+                {
+                    // 8 bytes at blk + 192 + 8h; the third dword is read only when
+                    // the field is 2 bytes past a dword (it then ends at blk + 210)
+                    const uint8_t* p = blk + 192 + 8 * h;
+                    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);
+                    const uint8_t* base = p - sh;
+                    const uint32_t w0 = ld4(base), w1 = ld4(base + 4);
+                    const uint32_t w2 = ld4(base + (sh ? 8 : 4));
+                    sc[n][i][0] = alignbyte(w1, w0, sh);
+                    sc[n][i][1] = alignbyte(w2, w1, sh);
                 }
+                sc[n][i][2] = sc[n][i][3] = 0u;
+                db[n][i] = ld2(blk + 208);
+            } else {
+                load_u2<8, LPR == 64>(blk + 64 * h + 32 * t, ql[n][i]);
+                load_u2<8, LPR == 64>(blk + 128 + 32 * h, qh[n][i]);
+                load_q6_tail<LPR == 64>(blk, sc[n][i], db[n][i]);
             }
+        };
+        if constexpr (SFIRST) {
+            // the first unit's weights in flight during the staging
+#pragma unroll
+            for (int n = 0; n < NR; n++) load6(n, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            stage();
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int n = 0; n < NR; n++)
+#pragma unroll
+                for (int i = 1; i < CPL; i++) load6(n, i);
+        } else {
+#pragma unroll
+            for (int n = 0; n < NR; n++)
+#pragma unroll
+                for (int i = 0; i < CPL; i++) load6(n, i);
         }
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (!SFIRST) stage();
