@@ -161,6 +161,15 @@ int axf_hip_gemv_q5_0_f32(axf_ctx* ctx, float* y, const void* W, const float* x,
  * W rows of cols halfs, W and x 16-byte aligned, cols % 8 == 0. */
 int axf_hip_gemv_f16_f32(axf_ctx* ctx, float* y, const void* W, const float* x, const float* b,
                          int rows, int cols);
+/* T-token product with fp32 token rows for Q8_0 / Q5_0 / F16 weights (qtype
+ * AXF_TYPE_Q8_0, AXF_TYPE_Q5_0 or AXF_TYPE_F16): Y[t*rows + o] (+= when
+ * accumulate) sum_k W[o][k] X[t*cols + k].  Replaces gemm_wt_q8's fallback in
+ * the batched prefill (llama_model.cpp:876-879), which runs gemv_wt (:670-731)
+ * on each token's fp32 row; each weight block is dequantised once per 16 or 32
+ * tokens here.  cols % 32 == 0; X and Y 4-byte aligned; F16: W 16-byte aligned
+ * and row_bytes a multiple of 16 (2*cols for packed rows). */
+int axf_hip_gemm_misc_f32(axf_ctx* ctx, int qtype, float* Y, const void* W, const float* X,
+                          int rows, int T, int cols, size_t row_bytes, int accumulate);
 
 /* Greedy pick: *idx_dev = first index of the maximum of x[0..n), the
  * std::max_element of sample() (llama_model.cpp:1470-1471).  idx_dev is a

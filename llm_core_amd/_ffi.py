@@ -137,6 +137,7 @@ SIGNATURES: dict[str, list] = {
     "axf_hip_gemv_q8_0w_f32": [vp, vp, vp, vp, i32, i32, sz],
     "axf_hip_gemv_q5_0_f32": [vp, vp, vp, vp, i32, i32, sz],
     "axf_hip_gemv_f16_f32": [vp, vp, vp, vp, vp, i32, i32],
+    "axf_hip_gemm_misc_f32": [vp, i32, vp, vp, vp, i32, i32, i32, sz, i32],
     "axf_hip_sample": [vp, vp, i32, C.POINTER(Sampling), vp, i32, f32, C.POINTER(C.c_int32)],
     "axf_mt19937": [C.c_uint32, vp, i32],
     "axf_sampling_uniforms": [C.c_uint32, vp, i32],

@@ -555,6 +555,25 @@ int axf_hip_gemv_f16_f32(axf_ctx* ctx, float* y, const void* W, const float* x, 
     return AXF_OK;
 }
 
+int axf_hip_gemm_misc_f32(axf_ctx* ctx, int qtype, float* Y, const void* W, const float* X,
+                          int rows, int T, int cols, size_t row_bytes, int accumulate) {
+    AXF_CHECK_CTX(ctx);
+    const char* fn = "axf_hip_gemm_misc_f32";
+    if (qtype != AXF_TYPE_Q8_0 && qtype != AXF_TYPE_Q5_0 && qtype != AXF_TYPE_F16)
+        return fail(AXF_ERR_UNSUPPORTED, std::string(fn) + ": qtype must be Q8_0, Q5_0 or F16");
+    if (T < 0 || T > 65535 * 16) return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": T out of range");
+    if (cols % 32) return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": cols must be a multiple of 32");
+    int rc = check_misc(fn, qtype, W, X, Y, rows, cols, qtype == AXF_TYPE_F16 ? (size_t)cols * 2 : row_bytes,
+                        false);
+    if (rc) return rc;
+    if (qtype == AXF_TYPE_F16 && (row_bytes < (size_t)cols * 2 || row_bytes % 16))
+        return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": F16 row_bytes must be >= 2*cols and a multiple of 16");
+    if (!rows || !cols || !T) return AXF_OK;
+    AXF_HIP(launch_gemm_misc_f32(qtype, Y, W, X, rows, cols, (long)row_bytes, T, accumulate ? 1 : 0,
+                                 ctx->stream));
+    return AXF_OK;
+}
+
 int axf_hip_timer_start(axf_ctx* ctx) {
     AXF_CHECK_CTX(ctx);
     AXF_HIP(hipEventRecord(ctx->ev0, ctx->stream));

@@ -702,6 +702,9 @@ hipError_t gemm_rows(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, 
 hipError_t gemm_any(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, const float* xf,
                     int rows, int T, int cols, hipStream_t st) {
     if (kquant(w.qtype)) return gemm_rows(m, w, Y, xq8, rows, T, cols, st);
+    // from 8 tokens: each weight block dequantised once per 16 or 32 tokens
+    if (T >= 8)
+        return launch_gemm_misc_f32(w.qtype, Y, w.d, xf, rows, cols, (long)w.row_bytes, T, 0, st);
     if (w.qtype == AXF_TYPE_Q8_0)
         return launch_gemv_q8w_f32(Y, w.d, xf, rows, cols / 32, (long)w.row_bytes, st, 0, T);
     if (w.qtype == AXF_TYPE_Q5_0)

@@ -207,7 +207,142 @@ __global__ __launch_bounds__(256) void k_embed_misc(float* __restrict__ out, int
 
 int misc_lpr(int units) { return units >= 64 ? 64 : (units >= 32 ? 32 : 16); }
 
+// ---------------------------------------------------------------------------
+// Batched prefill with fp32 rows (gemm_wt_q8's fallback, llama_model.cpp:876-879,
+// runs gemv_wt per token: Q8_0 / Q5_0 / F16 weights on each token's fp32 row).
+// The token-grid GEMVs above re-read every weight row once per token; here a
+// thread owns one row, dequantises each 32-element block of it once into
+// registers and applies it to TT tokens, whose rows every lane of the wave
+// reads at the same addresses (scalar-cache loads).  Per token the products are
+// summed in k order within each of the workgroup's KS waves (each a
+// contiguous range of K), and the KS partials added in wave order through LDS.
+// Workgroup = 64 rows x KS waves, grid y = token groups of TT.
+// ---------------------------------------------------------------------------
+constexpr int kGemmMiscRows = 64;
+
+template <int QT>
+__device__ __forceinline__ void misc_block_f32(const uint8_t* __restrict__ wr, int b,
+                                               float (&w)[32]) {
+    if constexpr (QT == 1) {  // F16: 32 halves, 64 bytes (16-byte aligned rows)
+        const uint4* p = reinterpret_cast<const uint4*>(wr + 64 * (long)b);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint4 v = p[k];
+            const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                w[8 * k + 2 * j] = h2f(u[j] & 0xffffu);
+                w[8 * k + 2 * j + 1] = h2f(u[j] >> 16);
+            }
+        }
+    } else if constexpr (QT == 8) {  // Q8_0: d * q (q8_0_weight_dot_row's weights)
+        const uint8_t* wb = wr + (long)b * 34;
+        const float d = h2f(ld2(wb));
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t q = ld2x2(wb + 2 + 4 * k);
+#pragma unroll
+            for (int j = 0; j < 4; j++) w[4 * k + j] = d * (float)(int8_t)((q >> (8 * j)) & 0xffu);
+        }
+    } else {  // Q5_0: d * (q5 - 16) (q5_0_dot_row's weights)
+        const uint8_t* wb = wr + (long)b * 22;
+        const float d = h2f(ld2(wb));
+        const uint32_t qh = ld2x2(wb + 2);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t qs = ld2x2(wb + 6 + 4 * k);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = 4 * k + j;  // low nibble: element i, high: element i + 16
+                w[i] = d * ((float)(((qs >> (8 * j)) & 0x0fu) | (((qh >> i) & 1u) << 4)) - 16.f);
+                w[i + 16] = d * ((float)(((qs >> (8 * j + 4)) & 0x0fu) | (((qh >> (i + 16)) & 1u) << 4)) - 16.f);
+            }
+        }
+    }
+}
+
+template <int QT, int TT, int KS>
+__global__ __launch_bounds__(KS * 64) void k_gemm_misc_f32(
+    float* __restrict__ Y, const uint8_t* __restrict__ W, const float* __restrict__ X, int rows,
+    int cols, long row_bytes, int T, int accumulate) {
+    __shared__ float red[KS][TT][kGemmMiscRows];
+    // the wave index as a wave-uniform value, so that the K range and with it
+    // every token-row address are uniform: those loads go through the scalar
+    // cache (a vector load of one address per lane moved 1 KB per instruction)
+    const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const long row = (long)blockIdx.x * kGemmMiscRows + lane;
+    const int t0 = (int)blockIdx.y * TT;
+    const uint8_t* wr = W + (row < rows ? row : rows - 1) * row_bytes;  // rows past the end: not stored
+    const int nb = cols / 32, nbq = (nb + KS - 1) / KS;
+    const int b0 = ks * nbq, b1 = min(nb, b0 + nbq);  // this wave's K range, in blocks
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[t] = 0.f;
+    for (int b = b0; b < b1; b++) {
+        float w[32];
+        misc_block_f32<QT>(wr, b, w);
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            // token rows past T repeat row T-1 (their sums are not stored)
+            const float* xt = X + (size_t)min(t0 + t, T - 1) * cols + 32 * b;
+#pragma unroll
+            for (int i = 0; i < 32; i++) acc[t] = fmaf(w[i], xt[i], acc[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) red[ks][t][lane] = acc[t];
+    __syncthreads();
+    // the KS partial sums of each output, in K order
+    for (int o = threadIdx.x; o < TT * kGemmMiscRows; o += KS * 64) {
+        const int t = o / kGemmMiscRows, r = o % kGemmMiscRows;
+        float v = red[0][t][r];
+#pragma unroll
+        for (int q = 1; q < KS; q++) v += red[q][t][r];
+        const long orow = (long)blockIdx.x * kGemmMiscRows + r;
+        if (orow < rows && t0 + t < T) {
+            float* y = Y + (size_t)(t0 + t) * rows + orow;
+            *y = accumulate ? *y + v : v;
+        }
+    }
+}
+
+template <int TT, int KS>
+hipError_t launch_gemm_misc_tt(int qtype, float* Y, const uint8_t* W, const float* X, int rows,
+                               int cols, long row_bytes, int T, int accumulate, hipStream_t st) {
+    const dim3 grid((unsigned)((rows + kGemmMiscRows - 1) / kGemmMiscRows), (unsigned)((T + TT - 1) / TT));
+    const dim3 block(KS * 64);
+    if (qtype == 1)
+        hipLaunchKernelGGL((k_gemm_misc_f32<1, TT, KS>), grid, block, 0, st, Y, W, X, rows, cols, row_bytes, T, accumulate);
+    else if (qtype == 8)
+        hipLaunchKernelGGL((k_gemm_misc_f32<8, TT, KS>), grid, block, 0, st, Y, W, X, rows, cols, row_bytes, T, accumulate);
+    else
+        hipLaunchKernelGGL((k_gemm_misc_f32<6, TT, KS>), grid, block, 0, st, Y, W, X, rows, cols, row_bytes, T, accumulate);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+// Y (+)= W x^T for T fp32 token rows of cols (Y token-major, rows floats per
+// token).  F16 rows must be 16-byte aligned (cols % 32 == 0 makes them so when
+// W is); 2-byte-aligned Q8_0 / Q5_0 blocks are read as 16-bit words.
+hipError_t launch_gemm_misc_f32(int qtype, float* Y, const void* W, const float* X, int rows,
+                                int cols, long row_bytes, int T, int accumulate, hipStream_t st) {
+    if (rows <= 0 || T <= 0 || cols <= 0 || cols % 32 || T > 65535 * 16) return hipErrorInvalidValue;
+    if (qtype != 1 && qtype != 8 && qtype != 6) return hipErrorInvalidValue;
+    if (qtype == 1 && (reinterpret_cast<uintptr_t>(W) & 15)) return hipErrorInvalidValue;
+    const auto* w8 = static_cast<const uint8_t*>(W);
+    // waves = row groups x token groups x K ranges: 32 tokens per group and 4
+    // K ranges where that gives 4096 waves (4 per SIMD) or K is under 16
+    // blocks, else 16 tokens with 4, then 8 K ranges (a wave past the last
+    // block adds zeros)
+    const long rg = (rows + kGemmMiscRows - 1) / kGemmMiscRows;
+    const int nb = cols / 32;
+    if (rg * ((T + 31) / 32) * 4 >= 4096 || nb < 16)
+        return launch_gemm_misc_tt<32, 4>(qtype, Y, w8, X, rows, cols, row_bytes, T, accumulate, st);
+    if (rg * ((T + 15) / 16) * 4 >= 4096)
+        return launch_gemm_misc_tt<16, 4>(qtype, Y, w8, X, rows, cols, row_bytes, T, accumulate, st);
+    return launch_gemm_misc_tt<16, 8>(qtype, Y, w8, X, rows, cols, row_bytes, T, accumulate, st);
+}
 
 #define AXF_MISC_LAUNCH(KERNEL, LPR_, ROWS, ...)                                           \
     do {                                                                                   \

@@ -72,6 +72,50 @@ def test_gemv_f32_activation(ctx, qtype, rows, cols):
     assert ok, err
 
 
+GEMM_SHAPES = [(4864, 896, 512), (896, 896, 37), (130, 4864, 16), (1000, 64, 3), (64, 32, 70)]
+
+
+@pytest.mark.parametrize("qtype", [AXF_TYPE_Q8_0, AXF_TYPE_Q5_0, AXF_TYPE_F16])
+@pytest.mark.parametrize("rows,cols,T", GEMM_SHAPES)
+def test_gemm_f32_rows(ctx, qtype, rows, cols, T):
+    """axf_hip_gemm_misc_f32 (the prefill's fp32-row GEMM) against the oracle's
+    per-token GEMV (gemv_wt on each row, as gemm_wt_q8's fallback runs it):
+    the Qwen2.5-0.5B ffn_gate / attn_q shapes, ragged rows and token groups,
+    fewer tokens than one group; then accumulate doubles the product."""
+    rng = np.random.default_rng(rows + 13 * cols + T)
+    if qtype == AXF_TYPE_F16:
+        W = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float16)
+    else:
+        W = blocks(qtype, rows, cols, rows * 5 + cols)
+    X = rng.standard_normal((T, cols)).astype(np.float32)
+    check_t = range(T) if T <= 40 else sorted({0, 1, 31, 32, T // 2, T - 1})
+    want = {t: O.gemv_misc(qtype, W, X[t], rows, cols) for t in check_t}
+    rb = O.misc_row_bytes(qtype, cols)
+    dW, dX = ctx.upload(W), ctx.upload(X)
+    dY = ctx.upload(np.full(T * rows, np.nan, np.float32))
+    call("axf_hip_gemm_misc_f32", ctx.handle, qtype, dY.ptr, dW.ptr, dX.ptr, rows, T, cols, rb, 0)
+    got = ctx.download(dY, np.float32, T * rows).reshape(T, rows)
+    assert not np.isnan(got).any(), "every output written"
+    for t in check_t:
+        ok, err = close(got[t], want[t])
+        assert ok, f"token {t}: {err}"
+    call("axf_hip_gemm_misc_f32", ctx.handle, qtype, dY.ptr, dW.ptr, dX.ptr, rows, T, cols, rb, 1)
+    got2 = ctx.download(dY, np.float32, T * rows).reshape(T, rows)
+    np.testing.assert_array_equal(got2, got + got)  # y + y: the accumulate adds the same sums
+
+
+def test_gemm_misc_rejects_bad_arguments(ctx):
+    W, X, Y = ctx.alloc(1 << 16), ctx.alloc(1 << 16), ctx.alloc(1 << 16)
+    with pytest.raises(AxfError, match="multiple of 32"):
+        call("axf_hip_gemm_misc_f32", ctx.handle, AXF_TYPE_Q5_0, Y.ptr, W.ptr, X.ptr, 4, 2, 48, 44, 0)
+    with pytest.raises(AxfError, match="qtype"):
+        call("axf_hip_gemm_misc_f32", ctx.handle, 12, Y.ptr, W.ptr, X.ptr, 4, 2, 256, 144, 0)
+    with pytest.raises(AxfError, match="16-byte aligned"):
+        call("axf_hip_gemm_misc_f32", ctx.handle, AXF_TYPE_F16, Y.ptr, W.ptr + 2, X.ptr, 4, 2, 64, 128, 0)
+    with pytest.raises(AxfError, match="row_bytes"):
+        call("axf_hip_gemm_misc_f32", ctx.handle, AXF_TYPE_Q8_0, Y.ptr, W.ptr, X.ptr, 4, 2, 64, 66, 0)
+
+
 @pytest.mark.parametrize("qtype", [AXF_TYPE_Q8_0, AXF_TYPE_Q5_0, AXF_TYPE_F16])
 def test_embed_rows_bitexact(ctx, qtype):
     rows, cols = 50, 896
