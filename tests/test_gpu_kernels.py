@@ -119,6 +119,11 @@ GEMV_SHAPES = [
     (Q6K, 77, 3072),
     (Q6K, 101, 11008),   # 9030-byte rows: odd rows start 2 bytes past a dword
     (Q6K, 17, 14336),
+    # half-block units of 16 lanes (5-8 blocks per row): 10 of 16 lanes live at
+    # 5 blocks, 2-byte-aligned Q6_K rows of 1050 and 1470 bytes, ragged row counts
+    (Q4K, 45, 1280),
+    (Q6K, 9, 1280),
+    (Q6K, 33, 1792),
 ]
 
 
