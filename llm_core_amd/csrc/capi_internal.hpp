@@ -112,12 +112,15 @@ bool gemm_stream_q4k_ok(int T, int nb, int rows);
 size_t gemm_stream_scratch_bytes(int T, int nb, int rows);
 hipError_t launch_gemm_stream_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
                                      int nb, long row_bytes, void* scratch, hipStream_t st);
+// accumulate (Y +=): the fp16 kernel only (T >= 65); the int8 kernels below it refuse it
 hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
-                                   int nb, long row_bytes, void* scratch, hipStream_t st);
+                                   int nb, long row_bytes, void* scratch, hipStream_t st,
+                                   int accumulate = 0);
 size_t gemm_mfma_q6k_scratch_bytes(int T, int nb);
 bool gemm_mfma_q6k_ok(const void* W, int rows, int nb, long row_bytes);
 hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
-                                   int nb, long row_bytes, void* scratch, hipStream_t st);
+                                   int nb, long row_bytes, void* scratch, hipStream_t st,
+                                   int accumulate = 0);
 // Other weight types (kernels/gemv_misc.hip): nb = 32-element blocks per row.
 // T tokens (T <= 65535): activation rows and y rows of token t follow each
 // other (x + t*cols, xq8 + t*nb blocks, y + t*rows); accumulate adds to y.

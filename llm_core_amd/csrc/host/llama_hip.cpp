@@ -696,6 +696,22 @@ hipError_t gemm_rows(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, 
                               GemmPath::Auto, m->pf_gemm, st);
 }
 
+// Y[T][rows] += W x^T for the residual projections: the matrix-core kernels the
+// automatic path picks for these sizes accumulate into Y themselves (the fp16
+// Q4_K kernel from 65 tokens, the Q6_K kernel from 8); otherwise the product
+// goes to tmp and a k_add follows.  Y + product is the same fp32 add either way.
+hipError_t gemm_rows_add(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, int rows,
+                         int T, int cols, float* tmp, hipStream_t st) {
+    const int nb = cols / QK_K;
+    if (w.qtype == AXF_TYPE_Q4_K && T > kGemmStreamMaxT)
+        return launch_gemm_mfma_q4k_q8(Y, w.d, xq8, rows, T, nb, (long)w.row_bytes, m->pf_gemm, st, 1);
+    if (w.qtype == AXF_TYPE_Q6_K && T >= kGemmMfmaMinT && gemm_mfma_q6k_ok(w.d, rows, nb, (long)w.row_bytes))
+        return launch_gemm_mfma_q6k_q8(Y, w.d, xq8, rows, T, nb, (long)w.row_bytes, m->pf_gemm, st, 1);
+    hipError_t e = gemm_rows(m, w, tmp, xq8, rows, T, cols, st);
+    if (e != hipSuccess) return e;
+    return launch_add(Y, Y, tmp, T * rows, st);
+}
+
 // Y[T][rows] by gemm_wt_q8's dispatch (llama_model.cpp:837-879): Q4_K and Q6_K
 // on the Q8_0 rows; every other type, Q8_0 included (the batched path has no
 // Q8_0 branch), on the fp32 rows XF through gemv_wt per token (:876-879).
@@ -795,8 +811,12 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
                             : launch_attention_prefill(a, HD, st));
     }
     // x += o (the attention's fp32 rows pf_ao and their Q8_0 pf_q8)
-    ST(gemm_any(m, L.wo, m->pf_tmp, m->pf_q8, m->pf_ao, E, T, qo, st));
-    ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
+    if (kquant(L.wo.qtype)) {
+        ST(gemm_rows_add(m, L.wo, m->pf_x, m->pf_q8, E, T, qo, m->pf_tmp, st));
+    } else {
+        ST(gemm_any(m, L.wo, m->pf_tmp, m->pf_q8, m->pf_ao, E, T, qo, st));
+        ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
+    }
     // SwiGLU(gate, up) of RMSNorm(x) * ffn_norm -> Q8_0 (and fp32 rows of h
     // where the down projection is of another type)
     const bool f_gu = !kquant(L.wgate.qtype) || !kquant(L.wup.qtype);
@@ -814,8 +834,12 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
                          m->pf_gu + (size_t)T * FD, T * FD, st));
     }
     // x += down
-    ST(gemm_any(m, L.wdown, m->pf_tmp, m->pf_q8, m->pf_h, E, T, FD, st));
-    ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
+    if (kquant(L.wdown.qtype)) {
+        ST(gemm_rows_add(m, L.wdown, m->pf_x, m->pf_q8, E, T, FD, m->pf_tmp, st));
+    } else {
+        ST(gemm_any(m, L.wdown, m->pf_tmp, m->pf_q8, m->pf_h, E, T, FD, st));
+        ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
+    }
 #undef ST
     return hipSuccess;
 }

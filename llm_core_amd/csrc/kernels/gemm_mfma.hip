@@ -792,7 +792,7 @@ template <int RT, int TTW, int S>
 __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
     float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ xh,
     const float* __restrict__ dxt, const float* __restrict__ gxt, int rows, int nb,
-    long row_bytes, int T, int Tp, int nrt) {
+    long row_bytes, int T, int Tp, int nrt, int accumulate) {
     using G = Stage16<RT, TTW, S>;
     constexpr int NW = G::NW, RW = G::RW, TW = G::TW;
     __shared__ __attribute__((aligned(16))) uint8_t smem[S * G::ALLOC];
@@ -849,7 +849,10 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
 #pragma unroll
             for (int ii = 0; ii < 4; ii++) {
                 const int o = row_base + kTile * wave + 4 * g + ii;
-                if (o < rows) Y[(size_t)tok * rows + o] = v[ii];
+                if (o < rows) {
+                    float* y = Y + (size_t)tok * rows + o;
+                    *y = accumulate ? *y + v[ii] : v[ii];
+                }
             }
         }
     }
@@ -857,7 +860,7 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
 
 template <int RT, int TTW, int S>
 void launch16_cfg(float* Y, const uint8_t* W, const uint8_t* XQ8, uint8_t* scratch, int rows,
-                  int nb, long row_bytes, int T, hipStream_t st) {
+                  int nb, long row_bytes, int T, hipStream_t st, int accumulate) {
     constexpr int TW = kTile * TTW;
     const int Tp = (T + TW - 1) / TW * TW, nkb = nb * 8;
     auto* xh = scratch;
@@ -869,7 +872,7 @@ void launch16_cfg(float* Y, const uint8_t* W, const uint8_t* XQ8, uint8_t* scrat
     const int nrt = (rows + kTile * RT - 1) / (kTile * RT);
     const unsigned grid = (unsigned)((nrt + 7) / 8 * 8 * (Tp / TW));
     hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S>), dim3(grid), dim3(RT * 64), 0, st, Y, W, xh,
-                       dxt, gxt, rows, nb, row_bytes, T, Tp, nrt);
+                       dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, accumulate);
 }
 
 // ---------------------------------------------------------------------------
@@ -1044,7 +1047,7 @@ __device__ __forceinline__ void gemm6_step(
 template <int RT, int TT, int KS, int TS, int S>
 __global__ __launch_bounds__(KS * RT * TS * 64) void k_gemm_mfma_q6k(
     float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ xs,
-    const float* __restrict__ dxs, int rows, int nb, long row_bytes, int T, int Tp) {
+    const float* __restrict__ dxs, int rows, int nb, long row_bytes, int T, int Tp, int accumulate) {
     using G = Stage6<RT, TT, KS, TS, S>;
     constexpr int RW = G::RW, TW = G::TW, NW = G::NW;
     __shared__ __attribute__((aligned(16))) uint8_t smem[S * G::ALLOC];
@@ -1138,7 +1141,10 @@ __global__ __launch_bounds__(KS * RT * TS * 64) void k_gemm_mfma_q6k(
 #pragma unroll
             for (int ii = 0; ii < 4; ii++) {
                 const int tok = tok_base + kTile * (tt0 + w) + 4 * g + ii;
-                if (tok < T) Y[(size_t)tok * rows + o] = acc[w][ii];
+                if (tok < T) {
+                    float* y = Y + (size_t)tok * rows + o;
+                    *y = accumulate ? *y + acc[w][ii] : acc[w][ii];
+                }
             }
         }
     }
@@ -1146,11 +1152,11 @@ __global__ __launch_bounds__(KS * RT * TS * 64) void k_gemm_mfma_q6k(
 
 template <int RT, int TT, int KS, int TS, int S>
 void launch6_cfg(float* Y, const uint8_t* W, const uint8_t* xs, const float* dxs, int rows,
-                 int nb, long row_bytes, int T, int Tp, hipStream_t st) {
+                 int nb, long row_bytes, int T, int Tp, hipStream_t st, int accumulate) {
     using G = Stage6<RT, TT, KS, TS, S>;
     const dim3 grid((unsigned)((rows + G::RW - 1) / G::RW), (unsigned)(Tp / G::TW));
     hipLaunchKernelGGL((k_gemm_mfma_q6k<RT, TT, KS, TS, S>), grid, dim3(G::NW * 64), 0, st, Y,
-                       W, xs, dxs, rows, nb, row_bytes, T, Tp);
+                       W, xs, dxs, rows, nb, row_bytes, T, Tp, accumulate);
 }
 
 // Tile choice: the largest of 64x64, 32x32, 16x16 (rows x tokens) whose grid
@@ -1222,7 +1228,8 @@ size_t gemm_mfma_q6k_scratch_bytes(int T, int nb) {
 }
 
 hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
-                                   int nb, long row_bytes, void* scratch, hipStream_t st) {
+                                   int nb, long row_bytes, void* scratch, hipStream_t st,
+                                   int accumulate) {
     if (rows <= 0 || T <= 0 || nb <= 0 || scratch == nullptr) return hipErrorInvalidValue;
     if (!gemm_mfma_q6k_ok(W, rows, nb, row_bytes)) return hipErrorInvalidValue;
     const Tile6 tile = pick6(rows, T);
@@ -1239,16 +1246,16 @@ hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int
     const auto* w = static_cast<const uint8_t*>(W);
     switch (tile) {
     case Tile6::R64T64:
-        launch6_cfg<4, 4, 2, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st);
+        launch6_cfg<4, 4, 2, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st, accumulate);
         break;
     case Tile6::R32T32:
-        launch6_cfg<2, 2, 4, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st);
+        launch6_cfg<2, 2, 4, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st, accumulate);
         break;
     case Tile6::R16T16:
-        launch6_cfg<1, 1, 4, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st);
+        launch6_cfg<1, 1, 4, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st, accumulate);
         break;
     default:
-        launch6_cfg<1, 1, 8, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st);
+        launch6_cfg<1, 1, 8, 1, 2>(Y, w, xs, dxs, rows, nb, row_bytes, T, Tp, st, accumulate);
         break;
     }
     return hipGetLastError();
@@ -1329,15 +1336,17 @@ hipError_t launch_gemm_stream_q4k_q8(float* Y, const void* W, const void* XQ8, i
 }
 
 hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
-                                   int nb, long row_bytes, void* scratch, hipStream_t st) {
+                                   int nb, long row_bytes, void* scratch, hipStream_t st,
+                                   int accumulate) {
     if (rows <= 0 || T <= 0 || nb <= 0 || scratch == nullptr) return hipErrorInvalidValue;
     if (T >= kF16MinTokens) {
         const auto* w = static_cast<const uint8_t*>(W);
         const auto* xq = static_cast<const uint8_t*>(XQ8);
         auto* sc = static_cast<uint8_t*>(scratch);
-        launch16_cfg<8, 2, 2>(Y, w, xq, sc, rows, nb, row_bytes, T, st);
+        launch16_cfg<8, 2, 2>(Y, w, xq, sc, rows, nb, row_bytes, T, st, accumulate);
         return hipGetLastError();
     }
+    if (accumulate) return hipErrorInvalidValue;  // the int8 kernels below overwrite Y
     const MfmaCfg c = pick_mfma(T, nb);
     const int Tp = padded_tokens(T, c);
     const int nkb = nb * 8;
