@@ -139,6 +139,36 @@ hipError_t launch_gemm_misc_f32(int qtype, float* Y, const void* W, const float*
                                 int cols, long row_bytes, int T, int accumulate, hipStream_t st);
 hipError_t launch_embed_misc(int qtype, float* out, const void* W, const int* tok_dev, int tok,
                              int T, int cols, long row_bytes, hipStream_t st);
+// A decode stage of Q8_0 / Q5_0 / F16 matrices in one launch: RMSNorm(x) * nw
+// in the prologue (the bits of launch_rmsnorm), then q, k, v rows (up to three
+// matrices, y = W * activation) or, with swiglu, y = SwiGLU(gate, up) (mats[0]
+// = gate with y = h, mats[1] = up).  n = K (n % 32 == 0, n <= 8192).
+struct MiscMat {
+    const void* W;
+    long row_bytes;
+    int rows;
+    int qtype;
+    float* y;
+};
+struct MiscStageArgs {
+    const float* x;
+    const float* nw;
+    float eps;
+    int n;
+    const uint8_t* W[3];
+    long rb[3];
+    int rows[3];
+    int qt[3];
+    float* y[3];
+    int nseg;
+    int swiglu;
+    int need_q8;
+};
+// False where the stage keeps the separate kernels: a K-quant matrix, K out of
+// range, or rows whose types take different lanes per row.
+bool misc_norm_stage_ok(const MiscMat* mats, int nmat, int n);
+hipError_t launch_misc_norm_stage(const MiscMat* mats, int nmat, bool swiglu, const float* x,
+                                  const float* nw, float eps, int n, hipStream_t st);
 hipError_t launch_dequant_q4k(float* y, const void* W, long nblocks, hipStream_t st);
 hipError_t launch_dequant_q6k(float* y, const void* W, long nblocks, hipStream_t st);
 hipError_t launch_quantize_q8_0(void* y, const float* x, int n, hipStream_t st);

@@ -426,6 +426,22 @@ bool embed_fusable(const axf_llama* m) {
     return m->tok_embd.qtype == AXF_TYPE_Q4_K && L.qk_fused && L.wv.qtype == AXF_TYPE_Q6_K;
 }
 
+// The q|k|v matrices of a layer as MiscMat segments (q|k as one matrix when
+// fused); false unless every one is Q8_0 / Q5_0 / F16.
+bool misc_qkv(const Layer& L, float* q, float* k, float* v, int qo, int kvo, MiscMat (&mm)[3]) {
+    int n = 0;
+    if (L.qk_fused) {
+        mm[n++] = {L.wq.d, (long)L.wq.row_bytes, qo + kvo, L.wq.qtype, q};
+    } else {
+        mm[n++] = {L.wq.d, (long)L.wq.row_bytes, qo, L.wq.qtype, q};
+        mm[n++] = {L.wk.d, (long)L.wk.row_bytes, kvo, L.wk.qtype, k};
+    }
+    mm[n++] = {L.wv.d, (long)L.wv.row_bytes, kvo, L.wv.qtype, v};
+    for (int i = 0; i < n; i++)
+        if (!misc_type(mm[i].qtype)) return false;
+    return true;
+}
+
 hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int first = 1,
                          int last = 5, const int* emb_tok_dev = nullptr, int emb_tok = -1) {
     const auto& hp = m->hp;
@@ -469,6 +485,11 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int f
             ST(gemv_norm(L.wk, k, m->x, L.attn_norm, hp.rms_eps, kvo, E, false, st));
         }
         ST(gemv_norm(L.wv, v, m->x, L.attn_norm, hp.rms_eps, kvo, E, false, st));
+    } else if (MiscMat mm[3]; misc_qkv(L, q, k, v, qo, kvo, mm) &&
+                                misc_norm_stage_ok(mm, L.qk_fused ? 2 : 3, E)) {
+        // all Q8_0 / Q5_0 / F16: the norm and the three projections in one launch
+        ST(launch_misc_norm_stage(mm, L.qk_fused ? 2 : 3, false, m->x, L.attn_norm, hp.rms_eps, E,
+                                  st));
     } else {
         // Q8_0 / Q5_0 / F16 projections: RMSNorm once (fp32 and Q8_0), then each
         // GEMV on the activation its type takes
@@ -541,6 +562,11 @@ hipError_t enqueue_layer(axf_llama* m, int l, const int* pos_dev, int pos, int f
         ST(gemv_norm(L.wgate, m->gateup, m->x, L.ffn_norm, hp.rms_eps, FD, E, false, st));
         ST(gemv_norm(L.wup, m->gateup + FD, m->x, L.ffn_norm, hp.rms_eps, FD, E, false, st));
         ST(launch_swiglu(m->h, nullptr, m->gateup, m->gateup + FD, FD, st));
+    } else if (MiscMat mm[2] = {{L.wgate.d, (long)L.wgate.row_bytes, FD, L.wgate.qtype, m->h},
+                                {L.wup.d, (long)L.wup.row_bytes, FD, L.wup.qtype, nullptr}};
+               misc_norm_stage_ok(mm, 2, E)) {
+        // all Q8_0 / Q5_0 / F16: norm, gate, up and SwiGLU in one launch
+        ST(launch_misc_norm_stage(mm, 2, true, m->x, L.ffn_norm, hp.rms_eps, E, st));
     } else {
         ST(launch_rmsnorm(m->xb, m->xq8, m->x, L.ffn_norm, E, hp.rms_eps, st));
         ST(gemv_any(L.wgate, m->gateup, m->xq8, m->xb, FD, E, false, st));

@@ -265,6 +265,15 @@ __device__ __forceinline__ uint32_t q8_quant4(float4 v, float& d) {
     return __builtin_isinf(id) ? 0x80808080u : (lo | hi);
 }
 
+// Q8_0 block (fp32 d + 32 int8) from 8 consecutive lanes' float4s (q8_quant4),
+// written at blk by lane sub = 0..7 of the group.
+__device__ __forceinline__ void q8_block_store(uint8_t* blk, int sub, float4 v) {
+    float d;
+    const uint32_t packed = q8_quant4(v, d);
+    *reinterpret_cast<uint32_t*>(blk + 4 + 4 * sub) = packed;
+    if (sub == 0) *reinterpret_cast<float*>(blk) = d;
+}
+
 // Q4_K scale/min pair for sub-blocks j0 = 2*part and j1 = 2*part + 1 from the
 // 12 packed scale bytes s[0..11] held in three dwords (get_scale_min_k4 logic:
 // j<4: sc=s[j]&63, m=s[j+4]&63;  j>=4: sc=(s[j+4]&15)|((s[j-4]>>6)<<4),

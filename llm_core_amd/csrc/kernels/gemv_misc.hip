@@ -46,6 +46,76 @@ __device__ __forceinline__ long misc_row() {
     return (long)blockIdx.x * (kMiscThreads / LPR) + threadIdx.x / LPR;
 }
 
+// Row dots, shared by the token-grid GEMVs below and the fused decode stage
+// kernel (activation in global memory or in LDS).  Lane rl of the row's LPR
+// lanes takes blocks rl, rl + LPR, ...; the activation's 32-float (or 36-byte
+// Q8_0) block b starts at float XS * b (XS = 32 in global memory, 36 in LDS,
+// where the padding spreads the lanes' blocks over the banks).
+template <int LPR>
+__device__ __forceinline__ float dot_q8w_q8(const uint8_t* __restrict__ wr,
+                                            const uint8_t* __restrict__ xq8, int nb, int rl) {
+    float acc = 0.f;
+    for (int b = rl; b < nb; b += LPR) {
+        const uint8_t* wb = wr + (long)b * 34;
+        const uint8_t* xb = xq8 + (long)b * Q8_0_BYTES;
+        const float scale = h2f(ld2(wb)) * __uint_as_float(ld4(xb));
+        int isum = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) isum = dot4((int)ld2x2(wb + 2 + 4 * k), (int)ld4(xb + 4 + 4 * k), isum);
+        acc = fmaf(scale, (float)isum, acc);
+    }
+    return acc;
+}
+
+template <int LPR, int XS>
+__device__ __forceinline__ float dot_q5_0_f32(const uint8_t* __restrict__ wr,
+                                              const float* __restrict__ x, int nb, int rl) {
+    float acc = 0.f;
+    for (int b = rl; b < nb; b += LPR) {
+        const uint8_t* wb = wr + (long)b * 22;
+        const float d = h2f(ld2(wb));
+        const uint32_t qh = ld2x2(wb + 2);
+        const float* xb = x + XS * b;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t qs = ld2x2(wb + 6 + 4 * k);  // bytes 4k..4k+3 of the 16
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = 4 * k + j;  // low nibble: element i, high: element i + 16
+                const uint32_t lo = (qs >> (8 * j)) & 0x0fu, hi = (qs >> (8 * j + 4)) & 0x0fu;
+                const float w0 = d * ((float)(lo | (((qh >> i) & 1u) << 4)) - 16.f);
+                const float w1 = d * ((float)(hi | (((qh >> (i + 16)) & 1u) << 4)) - 16.f);
+                acc = fmaf(w0, xb[i], acc);
+                acc = fmaf(w1, xb[i + 16], acc);
+            }
+        }
+    }
+    return acc;
+}
+
+template <int LPR, int XS>
+__device__ __forceinline__ float dot_f16_f32(const uint16_t* __restrict__ W,
+                                             const float* __restrict__ x, int cols, int rl) {
+    float acc = 0.f;
+    const uint4* wr = reinterpret_cast<const uint4*>(W);
+    const int ng = cols / 8;
+    for (int g = rl; g < ng; g += LPR) {
+        const uint4 w = wr[g];
+        const float* xg = x + XS * (g >> 2) + 8 * (g & 3);
+        const float4 x0 = reinterpret_cast<const float4*>(xg)[0];
+        const float4 x1 = reinterpret_cast<const float4*>(xg)[1];
+        acc = fmaf(h2f(w.x & 0xffffu), x0.x, acc);
+        acc = fmaf(h2f(w.x >> 16), x0.y, acc);
+        acc = fmaf(h2f(w.y & 0xffffu), x0.z, acc);
+        acc = fmaf(h2f(w.y >> 16), x0.w, acc);
+        acc = fmaf(h2f(w.z & 0xffffu), x1.x, acc);
+        acc = fmaf(h2f(w.z >> 16), x1.y, acc);
+        acc = fmaf(h2f(w.w & 0xffffu), x1.z, acc);
+        acc = fmaf(h2f(w.w >> 16), x1.w, acc);
+    }
+    return acc;
+}
+
 template <int LPR>
 __global__ __launch_bounds__(kMiscThreads) void k_gemv_q8w_q8(float* __restrict__ y,
                                                               const uint8_t* __restrict__ W,
@@ -57,18 +127,7 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_q8w_q8(float* __restrict_
     const long row = misc_row<LPR>();
     const int rl = threadIdx.x % LPR;
     float acc = 0.f;
-    if (row < rows) {
-        const uint8_t* wr = W + row * row_bytes;
-        for (int b = rl; b < nb; b += LPR) {
-            const uint8_t* wb = wr + (long)b * 34;
-            const uint8_t* xb = xq8 + (long)b * Q8_0_BYTES;
-            const float scale = h2f(ld2(wb)) * __uint_as_float(ld4(xb));
-            int isum = 0;
-#pragma unroll
-            for (int k = 0; k < 8; k++) isum = dot4((int)ld2x2(wb + 2 + 4 * k), (int)ld4(xb + 4 + 4 * k), isum);
-            acc = fmaf(scale, (float)isum, acc);
-        }
-    }
+    if (row < rows) acc = dot_q8w_q8<LPR>(W + row * row_bytes, xq8, nb, rl);
     acc = lanes_sum<LPR>(acc);
     if (row < rows && rl == 0) y[row] = accumulate ? y[row] + acc : acc;
 }
@@ -116,28 +175,7 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_q5_0_f32(float* __restric
     const long row = misc_row<LPR>();
     const int rl = threadIdx.x % LPR;
     float acc = 0.f;
-    if (row < rows) {
-        const uint8_t* wr = W + row * row_bytes;
-        for (int b = rl; b < nb; b += LPR) {
-            const uint8_t* wb = wr + (long)b * 22;
-            const float d = h2f(ld2(wb));
-            const uint32_t qh = ld2x2(wb + 2);
-            const float* xb = x + 32 * b;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t qs = ld2x2(wb + 6 + 4 * k);  // bytes 4k..4k+3 of the 16
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int i = 4 * k + j;  // low nibble: element i, high: element i + 16
-                    const uint32_t lo = (qs >> (8 * j)) & 0x0fu, hi = (qs >> (8 * j + 4)) & 0x0fu;
-                    const float w0 = d * ((float)(lo | (((qh >> i) & 1u) << 4)) - 16.f);
-                    const float w1 = d * ((float)(hi | (((qh >> (i + 16)) & 1u) << 4)) - 16.f);
-                    acc = fmaf(w0, xb[i], acc);
-                    acc = fmaf(w1, xb[i + 16], acc);
-                }
-            }
-        }
-    }
+    if (row < rows) acc = dot_q5_0_f32<LPR, 32>(W + row * row_bytes, x, nb, rl);
     acc = lanes_sum<LPR>(acc);
     if (row < rows && rl == 0) y[row] = accumulate ? y[row] + acc : acc;
 }
@@ -153,27 +191,99 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_f16_f32(float* __restrict
     const long row = misc_row<LPR>();
     const int rl = threadIdx.x % LPR;
     float acc = 0.f;
-    if (row < rows) {
-        const uint4* wr = reinterpret_cast<const uint4*>(W + row * (long)cols);
-        const int ng = cols / 8;
-        for (int g = rl; g < ng; g += LPR) {
-            const uint4 w = wr[g];
-            const float4 x0 = reinterpret_cast<const float4*>(x)[2 * g];
-            const float4 x1 = reinterpret_cast<const float4*>(x)[2 * g + 1];
-            acc = fmaf(h2f(w.x & 0xffffu), x0.x, acc);
-            acc = fmaf(h2f(w.x >> 16), x0.y, acc);
-            acc = fmaf(h2f(w.y & 0xffffu), x0.z, acc);
-            acc = fmaf(h2f(w.y >> 16), x0.w, acc);
-            acc = fmaf(h2f(w.z & 0xffffu), x1.x, acc);
-            acc = fmaf(h2f(w.z >> 16), x1.y, acc);
-            acc = fmaf(h2f(w.w & 0xffffu), x1.z, acc);
-            acc = fmaf(h2f(w.w >> 16), x1.w, acc);
-        }
-    }
+    if (row < rows) acc = dot_f16_f32<LPR, 32>(W + row * (long)cols, x, cols, rl);
     acc = lanes_sum<LPR>(acc);
     if (row < rows && rl == 0) {
         const float v = acc + (bias ? bias[row] : 0.f);
         y[row] = accumulate ? y[row] + v : v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// A decode stage whose matrices are all Q8_0 / Q5_0 / F16 in one launch:
+// RMSNorm(x) * w in every workgroup's prologue (rms_scale<256, 8> and
+// q8_block_store: the bits of k_rmsnorm's fp32 and Q8_0 outputs), held in LDS,
+// then the rows of up to three matrices (q, k, v) with the row dots above, each
+// type on the activation gemv_wt_q8 gives it (llama_model.cpp:767-831: Q8_0
+// weights the Q8_0 row, Q5_0 / F16 the fp32 row).  SwiGLU mode (gate, up):
+// a workgroup computes R/2 gate rows and the same up rows and writes
+// h = swiglu1(gate, up) for them (k_swiglu's arithmetic).  The row dots are
+// those of the separate GEMVs with the same LPR, so each output has the bits
+// of k_rmsnorm + the GEMV (+ k_swiglu).
+// ---------------------------------------------------------------------------
+template <int LPR>
+__global__ __launch_bounds__(kMiscThreads) void k_misc_norm_stage(MiscStageArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ float red[16];
+    constexpr int R = kMiscThreads / LPR;
+    __shared__ float gu[R];
+    float* xs = reinterpret_cast<float*>(smem);                    // [n/32][36] floats
+    uint8_t* xq = smem + (size_t)(a.n / 32) * 36 * sizeof(float);  // [n/32] Q8_0 blocks
+    const int n4 = a.n / 4;
+    float4 xv[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i4 = threadIdx.x + kMiscThreads * k;
+        xv[k] = i4 < n4 ? reinterpret_cast<const float4*>(a.x)[i4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float s = rms_scale<kMiscThreads, 8>(xv, a.n, a.eps, red);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i4 = threadIdx.x + kMiscThreads * k;
+        if (i4 < n4) {
+            const float4 v = xv[k];
+            const float4 g = reinterpret_cast<const float4*>(a.nw)[i4];
+            float4 o;
+            o.x = g.x * (v.x * s);
+            o.y = g.y * (v.y * s);
+            o.z = g.z * (v.z * s);
+            o.w = g.w * (v.w * s);
+            *reinterpret_cast<float4*>(xs + 36 * (i4 >> 3) + 4 * (i4 & 7)) = o;
+            if (a.need_q8) q8_block_store(xq + (size_t)(i4 >> 3) * Q8_0_BYTES, i4 & 7, o);
+        }
+    }
+    __syncthreads();
+    const int li = threadIdx.x / LPR, rl = threadIdx.x % LPR;
+    int sg = 0;
+    long row;
+    if (a.swiglu) {
+        sg = li / (R / 2);
+        row = (long)blockIdx.x * (R / 2) + li % (R / 2);
+    } else {
+        row = (long)blockIdx.x * R + li;
+        if (a.nseg > 1 && row >= a.rows[0]) {
+            row -= a.rows[0];
+            sg = 1;
+            if (a.nseg > 2 && row >= a.rows[1]) {
+                row -= a.rows[1];
+                sg = 2;
+            }
+        }
+    }
+    // per-segment fields by select (no dynamic indexing of the argument block)
+    const uint8_t* W = sg == 0 ? a.W[0] : (sg == 1 ? a.W[1] : a.W[2]);
+    const long rb = sg == 0 ? a.rb[0] : (sg == 1 ? a.rb[1] : a.rb[2]);
+    const int rows = sg == 0 ? a.rows[0] : (sg == 1 ? a.rows[1] : a.rows[2]);
+    const int qt = sg == 0 ? a.qt[0] : (sg == 1 ? a.qt[1] : a.qt[2]);
+    float* y = sg == 0 ? a.y[0] : (sg == 1 ? a.y[1] : a.y[2]);
+    const bool live = row < rows;
+    float acc = 0.f;
+    if (live) {
+        const uint8_t* wr = W + row * rb;
+        if (qt == AXF_TYPE_Q8_0) acc = dot_q8w_q8<LPR>(wr, xq, a.n / 32, rl);
+        else if (qt == AXF_TYPE_Q5_0) acc = dot_q5_0_f32<LPR, 36>(wr, xs, a.n / 32, rl);
+        else acc = dot_f16_f32<LPR, 36>(reinterpret_cast<const uint16_t*>(wr), xs, a.n, rl);
+    }
+    acc = lanes_sum<LPR>(acc);
+    if (!a.swiglu) {
+        if (live && rl == 0) y[row] = acc;
+        return;
+    }
+    if (rl == 0) gu[li] = acc;
+    __syncthreads();
+    if (threadIdx.x < R / 2) {
+        const long r = (long)blockIdx.x * (R / 2) + threadIdx.x;
+        if (r < a.rows[0]) a.y[0][r] = swiglu1(gu[threadIdx.x], gu[R / 2 + threadIdx.x]);
     }
 }
 
@@ -388,6 +498,56 @@ hipError_t launch_gemv_f16_f32(float* y, const void* W, const float* x, const fl
     if (T <= 0 || T > 65535) return hipErrorInvalidValue;
     AXF_MISC_DISPATCH(k_gemv_f16_f32, cols / 8, rows, y, static_cast<const uint16_t*>(W), x, bias,
                       rows, cols, accumulate);
+    return hipGetLastError();
+}
+
+static int misc_mat_lpr(int qtype, int n) { return misc_lpr(qtype == AXF_TYPE_F16 ? n / 8 : n / 32); }
+
+bool misc_norm_stage_ok(const MiscMat* mats, int nmat, int n) {
+    if (nmat < 1 || nmat > 3 || n <= 0 || n % 32 || n > 8192) return false;
+    for (int i = 0; i < nmat; i++) {
+        const int qt = mats[i].qtype;
+        if (qt != AXF_TYPE_Q8_0 && qt != AXF_TYPE_Q5_0 && qt != AXF_TYPE_F16) return false;
+        if (qt == AXF_TYPE_F16 && (reinterpret_cast<uintptr_t>(mats[i].W) & 15)) return false;
+        if (mats[i].rows <= 0 || misc_mat_lpr(qt, n) != misc_mat_lpr(mats[0].qtype, n)) return false;
+    }
+    return true;
+}
+
+hipError_t launch_misc_norm_stage(const MiscMat* mats, int nmat, bool swiglu, const float* x,
+                                  const float* nw, float eps, int n, hipStream_t st) {
+    if (!misc_norm_stage_ok(mats, nmat, n) || (swiglu && (nmat != 2 || mats[0].rows != mats[1].rows)))
+        return hipErrorInvalidValue;
+    MiscStageArgs a{};
+    a.x = x;
+    a.nw = nw;
+    a.eps = eps;
+    a.n = n;
+    a.nseg = nmat;
+    a.swiglu = swiglu ? 1 : 0;
+    long total = 0;
+    for (int i = 0; i < 3; i++) {
+        const MiscMat& mm = mats[i < nmat ? i : 0];
+        a.W[i] = static_cast<const uint8_t*>(mm.W);
+        a.rb[i] = mm.row_bytes;
+        a.rows[i] = i < nmat ? mm.rows : 0;
+        a.qt[i] = mm.qtype;
+        a.y[i] = mm.y;
+        if (i < nmat) {
+            total += mm.rows;
+            a.need_q8 |= mm.qtype == AXF_TYPE_Q8_0;
+        }
+    }
+    const int lpr = misc_mat_lpr(mats[0].qtype, n);
+    const int R = kMiscThreads / lpr;
+    const long wgs = swiglu ? (mats[0].rows + R / 2 - 1) / (R / 2) : (total + R - 1) / R;
+    const size_t lds = (size_t)(n / 32) * (36 * sizeof(float) + (a.need_q8 ? Q8_0_BYTES : 0));
+    if (lpr == 64)
+        hipLaunchKernelGGL(k_misc_norm_stage<64>, dim3((unsigned)wgs), dim3(kMiscThreads), lds, st, a);
+    else if (lpr == 32)
+        hipLaunchKernelGGL(k_misc_norm_stage<32>, dim3((unsigned)wgs), dim3(kMiscThreads), lds, st, a);
+    else
+        hipLaunchKernelGGL(k_misc_norm_stage<16>, dim3((unsigned)wgs), dim3(kMiscThreads), lds, st, a);
     return hipGetLastError();
 }
 

@@ -82,13 +82,6 @@ __global__ void k_dequant_q6k(float* __restrict__ out, const uint8_t* __restrict
 // Q8_0 quantisation: 8 lanes per 32-element block, 4 elements per lane.
 // d = amax/127, id = 127/amax (0 when amax == 0), q = rne(x*id) saturated.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void q8_block_store(uint8_t* blk, int sub, float4 v) {
-    float d;
-    const uint32_t packed = q8_quant4(v, d);
-    *reinterpret_cast<uint32_t*>(blk + 4 + 4 * sub) = packed;
-    if (sub == 0) *reinterpret_cast<float*>(blk) = d;
-}
-
 __global__ void k_quantize_q8_0(uint8_t* __restrict__ y, const float* __restrict__ x, int n) {
     const int nthreads = n / 4;  // n % 32 == 0
     for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < nthreads; t += gridDim.x * blockDim.x) {

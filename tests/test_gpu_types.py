@@ -84,6 +84,37 @@ def test_decode_stages_every_type(ctx, layer):
         assert np.array_equal(g.get_x(), x2)
 
 
+def test_decode_stages_all_f16(ctx):
+    """A layer whose q/k/v and gate/up matrices are all F16 runs each of those
+    stages as one launch (the norm in the prologue, F16 rows at 32 lanes per
+    row); stage by stage against the oracle, and the whole layer in one call
+    gives the same bits."""
+    from llm_core_amd import hip
+    from llm_core_amd.model import Hparams, LlamaHip, SynthLlama
+
+    types = {n: F16 for n in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
+                              "ffn_down")}
+    hp = Hparams(**{**TOY, "n_layer": 1, "n_ctx": 40})
+    m = SynthLlama(hp, seed=4, norm_std=0.1, with_bias=True, embd_type=Q8, head_type=None,
+                   layer_types=lambda layer: types)
+    T = {k: v[1] for k, v in m.tensors.items()}
+    kvo, prior = hp.n_kv_heads * hp.head_dim, 21
+    kc = hip.synth_normal(prior * kvo, 61).reshape(prior, kvo)
+    vc = hip.synth_normal(prior * kvo, 62).reshape(prior, kvo)
+    with LlamaHip(ctx, m) as g:
+        g.set_kv(0, kc, vc, prior)
+        x0 = hip.synth_normal(hp.n_embd, 63)
+        g.set_x(x0)
+        for tag, err, nbad, rel in layer_stage_errors(ctx, g, T, hp, 0, prior, types=types):
+            print(f"  {tag}: max |err| {err:.3e}, norm-wise {rel:.2e}", flush=True)
+            assert nbad == 0, f"{tag}: {nbad} elements outside tolerance, max |err| {err:.3e}"
+        x2 = g.get_x()
+        g.set_kv(0, kc, vc, prior)
+        g.set_x(x0)
+        g.forward_layer(0, prior)
+        assert np.array_equal(g.get_x(), x2)
+
+
 @pytest.mark.parametrize("seed", GREEDY_SEEDS)
 def test_greedy_32_tokens_every_type(ctx, seed):
     from llm_core_amd.model import LlamaHip
