@@ -582,10 +582,13 @@ __device__ __forceinline__ void rec_load(const uint32_t* rec, int c, uint32_t (&
 // 128 weights), lane (rl, i) owns unit u = rl + i*LPR; the two chunks share
 // the block header (Q4_K d, dmin, scales) or the half's qh bytes, scales and d
 // (Q6_K), which are loaded and decoded once.  CPL counts units per lane.
-template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI, bool PAIR>
+typedef __attribute__((address_space(1))) const void gmem_t;
+typedef __attribute__((address_space(3))) void lmem_t;
+
+template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI, bool PAIR, bool WL = false>
 __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __restrict__ W,
                                            long rb, int rows, float* __restrict__ y, int wg,
-                                           uint32_t* rec, float* red) {
+                                           uint32_t* rec, float* red, uint8_t* wlds = nullptr) {
     constexpr int RPP = 64 / LPR;
     constexpr int RW = (NT / 64) * RPP * NR;  // rows per workgroup
     constexpr int UC = PAIR ? 2 : 1;          // chunks per unit
@@ -600,6 +603,12 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
     // (staging before any weight load: 13.85 us, 1.779 ms; that with
     // 1024-thread workgroups: 1.787 ms)
     constexpr bool SFIRST = QT == kQ6K && ACT == (int)QAct::F32 && NT >= kWide && !PAIR;
+    // WL (Q6_K half-block units, rows of a multiple of 16 bytes): the wave's
+    // RPP*NR consecutive rows are copied into LDS by 16-byte global_load_lds
+    // (64 lanes x 16 B of one contiguous span per instruction) and the lanes
+    // read their units' fields from there, instead of ~28 scattered dword
+    // loads per lane from global memory
+    static_assert(!WL || (QT == kQ6K && PAIR), "LDS-staged weights: Q6_K half-block units");
     // float4s of x per thread: K / 4 <= 16 * LPR * CPL * UC
     constexpr int KPT = (16 * LPR * CPL * UC + NT - 1) / NT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -756,12 +765,31 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
     } else {
         // unit (n, i): ql (8 dwords per chunk), the half's qh (8 dwords), scales, d
         uint32_t ql[NR][CPL][8 * UC], qh[NR][CPL][8], sc[NR][CPL][4], db[NR][CPL];
+        const int wv_ = __builtin_amdgcn_readfirstlane(wave);
+        uint8_t* wl = wlds + (size_t)wv_ * (RPP * NR) * rb;  // this wave's rows in LDS
+        if constexpr (WL) {
+            // rows wg*RW + wave*RPP*NR .. +RPP*NR-1; past the matrix end the
+            // addresses are clamped to its last 16 bytes (rows never stored)
+            const long first = (long)wg * RW + (long)wv_ * (RPP * NR);
+            const int span = (RPP * NR) * (int)rb;
+            const uint8_t* g0 = W + first * rb;
+            const uint8_t* gend = W + (long)rows * rb - 16;
+            for (int o = 0; o < span; o += 1024) {
+                const int lo = o + 16 * lane;
+                const uint8_t* g = g0 + lo;
+                if (lo < span)
+                    __builtin_amdgcn_global_load_lds((gmem_t*)(g < gend ? g : gend),
+                                                     (lmem_t*)(wl + o), 16, 0, 0);
+            }
+        }
         auto load6 = [&](int n, int i) {
             const long row = min(row0 + (long)n * RPP, (long)rows - 1);
             const int u = min(rl + i * LPR, nunits - 1);
             const int c0 = u * UC;  // first chunk of the unit
             const int h = (c0 >> 1) & 1, t = c0 & 1;
-            const uint8_t* blk = W + row * rb + (long)(c0 >> 2) * Q6K_BYTES;
+            const uint8_t* blk = WL ? wl + (long)(rloc0 - wv_ * (RPP * NR) + n * RPP) * rb +
+                                          (long)(c0 >> 2) * Q6K_BYTES
+                                    : W + row * rb + (long)(c0 >> 2) * Q6K_BYTES;
             if constexpr (PAIR) {
                 // 64 ql bytes, 32 qh bytes, 8 scale bytes of half h, and d, as
                 // aligned dwords + v_alignbyte: against 16-byte vectors at the
@@ -789,7 +817,17 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
                 load_q6_tail<LPR == 64>(blk, sc[n][i], db[n][i]);
             }
         };
-        if constexpr (SFIRST) {
+        if constexpr (WL) {
+            // the copies are in flight during the activation staging; each wave
+            // reads only its own rows, so its own wait suffices
+            stage();
+            __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0) (gfx9 encoding, lgkm/exp at maxima)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int n = 0; n < NR; n++)
+#pragma unroll
+                for (int i = 0; i < CPL; i++) load6(n, i);
+        } else if constexpr (SFIRST) {
             // the first unit's weights in flight during the staging
 #pragma unroll
             for (int n = 0; n < NR; n++) load6(n, 0);
@@ -807,7 +845,7 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
                 for (int i = 0; i < CPL; i++) load6(n, i);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (!SFIRST) stage();
+        if constexpr (!SFIRST && !WL) stage();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
@@ -907,13 +945,15 @@ __device__ __forceinline__ void qgemv_body(const QGemvArgs& a, const uint8_t* __
     }
 }
 
-template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI, bool PAIR>
+template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI, bool PAIR, bool WL = false>
 __global__ __launch_bounds__(NT) void k_qgemv(QGemvArgs a) {
     extern __shared__ uint4 smem[];
     uint32_t* rec = reinterpret_cast<uint32_t*>(smem);
     float* red = reinterpret_cast<float*>(rec + 80 * a.nb);
-    qgemv_body<QT, NT, LPR, CPL, NR, ACT, EPI, PAIR>(a, a.W0, a.rb0, a.rows0, a.y0, blockIdx.x,
-                                                      rec, red);
+    // WL: the weight rows after rec and red (qgemv_lds, 16-byte aligned)
+    uint8_t* wl = reinterpret_cast<uint8_t*>(smem) + 320 * a.nb + 4 * (16 + 256);
+    qgemv_body<QT, NT, LPR, CPL, NR, ACT, EPI, PAIR, WL>(a, a.W0, a.rb0, a.rows0, a.y0,
+                                                          blockIdx.x, rec, red, wl);
 }
 
 // Workgroups [0, nwg0) run the Q4_K segment, the rest the Q6_K segment.
@@ -1257,13 +1297,20 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q6k_q8(float* __restrict__ Y,
 
 static inline size_t qgemv_lds(int nb) { return (size_t)320 * nb + 4 * (16 + 256); }
 
-template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI, bool PAIR>
+template <int QT, int NT, int LPR, int CPL, int NR, int ACT, int EPI, bool PAIR, bool WL = false>
 static hipError_t qgemv_cfg(const QGemvArgs& a, hipStream_t st) {
     constexpr int RW = (NT / 64) * (64 / LPR) * NR;
     const dim3 grid((unsigned)((a.rows0 + RW - 1) / RW));
-    hipLaunchKernelGGL((k_qgemv<QT, NT, LPR, CPL, NR, ACT, EPI, PAIR>), grid, dim3(NT),
-                       qgemv_lds(a.nb), st, a);
+    const size_t lds = qgemv_lds(a.nb) + (WL ? (size_t)RW * a.rb0 : 0);
+    hipLaunchKernelGGL((k_qgemv<QT, NT, LPR, CPL, NR, ACT, EPI, PAIR, WL>), grid, dim3(NT), lds, st,
+                       a);
     return hipGetLastError();
+}
+
+// the LDS-staged Q6_K rows: whole 16-byte rows, 16-byte aligned, in LDS
+static bool q6k_wl_ok(const QGemvArgs& a, int rw) {
+    return a.rb0 % 16 == 0 && (reinterpret_cast<uintptr_t>(a.W0) & 15) == 0 &&
+           qgemv_lds(a.nb) + (size_t)rw * a.rb0 <= 64 * 1024;
 }
 
 template <int QT, int NT, int ACT, int EPI>
@@ -1432,10 +1479,15 @@ static hipError_t launch_cfg(GemvKind kind, float* y, const void* W, const void*
                        : qgemv_cfg<kQ6K, kWide, 32, 1, 1, (int)QAct::Q8, EPI_Y, true>(a, st);
         // half-block units of 16 lanes, 512 threads (5-8 super-blocks per row):
         // the 151936 x 2048 Q6_K head 54.9 -> 47.4 us against one chunk per lane
-        // with aligned dwords (two rows per lane group 51.9 us, 256 threads 48.5 us)
+        // with aligned dwords (two rows per lane group 51.9 us, 256 threads 48.5 us).
+        // Q6_K rows of a multiple of 16 bytes (8 super-blocks) staged in LDS
+        // per wave, 256 threads (five workgroups per CU): 48.1 -> 44.4 us (512
+        // threads, two per CU: 49.5 us; 128 threads: 46.6-47.4 us)
         if (nb >= 5 && nb <= 8)
             return kind == GemvKind::Q4K_Q8
                        ? qgemv_cfg<kQ4K, kWide, 16, 1, 1, (int)QAct::Q8, EPI_Y, true>(a, st)
+                   : q6k_wl_ok(a, 16)
+                       ? qgemv_cfg<kQ6K, kThreads, 16, 1, 1, (int)QAct::Q8, EPI_Y, true, true>(a, st)
                        : qgemv_cfg<kQ6K, kWide, 16, 1, 1, (int)QAct::Q8, EPI_Y, true>(a, st);
         return kind == GemvKind::Q4K_Q8
                    ? qgemv_cfg<kQ4K, kThreads, LPR, CPL, NR, (int)QAct::Q8, EPI_Y, false>(a, st)

@@ -114,6 +114,8 @@ GEMV_SHAPES = [
     (Q4K, 1001, 4096),   # half-block units, last workgroup partly past the rows
     (Q6K, 1, 256),
     (Q6K, 37, 2048),
+    (Q6K, 1, 2048),      # 1680-byte rows: Q8_0 GEMV rows staged in LDS, one row
+    (Q6K, 70, 2048),     # ... three workgroups, the last with 6 of its 32 rows
     (Q6K, 64, 4096),
     (Q6K, 23, 2304),     # half-block units on 1890-byte rows (odd rows 2-byte aligned)
     (Q6K, 77, 3072),
