@@ -67,7 +67,18 @@ __device__ __forceinline__ float dot_q8w_q8(const uint8_t* __restrict__ wr,
     return acc;
 }
 
-template <int LPR, int XS>
+// bit j of the low 4 bits of s into bit 0 of byte j (the four products
+// s << 0, 7, 14, 21 do not overlap, so the multiply has no carries)
+__device__ __forceinline__ uint32_t spread4(uint32_t s) {
+    return __umul24(s, 0x00204081u) & 0x01010101u;
+}
+
+// Q5_0: w = d * (q5 - 16), q5 = nibble | (bit of qh) << 4.  Per block the
+// 32 products q5 * x are summed first and the block adds d * (sum - 16 * sx),
+// sx = the block's sum of x (SX: precomputed at float XS * b + 32; else summed
+// here): 4 q5 values are built per integer operation sequence as bytes and
+// converted with v_cvt_f32_ubyte*, and x is read as float4.
+template <int LPR, int XS, bool SX>
 __device__ __forceinline__ float dot_q5_0_f32(const uint8_t* __restrict__ wr,
                                               const float* __restrict__ x, int nb, int rl) {
     float acc = 0.f;
@@ -76,19 +87,27 @@ __device__ __forceinline__ float dot_q5_0_f32(const uint8_t* __restrict__ wr,
         const float d = h2f(ld2(wb));
         const uint32_t qh = ld2x2(wb + 2);
         const float* xb = x + XS * b;
+        float s = 0.f, sx = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const uint32_t qs = ld2x2(wb + 6 + 4 * k);  // bytes 4k..4k+3 of the 16
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = 4 * k + j;  // low nibble: element i, high: element i + 16
-                const uint32_t lo = (qs >> (8 * j)) & 0x0fu, hi = (qs >> (8 * j + 4)) & 0x0fu;
-                const float w0 = d * ((float)(lo | (((qh >> i) & 1u) << 4)) - 16.f);
-                const float w1 = d * ((float)(hi | (((qh >> (i + 16)) & 1u) << 4)) - 16.f);
-                acc = fmaf(w0, xb[i], acc);
-                acc = fmaf(w1, xb[i + 16], acc);
-            }
+            // elements 4k..4k+3 (low nibbles) and 4k+16..4k+19 (high nibbles)
+            const uint32_t lo = (qs & 0x0f0f0f0fu) | (spread4((qh >> (4 * k)) & 0xfu) << 4);
+            const uint32_t hi = ((qs >> 4) & 0x0f0f0f0fu) | (spread4((qh >> (16 + 4 * k)) & 0xfu) << 4);
+            const float4 xl = *reinterpret_cast<const float4*>(xb + 4 * k);
+            const float4 xh = *reinterpret_cast<const float4*>(xb + 16 + 4 * k);
+            s = fmaf((float)(lo & 0xffu), xl.x, s);
+            s = fmaf((float)((lo >> 8) & 0xffu), xl.y, s);
+            s = fmaf((float)((lo >> 16) & 0xffu), xl.z, s);
+            s = fmaf((float)(lo >> 24), xl.w, s);
+            s = fmaf((float)(hi & 0xffu), xh.x, s);
+            s = fmaf((float)((hi >> 8) & 0xffu), xh.y, s);
+            s = fmaf((float)((hi >> 16) & 0xffu), xh.z, s);
+            s = fmaf((float)(hi >> 24), xh.w, s);
+            if constexpr (!SX) sx += ((xl.x + xl.y) + (xl.z + xl.w)) + ((xh.x + xh.y) + (xh.z + xh.w));
         }
+        if constexpr (SX) sx = xb[32];
+        acc = fmaf(d, fmaf(-16.f, sx, s), acc);
     }
     return acc;
 }
@@ -175,7 +194,7 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_q5_0_f32(float* __restric
     const long row = misc_row<LPR>();
     const int rl = threadIdx.x % LPR;
     float acc = 0.f;
-    if (row < rows) acc = dot_q5_0_f32<LPR, 32>(W + row * row_bytes, x, nb, rl);
+    if (row < rows) acc = dot_q5_0_f32<LPR, 32, false>(W + row * row_bytes, x, nb, rl);
     acc = lanes_sum<LPR>(acc);
     if (row < rows && rl == 0) y[row] = accumulate ? y[row] + acc : acc;
 }
@@ -240,6 +259,13 @@ __global__ __launch_bounds__(kMiscThreads) void k_misc_norm_stage(MiscStageArgs 
             o.w = g.w * (v.w * s);
             *reinterpret_cast<float4*>(xs + 36 * (i4 >> 3) + 4 * (i4 & 7)) = o;
             if (a.need_q8) q8_block_store(xq + (size_t)(i4 >> 3) * Q8_0_BYTES, i4 & 7, o);
+            // the block's sum of x (Q5_0 rows), into the block's first pad float:
+            // the 8 lanes of the block (i4 & 7 == lane & 7) by a fixed butterfly
+            float bs = (o.x + o.y) + (o.z + o.w);
+            bs += __shfl_xor(bs, 1, 8);
+            bs += __shfl_xor(bs, 2, 8);
+            bs += __shfl_xor(bs, 4, 8);
+            if ((i4 & 7) == 0) xs[36 * (i4 >> 3) + 32] = bs;
         }
     }
     __syncthreads();
@@ -271,7 +297,7 @@ __global__ __launch_bounds__(kMiscThreads) void k_misc_norm_stage(MiscStageArgs 
     if (live) {
         const uint8_t* wr = W + row * rb;
         if (qt == AXF_TYPE_Q8_0) acc = dot_q8w_q8<LPR>(wr, xq, a.n / 32, rl);
-        else if (qt == AXF_TYPE_Q5_0) acc = dot_q5_0_f32<LPR, 36>(wr, xs, a.n / 32, rl);
+        else if (qt == AXF_TYPE_Q5_0) acc = dot_q5_0_f32<LPR, 36, true>(wr, xs, a.n / 32, rl);
         else acc = dot_f16_f32<LPR, 36>(reinterpret_cast<const uint16_t*>(wr), xs, a.n, rl);
     }
     acc = lanes_sum<LPR>(acc);
