@@ -227,8 +227,10 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_f16_f32(float* __restrict
 // weights the Q8_0 row, Q5_0 / F16 the fp32 row).  SwiGLU mode (gate, up):
 // a workgroup computes R/2 gate rows and the same up rows and writes
 // h = swiglu1(gate, up) for them (k_swiglu's arithmetic).  The row dots are
-// those of the separate GEMVs with the same LPR, so each output has the bits
-// of k_rmsnorm + the GEMV (+ k_swiglu).
+// those of the separate GEMVs with the same LPR, so the Q8_0 and F16 outputs
+// have the bits of k_rmsnorm + the GEMV (+ k_swiglu); Q5_0 rows take each
+// block's sum of x from the prologue (a fixed 8-lane butterfly) where the
+// GEMV sums it alongside the products, which differs in fp32 rounding only.
 // ---------------------------------------------------------------------------
 template <int LPR>
 __global__ __launch_bounds__(kMiscThreads) void k_misc_norm_stage(MiscStageArgs a) {
