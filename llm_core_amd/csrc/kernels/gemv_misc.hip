@@ -58,10 +58,21 @@ __device__ __forceinline__ float dot_q8w_q8(const uint8_t* __restrict__ wr,
     for (int b = rl; b < nb; b += LPR) {
         const uint8_t* wb = wr + (long)b * 34;
         const uint8_t* xb = xq8 + (long)b * Q8_0_BYTES;
+        // the 34-byte block is 2-byte aligned: d as a 16-bit word, the 32 codes
+        // from 8 aligned dwords starting at wb (sh = 0: d and codes 0..29) or
+        // wb + 2 (sh = 2: codes 0..31) and the 16-bit word at wb + 32 (codes
+        // 30, 31), joined by v_alignbyte; every byte read lies in the block
+        const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(wb) & 3u);
+        const uint8_t* wa = wb + sh;
+        uint32_t w[9];
+#pragma unroll
+        for (int k = 0; k < 8; k++) w[k] = ld4(wa + 4 * k);
+        w[8] = ld2(wb + 32);
         const float scale = h2f(ld2(wb)) * __uint_as_float(ld4(xb));
         int isum = 0;
 #pragma unroll
-        for (int k = 0; k < 8; k++) isum = dot4((int)ld2x2(wb + 2 + 4 * k), (int)ld4(xb + 4 + 4 * k), isum);
+        for (int k = 0; k < 8; k++)
+            isum = dot4((int)alignbyte(w[k + 1], w[k], 2u - sh), (int)ld4(xb + 4 + 4 * k), isum);
         acc = fmaf(scale, (float)isum, acc);
     }
     return acc;
