@@ -658,22 +658,26 @@ hipError_t launch_attention_prefill(const AttnArgs& a, int head_dim, hipStream_t
 }
 
 // Query heads per workgroup: all G of a kv head when kv heads x splits give
-// 128 workgroups or more; fewer (down to 1) when they do not, so that a model
-// with 2 kv heads of 8 query heads at context 1024 runs 136 workgroups of 2
-// heads instead of 34 of 8 (config-3 layer step 50.5 -> 43.0 us; 43.5 us with
-// 272 workgroups of one head, 45.4 us with 68 of four).  Groups of one kv head
-// each read its K/V rows (from L2 after the first).
-static int attn_heads_per_group(int G, long kv_work) {
+// `want` workgroups or more; fewer (down to 1) when they do not, so that a
+// model with 2 kv heads of 8 query heads at context 1024 runs 136 workgroups
+// of 2 heads instead of 34 of 8 (config-3 layer step 50.5 -> 43.0 us; 43.5 us
+// with 272 workgroups of one head, 45.4 us with 68 of four).  Groups of one kv
+// head each read its K/V rows (from L2 after the first).  want = 128, or 256
+// at head dimension 64, where a workgroup's rows are half the bytes
+// (Qwen2.5-0.5B shape, 2 kv heads of 7 at context 2048: 256 workgroups of 2
+// heads instead of 128 of 4, decode step 789 -> 766 us).
+static int attn_heads_per_group(int G, long kv_work, int hd) {
+    const long want = hd == 64 ? 256 : 128;
     int gm = 1;
     while (gm < G && gm < 8) gm *= 2;  // G rounded up to a power of two
-    while (gm > 1 && kv_work * ((G + gm - 1) / gm) < 128) gm /= 2;
+    while (gm > 1 && kv_work * ((G + gm - 1) / gm) < want) gm /= 2;
     return gm;
 }
 
 template <int HD>
 static hipError_t launch_attn_hd(const AttnArgs& a, int G, hipStream_t st) {
     const unsigned nt = a.n_tok > 1 ? (unsigned)a.n_tok : 1u;
-    const int gm = attn_heads_per_group(G, (long)a.n_kv_heads * a.nsplit * nt);
+    const int gm = attn_heads_per_group(G, (long)a.n_kv_heads * a.nsplit * nt, HD);
     const dim3 grid((unsigned)(a.n_kv_heads * ((G + gm - 1) / gm)), (unsigned)a.nsplit, nt);
     if (gm == 1)
         hipLaunchKernelGGL((k_attn_split<HD, 1>), grid, dim3(kAttnThreads), 0, st, a);
