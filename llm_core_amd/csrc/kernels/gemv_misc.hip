@@ -238,10 +238,11 @@ __global__ __launch_bounds__(kMiscThreads) void k_gemv_f16_f32(float* __restrict
 // weights the Q8_0 row, Q5_0 / F16 the fp32 row).  SwiGLU mode (gate, up):
 // a workgroup computes R/2 gate rows and the same up rows and writes
 // h = swiglu1(gate, up) for them (k_swiglu's arithmetic).  The row dots are
-// those of the separate GEMVs with the same LPR, so the Q8_0 and F16 outputs
-// have the bits of k_rmsnorm + the GEMV (+ k_swiglu); Q5_0 rows take each
-// block's sum of x from the prologue (a fixed 8-lane butterfly) where the
-// GEMV sums it alongside the products, which differs in fp32 rounding only.
+// those of the separate GEMVs; Q5_0 rows take each block's sum of x from the
+// prologue (a fixed 8-lane butterfly) where the GEMV sums it alongside the
+// products.  With the same lanes per row the Q8_0 and F16 outputs have the
+// bits of k_rmsnorm + the GEMV (+ k_swiglu); the lane count is chosen per
+// launch (misc_lpr_rows), so the two may differ in fp32 summation order.
 // ---------------------------------------------------------------------------
 template <int LPR>
 __global__ __launch_bounds__(kMiscThreads) void k_misc_norm_stage(MiscStageArgs a) {
@@ -355,6 +356,16 @@ __global__ __launch_bounds__(256) void k_embed_misc(float* __restrict__ out, int
 }
 
 int misc_lpr(int units) { return units >= 64 ? 64 : (units >= 32 ? 32 : 16); }
+
+// Lanes per row for a launch of `rows` rows (all tokens): misc_lpr, doubled
+// (up to 64) while the launch would have fewer than 256 workgroups; short
+// launches then spread each row over more lanes (Qwen2.5-0.5B shape: the
+// 896-row o projection 56 -> 224 workgroups, the q|k|v stage 72 -> 288)
+static int misc_lpr_rows(int units, long rows) {
+    int l = misc_lpr(units);
+    while (l < 64 && rows * l < 256L * kMiscThreads) l *= 2;
+    return l;
+}
 
 // ---------------------------------------------------------------------------
 // Batched prefill with fp32 rows (gemm_wt_q8's fallback, llama_model.cpp:876-879,
@@ -502,7 +513,7 @@ hipError_t launch_gemm_misc_f32(int qtype, float* Y, const void* W, const float*
 
 #define AXF_MISC_DISPATCH(KERNEL, UNITS, ROWS, ...)                                        \
     do {                                                                                   \
-        const int l_ = misc_lpr(UNITS);                                                    \
+        const int l_ = misc_lpr_rows(UNITS, (long)(ROWS) * T);                            \
         if (l_ == 64) AXF_MISC_LAUNCH(KERNEL, 64, ROWS, __VA_ARGS__);                      \
         else if (l_ == 32) AXF_MISC_LAUNCH(KERNEL, 32, ROWS, __VA_ARGS__);                 \
         else AXF_MISC_LAUNCH(KERNEL, 16, ROWS, __VA_ARGS__);                               \
@@ -577,7 +588,8 @@ hipError_t launch_misc_norm_stage(const MiscMat* mats, int nmat, bool swiglu, co
             a.need_q8 |= mm.qtype == AXF_TYPE_Q8_0;
         }
     }
-    const int lpr = misc_mat_lpr(mats[0].qtype, n);
+    const int lpr = misc_lpr_rows(mats[0].qtype == AXF_TYPE_F16 ? n / 8 : n / 32,
+                                  swiglu ? 2L * mats[0].rows : total);
     const int R = kMiscThreads / lpr;
     const long wgs = swiglu ? (mats[0].rows + R / 2 - 1) / (R / 2) : (total + R - 1) / R;
     const size_t lds = (size_t)(n / 32) * (36 * sizeof(float) + (a.need_q8 ? Q8_0_BYTES : 0));
