@@ -706,6 +706,7 @@ int prefill_alloc(axf_llama* m) {
                 const size_t b = gemm_scratch_bytes(qt, GemmPath::Auto, t, kmax / QK_K, rmax);
                 if (b > gs) gs = b;
             }
+    if (gs < (size_t)cap * 8) gs = (size_t)cap * 8;  // the misc GEMM's row scales
     LL_TRY(dalloc(m, gs, &p));
     m->pf_gemm = static_cast<uint8_t*>(p);
     m->pf_cap = cap;
@@ -744,9 +745,11 @@ hipError_t gemm_rows_add(axf_llama* m, const DevW& w, float* Y, const uint8_t* x
 hipError_t gemm_any(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, const float* xf,
                     int rows, int T, int cols, hipStream_t st) {
     if (kquant(w.qtype)) return gemm_rows(m, w, Y, xq8, rows, T, cols, st);
-    // from 8 tokens: each weight block dequantised once per 16 or 32 tokens
+    // from 8 tokens: each weight block dequantised once per 16 or 32 tokens, from
+    // 16 on the matrix cores (row scales in the GEMM scratch)
     if (T >= 8)
-        return launch_gemm_misc_f32(w.qtype, Y, w.d, xf, rows, cols, (long)w.row_bytes, T, 0, st);
+        return launch_gemm_misc_f32(w.qtype, Y, w.d, xf, rows, cols, (long)w.row_bytes, T, 0, st,
+                                    reinterpret_cast<float*>(m->pf_gemm));
     if (w.qtype == AXF_TYPE_Q8_0)
         return launch_gemv_q8w_f32(Y, w.d, xf, rows, cols / 32, (long)w.row_bytes, st, 0, T);
     if (w.qtype == AXF_TYPE_Q5_0)

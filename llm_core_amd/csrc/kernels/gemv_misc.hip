@@ -466,6 +466,186 @@ __global__ __launch_bounds__(KS * 64) void k_gemm_misc_f32(
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same product on the matrix cores (v_mfma_f32_16x16x32_f16):
+//   Y[t][o] = sum_b d[o,b] * sum_k c[o,b,k] * x[t, 32b + k]
+// with the weight codes c (Q5_0: q5 - 16, Q8_0: q, F16: the stored weight and
+// d = 1) exact in fp16.  Token row t is scaled by a power of two 2^E_t
+// (k_row_pow2: max|x_t| * 2^E_t < 2^14) and each scaled value xs (exact) is
+// split as hi = fp16(xs), lo = fp16(xs - hi): hi + lo equals xs within ~2^-23
+// relative (values below 2^-3 of the row maximum lose low bits of lo only,
+// < 2^-37 of the maximum).  Per 32-weight block two MFMAs (A = hi, then lo;
+// B = the codes) give the block's sum in fp32, which is scaled by d (Q5_0,
+// Q8_0; F16 accumulates in the MFMA), and the result by 2^-E_t.  The sums
+// differ from the per-token GEMV's sequential fp32 sums in rounding only.
+// Tokens are A's rows and weight rows B's columns: a result lane holds tokens
+// 4g..4g+3 of one weight row, so d is the lane's own row's.  A wave owns RTW
+// row tiles x TTW token tiles (16 x 16 each); a workgroup 4 waves on
+// consecutive row tiles of one token group.
+// ---------------------------------------------------------------------------
+typedef _Float16 mh8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 mh2_t __attribute__((ext_vector_type(2)));
+typedef float mf4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t mu4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMmRTW = 2, kMmTTW = 2, kMmWaves = 4;
+constexpr int kMiscMfmaMinT = 16;  // tokens from which the matrix-core form runs
+
+// scale[t] = 2^E with max|x_t| * 2^E < 2^14, inv[t] = 2^-E (E in [-126, 126];
+// one wave per row)
+__global__ __launch_bounds__(256) void k_row_pow2(const float* __restrict__ X, int cols, int T,
+                                                  float* __restrict__ scale, float* __restrict__ inv) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= T) return;  // the whole wave
+    const float4* xr = reinterpret_cast<const float4*>(X + (size_t)t * cols);
+    uint32_t m = 0u;  // bits of max |x| (non-negative floats order as integers)
+    for (int i = lane; i < cols / 4; i += 64) {
+        const float4 v = xr[i];
+        m = max(m, max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
+                       max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu)));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+    // max < 2^(e - 126) for biased exponent e: E = 140 - e keeps it below 2^14
+    const int E = max(min(140 - (int)(m >> 23), 126), -126);
+    if (lane == 0) {
+        scale[t] = __uint_as_float((uint32_t)(E + 127) << 23);
+        inv[t] = __uint_as_float((uint32_t)(127 - E) << 23);
+    }
+}
+
+// fp16 pair (1024 + b0 - off, 1024 + b1 - off) of bytes b0, b1 of u picked by sel
+__device__ __forceinline__ uint32_t bytes_f16(uint32_t u, uint32_t sel, mh2_t off2) {
+    const uint32_t bits = __builtin_amdgcn_perm(0x64646464u, u, sel);
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(mh2_t, bits) + off2);  // exact
+}
+
+// the 8 codes of k-group g of block b of row wr as fp16 (B operand) and its d
+template <int QT>
+__device__ __forceinline__ mh8_t misc_codes(const uint8_t* __restrict__ wr, int b, int g, float& d) {
+    if constexpr (QT == 1) {  // F16: the stored halves
+        d = 1.f;
+        return __builtin_bit_cast(mh8_t, *reinterpret_cast<const mu4_t*>(wr + 64 * (long)b + 16 * g));
+    } else {
+        uint32_t q0, q1;  // 8 bytes: Q5_0 q5 in [0, 31], Q8_0 q + 128
+        const uint8_t* wb = wr + (long)b * (QT == 8 ? 34 : 22);
+        d = h2f(ld2(wb));
+        const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(wb) & 3u), s = 2u - sh;
+        if constexpr (QT == 8) {
+            // codes 8g..8g+7 = bytes 2+8g..9+8g: two aligned dwords from wb+8g+sh and
+            // the 16-bit word at wb+8+8g (used when sh = 0), all inside the block
+            const uint8_t* wa = wb + 8 * g + sh;
+            const uint32_t w0 = ld4(wa), w1 = ld4(wa + 4), w2 = ld2(wb + 8 + 8 * g);
+            q0 = alignbyte(w1, w0, s) ^ 0x80808080u;
+            q1 = alignbyte(w2, w1, s) ^ 0x80808080u;
+        } else {
+            // qh and qs from 5 aligned dwords at wb+sh and the word at wb+20
+            const uint8_t* wa = wb + sh;
+            uint32_t w[6];
+#pragma unroll
+            for (int k = 0; k < 5; k++) w[k] = ld4(wa + 4 * k);
+            w[5] = ld2(wb + 20);
+            const uint32_t qh = alignbyte(w[1], w[0], s);
+            // k-group g: nibbles (low for g < 2) of qs bytes 8(g&1)..8(g&1)+7, qh bits 8g..8g+7
+            const uint32_t qa = alignbyte(w[2 + 2 * (g & 1)], w[1 + 2 * (g & 1)], s);
+            const uint32_t qb = alignbyte(w[3 + 2 * (g & 1)], w[2 + 2 * (g & 1)], s);
+            const uint32_t ns = 4u * (uint32_t)(g >> 1), hb = qh >> (8 * g);
+            q0 = ((qa >> ns) & 0x0f0f0f0fu) | (spread4(hb & 0xfu) << 4);
+            q1 = ((qb >> ns) & 0x0f0f0f0fu) | (spread4((hb >> 4) & 0xfu) << 4);
+        }
+        // fp16 1024 + byte, minus 1024 + 16 (Q5_0) or 1024 + 128 (Q8_0): the code, exact
+        const _Float16 o = (_Float16)(QT == 8 ? -1152.f : -1040.f);
+        const mh2_t off2 = {o, o};
+        const mu4_t v = {bytes_f16(q0, 0x04010400u, off2), bytes_f16(q0, 0x04030402u, off2),
+                         bytes_f16(q1, 0x04010400u, off2), bytes_f16(q1, 0x04030402u, off2)};
+        return __builtin_bit_cast(mh8_t, v);
+    }
+}
+
+// hi and lo halves of 8 scaled values of x (A operand)
+__device__ __forceinline__ void split_hl(const float* __restrict__ xp, float sc, mh8_t& hi, mh8_t& lo) {
+    const float4 a = reinterpret_cast<const float4*>(xp)[0], b = reinterpret_cast<const float4*>(xp)[1];
+    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        float xs = v[e] * sc;  // exact: a power-of-two scale
+        // hi and lo from this one rounded value (no fusion of the multiply
+        // into a mixed-precision conversion for one of them)
+        asm volatile("" : "+v"(xs));
+        const _Float16 h = (_Float16)xs;
+        hi[e] = h;
+        lo[e] = (_Float16)(xs - (float)h);
+    }
+}
+
+template <int QT>
+__global__ __launch_bounds__(kMmWaves * 64) void k_gemm_misc_mfma(
+    float* __restrict__ Y, const uint8_t* __restrict__ W, const float* __restrict__ X,
+    const float* __restrict__ scale, const float* __restrict__ inv, int rows, int cols,
+    long row_bytes, int T, int accumulate) {
+    constexpr int RW = 16 * kMmRTW, TW = 16 * kMmTTW;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, g = lane >> 4;
+    const long row0 = ((long)blockIdx.x * kMmWaves + wave) * RW;
+    const int t0 = blockIdx.y * TW;
+    const uint8_t* wr[kMmRTW];
+#pragma unroll
+    for (int i = 0; i < kMmRTW; i++)
+        wr[i] = W + min(row0 + 16 * i + col, (long)rows - 1) * row_bytes;  // past the end: not stored
+    const float* xr[kMmTTW];
+    float sc[kMmTTW];
+#pragma unroll
+    for (int j = 0; j < kMmTTW; j++) {
+        const int t = min(t0 + 16 * j + col, T - 1);  // past T: not stored
+        xr[j] = X + (size_t)t * cols + 8 * g;
+        sc[j] = scale[t];
+    }
+    const mf4_t zero = {0.f, 0.f, 0.f, 0.f};
+    mf4_t acc[kMmRTW][kMmTTW];
+#pragma unroll
+    for (int i = 0; i < kMmRTW; i++)
+#pragma unroll
+        for (int j = 0; j < kMmTTW; j++) acc[i][j] = zero;
+    const int nb = cols / 32;
+    for (int b = 0; b < nb; b++) {
+        mh8_t ah[kMmTTW], al[kMmTTW], bw[kMmRTW];
+        float d[kMmRTW];
+#pragma unroll
+        for (int i = 0; i < kMmRTW; i++) bw[i] = misc_codes<QT>(wr[i], b, g, d[i]);
+#pragma unroll
+        for (int j = 0; j < kMmTTW; j++) split_hl(xr[j] + 32 * b, sc[j], ah[j], al[j]);
+#pragma unroll
+        for (int i = 0; i < kMmRTW; i++)
+#pragma unroll
+            for (int j = 0; j < kMmTTW; j++) {
+                if constexpr (QT == 1) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], bw[i], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j], bw[i], acc[i][j], 0, 0, 0);
+                } else {
+                    mf4_t c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], bw[i], zero, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j], bw[i], c, 0, 0, 0);
+#pragma unroll
+                    for (int ii = 0; ii < 4; ii++) acc[i][j][ii] = fmaf(d[i], c[ii], acc[i][j][ii]);
+                }
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < kMmRTW; i++) {
+        const long o = row0 + 16 * i + col;
+#pragma unroll
+        for (int j = 0; j < kMmTTW; j++)
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) {
+                const int t = t0 + 16 * j + 4 * g + ii;
+                if (o < rows && t < T) {
+                    const float v = acc[i][j][ii] * inv[t];
+                    float* y = Y + (size_t)t * rows + o;
+                    *y = accumulate ? *y + v : v;
+                }
+            }
+    }
+}
+
 template <int TT, int KS>
 hipError_t launch_gemm_misc_tt(int qtype, float* Y, const uint8_t* W, const float* X, int rows,
                                int cols, long row_bytes, int T, int accumulate, hipStream_t st) {
@@ -486,11 +666,31 @@ hipError_t launch_gemm_misc_tt(int qtype, float* Y, const uint8_t* W, const floa
 // token).  F16 rows must be 16-byte aligned (cols % 32 == 0 makes them so when
 // W is); 2-byte-aligned Q8_0 / Q5_0 blocks are read as 16-bit words.
 hipError_t launch_gemm_misc_f32(int qtype, float* Y, const void* W, const float* X, int rows,
-                                int cols, long row_bytes, int T, int accumulate, hipStream_t st) {
+                                int cols, long row_bytes, int T, int accumulate, hipStream_t st,
+                                float* scratch) {
     if (rows <= 0 || T <= 0 || cols <= 0 || cols % 32 || T > 65535 * 16) return hipErrorInvalidValue;
     if (qtype != 1 && qtype != 8 && qtype != 6) return hipErrorInvalidValue;
     if (qtype == 1 && (reinterpret_cast<uintptr_t>(W) & 15)) return hipErrorInvalidValue;
     const auto* w8 = static_cast<const uint8_t*>(W);
+    // the matrix cores where there is scratch for the row scales (2 T floats)
+    if (scratch && T >= kMiscMfmaMinT && (reinterpret_cast<uintptr_t>(X) & 15) == 0) {
+        float* sc = scratch;
+        float* iv = scratch + T;
+        hipLaunchKernelGGL(k_row_pow2, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, X, cols, T,
+                           sc, iv);
+        const dim3 grid((unsigned)((rows + 16 * kMmRTW * kMmWaves - 1) / (16 * kMmRTW * kMmWaves)),
+                        (unsigned)((T + 16 * kMmTTW - 1) / (16 * kMmTTW)));
+        if (qtype == 1)
+            hipLaunchKernelGGL(k_gemm_misc_mfma<1>, grid, dim3(kMmWaves * 64), 0, st, Y, w8, X, sc, iv,
+                               rows, cols, row_bytes, T, accumulate);
+        else if (qtype == 8)
+            hipLaunchKernelGGL(k_gemm_misc_mfma<8>, grid, dim3(kMmWaves * 64), 0, st, Y, w8, X, sc, iv,
+                               rows, cols, row_bytes, T, accumulate);
+        else
+            hipLaunchKernelGGL(k_gemm_misc_mfma<6>, grid, dim3(kMmWaves * 64), 0, st, Y, w8, X, sc, iv,
+                               rows, cols, row_bytes, T, accumulate);
+        return hipGetLastError();
+    }
     // waves = row groups x token groups x K ranges: 32 tokens per group and 4
     // K ranges where that gives 4096 waves (4 per SIMD) or K is under 16
     // blocks, else 16 tokens with 4, then 8 K ranges (a wave past the last

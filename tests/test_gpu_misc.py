@@ -104,6 +104,34 @@ def test_gemm_f32_rows(ctx, qtype, rows, cols, T):
     np.testing.assert_array_equal(got2, got + got)  # y + y: the accumulate adds the same sums
 
 
+@pytest.mark.parametrize("qtype", [AXF_TYPE_Q8_0, AXF_TYPE_Q5_0, AXF_TYPE_F16])
+def test_gemm_f32_rows_activation_scales(ctx, qtype):
+    """Token rows of very different magnitudes (1e-7 to 1e4, one row with a
+    single 3e4 outlier, one all-zero row): the matrix-core form scales each row
+    by its own power of two before the fp16 hi/lo split, so every row keeps
+    fp32-level relative accuracy (1e-5 of its own largest output)."""
+    rows, cols, T = 200, 896, 48
+    rng = np.random.default_rng(77 + qtype)
+    if qtype == AXF_TYPE_F16:
+        W = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float16)
+    else:
+        W = blocks(qtype, rows, cols, 91 + qtype)
+    mags = np.array([10.0 ** (k % 12 - 7) for k in range(T)], np.float32)
+    X = (rng.standard_normal((T, cols)) * mags[:, None]).astype(np.float32)
+    X[5, 17] = 3e4
+    X[9] = 0.0
+    rb = O.misc_row_bytes(qtype, cols)
+    dW, dX = ctx.upload(W), ctx.upload(X)
+    dY = ctx.upload(np.full(T * rows, np.nan, np.float32))
+    call("axf_hip_gemm_misc_f32", ctx.handle, qtype, dY.ptr, dW.ptr, dX.ptr, rows, T, cols, rb, 0)
+    got = ctx.download(dY, np.float32, T * rows).reshape(T, rows)
+    for t in range(T):
+        want = O.gemv_misc(qtype, W, X[t], rows, cols).astype(np.float64)
+        scale = float(np.max(np.abs(want)))
+        err = float(np.max(np.abs(got[t] - want)))
+        assert err <= 1e-5 * scale + (0.0 if scale else 0.0), f"token {t}: {err:.3e} of {scale:.3e}"
+
+
 def test_gemm_misc_rejects_bad_arguments(ctx):
     W, X, Y = ctx.alloc(1 << 16), ctx.alloc(1 << 16), ctx.alloc(1 << 16)
     with pytest.raises(AxfError, match="multiple of 32"):
