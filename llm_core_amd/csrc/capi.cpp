@@ -569,8 +569,8 @@ int axf_hip_gemm_misc_f32(axf_ctx* ctx, int qtype, float* Y, const void* W, cons
     if (qtype == AXF_TYPE_F16 && (row_bytes < (size_t)cols * 2 || row_bytes % 16))
         return fail(AXF_ERR_INVALID_ARG, std::string(fn) + ": F16 row_bytes must be >= 2*cols and a multiple of 16");
     if (!rows || !cols || !T) return AXF_OK;
-    void* scratch = nullptr;  // the matrix-core form's row scales
-    rc = ctx_scratch(ctx, (size_t)T * 8, &scratch);
+    void* scratch = nullptr;  // the matrix-core form's hi/lo rows
+    rc = ctx_scratch(ctx, gemm_misc_scratch_bytes(T, cols), &scratch);
     if (rc) return rc;
     AXF_HIP(launch_gemm_misc_f32(qtype, Y, W, X, rows, cols, (long)row_bytes, T, accumulate ? 1 : 0,
                                  ctx->stream, static_cast<float*>(scratch)));

@@ -134,11 +134,16 @@ hipError_t launch_gemv_f16_f32(float* y, const void* W, const float* x, const fl
                                int rows, int cols, hipStream_t st, int accumulate = 0, int T = 1);
 // T fp32 token rows (Y token-major) through Q8_0 (8), Q5_0 (6) or F16 (1)
 // weights (the batched prefill's gemm_wt_q8 fallback): from 16 tokens with
-// scratch (2 T floats, 16-byte aligned X) on the matrix cores, else each
-// weight block dequantised once per 16 or 32 tokens on the VALU
+// scratch (gemm_misc_scratch_bytes; 16-byte aligned X) on the matrix cores,
+// else each weight block dequantised once per 16 or 32 tokens on the VALU
 hipError_t launch_gemm_misc_f32(int qtype, float* Y, const void* W, const float* X, int rows,
                                 int cols, long row_bytes, int T, int accumulate, hipStream_t st,
-                                float* scratch = nullptr);
+                                float* scratch = nullptr, bool prepared = false);
+size_t gemm_misc_scratch_bytes(int T, int cols);
+// The matrix-core form runs (given scratch); its prepared activation rows in
+// the scratch stay valid for further calls on the same X and cols (prepared =
+// true) until the scratch is written otherwise.
+bool gemm_misc_mfma_applies(int T, const float* X);
 hipError_t launch_embed_misc(int qtype, float* out, const void* W, const int* tok_dev, int tok,
                              int T, int cols, long row_bytes, hipStream_t st);
 // A decode stage of Q8_0 / Q5_0 / F16 matrices in one launch: RMSNorm(x) * nw

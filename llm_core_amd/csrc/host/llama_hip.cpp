@@ -706,7 +706,10 @@ int prefill_alloc(axf_llama* m) {
                 const size_t b = gemm_scratch_bytes(qt, GemmPath::Auto, t, kmax / QK_K, rmax);
                 if (b > gs) gs = b;
             }
-    if (gs < (size_t)cap * 8) gs = (size_t)cap * 8;  // the misc GEMM's row scales
+    {  // the misc GEMM's hi/lo rows
+        const size_t ms = gemm_misc_scratch_bytes(cap, kmax > qo ? kmax : qo);
+        if (gs < ms) gs = ms;
+    }
     LL_TRY(dalloc(m, gs, &p));
     m->pf_gemm = static_cast<uint8_t*>(p);
     m->pf_cap = cap;
@@ -739,22 +742,46 @@ hipError_t gemm_rows_add(axf_llama* m, const DevW& w, float* Y, const uint8_t* x
     return launch_add(Y, Y, tmp, T * rows, st);
 }
 
-// Y[T][rows] by gemm_wt_q8's dispatch (llama_model.cpp:837-879): Q4_K and Q6_K
-// on the Q8_0 rows; every other type, Q8_0 included (the batched path has no
-// Q8_0 branch), on the fp32 rows XF through gemv_wt per token (:876-879).
+// Y[T][rows] (+)= W rows by gemm_wt_q8's dispatch (llama_model.cpp:837-879):
+// Q4_K and Q6_K on the Q8_0 rows; every other type, Q8_0 included (the batched
+// path has no Q8_0 branch), on the fp32 rows XF through gemv_wt per token
+// (:876-879).  xf_ready (optional): whether the GEMM scratch holds XF's
+// prepared rows for the matrix-core misc GEMM, updated here; accumulate (misc
+// types only) adds to Y.
 hipError_t gemm_any(axf_llama* m, const DevW& w, float* Y, const uint8_t* xq8, const float* xf,
-                    int rows, int T, int cols, hipStream_t st) {
-    if (kquant(w.qtype)) return gemm_rows(m, w, Y, xq8, rows, T, cols, st);
+                    int rows, int T, int cols, hipStream_t st, bool* xf_ready = nullptr,
+                    int accumulate = 0) {
+    if (kquant(w.qtype)) {
+        if (xf_ready) *xf_ready = false;  // the K-quant GEMMs use the scratch
+        return gemm_rows(m, w, Y, xq8, rows, T, cols, st);
+    }
     // from 8 tokens: each weight block dequantised once per 16 or 32 tokens, from
-    // 16 on the matrix cores (row scales in the GEMM scratch)
-    if (T >= 8)
-        return launch_gemm_misc_f32(w.qtype, Y, w.d, xf, rows, cols, (long)w.row_bytes, T, 0, st,
-                                    reinterpret_cast<float*>(m->pf_gemm));
+    // 16 on the matrix cores (XF's prepared rows in the GEMM scratch)
+    if (T >= 8) {
+        const hipError_t e = launch_gemm_misc_f32(w.qtype, Y, w.d, xf, rows, cols, (long)w.row_bytes,
+                                                  T, accumulate, st,
+                                                  reinterpret_cast<float*>(m->pf_gemm),
+                                                  xf_ready && *xf_ready);
+        if (xf_ready && gemm_misc_mfma_applies(T, xf)) *xf_ready = true;
+        return e;
+    }
+    if (accumulate) return hipErrorInvalidValue;
     if (w.qtype == AXF_TYPE_Q8_0)
         return launch_gemv_q8w_f32(Y, w.d, xf, rows, cols / 32, (long)w.row_bytes, st, 0, T);
     if (w.qtype == AXF_TYPE_Q5_0)
         return launch_gemv_q5_0_f32(Y, w.d, xf, rows, cols / 32, (long)w.row_bytes, st, 0, T);
     return launch_gemv_f16_f32(Y, w.d, xf, nullptr, rows, cols, st, 0, T);
+}
+
+// x += W rows for a residual projection of another type: from 8 tokens the
+// misc GEMM adds into x itself (the same fp32 add as k_add), below that the
+// per-token GEMV writes pf_tmp and k_add follows.
+hipError_t gemm_misc_add(axf_llama* m, const DevW& w, float* x, const uint8_t* xq8,
+                         const float* xf, int rows, int T, int cols, hipStream_t st) {
+    if (T >= 8) return gemm_any(m, w, x, xq8, xf, rows, T, cols, st, nullptr, 1);
+    const hipError_t e = gemm_any(m, w, m->pf_tmp, xq8, xf, rows, T, cols, st);
+    if (e != hipSuccess) return e;
+    return launch_add(x, x, m->pf_tmp, T * rows, st);
 }
 
 hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
@@ -772,6 +799,7 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     const bool f_qkv = !kquant(L.wq.qtype) || !kquant(L.wk.qtype) || !kquant(L.wv.qtype);
     ST(launch_rmsnorm_rows(f_qkv ? m->pf_xb : nullptr, m->pf_q8, m->pf_x, L.attn_norm, E,
                            hp.rms_eps, T, st));
+    bool xb_ready = false;  // the GEMM scratch holds pf_xb's prepared rows (misc types)
     float* q = m->pf_qk;
     float* k;
     int q_ld, k_ld;
@@ -783,10 +811,10 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
         k = q + (size_t)T * qo;
         q_ld = qo;
         k_ld = kvo;
-        ST(gemm_any(m, L.wq, q, m->pf_q8, m->pf_xb, qo, T, E, st));
-        ST(gemm_any(m, L.wk, k, m->pf_q8, m->pf_xb, kvo, T, E, st));
+        ST(gemm_any(m, L.wq, q, m->pf_q8, m->pf_xb, qo, T, E, st, &xb_ready));
+        ST(gemm_any(m, L.wk, k, m->pf_q8, m->pf_xb, kvo, T, E, st, &xb_ready));
     }
-    ST(gemm_any(m, L.wv, m->pf_v, m->pf_q8, m->pf_xb, kvo, T, E, st));
+    ST(gemm_any(m, L.wv, m->pf_v, m->pf_q8, m->pf_xb, kvo, T, E, st, &xb_ready));
     // K, V rows into the cache, then attention of every row -> Q8_0
     const bool qkn = hp.qk_norm_order != 0;
     if (qkn) {  // per-head q/k norms: q rows finished in place, K/V rows stored
@@ -843,8 +871,7 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     if (kquant(L.wo.qtype)) {
         ST(gemm_rows_add(m, L.wo, m->pf_x, m->pf_q8, E, T, qo, m->pf_tmp, st));
     } else {
-        ST(gemm_any(m, L.wo, m->pf_tmp, m->pf_q8, m->pf_ao, E, T, qo, st));
-        ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
+        ST(gemm_misc_add(m, L.wo, m->pf_x, m->pf_q8, m->pf_ao, E, T, qo, st));
     }
     // SwiGLU(gate, up) of RMSNorm(x) * ffn_norm -> Q8_0 (and fp32 rows of h
     // where the down projection is of another type)
@@ -852,13 +879,15 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     const bool f_down = !kquant(L.wdown.qtype);
     ST(launch_rmsnorm_rows(f_gu ? m->pf_xb : nullptr, m->pf_q8, m->pf_x, L.ffn_norm, E,
                            hp.rms_eps, T, st));
+    xb_ready = false;
     if (L.gu_interleaved) {
         ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, 2 * FD, T, E, st));
         const int B = qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2;
         ST(launch_swiglu_gu(m->pf_q8, m->pf_gu, T, FD, B, st, f_down ? m->pf_h : nullptr));
     } else {
-        ST(gemm_any(m, L.wgate, m->pf_gu, m->pf_q8, m->pf_xb, FD, T, E, st));
-        ST(gemm_any(m, L.wup, m->pf_gu + (size_t)T * FD, m->pf_q8, m->pf_xb, FD, T, E, st));
+        ST(gemm_any(m, L.wgate, m->pf_gu, m->pf_q8, m->pf_xb, FD, T, E, st, &xb_ready));
+        ST(gemm_any(m, L.wup, m->pf_gu + (size_t)T * FD, m->pf_q8, m->pf_xb, FD, T, E, st,
+                    &xb_ready));
         ST(launch_swiglu(f_down ? m->pf_h : nullptr, m->pf_q8, m->pf_gu,
                          m->pf_gu + (size_t)T * FD, T * FD, st));
     }
@@ -866,8 +895,7 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     if (kquant(L.wdown.qtype)) {
         ST(gemm_rows_add(m, L.wdown, m->pf_x, m->pf_q8, E, T, FD, m->pf_tmp, st));
     } else {
-        ST(gemm_any(m, L.wdown, m->pf_tmp, m->pf_q8, m->pf_h, E, T, FD, st));
-        ST(launch_add(m->pf_x, m->pf_x, m->pf_tmp, T * E, st));
+        ST(gemm_misc_add(m, L.wdown, m->pf_x, m->pf_q8, m->pf_h, E, T, FD, st));
     }
 #undef ST
     return hipSuccess;

@@ -471,8 +471,8 @@ __global__ __launch_bounds__(KS * 64) void k_gemm_misc_f32(
 //   Y[t][o] = sum_b d[o,b] * sum_k c[o,b,k] * x[t, 32b + k]
 // with the weight codes c (Q5_0: q5 - 16, Q8_0: q, F16: the stored weight and
 // d = 1) exact in fp16.  Token row t is scaled by a power of two 2^E_t
-// (k_row_pow2: max|x_t| * 2^E_t < 2^14) and each scaled value xs (exact) is
-// split as hi = fp16(xs), lo = fp16(xs - hi): hi + lo equals xs within ~2^-23
+// (max|x_t| * 2^E_t < 2^14) and each scaled value xs (exact) is split as
+// hi = fp16(xs), lo = fp16(xs - hi), once per call (k_prep_hl_rows): hi + lo equals xs within ~2^-23
 // relative (values below 2^-3 of the row maximum lose low bits of lo only,
 // < 2^-37 of the maximum).  Per 32-weight block two MFMAs (A = hi, then lo;
 // B = the codes) give the block's sum in fp32, which is scaled by d (Q5_0,
@@ -491,26 +491,60 @@ typedef uint32_t mu4_t __attribute__((ext_vector_type(4)));
 constexpr int kMmRTW = 2, kMmTTW = 2, kMmWaves = 4;
 constexpr int kMiscMfmaMinT = 16;  // tokens from which the matrix-core form runs
 
-// scale[t] = 2^E with max|x_t| * 2^E < 2^14, inv[t] = 2^-E (E in [-126, 126];
-// one wave per row)
-__global__ __launch_bounds__(256) void k_row_pow2(const float* __restrict__ X, int cols, int T,
-                                                  float* __restrict__ scale, float* __restrict__ inv) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (t >= T) return;  // the whole wave
-    const float4* xr = reinterpret_cast<const float4*>(X + (size_t)t * cols);
-    uint32_t m = 0u;  // bits of max |x| (non-negative floats order as integers)
-    for (int i = lane; i < cols / 4; i += 64) {
-        const float4 v = xr[i];
-        m = max(m, max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
-                       max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu)));
-    }
+// The A operand of k_gemm_misc_mfma, once per activation: token row t is
+// scaled by 2^E_t (max|x_t| * 2^E_t < 2^14, E_t in [-126, 126]) and each group
+// of 8 values u = 4b + g (block b, k-group g) stored as 8 fp16 hi then 8 fp16
+// lo at xhl[(u * T + t) * 32 bytes]; inv[t] = 2^-E_t.  A workgroup takes 4
+// tokens: each wave finds one row's maximum, then the 256 threads convert
+// with the token fastest (128 contiguous bytes per group).
+__global__ __launch_bounds__(256) void k_prep_hl_rows(const float* __restrict__ X, int cols, int T,
+                                                      uint8_t* __restrict__ xhl,
+                                                      float* __restrict__ inv) {
+    __shared__ float scl[4];
+    const int t0 = blockIdx.x * 4, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    {
+        const int t = t0 + wave;
+        uint32_t m = 0u;  // bits of max |x| (non-negative floats order as integers)
+        if (t < T) {
+            const float4* xr = reinterpret_cast<const float4*>(X + (size_t)t * cols);
+            for (int k = lane; k < cols / 4; k += 64) {
+                const float4 v = xr[k];
+                m = max(m, max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
+                               max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu)));
+            }
+        }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
-    // max < 2^(e - 126) for biased exponent e: E = 140 - e keeps it below 2^14
-    const int E = max(min(140 - (int)(m >> 23), 126), -126);
-    if (lane == 0) {
-        scale[t] = __uint_as_float((uint32_t)(E + 127) << 23);
-        inv[t] = __uint_as_float((uint32_t)(127 - E) << 23);
+        for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+        // max < 2^(e - 126) for biased exponent e: E = 140 - e keeps it below 2^14
+        const int E = max(min(140 - (int)(m >> 23), 126), -126);
+        if (lane == 0) {
+            scl[wave] = __uint_as_float((uint32_t)(E + 127) << 23);
+            if (t < T) inv[t] = __uint_as_float((uint32_t)(127 - E) << 23);
+        }
+    }
+    __syncthreads();
+    const int tt = threadIdx.x & 3, t = t0 + tt;
+    if (t >= T) return;
+    const float sc = scl[tt];
+    const float* xr = X + (size_t)t * cols;
+    for (int u = threadIdx.x >> 2; u < cols / 8; u += 64) {
+        const float4 a = reinterpret_cast<const float4*>(xr + 8 * u)[0];
+        const float4 b = reinterpret_cast<const float4*>(xr + 8 * u)[1];
+        float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        mh8_t hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float xs = v[e] * sc;  // exact: a power-of-two scale
+            // hi and lo from this one rounded value (no fusion of the multiply
+            // into a mixed-precision conversion for one of them)
+            asm volatile("" : "+v"(xs));
+            const _Float16 h = (_Float16)xs;
+            hi[e] = h;
+            lo[e] = (_Float16)(xs - (float)h);
+        }
+        uint8_t* p = xhl + ((size_t)u * T + t) * 32;
+        *reinterpret_cast<mh8_t*>(p) = hi;
+        *reinterpret_cast<mh8_t*>(p + 16) = lo;
     }
 }
 
@@ -520,35 +554,61 @@ __device__ __forceinline__ uint32_t bytes_f16(uint32_t u, uint32_t sel, mh2_t of
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(mh2_t, bits) + off2);  // exact
 }
 
-// the 8 codes of k-group g of block b of row wr as fp16 (B operand) and its d
+// The raw words of k-group g of block b of a weight row (loaded one block
+// ahead of their use), then the 8 codes as fp16 (B operand) and d.
+//   F16: the 16 bytes of the 8 halves;
+//   Q8_0: d, two aligned dwords from wb + 8g + sh (sh = wb & 3) and the 16-bit
+//         word at wb + 8 + 8g (codes 8g..8g+7 = bytes 2+8g..9+8g);
+//   Q5_0: d, 5 aligned dwords from wb + sh and the word at wb + 20 (qh, qs).
+// Every byte read lies inside the block.
+struct MiscRaw {
+    uint32_t w[6];
+    uint32_t d;   // fp16 bits of d
+    uint32_t sh;  // wb & 3 (0 or 2)
+};
+
 template <int QT>
-__device__ __forceinline__ mh8_t misc_codes(const uint8_t* __restrict__ wr, int b, int g, float& d) {
-    if constexpr (QT == 1) {  // F16: the stored halves
+__device__ __forceinline__ void misc_load(const uint8_t* __restrict__ wr, int b, int g, MiscRaw& r) {
+    if constexpr (QT == 1) {
+        const uint4 v = *reinterpret_cast<const uint4*>(wr + 64 * (long)b + 16 * g);
+        r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+    } else {
+        const uint8_t* wb = wr + (long)b * (QT == 8 ? 34 : 22);
+        r.d = ld2(wb);
+        r.sh = (uint32_t)(reinterpret_cast<uintptr_t>(wb) & 3u);
+        if constexpr (QT == 8) {
+            const uint8_t* wa = wb + 8 * g + r.sh;
+            r.w[0] = ld4(wa);
+            r.w[1] = ld4(wa + 4);
+            r.w[2] = ld2(wb + 8 + 8 * g);
+        } else {
+            const uint8_t* wa = wb + r.sh;
+#pragma unroll
+            for (int k = 0; k < 5; k++) r.w[k] = ld4(wa + 4 * k);
+            r.w[5] = ld2(wb + 20);
+        }
+    }
+}
+
+template <int QT>
+__device__ __forceinline__ mh8_t misc_decode(const MiscRaw& r, int g, float& d) {
+    if constexpr (QT == 1) {
         d = 1.f;
-        return __builtin_bit_cast(mh8_t, *reinterpret_cast<const mu4_t*>(wr + 64 * (long)b + 16 * g));
+        const mu4_t v = {r.w[0], r.w[1], r.w[2], r.w[3]};
+        return __builtin_bit_cast(mh8_t, v);
     } else {
         uint32_t q0, q1;  // 8 bytes: Q5_0 q5 in [0, 31], Q8_0 q + 128
-        const uint8_t* wb = wr + (long)b * (QT == 8 ? 34 : 22);
-        d = h2f(ld2(wb));
-        const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(wb) & 3u), s = 2u - sh;
+        d = h2f(r.d);
+        const uint32_t s = 2u - r.sh;
         if constexpr (QT == 8) {
-            // codes 8g..8g+7 = bytes 2+8g..9+8g: two aligned dwords from wb+8g+sh and
-            // the 16-bit word at wb+8+8g (used when sh = 0), all inside the block
-            const uint8_t* wa = wb + 8 * g + sh;
-            const uint32_t w0 = ld4(wa), w1 = ld4(wa + 4), w2 = ld2(wb + 8 + 8 * g);
-            q0 = alignbyte(w1, w0, s) ^ 0x80808080u;
-            q1 = alignbyte(w2, w1, s) ^ 0x80808080u;
+            q0 = alignbyte(r.w[1], r.w[0], s) ^ 0x80808080u;
+            q1 = alignbyte(r.w[2], r.w[1], s) ^ 0x80808080u;
         } else {
-            // qh and qs from 5 aligned dwords at wb+sh and the word at wb+20
-            const uint8_t* wa = wb + sh;
-            uint32_t w[6];
-#pragma unroll
-            for (int k = 0; k < 5; k++) w[k] = ld4(wa + 4 * k);
-            w[5] = ld2(wb + 20);
-            const uint32_t qh = alignbyte(w[1], w[0], s);
+            const uint32_t qh = alignbyte(r.w[1], r.w[0], s);
             // k-group g: nibbles (low for g < 2) of qs bytes 8(g&1)..8(g&1)+7, qh bits 8g..8g+7
-            const uint32_t qa = alignbyte(w[2 + 2 * (g & 1)], w[1 + 2 * (g & 1)], s);
-            const uint32_t qb = alignbyte(w[3 + 2 * (g & 1)], w[2 + 2 * (g & 1)], s);
+            const int o = 2 * (g & 1);
+            const uint32_t qa = alignbyte(o ? r.w[4] : r.w[2], o ? r.w[3] : r.w[1], s);
+            const uint32_t qb = alignbyte(o ? r.w[5] : r.w[3], o ? r.w[4] : r.w[2], s);
             const uint32_t ns = 4u * (uint32_t)(g >> 1), hb = qh >> (8 * g);
             q0 = ((qa >> ns) & 0x0f0f0f0fu) | (spread4(hb & 0xfu) << 4);
             q1 = ((qb >> ns) & 0x0f0f0f0fu) | (spread4((hb >> 4) & 0xfu) << 4);
@@ -562,43 +622,31 @@ __device__ __forceinline__ mh8_t misc_codes(const uint8_t* __restrict__ wr, int 
     }
 }
 
-// hi and lo halves of 8 scaled values of x (A operand)
-__device__ __forceinline__ void split_hl(const float* __restrict__ xp, float sc, mh8_t& hi, mh8_t& lo) {
-    const float4 a = reinterpret_cast<const float4*>(xp)[0], b = reinterpret_cast<const float4*>(xp)[1];
-    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        float xs = v[e] * sc;  // exact: a power-of-two scale
-        // hi and lo from this one rounded value (no fusion of the multiply
-        // into a mixed-precision conversion for one of them)
-        asm volatile("" : "+v"(xs));
-        const _Float16 h = (_Float16)xs;
-        hi[e] = h;
-        lo[e] = (_Float16)(xs - (float)h);
-    }
-}
-
-template <int QT>
+// KS waves of a workgroup split K (contiguous block ranges, partial tiles added
+// in wave order through LDS) and kMmWaves / KS waves take consecutive row
+// groups; the block loop loads block b + 1 before computing block b.
+template <int QT, int KS>
 __global__ __launch_bounds__(kMmWaves * 64) void k_gemm_misc_mfma(
-    float* __restrict__ Y, const uint8_t* __restrict__ W, const float* __restrict__ X,
-    const float* __restrict__ scale, const float* __restrict__ inv, int rows, int cols,
-    long row_bytes, int T, int accumulate) {
-    constexpr int RW = 16 * kMmRTW, TW = 16 * kMmTTW;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ xhl,
+    const float* __restrict__ inv, int rows, int cols, long row_bytes, int T, int accumulate) {
+    constexpr int RW = 16 * kMmRTW, TW = 16 * kMmTTW, RG = kMmWaves / KS;
+    static_assert(RG * KS == kMmWaves, "waves");
+    __shared__ mf4_t part[KS > 1 ? KS - 1 : 1][RG][kMmRTW * kMmTTW][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ks = wave / RG, rg = wave % RG;
     const int col = lane & 15, g = lane >> 4;
-    const long row0 = ((long)blockIdx.x * kMmWaves + wave) * RW;
+    const long row0 = ((long)blockIdx.x * RG + rg) * RW;
     const int t0 = blockIdx.y * TW;
     const uint8_t* wr[kMmRTW];
 #pragma unroll
     for (int i = 0; i < kMmRTW; i++)
         wr[i] = W + min(row0 + 16 * i + col, (long)rows - 1) * row_bytes;  // past the end: not stored
-    const float* xr[kMmTTW];
-    float sc[kMmTTW];
+    const uint8_t* xr[kMmTTW];  // this lane's token: group u = 4b + g at xr + u*T*32
 #pragma unroll
     for (int j = 0; j < kMmTTW; j++) {
         const int t = min(t0 + 16 * j + col, T - 1);  // past T: not stored
-        xr[j] = X + (size_t)t * cols + 8 * g;
-        sc[j] = scale[t];
+        xr[j] = xhl + ((size_t)g * T + t) * 32;
     }
     const mf4_t zero = {0.f, 0.f, 0.f, 0.f};
     mf4_t acc[kMmRTW][kMmTTW];
@@ -606,14 +654,33 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_gemm_misc_mfma(
     for (int i = 0; i < kMmRTW; i++)
 #pragma unroll
         for (int j = 0; j < kMmTTW; j++) acc[i][j] = zero;
-    const int nb = cols / 32;
-    for (int b = 0; b < nb; b++) {
+    const int nb = cols / 32, nbq = (nb + KS - 1) / KS;
+    const int b0 = ks * nbq, b1 = min(nb, b0 + nbq);
+    MiscRaw raw[kMmRTW];
+    mh8_t xh[kMmTTW], xl[kMmTTW];
+    auto load = [&](int b) {
+        const int bb = min(b, nb - 1);  // past the range: a valid block, unused
+#pragma unroll
+        for (int i = 0; i < kMmRTW; i++) misc_load<QT>(wr[i], bb, g, raw[i]);
+#pragma unroll
+        for (int j = 0; j < kMmTTW; j++) {
+            const uint8_t* p = xr[j] + (size_t)bb * 4 * T * 32;
+            xh[j] = *reinterpret_cast<const mh8_t*>(p);
+            xl[j] = *reinterpret_cast<const mh8_t*>(p + 16);
+        }
+    };
+    if (b0 < b1) load(b0);
+    for (int b = b0; b < b1; b++) {
         mh8_t ah[kMmTTW], al[kMmTTW], bw[kMmRTW];
         float d[kMmRTW];
 #pragma unroll
-        for (int i = 0; i < kMmRTW; i++) bw[i] = misc_codes<QT>(wr[i], b, g, d[i]);
+        for (int i = 0; i < kMmRTW; i++) bw[i] = misc_decode<QT>(raw[i], g, d[i]);
 #pragma unroll
-        for (int j = 0; j < kMmTTW; j++) split_hl(xr[j] + 32 * b, sc[j], ah[j], al[j]);
+        for (int j = 0; j < kMmTTW; j++) {
+            ah[j] = xh[j];
+            al[j] = xl[j];
+        }
+        if (b + 1 < b1) load(b + 1);  // in flight during this block's products
 #pragma unroll
         for (int i = 0; i < kMmRTW; i++)
 #pragma unroll
@@ -628,6 +695,23 @@ __global__ __launch_bounds__(kMmWaves * 64) void k_gemm_misc_mfma(
                     for (int ii = 0; ii < 4; ii++) acc[i][j][ii] = fmaf(d[i], c[ii], acc[i][j][ii]);
                 }
             }
+    }
+    if constexpr (KS > 1) {
+        // partial tiles of K ranges 1..KS-1 through LDS, added to range 0's in order
+        if (ks > 0) {
+#pragma unroll
+            for (int i = 0; i < kMmRTW; i++)
+#pragma unroll
+                for (int j = 0; j < kMmTTW; j++) part[ks - 1][rg][i * kMmTTW + j][lane] = acc[i][j];
+        }
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int q = 0; q < KS - 1; q++)
+#pragma unroll
+            for (int i = 0; i < kMmRTW; i++)
+#pragma unroll
+                for (int j = 0; j < kMmTTW; j++) acc[i][j] += part[q][rg][i * kMmTTW + j][lane];
     }
 #pragma unroll
     for (int i = 0; i < kMmRTW; i++) {
@@ -665,30 +749,44 @@ hipError_t launch_gemm_misc_tt(int qtype, float* Y, const uint8_t* W, const floa
 // Y (+)= W x^T for T fp32 token rows of cols (Y token-major, rows floats per
 // token).  F16 rows must be 16-byte aligned (cols % 32 == 0 makes them so when
 // W is); 2-byte-aligned Q8_0 / Q5_0 blocks are read as 16-bit words.
+size_t gemm_misc_scratch_bytes(int T, int cols) {
+    return (size_t)(T + 3) / 4 * 16 + (size_t)T * cols * 4;  // inv, then hi/lo fp16 rows
+}
+
+bool gemm_misc_mfma_applies(int T, const float* X) {
+    return T >= kMiscMfmaMinT && (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+}
+
 hipError_t launch_gemm_misc_f32(int qtype, float* Y, const void* W, const float* X, int rows,
                                 int cols, long row_bytes, int T, int accumulate, hipStream_t st,
-                                float* scratch) {
+                                float* scratch, bool prepared) {
     if (rows <= 0 || T <= 0 || cols <= 0 || cols % 32 || T > 65535 * 16) return hipErrorInvalidValue;
     if (qtype != 1 && qtype != 8 && qtype != 6) return hipErrorInvalidValue;
     if (qtype == 1 && (reinterpret_cast<uintptr_t>(W) & 15)) return hipErrorInvalidValue;
     const auto* w8 = static_cast<const uint8_t*>(W);
     // the matrix cores where there is scratch for the row scales (2 T floats)
-    if (scratch && T >= kMiscMfmaMinT && (reinterpret_cast<uintptr_t>(X) & 15) == 0) {
-        float* sc = scratch;
-        float* iv = scratch + T;
-        hipLaunchKernelGGL(k_row_pow2, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, X, cols, T,
-                           sc, iv);
-        const dim3 grid((unsigned)((rows + 16 * kMmRTW * kMmWaves - 1) / (16 * kMmRTW * kMmWaves)),
-                        (unsigned)((T + 16 * kMmTTW - 1) / (16 * kMmTTW)));
-        if (qtype == 1)
-            hipLaunchKernelGGL(k_gemm_misc_mfma<1>, grid, dim3(kMmWaves * 64), 0, st, Y, w8, X, sc, iv,
-                               rows, cols, row_bytes, T, accumulate);
-        else if (qtype == 8)
-            hipLaunchKernelGGL(k_gemm_misc_mfma<8>, grid, dim3(kMmWaves * 64), 0, st, Y, w8, X, sc, iv,
-                               rows, cols, row_bytes, T, accumulate);
-        else
-            hipLaunchKernelGGL(k_gemm_misc_mfma<6>, grid, dim3(kMmWaves * 64), 0, st, Y, w8, X, sc, iv,
-                               rows, cols, row_bytes, T, accumulate);
+    if (scratch && gemm_misc_mfma_applies(T, X)) {
+        float* iv = scratch;
+        auto* xhl = reinterpret_cast<uint8_t*>(scratch + (T + 3) / 4 * 4);  // 16-byte aligned
+        if (!prepared)
+            hipLaunchKernelGGL(k_prep_hl_rows, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, X,
+                               cols, T, xhl, iv);
+        // K split over the workgroup's waves where the row groups x token groups
+        // leave fewer than 2048 workgroups (K ranges of at least 4 blocks)
+        const long tg = (T + 16 * kMmTTW - 1) / (16 * kMmTTW), nb = cols / 32;
+        auto wgs = [&](int ks) { return (rows + 16L * kMmRTW * (kMmWaves / ks) - 1) / (16L * kMmRTW * (kMmWaves / ks)) * tg; };
+        int ks = 1;
+        while (ks < kMmWaves && wgs(ks) < 2048 && nb >= 8L * ks) ks *= 2;
+        const dim3 grid((unsigned)(wgs(ks) / tg), (unsigned)tg);
+#define AXF_MM(QT_, KS_) \
+    hipLaunchKernelGGL((k_gemm_misc_mfma<QT_, KS_>), grid, dim3(kMmWaves * 64), 0, st, Y, w8, xhl, iv, rows, cols, row_bytes, T, accumulate)
+#define AXF_MM_KS(QT_) \
+    do { if (ks == 4) AXF_MM(QT_, 4); else if (ks == 2) AXF_MM(QT_, 2); else AXF_MM(QT_, 1); } while (0)
+        if (qtype == 1) AXF_MM_KS(1);
+        else if (qtype == 8) AXF_MM_KS(8);
+        else AXF_MM_KS(6);
+#undef AXF_MM_KS
+#undef AXF_MM
         return hipGetLastError();
     }
     // waves = row groups x token groups x K ranges: 32 tokens per group and 4
