@@ -488,7 +488,10 @@ typedef _Float16 mh2_t __attribute__((ext_vector_type(2)));
 typedef float mf4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t mu4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kMmRTW = 2, kMmTTW = 2, kMmWaves = 4;
+// wave tile 16 rows x 64 tokens: the Qwen2.5-0.5B-shape 512-token prefill
+// 6.60 ms against 6.79 (1 x 8 token tiles), 6.76 (2 x 4), 7.17 (2 x 2),
+// 7.32 (1 x 2), 7.83 (4 x 2), 8.98 (2 x 1), 9.59 (4 x 4), 11.0 ms (8 x 2)
+constexpr int kMmRTW = 1, kMmTTW = 4, kMmWaves = 4;
 constexpr int kMiscMfmaMinT = 16;  // tokens from which the matrix-core form runs
 
 // The A operand of k_gemm_misc_mfma, once per activation: token row t is
