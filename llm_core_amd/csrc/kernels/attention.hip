@@ -632,12 +632,213 @@ __global__ __launch_bounds__(256) void k_attn_prefill(AttnArgs a, int G, int QT)
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same attention with the keys split over the workgroup's waves (head
+// dimensions 64 and 128): a workgroup owns 16 query rows of one kv head (QT =
+// 16 / G tokens x the G query heads that share it) and its 4 waves take the
+// 16-key tiles kt = wave, wave + 4, ... of keys 0 .. (its last token's
+// position), each with its own online softmax state (running max m, sum l, O),
+// merged at the end in wave order through LDS.  Per tile, straight from the
+// cache into registers (no LDS staging):
+//   S^T = K Q^T   v_mfma_f32_16x16x4_f32, A = 16 keys (lane: key col, dims
+//                 grp*HD/4 .. +HD/4, contiguous), B = the 16 query rows (same
+//                 dims); result lane: keys 4*grp + r of query col;
+//   O^T += V^T P^T  A = V (lane: keys 4*grp + r, dims col*HD/16 .. +HD/16),
+//                 B = P as the S^T result lane holds it (no transpose);
+//                 result lane: dims (4*grp + r)*HD/16 + dt of query col.
+// So the max over a tile's 16 keys is 4 values in the lane and two shuffles;
+// l stays per lane until the merge.  Four times the workgroups of the 64-row
+// kernel, longest key ranges first.  fp32 throughout; results differ from the
+// per-token softmax only in summation order.
+// ---------------------------------------------------------------------------
+constexpr int kPfKsRows = 16;
+constexpr int kPfKsWaves = 4;
+
+template <int HD>
+__global__ __launch_bounds__(kPfKsWaves * 64) void k_attn_prefill_ks(AttnArgs a, int G, int QT) {
+    constexpr int KQ = HD / 4;   // dims per lane group: the k-steps of S^T
+    constexpr int DT = HD / 16;  // dims per lane of a V row: the output tiles
+    constexpr int HALF = HD / 2;
+    constexpr int QS = HD + 4;   // LDS row stride (Q tile, then the waves' O rows)
+    constexpr int R = kPfKsRows, NW = kPfKsWaves;
+    __shared__ __attribute__((aligned(16))) float qs[NW * R * QS];
+    __shared__ float mm[NW][R], ll[NW][R];
+
+    const int kvh = blockIdx.x;
+    const int qt0 = (int)(gridDim.y - 1 - blockIdx.y) * QT;  // longest key ranges first
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+    const int pos0 = a.pos_dev ? *a.pos_dev : a.pos;
+    const int n_tok = a.n_tok > 1 ? a.n_tok : 1;
+    const int t_end = min(qt0 + QT, n_tok);
+    const int kmax = pos0 + t_end - 1;  // last key any row attends to
+    const size_t kve = (size_t)a.n_kv_heads * HD;
+
+    // 1. Q tile: row r = token qt0 + r / G, head kvh*G + r % G (+ bias, RoPE)
+    for (int idx = tid; idx < R * HD; idx += NW * 64) {
+        const int r = idx / HD, d = idx % HD, tl = r / G;
+        float v = 0.f;
+        if (tl < QT && qt0 + tl < n_tok) {
+            const size_t e = (size_t)(kvh * G + r % G) * HD + d;
+            v = a.q[(size_t)(qt0 + tl) * a.q_ld + e];
+            if (a.bq) v += a.bq[e];
+        }
+        qs[r * QS + d] = v;
+    }
+    __syncthreads();
+    if (a.cos_t) {
+        for (int idx = tid; idx < R * HALF; idx += NW * 64) {
+            const int r = idx / HALF, i = idx % HALF, tl = r / G;
+            if (tl < QT && qt0 + tl < n_tok) {
+                const size_t pr = (size_t)(pos0 + qt0 + tl) * HALF + i;
+                const float c = a.cos_t[pr], sn = a.sin_t[pr];
+                float* h = qs + r * QS;
+                const float x0 = h[i], x1 = h[i + HALF];
+                h[i] = fmaf(x0, c, -(x1 * sn));
+                h[i + HALF] = fmaf(x0, sn, x1 * c);
+            }
+        }
+        __syncthreads();
+    }
+    float qb[KQ];  // B operand of S^T: query col, dims grp*KQ + s
+#pragma unroll
+    for (int u = 0; u < KQ / 4; u++) {
+        const float4 v = *reinterpret_cast<const float4*>(qs + col * QS + grp * KQ + 4 * u);
+        qb[4 * u] = v.x; qb[4 * u + 1] = v.y; qb[4 * u + 2] = v.z; qb[4 * u + 3] = v.w;
+    }
+    const int qpos = (col / G < QT && qt0 + col / G < n_tok) ? pos0 + qt0 + col / G : -1;
+    const float scale = 1.f / sqrtf((float)HD);
+
+    float m = -INFINITY, l = 0.f;
+    v4f_t o[DT];
+#pragma unroll
+    for (int t = 0; t < DT; t++) o[t] = v4f_t{0.f, 0.f, 0.f, 0.f};
+    const float* kb = a.kcache + (size_t)kvh * HD;
+    const float* vb = a.vcache + (size_t)kvh * HD;
+    const int ntile = kmax / 16 + 1;
+    // this lane's K row (key 16kt + col) and V rows (keys 16kt + 4grp + r), keys
+    // past kmax re-read row kmax (masked below)
+    float kr[KQ], vr[4][DT];
+    auto load = [&](int kt) {
+        const float4* kp = reinterpret_cast<const float4*>(
+            kb + (size_t)min(16 * kt + col, kmax) * kve + grp * KQ);
+#pragma unroll
+        for (int u = 0; u < KQ / 4; u++) {
+            const float4 v = kp[u];
+            kr[4 * u] = v.x; kr[4 * u + 1] = v.y; kr[4 * u + 2] = v.z; kr[4 * u + 3] = v.w;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float4* vp = reinterpret_cast<const float4*>(
+                vb + (size_t)min(16 * kt + 4 * grp + r, kmax) * kve + col * DT);
+#pragma unroll
+            for (int u = 0; u < DT / 4; u++) {
+                const float4 v = vp[u];
+                vr[r][4 * u] = v.x; vr[r][4 * u + 1] = v.y; vr[r][4 * u + 2] = v.z; vr[r][4 * u + 3] = v.w;
+            }
+        }
+    };
+    if (wave < ntile) load(wave);
+    for (int kt = wave; kt < ntile; kt += NW) {
+        float kc[KQ], vc[4][DT];
+#pragma unroll
+        for (int s = 0; s < KQ; s++) kc[s] = kr[s];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int t = 0; t < DT; t++) vc[r][t] = vr[r][t];
+        if (kt + NW < ntile) load(kt + NW);  // in flight during this tile
+        v4f_t s4 = v4f_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KQ; s++) s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kc[s], qb[s], s4, 0, 0, 0);
+        // online softmax of query col over keys 16kt + 4grp + r
+        float sv[4], tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int key = 16 * kt + 4 * grp + r;
+            sv[r] = (qpos >= 0 && key <= qpos) ? s4[r] * scale : -INFINITY;
+            tmax = fmaxf(tmax, sv[r]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mn = fmaxf(m, tmax);
+        // a row with nothing to attend to yet keeps zero weights
+        const float alpha = mn == -INFINITY ? 1.f : expf(m - mn);
+        float p[4], ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            p[r] = mn == -INFINITY ? 0.f : expf(sv[r] - mn);
+            ps += p[r];
+        }
+        l = fmaf(l, alpha, ps);
+        m = mn;
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            o[t] *= alpha;
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vc[r][t], p[r], o[t], 0, 0, 0);
+        }
+    }
+
+    // 2. merge the waves' states (the Q tile is no longer read)
+    __syncthreads();
+    {
+        float* ow = qs + (wave * R + col) * QS + grp * KQ;  // dims grp*KQ + r*DT + t
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int t4 = 0; t4 < DT / 4; t4++)
+                *reinterpret_cast<float4*>(ow + r * DT + 4 * t4) =
+                    make_float4(o[4 * t4][r], o[4 * t4 + 1][r], o[4 * t4 + 2][r], o[4 * t4 + 3][r]);
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        if (grp == 0) {
+            mm[wave][col] = m;
+            ll[wave][col] = l;
+        }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < R * HD / 4; idx += NW * 64) {
+        const int r = idx / (HD / 4), c4 = idx % (HD / 4), tl = r / G;
+        float M = mm[0][r];
+#pragma unroll
+        for (int w = 1; w < NW; w++) M = fmaxf(M, mm[w][r]);
+        float L = 0.f;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = mm[w][r] == -INFINITY ? 0.f : expf(mm[w][r] - M);
+            L = fmaf(ll[w][r], f, L);
+            v = fma4(f, *reinterpret_cast<const float4*>(qs + (w * R + r) * QS + 4 * c4), v);
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        v = make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+        // the 8 lanes of a Q8_0 block are consecutive and share r: all store or none
+        if (tl < QT && qt0 + tl < n_tok) {
+            const size_t e0 = (size_t)(qt0 + tl) * a.out_ld + (size_t)(kvh * G + r % G) * HD + 4 * c4;
+            float* dst = a.out + e0;
+            dst[0] = v.x;
+            dst[1] = v.y;
+            dst[2] = v.z;
+            dst[3] = v.w;
+            if (a.outq8) q8_store4(a.outq8 + (e0 >> 5) * Q8_0_BYTES, c4 & 7, v);
+        }
+    }
+}
+
 int attn_nsplit(int max_seq) { return (max_seq + kAttnSplit - 1) / kAttnSplit; }
 
 template <int HD>
 static hipError_t launch_prefill_hd(const AttnArgs& a, int G, hipStream_t st) {
-    const int QT = kPfRows / G;
     const int nt = a.n_tok > 1 ? a.n_tok : 1;
+    if constexpr (HD <= 128) {
+        const int QT = kPfKsRows / G;
+        const dim3 grid((unsigned)a.n_kv_heads, (unsigned)((nt + QT - 1) / QT));
+        hipLaunchKernelGGL((k_attn_prefill_ks<HD>), grid, dim3(kPfKsWaves * 64), 0, st, a, G, QT);
+        return hipGetLastError();
+    }
+    const int QT = kPfRows / G;
     const dim3 grid((unsigned)a.n_kv_heads, (unsigned)((nt + QT - 1) / QT));
     hipLaunchKernelGGL((k_attn_prefill<HD>), grid, dim3(256), 0, st, a, G, QT);
     return hipGetLastError();
