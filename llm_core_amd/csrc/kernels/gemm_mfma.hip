@@ -730,10 +730,14 @@ __device__ __forceinline__ void gemm16_step(
     for (int j = 0; j < TTW; j++) accb[j] = zero;
 #pragma unroll
     for (int s = 0; s < 8; s++) {
-        const uint32_t scv = ((s < 4 ? sc03 : sc47) >> (8 * (s & 3))) & 0xffu;
-        const _Float16 scf = (_Float16)(float)scv;               // exact
-        const _Float16 offf = (_Float16)(-1024.f * (float)scv);  // exact (<= 64512)
-        const h2_t sc2 = {scf, scf}, off2 = {offf, offf};
+        // fp16 pair (1024 + sc, 1024 + sc) from byte s & 3 of the scale word
+        // (v_perm_b32), minus 1024: sc exactly, and -1024*sc (<= 64512) exactly
+        const uint32_t k = (uint32_t)(s & 3);
+        const uint32_t scb = __builtin_amdgcn_perm(0x64646464u, s < 4 ? sc03 : sc47,
+                                                   0x04000400u | (k << 16) | k);
+        const h2_t m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+        const h2_t sc2 = __builtin_bit_cast(h2_t, scb) + m1024;
+        const h2_t off2 = sc2 * m1024;
         const int sh = 4 * (s & 1);
         const uint32_t u0 = ((uint32_t)qv[s >> 1] >> sh) & 0x0f0f0f0fu;
         const uint32_t u1 = ((uint32_t)((uint64_t)qv[s >> 1] >> 32) >> sh) & 0x0f0f0f0fu;
