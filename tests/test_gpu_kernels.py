@@ -406,7 +406,9 @@ def test_attention(ctx, seq, H, KVH, hd):
 @pytest.mark.parametrize("hd,H,KVH,T,pos0", [(128, 32, 32, 64, 0), (128, 16, 2, 48, 100),
                                              (64, 8, 4, 37, 5), (256, 8, 8, 20, 40),
                                              (128, 14, 2, 70, 0), (128, 32, 32, 256, 256),
-                                             (64, 8, 2, 1, 0), (128, 16, 2, 9, 3000)])
+                                             (64, 8, 2, 1, 0), (128, 16, 2, 9, 3000),
+                                             # 12 kv heads, one query head each
+                                             (64, 12, 12, 33, 7)])
 def test_attn_prefill(ctx, hd, H, KVH, T, pos0):
     """Causal multi-row attention (bias and RoPE of q inside): the matrix-core
     kernel and the split/combine token grid against the oracle's per-row
