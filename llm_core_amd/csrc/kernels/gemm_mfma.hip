@@ -1163,6 +1163,244 @@ void launch6_cfg(float* Y, const uint8_t* W, const uint8_t* xs, const float* dxs
                        W, xs, dxs, rows, nb, row_bytes, T, Tp, accumulate);
 }
 
+// ---------------------------------------------------------------------------
+// Q6_K x Q8_0 for wide token tiles on the fp16 matrix cores.  The per-16 scale
+// goes into the weight operand as two exact fp16 codes per weight: with
+// q - 32 = 16 hb + l (l = the low nibble in [0, 15], hb = the two high bits
+// minus 2, in [-2, 1]),
+//   c1 = sc * l       |c1| <= 128 * 15 = 1920: an fp16 integer
+//   c2 = 16 * sc * hb |c2| <= 4096, a multiple of 16: an fp16 integer
+// and B = the int8 activations as fp16 (exact).  Per Q8_0 block and token tile
+// two v_mfma_f32_16x16x32_f16 (A = c1, then c2, one accumulator) return
+// sum sc * (q - 32) * x over the block's two sub-blocks: integers below 2^24
+// (|sc (q - 32) x| <= 128 * 32 * 127, 32 of them), so exact in fp32 and equal
+// to the int8 kernel's sc1*S1 + sc2*S2.  Then one FMA with dx per result (the
+// int8 kernel: two 24-bit multiplies, a conversion and the FMA) and d per
+// super-block, as there.  Weights as A (rows), tokens as B, as in the fp16
+// Q4_K kernel, whose activation re-layout (k_gemm_prep16) this one reads; d
+// of the result rows 4g..4g+3 comes from the lanes holding those rows.
+// Workgroup: RT waves, wave w owns rows 16w..16w+15 and the 16*TTW tokens;
+// one super-block per ring stage: RW rows of 240-byte slots holding each
+// row's 16-byte-aligned 224-byte span (as k_gemm_mfma_q6k), then the
+// super-block's fp16 activations and dx (no min term for Q6_K).
+// ---------------------------------------------------------------------------
+template <int RT, int TTW, int S>
+struct Stage6h {
+    static constexpr int NW = RT, RW = kTile * RT, TW = kTile * TTW;
+    static constexpr int SPAN = 224, SLOT = 240;
+    static constexpr int WB = RW * SLOT;
+    static constexpr int XB = 8 * 4 * TW * 16;
+    static constexpr int DB = 8 * TW * 4;
+    static constexpr int BYTES = WB + XB + DB;
+    static constexpr int PIECES = (BYTES + 1023) / 1024;
+    static constexpr int ALLOC = PIECES * 1024;
+    static constexpr int PMAX = (PIECES + NW - 1) / NW;
+    static constexpr int PMIN = PIECES / NW;
+    static_assert(WB % 1024 == 0 && XB % 1024 == 0 && DB % 256 == 0, "piece alignment");
+    static_assert(S * ALLOC <= 160 * 1024, "LDS");
+};
+
+// fp16 pairs of (byte - off) * scale for 4 bytes of u, exact where the
+// products are fp16 integers: v_perm_b32 makes 1024 + byte, then one packed
+// add and one packed multiply
+__device__ __forceinline__ void bytes_scaled(uint32_t u, h2_t off2, h2_t sc2, uint32_t& lo,
+                                             uint32_t& hi) {
+    const h2_t a = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
+    const h2_t b = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
+    lo = __builtin_bit_cast(uint32_t, (a + off2) * sc2);
+    hi = __builtin_bit_cast(uint32_t, (b + off2) * sc2);
+}
+
+template <int RT, int TTW, int S>
+__device__ __forceinline__ void gemm6h_step(
+    const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt, bool do_copy, int bnext, int i,
+    int nb, const uint64_t (&base)[Stage6h<RT, TTW, S>::PMAX],
+    const uint32_t (&aux)[Stage6h<RT, TTW, S>::PMAX], __amdgpu_buffer_rsrc_t wrsrc, int wave,
+    int col, int g, uint32_t wlo, v4f_t (&acc)[TTW]) {
+    using G = Stage6h<RT, TTW, S>;
+    constexpr int NW = G::NW, TW = G::TW;
+    if (do_copy) {
+#pragma unroll
+        for (int j = 0; j < G::PMAX; j++) {
+            const int piece = wave + NW * j;
+            if (piece * 1024 < G::WB) {
+                // the aligned span of the row's block bnext; this lane's 16 bytes
+                // sit aux[j] bytes into the slot
+                const uint32_t o = (((uint32_t)base[j] + (uint32_t)bnext * (uint32_t)Q6K_BYTES) & ~15u) + aux[j];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, (lmem_t*)(nxt + piece * 1024), 16,
+                                                         o, 0, 0, 0);
+            } else if (piece < G::PIECES) {
+                const uint8_t* a = reinterpret_cast<const uint8_t*>(base[j]) + (size_t)bnext * aux[j];
+                __builtin_amdgcn_global_load_lds((gmem_t*)a, (lmem_t*)(nxt + piece * 1024), 16, 0,
+                                                 0);
+            }
+        }
+    }
+    if (i < 0) return;
+    wait_later<G::PMIN, S - 1>(min(S - 1, nb - 1 - i));
+    __builtin_amdgcn_s_barrier();
+
+    // this lane's row: its block starts (wlo + 2i) & 15 bytes into the slot
+    const uint8_t* wl = cur + (kTile * wave + col) * G::SLOT;
+    const uint32_t wo = (wlo + 2u * (uint32_t)i) & 15u;
+    const uint8_t* xl = cur + G::WB;
+    const float* dl = reinterpret_cast<const float*>(cur + G::WB + G::XB);
+    uint32_t ql[2][2][2], qh[2][2], sc[4], dw[1];
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) lds_bytes<2>(wl, wo + 64 * n + 32 * h + 8 * g, ql[n][h]);
+        lds_bytes<2>(wl, wo + 128 + 32 * n + 8 * g, qh[n]);
+    }
+    lds_bytes<4>(wl, wo + 192, sc);
+    lds_bytes<1>(wl, wo + 208, dw);
+    const v4f_t zero = {0.f, 0.f, 0.f, 0.f};
+    v4f_t accb[TTW];
+#pragma unroll
+    for (int j = 0; j < TTW; j++) accb[j] = zero;
+    const h2_t offl = {(_Float16)-1024.f, (_Float16)-1024.f};
+    const h2_t offh = {(_Float16)-1026.f, (_Float16)-1026.f};
+#pragma unroll
+    for (int kb = 0; kb < 8; kb++) {
+        const int n = kb >> 2, q = kb & 3, h = q & 1, nib = q >> 1;
+        // k-group g: sub-block 2kb + (g >> 1), scale byte 2(kb & 1) + (g >> 1) of sc[kb >> 1]
+        const int scv = (int)(int8_t)(sc[kb >> 1] >> (16 * (kb & 1) + 8 * (g >> 1)));
+        const _Float16 s1 = (_Float16)(float)scv, s16 = (_Float16)(16.f * (float)scv);
+        const h2_t sc1 = {s1, s1}, sc16 = {s16, s16};
+        uint32_t c1[4], c2[4];
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            const uint32_t l = (ql[n][h][x] >> (4 * nib)) & 0x0f0f0f0fu;
+            const uint32_t hb = (qh[n][x] >> (2 * q)) & 0x03030303u;
+            bytes_scaled(l, offl, sc1, c1[2 * x], c1[2 * x + 1]);
+            bytes_scaled(hb, offh, sc16, c2[2 * x], c2[2 * x + 1]);
+        }
+        const v8h_t a1 = __builtin_bit_cast(v8h_t, u32x4_t{c1[0], c1[1], c1[2], c1[3]});
+        const v8h_t a2 = __builtin_bit_cast(v8h_t, u32x4_t{c2[0], c2[1], c2[2], c2[3]});
+        float dxs[TTW];
+        lds_floats<TTW>(dl + (kb * 16 + col) * TTW, dxs);
+#pragma unroll
+        for (int j = 0; j < TTW; j++) {
+            const v8h_t b =
+                *reinterpret_cast<const v8h_t*>(xl + ((kb * 4 + g) * TW + 16 * j + col) * 16);
+            v4f_t c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, zero, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, b, c, 0, 0, 0);
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) accb[j][ii] = fmaf(c[ii], dxs[j], accb[j][ii]);
+        }
+    }
+    // d of the result rows 4g..4g+3: lane 4g + ii (g = 0 there) holds row 4g + ii
+    const float down = h2f(dw[0] & 0xffffu);
+    float dout[4];
+#pragma unroll
+    for (int ii = 0; ii < 4; ii++) dout[ii] = __shfl(down, 4 * g + ii, 64);
+#pragma unroll
+    for (int j = 0; j < TTW; j++)
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++) acc[j][ii] = fmaf(dout[ii], accb[j][ii], acc[j][ii]);
+    // stage free for chunk i + S
+    __builtin_amdgcn_s_barrier();
+}
+
+// grid = 8 * ceil(nrt / 8) * (Tp / TW) workgroups, XCD-aware as k_gemm_f16_q4k
+template <int RT, int TTW, int S>
+__global__ __launch_bounds__(RT * 64) void k_gemm_f16_q6k(
+    float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ xh,
+    const float* __restrict__ dxt, int rows, int nb, long row_bytes, int T, int Tp, int nrt,
+    int accumulate) {
+    using G = Stage6h<RT, TTW, S>;
+    constexpr int NW = G::NW, RW = G::RW, TW = G::TW;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[S * G::ALLOC];
+    const int ntg = Tp / TW;
+    const int L = blockIdx.x, xcd = L & 7, k = L >> 3;
+    const int rt = (k / ntg) * 8 + xcd, ty = k % ntg;
+    if (rt >= nrt) return;  // the whole workgroup, before any barrier
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int col = lane & 15, g = lane >> 4;
+    const int row_base = rt * RW, tok_base = ty * TW;
+
+    // weights through a buffer resource from W rounded down to 16 bytes to the
+    // end of the last block (the host checks that this is under 2 GiB)
+    const uint32_t w0 = (uint32_t)(reinterpret_cast<uintptr_t>(W) & 15);
+    const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(W - w0), 0,
+        (int)(w0 + (uint32_t)(rows - 1) * (uint32_t)row_bytes + (uint32_t)nb * Q6K_BYTES),
+        0x00020000);
+    // per piece of this lane: weights — base = the row's offset in the buffer
+    // resource, aux = the lane's offset in the slot; activations — base = the
+    // address for super-block 0, aux = bytes per super-block
+    uint64_t base[G::PMAX];
+    uint32_t aux[G::PMAX];
+#pragma unroll
+    for (int j = 0; j < G::PMAX; j++) {
+        int o = (wave + NW * j) * 1024 + lane * 16;
+        if (o >= G::BYTES) o = G::WB;  // tail of the last piece: a harmless duplicate
+        if (o < G::WB) {
+            const int r = o / G::SLOT, a = o - r * G::SLOT;
+            base[j] = w0 + (uint32_t)min(row_base + r, rows - 1) * (uint32_t)row_bytes;
+            aux[j] = (uint32_t)(a < G::SPAN ? a : 0);  // slot padding: a duplicate
+        } else if (o < G::WB + G::XB) {
+            const int x = o - G::WB, s = x / (4 * TW * 16), gg = (x / (TW * 16)) & 3,
+                      t = (x % (TW * 16)) / 16;
+            base[j] = reinterpret_cast<uint64_t>(xh + (((size_t)s * 4 + gg) * Tp + tok_base + t) * 16);
+            aux[j] = 8u * 4u * (uint32_t)Tp * 16u;
+        } else {
+            const int z = o - G::WB - G::XB;
+            base[j] = reinterpret_cast<uint64_t>(
+                reinterpret_cast<const uint8_t*>(dxt) +
+                ((size_t)(z / (TW * 4)) * (Tp / TW) + tok_base / TW) * (TW * 4) + (z % (TW * 4)));
+            aux[j] = 8u * (uint32_t)Tp * 4u;
+        }
+    }
+    const uint32_t wlo =
+        (w0 + (uint32_t)min(row_base + kTile * wave + col, rows - 1) * (uint32_t)row_bytes) & 15u;
+    v4f_t acc[TTW];
+#pragma unroll
+    for (int j = 0; j < TTW; j++) acc[j] = v4f_t{0.f, 0.f, 0.f, 0.f};
+    for (int i = 1 - S; i < nb; i++) {
+        const int inext = i + S - 1;
+        gemm6h_step<RT, TTW, S>(smem + ((i + S) % S) * G::ALLOC, smem + (inext % S) * G::ALLOC,
+                                inext < nb, inext, i, nb, base, aux, wrsrc, wave, col, g, wlo,
+                                acc);
+    }
+#pragma unroll
+    for (int j = 0; j < TTW; j++) {
+        const int tok = tok_base + 16 * j + col;
+        if (tok < T) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) {
+                const int o = row_base + kTile * wave + 4 * g + ii;
+                if (o < rows) {
+                    float* y = Y + (size_t)tok * rows + o;
+                    *y = accumulate ? *y + acc[j][ii] : acc[j][ii];
+                }
+            }
+        }
+    }
+}
+
+// 128 rows x 64 tokens per workgroup (8 waves, one super-block per stage,
+// two 64 KiB stages)
+constexpr int kF16Q6RT = 8, kF16Q6TTW = 4, kF16Q6S = 2;
+
+void launch6h(float* Y, const uint8_t* W, const uint8_t* XQ8, uint8_t* scratch, int rows, int nb,
+              long row_bytes, int T, hipStream_t st, int accumulate) {
+    constexpr int TW = kTile * kF16Q6TTW;
+    const int Tp = (T + TW - 1) / TW * TW, nkb = nb * 8;
+    auto* xh = scratch;
+    auto* dxt = reinterpret_cast<float*>(xh + (size_t)nkb * Tp * 64);
+    auto* gxt = dxt + (size_t)nkb * Tp;  // written by the shared re-layout, unused here
+    const long n = (long)nkb * Tp;
+    hipLaunchKernelGGL(k_gemm_prep16<kF16Q6TTW>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       st, XQ8, T, Tp, nkb, xh, dxt, gxt);
+    const int nrt = (rows + kTile * kF16Q6RT - 1) / (kTile * kF16Q6RT);
+    const unsigned grid = (unsigned)((nrt + 7) / 8 * 8 * (Tp / TW));
+    hipLaunchKernelGGL((k_gemm_f16_q6k<kF16Q6RT, kF16Q6TTW, kF16Q6S>), dim3(grid),
+                       dim3(kF16Q6RT * 64), 0, st, Y, W, xh, dxt, rows, nb, row_bytes, T, Tp, nrt,
+                       accumulate);
+}
+
 // Tile choice: the largest of 64x64, 32x32, 16x16 (rows x tokens) whose grid
 // still has one workgroup per CU; below that the 16x16 tile with the widest
 // K split.  (Measured on 4096 x 11008 and 2048 x 11008 matrices, T = 8..256.)
@@ -1228,7 +1466,7 @@ bool gemm_mfma_q6k_ok(const void* W, int rows, int nb, long row_bytes) {
 size_t gemm_mfma_q6k_scratch_bytes(int T, int nb) {
     if (T <= 0 || nb <= 0) return 0;
     const size_t tp = (size_t)((T + 63) / 64 * 64);  // the widest token tile's padding
-    return (size_t)nb * 8 * tp * (32 + 4 + 4);
+    return (size_t)nb * 8 * tp * (64 + 4 + 4);        // fp16 re-layout (int8: 32 + 4 + 4)
 }
 
 hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
@@ -1236,6 +1474,13 @@ hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int
                                    int accumulate) {
     if (rows <= 0 || T <= 0 || nb <= 0 || scratch == nullptr) return hipErrorInvalidValue;
     if (!gemm_mfma_q6k_ok(W, rows, nb, row_bytes)) return hipErrorInvalidValue;
+    // wide token tiles on the fp16 matrix cores where 128 x 64 tiles still give
+    // one workgroup per CU
+    if (T >= 64 && (long)((rows + 127) / 128) * ((T + 63) / 64) >= 256) {
+        launch6h(Y, static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(XQ8),
+                 static_cast<uint8_t*>(scratch), rows, nb, row_bytes, T, st, accumulate);
+        return hipGetLastError();
+    }
     const Tile6 tile = pick6(rows, T);
     const int q = tokens6(tile);
     const int Tp = (T + q - 1) / q * q;

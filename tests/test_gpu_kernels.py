@@ -261,7 +261,10 @@ GEMM6_CASES = [(4096, 4096, 1), (4096, 11008, 4), (512, 11008, 9), (2048, 2048, 
                # the wider tiles: 64x64 (ragged rows and tokens), 32x32, 16x16
                (4096, 768, 256), (4100, 768, 250), (2048, 1280, 128), (2040, 1280, 120),
                # the 7B down projection at config-4 token counts
-               (4096, 11008, 16), (4096, 11008, 64)]
+               (4096, 11008, 16), (4096, 11008, 64),
+               # the fp16 kernel (128 x 64 tiles, taken from 256 such tiles):
+               # exactly 256 tiles, ragged rows and tokens, one super-block
+               (4096, 2048, 512), (4100, 1024, 520), (16384, 256, 70)]
 
 
 def _gemm6_want(W, XQ, rows, cols, T):
