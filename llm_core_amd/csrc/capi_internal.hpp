@@ -117,6 +117,12 @@ hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int
                                    int nb, long row_bytes, void* scratch, hipStream_t st,
                                    int accumulate = 0);
 size_t gemm_mfma_q6k_scratch_bytes(int T, int nb);
+// ffn_gate|ffn_up interleaved by blocks of 8 rows, rows % 128 == 0, T >= 65:
+// the fp16 Q4_K GEMM with SwiGLU in its epilogue, h written as Q8_0 blocks of
+// [T][rows/2] (and as fp32 rows when hf is set); scratch gemm_mfma_scratch_bytes
+hipError_t launch_gemm_f16_q4k_swiglu(uint8_t* hq8, float* hf, const void* W, const void* XQ8,
+                                      int rows, int T, int nb, long row_bytes, void* scratch,
+                                      hipStream_t st);
 bool gemm_mfma_q6k_ok(const void* W, int rows, int nb, long row_bytes);
 hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
                                    int nb, long row_bytes, void* scratch, hipStream_t st,

@@ -881,9 +881,17 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
                            hp.rms_eps, T, st));
     xb_ready = false;
     if (L.gu_interleaved) {
-        ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, 2 * FD, T, E, st));
         const int B = qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2;
-        ST(launch_swiglu_gu(m->pf_q8, m->pf_gu, T, FD, B, st, f_down ? m->pf_h : nullptr));
+        if (L.wgate.qtype == AXF_TYPE_Q4_K && B == 8 && T > kGemmStreamMaxT && (2 * FD) % 128 == 0) {
+            // SwiGLU and its Q8_0 blocks in the fp16 GEMM's epilogue (the GEMM
+            // reads its re-laid copy of the input blocks, so h may overwrite them)
+            ST(launch_gemm_f16_q4k_swiglu(m->pf_q8, f_down ? m->pf_h : nullptr, L.wgate.d, m->pf_q8,
+                                          2 * FD, T, E / QK_K, (long)L.wgate.row_bytes, m->pf_gemm,
+                                          st));
+        } else {
+            ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, 2 * FD, T, E, st));
+            ST(launch_swiglu_gu(m->pf_q8, m->pf_gu, T, FD, B, st, f_down ? m->pf_h : nullptr));
+        }
     } else {
         ST(gemm_any(m, L.wgate, m->pf_gu, m->pf_q8, m->pf_xb, FD, T, E, st, &xb_ready));
         ST(gemm_any(m, L.wup, m->pf_gu + (size_t)T * FD, m->pf_q8, m->pf_xb, FD, T, E, st,

@@ -792,11 +792,17 @@ __device__ __forceinline__ void gemm16_step(
 // grid = 8 * ceil(nrt / 8) * (Tp / TW) workgroups, XCD-aware: workgroup L runs
 // on XCD L % 8 (round-robin dispatch), and every token group of a row tile
 // runs on one XCD, so the tile's weights are fetched into that XCD's L2 once.
-template <int RT, int TTW, int S>
+// SW: the matrix is ffn_gate|ffn_up interleaved by blocks of 8 rows (8 gate
+// rows, then the same 8 up rows), so a workgroup's 128 rows are 64
+// consecutive SwiGLU pairs: the epilogue writes h = swiglu(gate, up) as the
+// Q8_0 blocks of [T][rows / 2] (hq8) and, when hf is set, as fp32 rows,
+// instead of Y; the arithmetic of k_swiglu_gu.
+template <int RT, int TTW, int S, bool SW = false>
 __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
     float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ xh,
     const float* __restrict__ dxt, const float* __restrict__ gxt, int rows, int nb,
-    long row_bytes, int T, int Tp, int nrt, int accumulate) {
+    long row_bytes, int T, int Tp, int nrt, int accumulate, uint8_t* __restrict__ hq8 = nullptr,
+    float* __restrict__ hf = nullptr) {
     using G = Stage16<RT, TTW, S>;
     constexpr int NW = G::NW, RW = G::RW, TW = G::TW;
     __shared__ __attribute__((aligned(16))) uint8_t smem[S * G::ALLOC];
@@ -845,6 +851,35 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
                                 inext < nb, inext, i, nb, src, step, wave, lane, col, g, acc,
                                 macc);
     }
+    if constexpr (SW) {
+        static_assert(RT == 8, "64 SwiGLU pairs per workgroup: two Q8_0 blocks");
+        // lane (col, g < 2) holds gate rows 4g..4g+3 of the wave's 8 pairs, lane
+        // (col, g + 2) the matching up rows; the ring's LDS is free (the last
+        // step ended with a barrier): h[token][64] of this workgroup
+        float* hs = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (int j = 0; j < TTW; j++) {
+            const v4f_t v = acc[j] - macc[j];
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) {
+                const float up = __shfl_xor(v[ii], 32, 64);
+                if (g < 2) hs[(16 * j + col) * 64 + 8 * wave + 4 * g + ii] = swiglu1(v[ii], up);
+            }
+        }
+        __syncthreads();
+        // 8 lanes per Q8_0 block (4 values each), as k_swiglu_gu: 2 blocks x TW tokens
+        const int nh = rows / 2;
+        for (int q = threadIdx.x; q < TW * 16; q += RT * 64) {
+            const int tl = q >> 4, half = (q >> 3) & 1, sub = q & 7, tok = tok_base + tl;
+            const float4 o = *reinterpret_cast<const float4*>(hs + tl * 64 + 32 * half + 4 * sub);
+            if (tok < T) {  // the 8 lanes of a block share the token
+                const size_t e = (size_t)tok * nh + 64 * rt + 32 * half + 4 * sub;
+                if (hf) *reinterpret_cast<float4*>(hf + e) = o;
+                q8_block_store(hq8 + (e >> 5) * Q8_0_BYTES, sub, o);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < TTW; j++) {
         const v4f_t v = acc[j] - macc[j];
@@ -862,9 +897,10 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
     }
 }
 
-template <int RT, int TTW, int S>
+template <int RT, int TTW, int S, bool SW = false>
 void launch16_cfg(float* Y, const uint8_t* W, const uint8_t* XQ8, uint8_t* scratch, int rows,
-                  int nb, long row_bytes, int T, hipStream_t st, int accumulate) {
+                  int nb, long row_bytes, int T, hipStream_t st, int accumulate,
+                  uint8_t* hq8 = nullptr, float* hf = nullptr) {
     constexpr int TW = kTile * TTW;
     const int Tp = (T + TW - 1) / TW * TW, nkb = nb * 8;
     auto* xh = scratch;
@@ -875,8 +911,8 @@ void launch16_cfg(float* Y, const uint8_t* W, const uint8_t* XQ8, uint8_t* scrat
                        XQ8, T, Tp, nkb, xh, dxt, gxt);
     const int nrt = (rows + kTile * RT - 1) / (kTile * RT);
     const unsigned grid = (unsigned)((nrt + 7) / 8 * 8 * (Tp / TW));
-    hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S>), dim3(grid), dim3(RT * 64), 0, st, Y, W, xh,
-                       dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, accumulate);
+    hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S, SW>), dim3(grid), dim3(RT * 64), 0, st, Y, W,
+                       xh, dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, accumulate, hq8, hf);
 }
 
 // ---------------------------------------------------------------------------
@@ -1514,6 +1550,20 @@ hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int
 // 36 KiB stages: two workgroups per CU), measured on the 512-token prefill
 // against 64-token workgroups and 3-deep rings
 constexpr int kF16MinTokens = 65;
+
+// ffn_gate|ffn_up interleaved by 8-row blocks, T >= 65 tokens: the fp16 GEMM
+// with the SwiGLU epilogue (h as Q8_0 blocks [T][rows/2], and fp32 rows when
+// hf is set); scratch as gemm_mfma_scratch_bytes
+hipError_t launch_gemm_f16_q4k_swiglu(uint8_t* hq8, float* hf, const void* W, const void* XQ8,
+                                      int rows, int T, int nb, long row_bytes, void* scratch,
+                                      hipStream_t st) {
+    if (T < kF16MinTokens || nb <= 0 || rows <= 0 || rows % 128 || scratch == nullptr)
+        return hipErrorInvalidValue;
+    launch16_cfg<8, 2, 2, true>(nullptr, static_cast<const uint8_t*>(W),
+                                static_cast<const uint8_t*>(XQ8), static_cast<uint8_t*>(scratch),
+                                rows, nb, row_bytes, T, st, 0, hq8, hf);
+    return hipGetLastError();
+}
 
 size_t gemm_mfma_scratch_bytes(int T, int nb) {
     if (T <= 0 || nb <= 0) return 0;

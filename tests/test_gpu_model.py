@@ -336,13 +336,13 @@ def test_generate_rejects_bad_input(ctx):
 # batched prefill (llama_forward_batch)
 # ---------------------------------------------------------------------------
 
-def _prefill_case(ctx, hp_kwargs, seed, T, splits=(), with_bias=False):
+def _prefill_case(ctx, hp_kwargs, seed, T, splits=(), with_bias=False, layer_types=None):
     """Last-row logits and residual after a batched prefill of T tokens (run as
     the given chunk boundaries on the GPU), against the oracle's single batch."""
     from llm_core_amd.model import Hparams, LlamaHip, SynthLlama
 
     hp = Hparams(**hp_kwargs)
-    m = SynthLlama(hp, seed=seed, norm_std=0.1, with_bias=with_bias)
+    m = SynthLlama(hp, seed=seed, norm_std=0.1, with_bias=with_bias, layer_types=layer_types)
     rng = np.random.default_rng(seed)
     toks = np.concatenate([[1], rng.integers(0, hp.n_vocab, T - 1)]).astype(np.int32)
     om = O.OracleModel(hp, m.tensors)
@@ -409,6 +409,24 @@ def test_forward_batch_qwen25_3b_layer(ctx):
     rel = np.linalg.norm(gx.astype(np.float64) - ox) / np.linalg.norm(ox)
     assert rel < 1e-3, f"final-norm row relative error {rel}"
     _check_prefill(gl, ol, max(noise, 1e-3))
+
+
+@pytest.mark.parametrize("down", ["q6_k", "q8_0"])
+def test_forward_batch_swiglu_epilogue(ctx, down):
+    """Hidden 2304 (9 super-blocks per row: ffn_gate|ffn_up interleaved by
+    8-row blocks) prefilling 80 tokens: the fp16 gate|up GEMM writes SwiGLU's
+    Q8_0 blocks in its epilogue (and, for a Q8_0 down projection, which takes
+    the fp32 rows, those too); last-row logits and residual against the
+    oracle's batch."""
+    from llm_core_amd.model import AXF_TYPE_Q8_0, Q4K_M_TYPES
+
+    cfg = dict(n_layer=1, n_embd=2304, n_heads=18, n_kv_heads=6, ffn_dim=1024, n_vocab=512,
+               n_ctx=96, rms_eps=1e-5, rope_theta=10000.0)
+    types = dict(Q4K_M_TYPES, ffn_down=AXF_TYPE_Q8_0) if down == "q8_0" else None
+    gl, ol, gx, ox, noise = _prefill_case(ctx, cfg, 5, 80, layer_types=types)
+    _check_prefill(gl, ol, noise)
+    rel = np.linalg.norm(gx.astype(np.float64) - ox) / np.linalg.norm(ox)
+    assert rel < 1e-3 or noise > 1e-3, f"final-norm row relative error {rel}"
 
 
 @pytest.mark.parametrize("order", [1, 2])
