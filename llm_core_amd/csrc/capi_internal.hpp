@@ -117,12 +117,20 @@ hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int
                                    int nb, long row_bytes, void* scratch, hipStream_t st,
                                    int accumulate = 0);
 size_t gemm_mfma_q6k_scratch_bytes(int T, int nb);
-// ffn_gate|ffn_up interleaved by blocks of 8 rows, rows % 128 == 0, T >= 65:
-// the fp16 Q4_K GEMM with SwiGLU in its epilogue, h written as Q8_0 blocks of
-// [T][rows/2] (and as fp32 rows when hf is set); scratch gemm_mfma_scratch_bytes
-hipError_t launch_gemm_f16_q4k_swiglu(uint8_t* hq8, float* hf, const void* W, const void* XQ8,
-                                      int rows, int T, int nb, long row_bytes, void* scratch,
-                                      hipStream_t st);
+// The fp16 GEMMs on a re-layout written elsewhere (launch_rmsnorm_rows_prep):
+// xh / dxt / gxt as k_gemm_prep16 lays them out for Tp tokens (a multiple of
+// 64 serves both).  Q6_K: where gemm_f16_q6k_applies.  Q4_K with swiglu: the
+// matrix is ffn_gate|ffn_up interleaved by blocks of 8 rows (rows % 128 ==
+// 0); SwiGLU runs in the epilogue and h is written as the Q8_0 blocks of
+// [T][rows/2] (hq8) and, when hf is set, as fp32 rows, instead of Y.
+hipError_t launch_gemm_f16_q4k_xh(float* Y, uint8_t* hq8, float* hf, const void* W,
+                                  const uint8_t* xh, const float* dxt, const float* gxt, int rows,
+                                  int nb, long row_bytes, int T, int Tp, hipStream_t st,
+                                  int accumulate, bool swiglu);
+bool gemm_f16_q6k_applies(const void* W, int rows, int nb, long row_bytes, int T);
+hipError_t launch_gemm_f16_q6k_xh(float* Y, const void* W, const uint8_t* xh, const float* dxt,
+                                  int rows, int nb, long row_bytes, int T, int Tp, hipStream_t st,
+                                  int accumulate);
 bool gemm_mfma_q6k_ok(const void* W, int rows, int nb, long row_bytes);
 hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int rows, int T,
                                    int nb, long row_bytes, void* scratch, hipStream_t st,
@@ -188,6 +196,12 @@ hipError_t launch_quantize_q8_0(void* y, const float* x, int n, hipStream_t st);
 hipError_t launch_rmsnorm(float* y, void* yq8, const float* x, const float* w, int n, float eps,
                           hipStream_t st);
 // rows independent RMSNorms of [rows][n] (same arithmetic as launch_rmsnorm)
+// launch_rmsnorm_rows plus the fp16 GEMMs' re-layout of its Q8_0 blocks for Tp
+// tokens (Tp % 64 == 0): xh (n/32 * Tp * 64 bytes), dx2 and gx2 (32-token
+// groups), dx4 (64-token groups), n/32 * Tp floats each; rows T..Tp-1 zero
+hipError_t launch_rmsnorm_rows_prep(float* y, void* yq8, const float* x, const float* w, int n,
+                                    float eps, int T, int Tp, uint8_t* xh, float* dx2, float* gx2,
+                                    float* dx4, hipStream_t st);
 hipError_t launch_rmsnorm_rows(float* y, void* yq8, const float* x, const float* w, int n,
                                float eps, int rows, hipStream_t st);
 hipError_t launch_rope_kv_rows(const float* k, int k_ld, const float* v, int v_ld,

@@ -95,6 +95,9 @@ struct axf_llama {
           *pf_gu = nullptr, *pf_part = nullptr;
     float *pf_xb = nullptr, *pf_h = nullptr;  // fp32 normalised rows and SwiGLU rows
     uint8_t *pf_q8 = nullptr, *pf_gemm = nullptr;
+    // the fp16 GEMMs' re-layout of the RMSNorm rows (launch_rmsnorm_rows_prep)
+    uint8_t* pf_xh = nullptr;
+    float *pf_dx2 = nullptr, *pf_gx2 = nullptr, *pf_dx4 = nullptr;
     // prefill attention: the matrix-core kernel, or (testing) the decode
     // split/combine kernels over a token grid
     bool pf_attn_split = false;
@@ -712,6 +715,15 @@ int prefill_alloc(axf_llama* m) {
     }
     LL_TRY(dalloc(m, gs, &p));
     m->pf_gemm = static_cast<uint8_t*>(p);
+    {  // the RMSNorm rows' fp16 re-layout, 64-token padding
+        const size_t tp = (C + 63) / 64 * 64, nkb = (size_t)E / 32;
+        LL_TRY(dalloc(m, nkb * tp * 64, &p));
+        m->pf_xh = static_cast<uint8_t*>(p);
+        LL_TRY(dalloc(m, nkb * tp * 4 * 3, &p));
+        m->pf_dx2 = static_cast<float*>(p);
+        m->pf_gx2 = m->pf_dx2 + nkb * tp;
+        m->pf_dx4 = m->pf_gx2 + nkb * tp;
+    }
     m->pf_cap = cap;
     return AXF_OK;
 }
@@ -797,24 +809,43 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     // q|k and v projections of RMSNorm(x) * attn_norm (fp32 rows too where a
     // projection of another type takes them)
     const bool f_qkv = !kquant(L.wq.qtype) || !kquant(L.wk.qtype) || !kquant(L.wv.qtype);
-    ST(launch_rmsnorm_rows(f_qkv ? m->pf_xb : nullptr, m->pf_q8, m->pf_x, L.attn_norm, E,
-                           hp.rms_eps, T, st));
+    // above 64 tokens the norm also writes the fp16 GEMMs' re-layout of its
+    // Q8_0 blocks (k_gemm_prep16's, for 64-token groups), read by the Q4_K
+    // q|k, v and gate|up GEMMs and the fp16 Q6_K v GEMM in place of their own
+    const bool prep = T > kGemmStreamMaxT;
+    const int Tp = (T + 63) / 64 * 64, nbE = E / QK_K;
+    auto norm_rows = [&](const float* w, float* fp32_rows) -> hipError_t {
+        if (!prep) return launch_rmsnorm_rows(fp32_rows, m->pf_q8, m->pf_x, w, E, hp.rms_eps, T, st);
+        return launch_rmsnorm_rows_prep(fp32_rows, m->pf_q8, m->pf_x, w, E, hp.rms_eps, T, Tp,
+                                        m->pf_xh, m->pf_dx2, m->pf_gx2, m->pf_dx4, st);
+    };
+    // Y = W rows of the normalised rows: the prepared fp16 GEMMs where they apply
+    auto proj = [&](const DevW& w, float* Y, int rows, bool* xf_ready) -> hipError_t {
+        if (prep && w.qtype == AXF_TYPE_Q4_K)
+            return launch_gemm_f16_q4k_xh(Y, nullptr, nullptr, w.d, m->pf_xh, m->pf_dx2, m->pf_gx2,
+                                          rows, nbE, (long)w.row_bytes, T, Tp, st, 0, false);
+        if (prep && w.qtype == AXF_TYPE_Q6_K && gemm_f16_q6k_applies(w.d, rows, nbE, (long)w.row_bytes, T))
+            return launch_gemm_f16_q6k_xh(Y, w.d, m->pf_xh, m->pf_dx4, rows, nbE, (long)w.row_bytes,
+                                          T, Tp, st, 0);
+        return gemm_any(m, w, Y, m->pf_q8, m->pf_xb, rows, T, E, st, xf_ready);
+    };
+    ST(norm_rows(L.attn_norm, f_qkv ? m->pf_xb : nullptr));
     bool xb_ready = false;  // the GEMM scratch holds pf_xb's prepared rows (misc types)
     float* q = m->pf_qk;
     float* k;
     int q_ld, k_ld;
     if (L.qk_fused) {
-        ST(gemm_rows(m, L.wq, q, m->pf_q8, qo + kvo, T, E, st));
+        ST(proj(L.wq, q, qo + kvo, &xb_ready));
         k = q + qo;
         q_ld = k_ld = qo + kvo;
     } else {
         k = q + (size_t)T * qo;
         q_ld = qo;
         k_ld = kvo;
-        ST(gemm_any(m, L.wq, q, m->pf_q8, m->pf_xb, qo, T, E, st, &xb_ready));
-        ST(gemm_any(m, L.wk, k, m->pf_q8, m->pf_xb, kvo, T, E, st, &xb_ready));
+        ST(proj(L.wq, q, qo, &xb_ready));
+        ST(proj(L.wk, k, kvo, &xb_ready));
     }
-    ST(gemm_any(m, L.wv, m->pf_v, m->pf_q8, m->pf_xb, kvo, T, E, st, &xb_ready));
+    ST(proj(L.wv, m->pf_v, kvo, &xb_ready));
     // K, V rows into the cache, then attention of every row -> Q8_0
     const bool qkn = hp.qk_norm_order != 0;
     if (qkn) {  // per-head q/k norms: q rows finished in place, K/V rows stored
@@ -877,17 +908,16 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     // where the down projection is of another type)
     const bool f_gu = !kquant(L.wgate.qtype) || !kquant(L.wup.qtype);
     const bool f_down = !kquant(L.wdown.qtype);
-    ST(launch_rmsnorm_rows(f_gu ? m->pf_xb : nullptr, m->pf_q8, m->pf_x, L.ffn_norm, E,
-                           hp.rms_eps, T, st));
+    ST(norm_rows(L.ffn_norm, f_gu ? m->pf_xb : nullptr));
     xb_ready = false;
     if (L.gu_interleaved) {
         const int B = qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2;
         if (L.wgate.qtype == AXF_TYPE_Q4_K && B == 8 && T > kGemmStreamMaxT && (2 * FD) % 128 == 0) {
             // SwiGLU and its Q8_0 blocks in the fp16 GEMM's epilogue (the GEMM
             // reads its re-laid copy of the input blocks, so h may overwrite them)
-            ST(launch_gemm_f16_q4k_swiglu(m->pf_q8, f_down ? m->pf_h : nullptr, L.wgate.d, m->pf_q8,
-                                          2 * FD, T, E / QK_K, (long)L.wgate.row_bytes, m->pf_gemm,
-                                          st));
+            ST(launch_gemm_f16_q4k_xh(nullptr, m->pf_q8, f_down ? m->pf_h : nullptr, L.wgate.d,
+                                      m->pf_xh, m->pf_dx2, m->pf_gx2, 2 * FD, nbE,
+                                      (long)L.wgate.row_bytes, T, Tp, st, 0, true));
         } else {
             ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, 2 * FD, T, E, st));
             ST(launch_swiglu_gu(m->pf_q8, m->pf_gu, T, FD, B, st, f_down ? m->pf_h : nullptr));

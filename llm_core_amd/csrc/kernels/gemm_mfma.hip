@@ -897,10 +897,9 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
     }
 }
 
-template <int RT, int TTW, int S, bool SW = false>
+template <int RT, int TTW, int S>
 void launch16_cfg(float* Y, const uint8_t* W, const uint8_t* XQ8, uint8_t* scratch, int rows,
-                  int nb, long row_bytes, int T, hipStream_t st, int accumulate,
-                  uint8_t* hq8 = nullptr, float* hf = nullptr) {
+                  int nb, long row_bytes, int T, hipStream_t st, int accumulate) {
     constexpr int TW = kTile * TTW;
     const int Tp = (T + TW - 1) / TW * TW, nkb = nb * 8;
     auto* xh = scratch;
@@ -911,8 +910,8 @@ void launch16_cfg(float* Y, const uint8_t* W, const uint8_t* XQ8, uint8_t* scrat
                        XQ8, T, Tp, nkb, xh, dxt, gxt);
     const int nrt = (rows + kTile * RT - 1) / (kTile * RT);
     const unsigned grid = (unsigned)((nrt + 7) / 8 * 8 * (Tp / TW));
-    hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S, SW>), dim3(grid), dim3(RT * 64), 0, st, Y, W,
-                       xh, dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, accumulate, hq8, hf);
+    hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S>), dim3(grid), dim3(RT * 64), 0, st, Y, W, xh,
+                       dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, accumulate);
 }
 
 // ---------------------------------------------------------------------------
@@ -1512,7 +1511,7 @@ hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int
     if (!gemm_mfma_q6k_ok(W, rows, nb, row_bytes)) return hipErrorInvalidValue;
     // wide token tiles on the fp16 matrix cores where 128 x 64 tiles still give
     // one workgroup per CU
-    if (T >= 64 && (long)((rows + 127) / 128) * ((T + 63) / 64) >= 256) {
+    if (gemm_f16_q6k_applies(W, rows, nb, row_bytes, T)) {
         launch6h(Y, static_cast<const uint8_t*>(W), static_cast<const uint8_t*>(XQ8),
                  static_cast<uint8_t*>(scratch), rows, nb, row_bytes, T, st, accumulate);
         return hipGetLastError();
@@ -1551,17 +1550,47 @@ hipError_t launch_gemm_mfma_q6k_q8(float* Y, const void* W, const void* XQ8, int
 // against 64-token workgroups and 3-deep rings
 constexpr int kF16MinTokens = 65;
 
-// ffn_gate|ffn_up interleaved by 8-row blocks, T >= 65 tokens: the fp16 GEMM
-// with the SwiGLU epilogue (h as Q8_0 blocks [T][rows/2], and fp32 rows when
-// hf is set); scratch as gemm_mfma_scratch_bytes
-hipError_t launch_gemm_f16_q4k_swiglu(uint8_t* hq8, float* hf, const void* W, const void* XQ8,
-                                      int rows, int T, int nb, long row_bytes, void* scratch,
-                                      hipStream_t st) {
-    if (T < kF16MinTokens || nb <= 0 || rows <= 0 || rows % 128 || scratch == nullptr)
+// The fp16 GEMMs on an activation re-layout written elsewhere (the prefill's
+// RMSNorm rows): xh, dxt (and gxt) as k_gemm_prep16 lays them out for Tp
+// tokens (Tp a multiple of the kernel's token group: 32 for Q4_K, 64 for
+// Q6_K).  Q4_K with swiglu: ffn_gate|ffn_up interleaved by 8-row blocks, the
+// SwiGLU epilogue of k_gemm_f16_q4k (h as Q8_0 blocks, and fp32 rows when hf is set).
+hipError_t launch_gemm_f16_q4k_xh(float* Y, uint8_t* hq8, float* hf, const void* W,
+                                  const uint8_t* xh, const float* dxt, const float* gxt, int rows,
+                                  int nb, long row_bytes, int T, int Tp, hipStream_t st,
+                                  int accumulate, bool swiglu) {
+    constexpr int RT = 8, TTW = 2, S = 2, TW = kTile * TTW;
+    if (rows <= 0 || nb <= 0 || T <= 0 || Tp < T || Tp % TW || (swiglu && rows % 128))
         return hipErrorInvalidValue;
-    launch16_cfg<8, 2, 2, true>(nullptr, static_cast<const uint8_t*>(W),
-                                static_cast<const uint8_t*>(XQ8), static_cast<uint8_t*>(scratch),
-                                rows, nb, row_bytes, T, st, 0, hq8, hf);
+    const int nrt = (rows + kTile * RT - 1) / (kTile * RT);
+    const unsigned grid = (unsigned)((nrt + 7) / 8 * 8 * (Tp / TW));
+    const auto* w = static_cast<const uint8_t*>(W);
+    if (swiglu)
+        hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S, true>), dim3(grid), dim3(RT * 64), 0, st,
+                           nullptr, w, xh, dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, 0, hq8, hf);
+    else
+        hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S, false>), dim3(grid), dim3(RT * 64), 0, st,
+                           Y, w, xh, dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, accumulate,
+                           nullptr, nullptr);
+    return hipGetLastError();
+}
+
+bool gemm_f16_q6k_applies(const void* W, int rows, int nb, long row_bytes, int T) {
+    return T >= 64 && (long)((rows + 127) / 128) * ((T + 63) / 64) >= 256 &&
+           gemm_mfma_q6k_ok(W, rows, nb, row_bytes);
+}
+
+hipError_t launch_gemm_f16_q6k_xh(float* Y, const void* W, const uint8_t* xh, const float* dxt,
+                                  int rows, int nb, long row_bytes, int T, int Tp, hipStream_t st,
+                                  int accumulate) {
+    constexpr int TW = kTile * kF16Q6TTW;
+    if (rows <= 0 || nb <= 0 || T <= 0 || Tp < T || Tp % TW || !gemm_mfma_q6k_ok(W, rows, nb, row_bytes))
+        return hipErrorInvalidValue;
+    const int nrt = (rows + kTile * kF16Q6RT - 1) / (kTile * kF16Q6RT);
+    const unsigned grid = (unsigned)((nrt + 7) / 8 * 8 * (Tp / TW));
+    hipLaunchKernelGGL((k_gemm_f16_q6k<kF16Q6RT, kF16Q6TTW, kF16Q6S>), dim3(grid),
+                       dim3(kF16Q6RT * 64), 0, st, Y, static_cast<const uint8_t*>(W), xh, dxt,
+                       rows, nb, row_bytes, T, Tp, nrt, accumulate);
     return hipGetLastError();
 }
 

@@ -136,6 +136,84 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(float* __restrict__ y,
     }
 }
 
+// The row RMSNorm of k_rmsnorm (same arithmetic, same Q8_0 blocks) that also
+// writes the prefill GEMMs' activation re-layout in the same pass, as
+// k_gemm_prep16 would from the blocks: for row t and Q8_0 block kb,
+//   xh[kb][g][Tp][8]  fp16 copies of values 8g..8g+7,
+//   dx2, gx2          d and d * (sum of the 32 int8) at the 32-token-group
+//                     index of the fp16 Q4_K GEMM,
+//   dx4               d at the 64-token-group index of the fp16 Q6_K GEMM.
+// The grid covers Tp rows: rows T..Tp-1 write zeros there (and nothing else).
+__global__ __launch_bounds__(kNormThreads) void k_rmsnorm_prep(
+    float* __restrict__ y, uint8_t* __restrict__ yq8, const float* __restrict__ x,
+    const float* __restrict__ w, int n, float eps, int T, int Tp, uint8_t* __restrict__ xh,
+    float* __restrict__ dx2, float* __restrict__ gx2, float* __restrict__ dx4) {
+    __shared__ float red[16];
+    const int t = blockIdx.x, n4 = n / 4;
+    auto idx = [&](int kb, int ttw) {  // k_gemm_prep16's dx index for 16*ttw-token groups
+        const int tw = 16 * ttw;
+        return (((size_t)kb * (Tp / tw) + t / tw) * 16 + (t & 15)) * ttw + ((t >> 4) % ttw);
+    };
+    if (t >= T) {  // padding rows: zero activations
+        for (int i4 = threadIdx.x; i4 < n4; i4 += kNormThreads) {
+            const int kb = i4 >> 3, sub = i4 & 7;
+            *reinterpret_cast<uint2*>(xh + (((size_t)kb * 4 + (sub >> 1)) * Tp + t) * 16 +
+                                      (sub & 1) * 8) = make_uint2(0u, 0u);
+            if (sub == 0) {
+                dx2[idx(kb, 2)] = 0.f;
+                gx2[idx(kb, 2)] = 0.f;
+                dx4[idx(kb, 4)] = 0.f;
+            }
+        }
+        return;  // the whole workgroup (before any barrier)
+    }
+    x += (size_t)t * n;
+    if (y) y += (size_t)t * n;
+    yq8 += (size_t)t * (n / 32) * Q8_0_BYTES;
+    float4 xv[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i4 = threadIdx.x + kNormThreads * k;
+        xv[k] = i4 < n4 ? reinterpret_cast<const float4*>(x)[i4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float s = rms_scale<kNormThreads, 8>(xv, n, eps, red);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i4 = threadIdx.x + kNormThreads * k;
+        if (i4 < n4) {  // the 8 lanes of a block share it
+            const float4 v = xv[k];
+            const float4 g = reinterpret_cast<const float4*>(w)[i4];
+            float4 o;
+            o.x = g.x * (v.x * s);
+            o.y = g.y * (v.y * s);
+            o.z = g.z * (v.z * s);
+            o.w = g.w * (v.w * s);
+            if (y) reinterpret_cast<float4*>(y)[i4] = o;
+            const int kb = i4 >> 3, sub = i4 & 7;
+            float d;
+            const uint32_t p = q8_quant4(o, d);  // q8_block_store's block
+            uint8_t* blk = yq8 + (size_t)kb * Q8_0_BYTES;
+            *reinterpret_cast<uint32_t*>(blk + 4 + 4 * sub) = p;
+            if (sub == 0) *reinterpret_cast<float*>(blk) = d;
+            // fp16 of the 4 int8, then d and d * sum for the block (8 lanes)
+            _Float16 hv[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) hv[e] = (_Float16)(float)(int8_t)(p >> (8 * e));
+            *reinterpret_cast<uint2*>(xh + (((size_t)kb * 4 + (sub >> 1)) * Tp + t) * 16 +
+                                      (sub & 1) * 8) = *reinterpret_cast<const uint2*>(hv);
+            int sum = dot4((int)p, 0x01010101, 0);
+            sum += __shfl_xor(sum, 1, 8);
+            sum += __shfl_xor(sum, 2, 8);
+            sum += __shfl_xor(sum, 4, 8);
+            if (sub == 0) {
+                dx2[idx(kb, 2)] = d;
+                gx2[idx(kb, 2)] = d * (float)sum;
+                dx4[idx(kb, 4)] = d;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // RoPE (rotate-half pairs (i, i+hd/2)) with the host-built cos/sin table:
 //   a = fma(x0, c, -(x1*s)),  b = fma(x0, s, x1*c)
@@ -465,6 +543,14 @@ hipError_t launch_rmsnorm_rows(float* y, void* yq8, const float* x, const float*
                                float eps, int rows, hipStream_t st) {
     hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(kNormThreads), 0, st, y,
                        static_cast<uint8_t*>(yq8), x, w, n, eps);
+    return hipGetLastError();
+}
+hipError_t launch_rmsnorm_rows_prep(float* y, void* yq8, const float* x, const float* w, int n,
+                                    float eps, int T, int Tp, uint8_t* xh, float* dx2, float* gx2,
+                                    float* dx4, hipStream_t st) {
+    if (n % 32 || n > 32 * kNormThreads || Tp % 64 || T > Tp || T <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rmsnorm_prep, dim3((unsigned)Tp), dim3(kNormThreads), 0, st, y,
+                       static_cast<uint8_t*>(yq8), x, w, n, eps, T, Tp, xh, dx2, gx2, dx4);
     return hipGetLastError();
 }
 hipError_t launch_rope_kv_rows(const float* k, int k_ld, const float* v, int v_ld,
