@@ -122,11 +122,15 @@ size_t gemm_mfma_q6k_scratch_bytes(int T, int nb);
 // 64 serves both).  Q6_K: where gemm_f16_q6k_applies.  Q4_K with swiglu: the
 // matrix is ffn_gate|ffn_up interleaved by blocks of 8 rows (rows % 128 ==
 // 0); SwiGLU runs in the epilogue and h is written as the Q8_0 blocks of
-// [T][rows/2] (hq8) and, when hf is set, as fp32 rows, instead of Y.
+// [T][rows/2] (hq8) and, when hf is set, as fp32 rows, instead of Y; with hxh
+// set (Tp % 64 == 0) also their re-layout for the down projection (as
+// launch_rmsnorm_rows_prep's, rows/64 blocks per token).
 hipError_t launch_gemm_f16_q4k_xh(float* Y, uint8_t* hq8, float* hf, const void* W,
                                   const uint8_t* xh, const float* dxt, const float* gxt, int rows,
                                   int nb, long row_bytes, int T, int Tp, hipStream_t st,
-                                  int accumulate, bool swiglu);
+                                  int accumulate, bool swiglu, uint8_t* hxh = nullptr,
+                                  float* hdx2 = nullptr, float* hgx2 = nullptr,
+                                  float* hdx4 = nullptr);
 bool gemm_f16_q6k_applies(const void* W, int rows, int nb, long row_bytes, int T);
 hipError_t launch_gemm_f16_q6k_xh(float* Y, const void* W, const uint8_t* xh, const float* dxt,
                                   int rows, int nb, long row_bytes, int T, int Tp, hipStream_t st,

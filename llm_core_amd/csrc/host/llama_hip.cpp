@@ -98,6 +98,9 @@ struct axf_llama {
     // the fp16 GEMMs' re-layout of the RMSNorm rows (launch_rmsnorm_rows_prep)
     uint8_t* pf_xh = nullptr;
     float *pf_dx2 = nullptr, *pf_gx2 = nullptr, *pf_dx4 = nullptr;
+    // and of h's Q8_0 blocks, written by the gate|up GEMM's SwiGLU epilogue
+    uint8_t* pf_hxh = nullptr;
+    float *pf_hdx2 = nullptr, *pf_hgx2 = nullptr, *pf_hdx4 = nullptr;
     // prefill attention: the matrix-core kernel, or (testing) the decode
     // split/combine kernels over a token grid
     bool pf_attn_split = false;
@@ -723,6 +726,13 @@ int prefill_alloc(axf_llama* m) {
         m->pf_dx2 = static_cast<float*>(p);
         m->pf_gx2 = m->pf_dx2 + nkb * tp;
         m->pf_dx4 = m->pf_gx2 + nkb * tp;
+        const size_t nkh = (size_t)FD / 32;
+        LL_TRY(dalloc(m, nkh * tp * 64, &p));
+        m->pf_hxh = static_cast<uint8_t*>(p);
+        LL_TRY(dalloc(m, nkh * tp * 4 * 3, &p));
+        m->pf_hdx2 = static_cast<float*>(p);
+        m->pf_hgx2 = m->pf_hdx2 + nkh * tp;
+        m->pf_hdx4 = m->pf_hgx2 + nkh * tp;
     }
     m->pf_cap = cap;
     return AXF_OK;
@@ -908,6 +918,7 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     // where the down projection is of another type)
     const bool f_gu = !kquant(L.wgate.qtype) || !kquant(L.wup.qtype);
     const bool f_down = !kquant(L.wdown.qtype);
+    bool h_prep = false;  // the SwiGLU epilogue wrote h's re-layout (pf_hxh ...)
     ST(norm_rows(L.ffn_norm, f_gu ? m->pf_xb : nullptr));
     xb_ready = false;
     if (L.gu_interleaved) {
@@ -917,7 +928,9 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
             // reads its re-laid copy of the input blocks, so h may overwrite them)
             ST(launch_gemm_f16_q4k_xh(nullptr, m->pf_q8, f_down ? m->pf_h : nullptr, L.wgate.d,
                                       m->pf_xh, m->pf_dx2, m->pf_gx2, 2 * FD, nbE,
-                                      (long)L.wgate.row_bytes, T, Tp, st, 0, true));
+                                      (long)L.wgate.row_bytes, T, Tp, st, 0, true, m->pf_hxh,
+                                      m->pf_hdx2, m->pf_hgx2, m->pf_hdx4));
+            h_prep = true;
         } else {
             ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, 2 * FD, T, E, st));
             ST(launch_swiglu_gu(m->pf_q8, m->pf_gu, T, FD, B, st, f_down ? m->pf_h : nullptr));
@@ -929,8 +942,16 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
         ST(launch_swiglu(f_down ? m->pf_h : nullptr, m->pf_q8, m->pf_gu,
                          m->pf_gu + (size_t)T * FD, T * FD, st));
     }
-    // x += down
-    if (kquant(L.wdown.qtype)) {
+    // x += down (on h's re-layout where the epilogue wrote it)
+    const int nbF = FD / QK_K;
+    if (h_prep && L.wdown.qtype == AXF_TYPE_Q4_K) {
+        ST(launch_gemm_f16_q4k_xh(m->pf_x, nullptr, nullptr, L.wdown.d, m->pf_hxh, m->pf_hdx2,
+                                  m->pf_hgx2, E, nbF, (long)L.wdown.row_bytes, T, Tp, st, 1, false));
+    } else if (h_prep && L.wdown.qtype == AXF_TYPE_Q6_K &&
+               gemm_f16_q6k_applies(L.wdown.d, E, nbF, (long)L.wdown.row_bytes, T)) {
+        ST(launch_gemm_f16_q6k_xh(m->pf_x, L.wdown.d, m->pf_hxh, m->pf_hdx4, E, nbF,
+                                  (long)L.wdown.row_bytes, T, Tp, st, 1));
+    } else if (kquant(L.wdown.qtype)) {
         ST(gemm_rows_add(m, L.wdown, m->pf_x, m->pf_q8, E, T, FD, m->pf_tmp, st));
     } else {
         ST(gemm_misc_add(m, L.wdown, m->pf_x, m->pf_q8, m->pf_h, E, T, FD, st));

@@ -796,13 +796,18 @@ __device__ __forceinline__ void gemm16_step(
 // rows, then the same 8 up rows), so a workgroup's 128 rows are 64
 // consecutive SwiGLU pairs: the epilogue writes h = swiglu(gate, up) as the
 // Q8_0 blocks of [T][rows / 2] (hq8) and, when hf is set, as fp32 rows,
-// instead of Y; the arithmetic of k_swiglu_gu.
+// instead of Y; the arithmetic of k_swiglu_gu.  With hxh set it also writes
+// those blocks' re-layout for the down projection's fp16 GEMM (hxh, hdx2,
+// hgx2, hdx4 as k_rmsnorm_prep's, for the Tp tokens of the grid; tokens T..Tp-1
+// zero).
 template <int RT, int TTW, int S, bool SW = false>
 __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
     float* __restrict__ Y, const uint8_t* __restrict__ W, const uint8_t* __restrict__ xh,
     const float* __restrict__ dxt, const float* __restrict__ gxt, int rows, int nb,
     long row_bytes, int T, int Tp, int nrt, int accumulate, uint8_t* __restrict__ hq8 = nullptr,
-    float* __restrict__ hf = nullptr) {
+    float* __restrict__ hf = nullptr, uint8_t* __restrict__ hxh = nullptr,
+    float* __restrict__ hdx2 = nullptr, float* __restrict__ hgx2 = nullptr,
+    float* __restrict__ hdx4 = nullptr) {
     using G = Stage16<RT, TTW, S>;
     constexpr int NW = G::NW, RW = G::RW, TW = G::TW;
     __shared__ __attribute__((aligned(16))) uint8_t smem[S * G::ALLOC];
@@ -872,10 +877,35 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
         for (int q = threadIdx.x; q < TW * 16; q += RT * 64) {
             const int tl = q >> 4, half = (q >> 3) & 1, sub = q & 7, tok = tok_base + tl;
             const float4 o = *reinterpret_cast<const float4*>(hs + tl * 64 + 32 * half + 4 * sub);
-            if (tok < T) {  // the 8 lanes of a block share the token
+            // the 8 lanes of a block share the token
+            const int kb = 2 * rt + half;  // block of h's row
+            float d = 0.f;
+            uint32_t p = 0u;
+            if (tok < T) {
                 const size_t e = (size_t)tok * nh + 64 * rt + 32 * half + 4 * sub;
                 if (hf) *reinterpret_cast<float4*>(hf + e) = o;
-                q8_block_store(hq8 + (e >> 5) * Q8_0_BYTES, sub, o);
+                p = q8_quant4(o, d);  // q8_block_store's block
+                uint8_t* blk = hq8 + (e >> 5) * Q8_0_BYTES;
+                *reinterpret_cast<uint32_t*>(blk + 4 + 4 * sub) = p;
+                if (sub == 0) *reinterpret_cast<float*>(blk) = d;
+            }
+            if (hxh) {  // k_gemm_prep16's re-layout of the block (zeros past T)
+                _Float16 hv[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) hv[e] = (_Float16)(float)(int8_t)(p >> (8 * e));
+                *reinterpret_cast<uint2*>(hxh + (((size_t)kb * 4 + (sub >> 1)) * Tp + tok) * 16 +
+                                          (sub & 1) * 8) = *reinterpret_cast<const uint2*>(hv);
+                int sum = dot4((int)p, 0x01010101, 0);
+                sum += __shfl_xor(sum, 1, 8);
+                sum += __shfl_xor(sum, 2, 8);
+                sum += __shfl_xor(sum, 4, 8);
+                if (sub == 0) {
+                    const size_t i2 = (((size_t)kb * (Tp / 32) + tok / 32) * 16 + (tok & 15)) * 2 + ((tok >> 4) & 1);
+                    const size_t i4 = (((size_t)kb * (Tp / 64) + tok / 64) * 16 + (tok & 15)) * 4 + ((tok >> 4) & 3);
+                    hdx2[i2] = d;
+                    hgx2[i2] = d * (float)sum;
+                    hdx4[i4] = d;
+                }
             }
         }
         return;
@@ -1558,20 +1588,22 @@ constexpr int kF16MinTokens = 65;
 hipError_t launch_gemm_f16_q4k_xh(float* Y, uint8_t* hq8, float* hf, const void* W,
                                   const uint8_t* xh, const float* dxt, const float* gxt, int rows,
                                   int nb, long row_bytes, int T, int Tp, hipStream_t st,
-                                  int accumulate, bool swiglu) {
+                                  int accumulate, bool swiglu, uint8_t* hxh, float* hdx2,
+                                  float* hgx2, float* hdx4) {
     constexpr int RT = 8, TTW = 2, S = 2, TW = kTile * TTW;
-    if (rows <= 0 || nb <= 0 || T <= 0 || Tp < T || Tp % TW || (swiglu && rows % 128))
+    if (rows <= 0 || nb <= 0 || T <= 0 || Tp < T || Tp % TW || (swiglu && rows % 128) ||
+        (hxh && (Tp % 64 || !hdx2 || !hgx2 || !hdx4)))
         return hipErrorInvalidValue;
     const int nrt = (rows + kTile * RT - 1) / (kTile * RT);
     const unsigned grid = (unsigned)((nrt + 7) / 8 * 8 * (Tp / TW));
     const auto* w = static_cast<const uint8_t*>(W);
     if (swiglu)
         hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S, true>), dim3(grid), dim3(RT * 64), 0, st,
-                           nullptr, w, xh, dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, 0, hq8, hf);
+                           nullptr, w, xh, dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, 0, hq8, hf,
+                           hxh, hdx2, hgx2, hdx4);
     else
         hipLaunchKernelGGL((k_gemm_f16_q4k<RT, TTW, S, false>), dim3(grid), dim3(RT * 64), 0, st,
-                           Y, w, xh, dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, accumulate,
-                           nullptr, nullptr);
+                           Y, w, xh, dxt, gxt, rows, nb, row_bytes, T, Tp, nrt, accumulate);
     return hipGetLastError();
 }
 

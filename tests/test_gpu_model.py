@@ -411,18 +411,20 @@ def test_forward_batch_qwen25_3b_layer(ctx):
     _check_prefill(gl, ol, max(noise, 1e-3))
 
 
-@pytest.mark.parametrize("down", ["q6_k", "q8_0"])
+@pytest.mark.parametrize("down", ["q6_k", "q4_k", "q8_0"])
 def test_forward_batch_swiglu_epilogue(ctx, down):
     """Hidden 2304 (9 super-blocks per row: ffn_gate|ffn_up interleaved by
     8-row blocks) prefilling 80 tokens: the fp16 gate|up GEMM writes SwiGLU's
-    Q8_0 blocks in its epilogue (and, for a Q8_0 down projection, which takes
-    the fp32 rows, those too); last-row logits and residual against the
-    oracle's batch."""
-    from llm_core_amd.model import AXF_TYPE_Q8_0, Q4K_M_TYPES
+    Q8_0 blocks in its epilogue, with their fp16 re-layout, which a Q4_K down
+    projection reads (the fp16 Q6_K kernel would, at 256 tiles and more), and
+    for a Q8_0 down projection, which takes the fp32 rows, those too; last-row
+    logits and residual against the oracle's batch."""
+    from llm_core_amd.model import AXF_TYPE_Q4_K, AXF_TYPE_Q8_0, Q4K_M_TYPES
 
     cfg = dict(n_layer=1, n_embd=2304, n_heads=18, n_kv_heads=6, ffn_dim=1024, n_vocab=512,
                n_ctx=96, rms_eps=1e-5, rope_theta=10000.0)
-    types = dict(Q4K_M_TYPES, ffn_down=AXF_TYPE_Q8_0) if down == "q8_0" else None
+    types = {"q6_k": None, "q4_k": dict(Q4K_M_TYPES, ffn_down=AXF_TYPE_Q4_K),
+             "q8_0": dict(Q4K_M_TYPES, ffn_down=AXF_TYPE_Q8_0)}[down]
     gl, ol, gx, ox, noise = _prefill_case(ctx, cfg, 5, 80, layer_types=types)
     _check_prefill(gl, ol, noise)
     rel = np.linalg.norm(gx.astype(np.float64) - ox) / np.linalg.norm(ox)
