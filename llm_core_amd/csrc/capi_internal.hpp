@@ -244,6 +244,11 @@ struct AttnArgs {
     // Batched prefill: n_tok query rows (0 means 1), row t at q + t*q_ld, at
     // position pos + t, attending to cache rows 0..pos+t (store_kv must be 0).
     int n_tok, q_ld, out_ld;
+    // prefill (k_attn_prefill_ks): when xh is set, also the out rows' Q8_0
+    // blocks re-laid for the fp16 GEMMs for Tp tokens (as launch_rmsnorm_rows_prep)
+    uint8_t* xh;
+    float *dx2, *gx2, *dx4;
+    int Tp;
 };
 int attn_nsplit(int max_seq);
 hipError_t launch_attention_fused(const AttnArgs& a, int head_dim, hipStream_t st);

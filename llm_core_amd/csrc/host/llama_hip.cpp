@@ -718,8 +718,8 @@ int prefill_alloc(axf_llama* m) {
     }
     LL_TRY(dalloc(m, gs, &p));
     m->pf_gemm = static_cast<uint8_t*>(p);
-    {  // the RMSNorm rows' fp16 re-layout, 64-token padding
-        const size_t tp = (C + 63) / 64 * 64, nkb = (size_t)E / 32;
+    {  // the RMSNorm rows' (and attention rows') fp16 re-layout, 64-token padding
+        const size_t tp = (C + 63) / 64 * 64, nkb = (size_t)(E > qo ? E : qo) / 32;
         LL_TRY(dalloc(m, nkb * tp * 64, &p));
         m->pf_xh = static_cast<uint8_t*>(p);
         LL_TRY(dalloc(m, nkb * tp * 4 * 3, &p));
@@ -886,6 +886,9 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
         ST(launch_rope_kv_rows(k, k_ld, m->pf_v, kvo, L.bk, L.bv, m->kv_k + loff,
                                m->kv_v + loff, pos0, T, KVH, HD, m->rope_cos, m->rope_sin, st));
     }
+    // above 64 tokens the key-split attention (head dimension <= 128) also writes
+    // the o projection's re-layout of its Q8_0 rows
+    const bool o_prep = prep && !m->pf_attn_split && HD <= 128 && qo % QK_K == 0;
     {
         AttnArgs a{};
         a.q = q;
@@ -905,11 +908,26 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
         a.n_tok = T;
         a.q_ld = q_ld;
         a.out_ld = qo;
+        if (o_prep) {  // the o projection's re-layout (the q|k|v GEMMs are done with pf_xh)
+            a.xh = m->pf_xh;
+            a.dx2 = m->pf_dx2;
+            a.gx2 = m->pf_gx2;
+            a.dx4 = m->pf_dx4;
+            a.Tp = Tp;
+        }
         ST(m->pf_attn_split ? launch_attention_fused(a, HD, st)
                             : launch_attention_prefill(a, HD, st));
     }
     // x += o (the attention's fp32 rows pf_ao and their Q8_0 pf_q8)
-    if (kquant(L.wo.qtype)) {
+    const int nbO = qo / QK_K;
+    if (o_prep && L.wo.qtype == AXF_TYPE_Q4_K) {
+        ST(launch_gemm_f16_q4k_xh(m->pf_x, nullptr, nullptr, L.wo.d, m->pf_xh, m->pf_dx2,
+                                  m->pf_gx2, E, nbO, (long)L.wo.row_bytes, T, Tp, st, 1, false));
+    } else if (o_prep && L.wo.qtype == AXF_TYPE_Q6_K &&
+               gemm_f16_q6k_applies(L.wo.d, E, nbO, (long)L.wo.row_bytes, T)) {
+        ST(launch_gemm_f16_q6k_xh(m->pf_x, L.wo.d, m->pf_xh, m->pf_dx4, E, nbO, (long)L.wo.row_bytes,
+                                  T, Tp, st, 1));
+    } else if (kquant(L.wo.qtype)) {
         ST(gemm_rows_add(m, L.wo, m->pf_x, m->pf_q8, E, T, qo, m->pf_tmp, st));
     } else {
         ST(gemm_misc_add(m, L.wo, m->pf_x, m->pf_q8, m->pf_ao, E, T, qo, st));

@@ -822,13 +822,40 @@ __global__ __launch_bounds__(kPfKsWaves * 64) void k_attn_prefill_ks(AttnArgs a,
         v = make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
         // the 8 lanes of a Q8_0 block are consecutive and share r: all store or none
         if (tl < QT && qt0 + tl < n_tok) {
-            const size_t e0 = (size_t)(qt0 + tl) * a.out_ld + (size_t)(kvh * G + r % G) * HD + 4 * c4;
+            const int t = qt0 + tl;
+            const size_t e0 = (size_t)t * a.out_ld + (size_t)(kvh * G + r % G) * HD + 4 * c4;
             float* dst = a.out + e0;
             dst[0] = v.x;
             dst[1] = v.y;
             dst[2] = v.z;
             dst[3] = v.w;
-            if (a.outq8) q8_store4(a.outq8 + (e0 >> 5) * Q8_0_BYTES, c4 & 7, v);
+            if (a.outq8) {
+                const int sub = c4 & 7;
+                float d;
+                const uint32_t p = q8_quant4(v, d);  // q8_store4's block
+                uint8_t* blk = a.outq8 + (e0 >> 5) * Q8_0_BYTES;
+                *reinterpret_cast<uint32_t*>(blk + 4 + 4 * sub) = p;
+                if (sub == 0) *reinterpret_cast<float*>(blk) = d;
+                if (a.xh) {  // k_gemm_prep16's re-layout of the block (out_ld % 32 == 0)
+                    const int kb = (int)((e0 - (size_t)t * a.out_ld) >> 5), Tp = a.Tp;
+                    _Float16 hv[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) hv[e] = (_Float16)(float)(int8_t)(p >> (8 * e));
+                    *reinterpret_cast<uint2*>(a.xh + (((size_t)kb * 4 + (sub >> 1)) * Tp + t) * 16 +
+                                              (sub & 1) * 8) = *reinterpret_cast<const uint2*>(hv);
+                    int sum = dot4((int)p, 0x01010101, 0);
+                    sum += __shfl_xor(sum, 1, 8);
+                    sum += __shfl_xor(sum, 2, 8);
+                    sum += __shfl_xor(sum, 4, 8);
+                    if (sub == 0) {
+                        const size_t i2 = (((size_t)kb * (Tp / 32) + t / 32) * 16 + (t & 15)) * 2 + ((t >> 4) & 1);
+                        const size_t i4 = (((size_t)kb * (Tp / 64) + t / 64) * 16 + (t & 15)) * 4 + ((t >> 4) & 3);
+                        a.dx2[i2] = d;
+                        a.gx2[i2] = d * (float)sum;
+                        a.dx4[i4] = d;
+                    }
+                }
+            }
         }
     }
 }
