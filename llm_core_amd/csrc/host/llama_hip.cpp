@@ -824,22 +824,31 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     // q|k, v and gate|up GEMMs and the fp16 Q6_K v GEMM in place of their own
     const bool prep = T > kGemmStreamMaxT;
     const int Tp = (T + 63) / 64 * 64, nbE = E / QK_K;
-    auto norm_rows = [&](const float* w, float* fp32_rows) -> hipError_t {
-        if (!prep) return launch_rmsnorm_rows(fp32_rows, m->pf_q8, m->pf_x, w, E, hp.rms_eps, T, st);
+    auto norm_rows = [&](const float* w, float* fp32_rows, bool re_layout) -> hipError_t {
+        if (!re_layout)
+            return launch_rmsnorm_rows(fp32_rows, m->pf_q8, m->pf_x, w, E, hp.rms_eps, T, st);
         return launch_rmsnorm_rows_prep(fp32_rows, m->pf_q8, m->pf_x, w, E, hp.rms_eps, T, Tp,
                                         m->pf_xh, m->pf_dx2, m->pf_gx2, m->pf_dx4, st);
     };
+    // the re-layout only where a projection reads it
+    auto reads_xh = [&](const DevW& w, int rows) {
+        return w.qtype == AXF_TYPE_Q4_K ||
+               (w.qtype == AXF_TYPE_Q6_K && gemm_f16_q6k_applies(w.d, rows, nbE, (long)w.row_bytes, T));
+    };
+    const bool qkv_xh = prep && (reads_xh(L.wq, L.qk_fused ? qo + kvo : qo) ||
+                                 (!L.qk_fused && reads_xh(L.wk, kvo)) || reads_xh(L.wv, kvo));
     // Y = W rows of the normalised rows: the prepared fp16 GEMMs where they apply
     auto proj = [&](const DevW& w, float* Y, int rows, bool* xf_ready) -> hipError_t {
-        if (prep && w.qtype == AXF_TYPE_Q4_K)
+        if (!qkv_xh) return gemm_any(m, w, Y, m->pf_q8, m->pf_xb, rows, T, E, st, xf_ready);
+        if (w.qtype == AXF_TYPE_Q4_K)
             return launch_gemm_f16_q4k_xh(Y, nullptr, nullptr, w.d, m->pf_xh, m->pf_dx2, m->pf_gx2,
                                           rows, nbE, (long)w.row_bytes, T, Tp, st, 0, false);
-        if (prep && w.qtype == AXF_TYPE_Q6_K && gemm_f16_q6k_applies(w.d, rows, nbE, (long)w.row_bytes, T))
+        if (w.qtype == AXF_TYPE_Q6_K && gemm_f16_q6k_applies(w.d, rows, nbE, (long)w.row_bytes, T))
             return launch_gemm_f16_q6k_xh(Y, w.d, m->pf_xh, m->pf_dx4, rows, nbE, (long)w.row_bytes,
                                           T, Tp, st, 0);
         return gemm_any(m, w, Y, m->pf_q8, m->pf_xb, rows, T, E, st, xf_ready);
     };
-    ST(norm_rows(L.attn_norm, f_qkv ? m->pf_xb : nullptr));
+    ST(norm_rows(L.attn_norm, f_qkv ? m->pf_xb : nullptr, qkv_xh));
     bool xb_ready = false;  // the GEMM scratch holds pf_xb's prepared rows (misc types)
     float* q = m->pf_qk;
     float* k;
@@ -888,7 +897,8 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     }
     // above 64 tokens the key-split attention (head dimension <= 128) also writes
     // the o projection's re-layout of its Q8_0 rows
-    const bool o_prep = prep && !m->pf_attn_split && HD <= 128 && qo % QK_K == 0;
+    const bool o_prep = prep && !m->pf_attn_split && HD <= 128 && kquant(L.wo.qtype) &&
+                        qo % QK_K == 0;
     {
         AttnArgs a{};
         a.q = q;
@@ -936,19 +946,26 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
     // where the down projection is of another type)
     const bool f_gu = !kquant(L.wgate.qtype) || !kquant(L.wup.qtype);
     const bool f_down = !kquant(L.wdown.qtype);
-    bool h_prep = false;  // the SwiGLU epilogue wrote h's re-layout (pf_hxh ...)
-    ST(norm_rows(L.ffn_norm, f_gu ? m->pf_xb : nullptr));
+    const int B = L.gu_interleaved ? qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2 : 0;
+    // SwiGLU in the fp16 gate|up GEMM's epilogue, on the norm's re-layout
+    const bool sw = L.gu_interleaved && L.wgate.qtype == AXF_TYPE_Q4_K && B == 8 && prep &&
+                    (2 * FD) % 128 == 0;
+    const int nbF = FD / QK_K;
+    // and h's re-layout from the epilogue where the down projection reads it
+    const bool h_prep = sw && (L.wdown.qtype == AXF_TYPE_Q4_K ||
+                               (L.wdown.qtype == AXF_TYPE_Q6_K &&
+                                gemm_f16_q6k_applies(L.wdown.d, E, nbF, (long)L.wdown.row_bytes, T)));
+    ST(norm_rows(L.ffn_norm, f_gu ? m->pf_xb : nullptr, sw));
     xb_ready = false;
     if (L.gu_interleaved) {
-        const int B = qgemv_rows_per_wg(E / QK_K, gateup_threads(E)) / 2;
-        if (L.wgate.qtype == AXF_TYPE_Q4_K && B == 8 && T > kGemmStreamMaxT && (2 * FD) % 128 == 0) {
+        if (sw) {
             // SwiGLU and its Q8_0 blocks in the fp16 GEMM's epilogue (the GEMM
             // reads its re-laid copy of the input blocks, so h may overwrite them)
             ST(launch_gemm_f16_q4k_xh(nullptr, m->pf_q8, f_down ? m->pf_h : nullptr, L.wgate.d,
                                       m->pf_xh, m->pf_dx2, m->pf_gx2, 2 * FD, nbE,
-                                      (long)L.wgate.row_bytes, T, Tp, st, 0, true, m->pf_hxh,
-                                      m->pf_hdx2, m->pf_hgx2, m->pf_hdx4));
-            h_prep = true;
+                                      (long)L.wgate.row_bytes, T, Tp, st, 0, true,
+                                      h_prep ? m->pf_hxh : nullptr, m->pf_hdx2, m->pf_hgx2,
+                                      m->pf_hdx4));
         } else {
             ST(gemm_rows(m, L.wgate, m->pf_gu, m->pf_q8, 2 * FD, T, E, st));
             ST(launch_swiglu_gu(m->pf_q8, m->pf_gu, T, FD, B, st, f_down ? m->pf_h : nullptr));
@@ -961,12 +978,10 @@ hipError_t enqueue_prefill_layer(axf_llama* m, int l, int T, int pos0) {
                          m->pf_gu + (size_t)T * FD, T * FD, st));
     }
     // x += down (on h's re-layout where the epilogue wrote it)
-    const int nbF = FD / QK_K;
     if (h_prep && L.wdown.qtype == AXF_TYPE_Q4_K) {
         ST(launch_gemm_f16_q4k_xh(m->pf_x, nullptr, nullptr, L.wdown.d, m->pf_hxh, m->pf_hdx2,
                                   m->pf_hgx2, E, nbF, (long)L.wdown.row_bytes, T, Tp, st, 1, false));
-    } else if (h_prep && L.wdown.qtype == AXF_TYPE_Q6_K &&
-               gemm_f16_q6k_applies(L.wdown.d, E, nbF, (long)L.wdown.row_bytes, T)) {
+    } else if (h_prep) {  // Q6_K where the fp16 kernel applies
         ST(launch_gemm_f16_q6k_xh(m->pf_x, L.wdown.d, m->pf_hxh, m->pf_hdx4, E, nbF,
                                   (long)L.wdown.row_bytes, T, Tp, st, 1));
     } else if (kquant(L.wdown.qtype)) {
