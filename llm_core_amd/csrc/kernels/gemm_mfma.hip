@@ -1703,7 +1703,16 @@ hipError_t launch_gemm_mfma_q4k_q8(float* Y, const void* W, const void* XQ8, int
         const auto* w = static_cast<const uint8_t*>(W);
         const auto* xq = static_cast<const uint8_t*>(XQ8);
         auto* sc = static_cast<uint8_t*>(scratch);
-        launch16_cfg<8, 2, 2>(Y, w, xq, sc, rows, nb, row_bytes, T, st, accumulate);
+        // 128-row tiles; 64- or 32-row tiles where those leave fewer than 256
+        // workgroups (the 896-row matrices of hidden-896 models)
+        const long ntg = (T + 31) / 32;
+        auto wgs = [&](int rt) { return (long)((rows + kTile * rt - 1) / (kTile * rt)) * ntg; };
+        if (wgs(8) >= 256)
+            launch16_cfg<8, 2, 2>(Y, w, xq, sc, rows, nb, row_bytes, T, st, accumulate);
+        else if (wgs(4) >= 256)
+            launch16_cfg<4, 2, 2>(Y, w, xq, sc, rows, nb, row_bytes, T, st, accumulate);
+        else
+            launch16_cfg<2, 2, 2>(Y, w, xq, sc, rows, nb, row_bytes, T, st, accumulate);
         return hipGetLastError();
     }
     if (accumulate) return hipErrorInvalidValue;  // the int8 kernels below overwrite Y

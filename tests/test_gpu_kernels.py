@@ -202,7 +202,10 @@ GEMM_CASES = [(11008, 4096, 1), (11008, 4096, 4), (1024, 4096, 16), (512, 4096, 
               (11008, 4096, 16), (11008, 4096, 64),  # config 4 at full size
               (75, 11008, 5), (33, 256, 9), (40, 512, 17), (300, 1024, 33), (64, 768, 130),
               # the fp16 matrix-core kernel (65+ tokens): ragged 128-row and 64-token tiles
-              (300, 1024, 200), (520, 2048, 65), (1100, 4096, 96)]
+              # (32-row tiles below 256 workgroups of 64 rows)
+              (300, 1024, 200), (520, 2048, 65), (1100, 4096, 96),
+              # 64-row tiles (fewer than 256 workgroups of 128 rows)
+              (1536, 1024, 512)]
 
 
 @functools.lru_cache(maxsize=2)
