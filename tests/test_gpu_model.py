@@ -431,6 +431,18 @@ def test_forward_batch_swiglu_epilogue(ctx, down):
     assert rel < 1e-3 or noise > 1e-3, f"final-norm row relative error {rel}"
 
 
+def test_forward_batch_swiglu_epilogue_in_chunks(ctx):
+    """The same model prefilling 160 tokens as two 80-token calls (the second at
+    position 80: the re-layouts of a chunk that attends to the cache rows of
+    the first) against the oracle's single batch."""
+    cfg = dict(n_layer=1, n_embd=2304, n_heads=18, n_kv_heads=6, ffn_dim=1024, n_vocab=512,
+               n_ctx=192, rms_eps=1e-5, rope_theta=10000.0)
+    gl, ol, gx, ox, noise = _prefill_case(ctx, cfg, 6, 160, splits=(80,))
+    _check_prefill(gl, ol, noise)
+    rel = np.linalg.norm(gx.astype(np.float64) - ox) / np.linalg.norm(ox)
+    assert rel < 1e-3 or noise > 1e-3, f"final-norm row relative error {rel}"
+
+
 @pytest.mark.parametrize("order", [1, 2])
 def test_forward_batch_qk_norm(ctx, order):
     """Per-head q/k RMSNorm before RoPE (qwen3) or after it (hunyuan-dense),
