@@ -118,22 +118,35 @@ def c3_run(ctx, warmup=10, steps=100):
     from llm_core_amd import hip
     from llm_core_amd.model import QWEN25_3B_LAYER, Hparams, LlamaHip, SynthLlama
 
-    hp = Hparams(n_ctx=1025, **{**QWEN25_3B_LAYER, "n_vocab": 512})
-    model = SynthLlama(hp, seed=7, with_bias=True)
-    kve = hp.n_kv_heads * hp.head_dim
     pos = 1024
-    k = hip.synth_normal(hp.n_ctx * kve, 701).reshape(hp.n_ctx, kve)
-    v = hip.synth_normal(hp.n_ctx * kve, 702).reshape(hp.n_ctx, kve)
-    with LlamaHip(ctx, model) as gpu:
-        gpu.set_kv(0, k, v, pos)
-        ms = gpu.bench_decode(pos, warmup, steps) / steps
-    nbytes = model.weight_bytes_per_token() + 2 * pos * kve * 4
+
+    def step_ms(n_layer):
+        hp = Hparams(n_ctx=1025, **{**QWEN25_3B_LAYER, "n_vocab": 512, "n_layer": n_layer})
+        model = SynthLlama(hp, seed=7, with_bias=True)
+        kve = hp.n_kv_heads * hp.head_dim
+        k = hip.synth_normal(hp.n_ctx * kve, 701).reshape(hp.n_ctx, kve)
+        v = hip.synth_normal(hp.n_ctx * kve, 702).reshape(hp.n_ctx, kve)
+        with LlamaHip(ctx, model) as gpu:
+            for layer in range(n_layer):
+                gpu.set_kv(layer, k, v, pos)
+            ms = gpu.bench_decode(pos, warmup, steps) / steps
+        return ms, model.weight_bytes_per_token() + 2 * n_layer * pos * kve * 4
+
+    ms, nbytes = step_ms(1)
+    # the decoder layer alone: a 2-layer model's step minus the 1-layer model's
+    # (the same embedding, head and argmax in both)
+    ms2, nbytes2 = step_ms(2)
+    lay_us, lay_bytes = (ms2 - ms) * 1e3, nbytes2 - nbytes
     log(f"config 3 layer (1-layer model, vocab 512) decode step @pos {pos}: {ms * 1e3:.1f} us, "
-        f"{nbytes / (ms * 1e-3) / 1e9:.0f} GB/s over {nbytes / 1e6:.1f} MB")
+        f"{nbytes / (ms * 1e-3) / 1e9:.0f} GB/s over {nbytes / 1e6:.1f} MB; the layer alone "
+        f"(2-layer step - 1-layer step): {lay_us:.1f} us, {lay_bytes / (lay_us * 1e-6) / 1e9:.0f} "
+        f"GB/s over {lay_bytes / 1e6:.1f} MB")
     return {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": int(nbytes),
             "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "layer_us": round(lay_us, 2), "layer_bytes": int(lay_bytes),
             "what": "decode step of a 1-layer Qwen2.5-3B-like model (vocab 512) at position "
-                    "1024: the layer plus embedding, a 512-row head and argmax"}
+                    "1024: the layer plus embedding, a 512-row head and argmax; layer_us: a "
+                    "2-layer model's step minus it (the decoder layer alone)"}
 
 
 def qwen05b_run(ctx, warmup=10, steps=50, n_ctx=2048):
