@@ -615,6 +615,27 @@ typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// Rows o..o+3 of one token's output row y (o % 4 == 0): y[o+i] = v[i], or
+// y[o+i] + v[i] when accumulating; one 16-byte access when vec (rows % 4 == 0
+// and y 16-byte aligned), else per row below `rows`.
+__device__ __forceinline__ void store_rows4(float* __restrict__ y, int o, int rows, v4f_t v,
+                                            int accumulate, bool vec) {
+    if (vec) {
+        if (o >= rows) return;
+        float4* p = reinterpret_cast<float4*>(y + o);
+        float4 r = make_float4(v[0], v[1], v[2], v[3]);
+        if (accumulate) {
+            const float4 a = *p;
+            r = make_float4(a.x + v[0], a.y + v[1], a.z + v[2], a.w + v[3]);
+        }
+        *p = r;
+        return;
+    }
+#pragma unroll
+    for (int ii = 0; ii < 4; ii++)
+        if (o + ii < rows) y[o + ii] = accumulate ? y[o + ii] + v[ii] : v[ii];
+}
+
 // Activation re-layout for the fp16 kernel (TW = 16*TTW tokens per workgroup,
 // Tp % TW == 0; slots past T zero):
 //   xh [kb][g][t][8]                   fp16 copies of values 8g..8g+7 of record kb
@@ -910,20 +931,15 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q4k(
         }
         return;
     }
+    // a lane's 4 consecutive rows of one token as one 16-byte access where
+    // rows % 4 == 0 (the same adds)
+    const bool vec = (rows & 3) == 0 && ((uintptr_t)Y & 15) == 0;
 #pragma unroll
     for (int j = 0; j < TTW; j++) {
         const v4f_t v = acc[j] - macc[j];
         const int tok = tok_base + 16 * j + col;
-        if (tok < T) {
-#pragma unroll
-            for (int ii = 0; ii < 4; ii++) {
-                const int o = row_base + kTile * wave + 4 * g + ii;
-                if (o < rows) {
-                    float* y = Y + (size_t)tok * rows + o;
-                    *y = accumulate ? *y + v[ii] : v[ii];
-                }
-            }
-        }
+        if (tok < T) store_rows4(Y + (size_t)tok * rows, row_base + kTile * wave + 4 * g, rows,
+                                 v, accumulate, vec);
     }
 }
 
@@ -1429,19 +1445,12 @@ __global__ __launch_bounds__(RT * 64) void k_gemm_f16_q6k(
                                 inext < nb, inext, i, nb, base, aux, wrsrc, wave, col, g, wlo,
                                 acc);
     }
+    const bool vec = (rows & 3) == 0 && ((uintptr_t)Y & 15) == 0;
 #pragma unroll
     for (int j = 0; j < TTW; j++) {
         const int tok = tok_base + 16 * j + col;
-        if (tok < T) {
-#pragma unroll
-            for (int ii = 0; ii < 4; ii++) {
-                const int o = row_base + kTile * wave + 4 * g + ii;
-                if (o < rows) {
-                    float* y = Y + (size_t)tok * rows + o;
-                    *y = accumulate ? *y + acc[j][ii] : acc[j][ii];
-                }
-            }
-        }
+        if (tok < T) store_rows4(Y + (size_t)tok * rows, row_base + kTile * wave + 4 * g, rows,
+                                 acc[j], accumulate, vec);
     }
 }
 
