@@ -204,6 +204,8 @@ GEMM_CASES = [(11008, 4096, 1), (11008, 4096, 4), (1024, 4096, 16), (512, 4096, 
               # the fp16 matrix-core kernel (65+ tokens): ragged 128-row and 64-token tiles
               # (32-row tiles below 256 workgroups of 64 rows)
               (300, 1024, 200), (520, 2048, 65), (1100, 4096, 96),
+              # rows % 4 != 0: the epilogue's per-row stores instead of 16-byte ones
+              (301, 1024, 70), (1026, 2048, 96),
               # 64-row tiles (fewer than 256 workgroups of 128 rows)
               (1536, 1024, 512)]
 
