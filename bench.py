@@ -133,17 +133,20 @@ def c3_run(ctx, warmup=10, steps=100):
         return ms, model.weight_bytes_per_token() + 2 * n_layer * pos * kve * 4
 
     ms, nbytes = step_ms(1)
-    # the decoder layer alone: a 2-layer model's step minus the 1-layer model's
-    # (the same embedding, head and argmax in both)
-    ms2, nbytes2 = step_ms(2)
-    lay_us, lay_bytes = (ms2 - ms) * 1e3, nbytes2 - nbytes
     log(f"config 3 layer (1-layer model, vocab 512) decode step @pos {pos}: {ms * 1e3:.1f} us, "
-        f"{nbytes / (ms * 1e-3) / 1e9:.0f} GB/s over {nbytes / 1e6:.1f} MB; the layer alone "
-        f"(2-layer step - 1-layer step): {lay_us:.1f} us, {lay_bytes / (lay_us * 1e-6) / 1e9:.0f} "
-        f"GB/s over {lay_bytes / 1e6:.1f} MB")
+        f"{nbytes / (ms * 1e-3) / 1e9:.0f} GB/s over {nbytes / 1e6:.1f} MB")
+    lay_us = lay_bytes = None
+    if not under_profiler():  # a kernel trace covers the 1-layer model alone
+        # the decoder layer alone: a 2-layer model's step minus the 1-layer
+        # model's (the same embedding, head and argmax in both)
+        ms2, nbytes2 = step_ms(2)
+        lay_us, lay_bytes = (ms2 - ms) * 1e3, nbytes2 - nbytes
+        log(f"config 3 decoder layer alone (2-layer step - 1-layer step): {lay_us:.1f} us, "
+            f"{lay_bytes / (lay_us * 1e-6) / 1e9:.0f} GB/s over {lay_bytes / 1e6:.1f} MB")
     return {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": int(nbytes),
             "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "layer_us": round(lay_us, 2), "layer_bytes": int(lay_bytes),
+            "layer_us": None if lay_us is None else round(lay_us, 2),
+            "layer_bytes": None if lay_bytes is None else int(lay_bytes),
             "what": "decode step of a 1-layer Qwen2.5-3B-like model (vocab 512) at position "
                     "1024: the layer plus embedding, a 512-row head and argmax; layer_us: a "
                     "2-layer model's step minus it (the decoder layer alone)"}
